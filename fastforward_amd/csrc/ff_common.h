@@ -1,0 +1,153 @@
+// Shared device helpers for the gfx950 kernels: rounding to bf16 / e4m3fn,
+// 16-byte vector types, wave64 reductions and the C-ABI status plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ff_amd.h"
+
+namespace ff {
+
+typedef uint16_t bf16_t;  // raw bf16 bits
+
+struct __align__(16) u32x4 { uint32_t x, y, z, w; };
+struct __align__(8) u32x2 { uint32_t x, y; };
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// ------------------------------------------------------------------ bf16
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// fp32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32; NaN stays a
+// quiet NaN).
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+// Round fp32 to the nearest bf16 value and return it as fp32.
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Unpack 8 bf16 (one 16-byte vector) into fp32.
+__device__ __forceinline__ void unpack8(const u32x4 v, float* f) {
+  f[0] = __uint_as_float(v.x << 16); f[1] = __uint_as_float(v.x & 0xFFFF0000u);
+  f[2] = __uint_as_float(v.y << 16); f[3] = __uint_as_float(v.y & 0xFFFF0000u);
+  f[4] = __uint_as_float(v.z << 16); f[5] = __uint_as_float(v.z & 0xFFFF0000u);
+  f[6] = __uint_as_float(v.w << 16); f[7] = __uint_as_float(v.w & 0xFFFF0000u);
+}
+
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  u32x4 v;
+  v.x = pack_bf16x2(f[0], f[1]); v.y = pack_bf16x2(f[2], f[3]);
+  v.z = pack_bf16x2(f[4], f[5]); v.w = pack_bf16x2(f[6], f[7]);
+  return v;
+}
+
+// ------------------------------------------------------------------ e4m3fn
+
+// fp32 -> OCP e4m3fn code, round to nearest even. |x| must already be clamped
+// to <= 448 (the callers clamp, as the reference does before its cast). NaN maps
+// to the NaN code with the sign kept; -0 and negative values that round to zero
+// keep the sign bit. Normal range: drop 20 mantissa bits with RNE after
+// re-biasing the exponent (127 -> 7); subnormal range (|x| < 2^-6): the code is
+// rint(|x| * 2^9), which is exact scaling followed by RNE.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
+  uint32_t u = __float_as_uint(x);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7FFFFFFFu;
+  uint32_t code;
+  if (a > 0x7F800000u) {
+    code = 0x7Fu;
+  } else if (a >= 0x3C800000u) {
+    uint32_t r = a + 0x7FFFFu + ((a >> 20) & 1u);
+    code = (r >> 20) - (120u << 3);
+  } else {
+    code = (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.0f);
+  }
+  return sign | code;
+}
+
+__device__ __forceinline__ float clamp448(float v) {
+  // fminf/fmaxf would drop a NaN; keep it so it encodes as NaN like torch's clamp.
+  return v != v ? v : fminf(448.0f, fmaxf(-448.0f, v));
+}
+
+// ------------------------------------------------------------------ reductions
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Block-wide sum / max over NW waves; every thread gets the result.
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) s += red[i];
+  return s;
+}
+
+template <int NW>
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float s = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) s = fmaxf(s, red[i]);
+  return s;
+}
+
+// 1/sqrt with correctly rounded sqrt and divide (matches 1/std::sqrt on the host).
+__device__ __forceinline__ float rsqrt_rn(float v) { return 1.0f / __builtin_sqrtf(v); }
+
+}  // namespace ff
+
+// ------------------------------------------------------------------ host side
+
+void ff_set_error(const char* fmt, ...);
+
+#define FF_REQUIRE(cond, ...)          \
+  do {                                 \
+    if (!(cond)) {                     \
+      ff_set_error(__VA_ARGS__);       \
+      return FF_EINVAL;                \
+    }                                  \
+  } while (0)
+
+#define FF_LAUNCH_CHECK(what)                                               \
+  do {                                                                      \
+    hipError_t e_ = hipGetLastError();                                      \
+    if (e_ != hipSuccess) {                                                 \
+      ff_set_error("%s: launch failed: %s", what, hipGetErrorString(e_));   \
+      return FF_ELAUNCH;                                                    \
+    }                                                                       \
+  } while (0)
+
+static inline bool ff_aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }

@@ -1,0 +1,144 @@
+"""Linear-op protocol of the reference on gfx950 GEMMs.
+
+An op is a callable ``op(x) -> y2d`` with ``op.weight`` (N,K) (its ``.shape`` is
+read by ``Linear.apply``), used through ``Linear.apply(x, op)``
+(scaled_qwen_runtime.py:35-39). Three families, each keeping the reference's
+attributes:
+
+* ``FP8Linear``: per-token dynamic activation scale, per-output-channel weight
+  scale (_legacy/fp8_private.py:21-38) -- the measured configuration.
+* ``StaticFP8Linear`` / ``RuntimeScaleLinear``: per-tensor weight scale and a
+  static activation scale ``input_scale`` = 1/``inverse_scale`` from a
+  calibration profile (_legacy/limit_kernels.py:110-135, _family/depth_fp8.py:22-26).
+* ``Int4``: W4A16 with nibble codes and [K/g, N, 2] (scale, zero) pairs
+  (_family/night_runtime.py:15-42); symmetric group-128 or the reference's
+  asymmetric group-32 quantizer.
+
+Weight quantization runs once on the GPU at construction. All calls allocate
+their outputs with torch.empty and launch on the current stream.
+"""
+import types
+
+import torch
+
+from ._lib import call, ptr, stream
+
+E4M3 = torch.float8_e4m3fn
+BF16 = torch.bfloat16
+
+
+def _rows(x):
+    return x.reshape(-1, x.shape[-1])
+
+
+class Linear:
+    @staticmethod
+    def apply(x, op):
+        """``Linear.apply`` (scaled_qwen_runtime.py:35-39), forward only."""
+        return op(x).reshape(*x.shape[:-1], op.weight.shape[0])
+
+
+class FP8Linear:
+    """Per-channel e4m3 weights + per-token dynamic activation quant
+    (_legacy/fp8_private.py:21-38). ``scale`` is (1, N) fp32 as in the reference."""
+
+    def __init__(self, weight):
+        assert weight.is_cuda and weight.ndim == 2 and weight.shape[0] % 16 == weight.shape[1] % 16 == 0
+        w = weight.detach().to(BF16).contiguous()
+        n, k = w.shape
+        self.weight = torch.empty((n, k), device=w.device, dtype=E4M3)
+        scale = torch.empty((n,), device=w.device, dtype=torch.float32)
+        call("ff_quant_weight_fp8", ptr(w), ptr(self.weight), ptr(scale), None, n, k, 1, stream())
+        self.scale = scale.reshape(1, n)
+
+    def quantize(self, x):
+        """Per-token e4m3 codes and scales of x (2-D view, bf16)."""
+        flat = _rows(x)
+        if flat.stride(-1) != 1:
+            flat = flat.contiguous()
+        m, k = flat.shape
+        q = torch.empty((m, k), device=x.device, dtype=E4M3)
+        s = torch.empty((m,), device=x.device, dtype=torch.float32)
+        call("ff_quant_rows_fp8", ptr(flat), flat.stride(0), ptr(q), ptr(s), m, k, stream())
+        return q, s
+
+    def gemm(self, q, s, out=None):
+        """y = bf16(q_a . W^T * s_a * s_w) from pre-quantized activations."""
+        m, k = q.shape
+        n = self.weight.shape[0]
+        y = torch.empty((m, n), device=q.device, dtype=BF16) if out is None else out
+        call("ff_gemm_fp8", ptr(q), ptr(s), 1, ptr(self.weight), ptr(self.scale), 1, ptr(y), y.stride(0),
+             m, n, k, stream())
+        return y
+
+    def __call__(self, x):
+        assert x.is_cuda and x.dtype == BF16
+        q, s = self.quantize(x)
+        return self.gemm(q, s).reshape(*x.shape[:-1], self.weight.shape[0])
+
+
+class StaticFP8Linear:
+    """Per-tensor e4m3 weight scale and a static activation scale
+    (_legacy/limit_kernels.py:110-135). ``input_scale`` is an fp32 (1,) device
+    tensor that callers may update in place (``select``,
+    _family/night_runtime.py:48-54); ``inverse_scale`` is the quant multiplier."""
+
+    def __init__(self, weight, inverse_scale=16.):
+        w = weight.detach().to(BF16).contiguous()
+        n, k = w.shape
+        self.weight = torch.empty((n, k), device=w.device, dtype=E4M3)
+        self.weight_scale = torch.empty((1,), device=w.device, dtype=torch.float32)
+        work = torch.empty((n,), device=w.device, dtype=torch.float32)
+        call("ff_quant_weight_fp8", ptr(w), ptr(self.weight), ptr(self.weight_scale), ptr(work), n, k, 0,
+             stream())
+        self.inverse_scale = inverse_scale
+        self.input_scale = torch.tensor([1. / inverse_scale], device=w.device, dtype=torch.float32)
+        self.fast_accum = True
+
+    def __call__(self, x):
+        flat = _rows(x)
+        if not flat.is_contiguous():
+            flat = flat.contiguous()
+        m, k = flat.shape
+        n = self.weight.shape[0]
+        q = torch.empty((m, k), device=x.device, dtype=E4M3)
+        call("ff_quant_static_fp8", ptr(flat), ptr(q), m, m, k, float(self.inverse_scale), stream())
+        y = torch.empty((m, n), device=x.device, dtype=BF16)
+        call("ff_gemm_fp8", ptr(q), ptr(self.input_scale), 0, ptr(self.weight), ptr(self.weight_scale), 0,
+             ptr(y), n, m, n, k, stream())
+        return y
+
+
+class RuntimeScaleLinear(StaticFP8Linear):
+    """``RuntimeScaleLinear`` (_family/depth_fp8.py:22-26): the activation multiplier is
+    read at call time, so ``select`` can change it without re-building the op.
+    Accumulation is fp32 in every mode (``fast_accum`` is kept as an attribute)."""
+
+
+class Int4:
+    """W4A16 linear (_family/night_runtime.py:15-42). ``symmetric=True`` (default,
+    group 128) stores s = bf16(amax/7) and z = 0; ``symmetric=False`` is the
+    reference's asymmetric min/max quantizer (group 32 there)."""
+
+    def __init__(self, w, group=128, symmetric=True):
+        n, k = w.shape
+        assert n % 8 == 0 and k % 128 == 0 and k % group == 0
+        w = w.detach().to(BF16).contiguous()
+        self.weight = types.SimpleNamespace(shape=(n, k))
+        self.group = group
+        self.symmetric = symmetric
+        self.packed = torch.empty((n, k // 2), device=w.device, dtype=torch.uint8)
+        self.scales = torch.empty((k // group, n, 2), device=w.device, dtype=BF16)
+        call("ff_quant_weight_int4", ptr(w), ptr(self.packed), ptr(self.scales), n, k, group,
+             1 if symmetric else 0, stream())
+
+    def __call__(self, x, out=None):
+        flat = _rows(x)
+        if flat.stride(-1) != 1 or flat.stride(0) % 8:
+            flat = flat.contiguous()
+        m, k = flat.shape
+        n = self.weight.shape[0]
+        y = torch.empty((m, n), device=x.device, dtype=BF16) if out is None else out
+        call("ff_gemm_w4a16", ptr(flat), flat.stride(0), ptr(self.packed), ptr(self.scales), self.group,
+             ptr(y), y.stride(0), m, n, k, stream())
+        return y

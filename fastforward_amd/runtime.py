@@ -1,0 +1,355 @@
+"""Qwen3-VL LM prefill + choice-score step on gfx950 kernels, hipGraph-captured.
+
+Restates ``Runtime.prefix`` / ``attention`` / ``mlp`` (scaled_qwen_runtime.py:143-176)
+and the pick-only tail of the fp8/precise execution modes
+(_family/night_runtime.py:92-105), with graph capture and input refill as in
+``graph`` (_family/night_runtime.py:106-125).
+
+Two step bodies produce identical numbers:
+
+* ``fused`` (FP8Linear weights): every activation buffer is allocated once per
+  token bucket; the per-token e4m3 quantization of each GEMM input is fused into
+  the kernel that produces it (add_rms, fast_norm, swiglu), and V is written
+  transposed by the q/k-norm + rotary kernel. 10 launches per layer.
+* ``generic`` (any linear op): the reference's own op sequence through the
+  drop-in ops of ``fastforward_amd.ops`` and ``Linear.apply``.
+
+Inputs are a bucket-sized token id buffer (zero padded), M-RoPE positions
+(3, T) and the picked row; the step writes the choice logits (n_options,) fp32.
+"""
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import ops
+from ._lib import call, ptr, stream
+from .linear import FP8Linear, Linear
+
+BF16 = torch.bfloat16
+E4M3 = torch.float8_e4m3fn
+
+
+@dataclass(frozen=True)
+class LMConfig:
+    """Language-model dimensions (Qwen3-VL text config)."""
+    name: str
+    layers: int
+    hidden: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    inter: int
+    vocab: int
+    eps: float = 1e-6
+    theta: float = 5e6
+    sections: tuple = (24, 20, 20)
+    tie_embed: bool = False
+
+    @property
+    def scaling(self):
+        return self.head_dim ** -0.5
+
+    @property
+    def qkv_out(self):
+        return (self.heads + 2 * self.kv_heads) * self.head_dim
+
+
+PRESETS = {
+    "qwen3vl-2b": LMConfig("qwen3vl-2b", 28, 2048, 16, 8, 128, 6144, 151936, tie_embed=True),
+    "qwen3vl-8b": LMConfig("qwen3vl-8b", 36, 4096, 32, 8, 128, 12288, 151936),
+    "qwen3vl-32b": LMConfig("qwen3vl-32b", 64, 5120, 64, 8, 128, 25600, 151936),
+}
+
+
+def mrope_positions(prefix_tokens, grid_h, grid_w, total):
+    """M-RoPE position ids (3, total) int64 for a prompt with one image of merged
+    grid (grid_h, grid_w) after ``prefix_tokens`` text tokens, the layout the
+    reference precomputes per bucket with transformers' get_rope_index
+    (_family/depth_runtime.py:45-49): text t -> (t,t,t); image (r,c) ->
+    (s0, s0+r, s0+c); later text continues at s0 + max(gh, gw)."""
+    s0, nv = prefix_tokens, grid_h * grid_w
+    if s0 + nv > total:
+        raise ValueError("image does not fit in the bucket")
+    pos = np.empty((3, total), dtype=np.int64)
+    pos[:, :s0] = np.arange(s0)
+    rows = np.repeat(np.arange(grid_h), grid_w)
+    cols = np.tile(np.arange(grid_w), grid_h)
+    pos[0, s0:s0 + nv] = s0
+    pos[1, s0:s0 + nv] = s0 + rows
+    pos[2, s0:s0 + nv] = s0 + cols
+    pos[:, s0 + nv:] = s0 + max(grid_h, grid_w) + np.arange(total - s0 - nv)
+    return pos
+
+
+def rope_inv_freq(theta, head_dim):
+    """The rotary module's constant ``inv_freq`` buffer, computed once at setup
+    on the host exactly as transformers does at module init (fp32)."""
+    return 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float) / head_dim))
+
+
+@dataclass
+class LayerWeights:
+    input_norm: ops.RMSNorm
+    post_norm: ops.RMSNorm
+    q_norm: ops.RMSNorm
+    k_norm: ops.RMSNorm
+    qkv: object
+    o: object
+    gateup: object
+    down: object
+
+
+@dataclass
+class ModelWeights:
+    embed: torch.Tensor       # (vocab, H) bf16
+    layers: list
+    norm: ops.RMSNorm
+    head: torch.Tensor        # (n_options, H) bf16, option rows of lm_head
+    extra: dict = field(default_factory=dict)
+
+
+class Runtime:
+    """One bucket (T tokens) of the LM step with static device buffers."""
+
+    def __init__(self, cfg, weights, tokens, path=None, visual_rows=0, image_start=0, deep_layers=0):
+        self.cfg, self.w = cfg, weights
+        self.T = tokens
+        self.Tp = (tokens + 63) // 64 * 64
+        dev = weights.embed.device
+        self.dev = dev
+        fp8 = all(isinstance(op, FP8Linear) for L in weights.layers for op in (L.qkv, L.o, L.gateup, L.down))
+        self.path = path or ("fused" if fp8 else "generic")
+        if self.path == "fused" and not fp8:
+            raise ValueError("the fused path needs FP8Linear (per-token / per-channel) weights")
+        T, H, D = tokens, cfg.hidden, cfg.head_dim
+        HQ, HK, I = cfg.heads, cfg.kv_heads, cfg.inter
+        e = lambda *s, dt=BF16: torch.empty(s, device=dev, dtype=dt)  # noqa: E731
+        # static inputs
+        self.ids = torch.zeros(T, device=dev, dtype=torch.int64)
+        self.pos = torch.zeros(3, T, device=dev, dtype=torch.int64)
+        self.pick = torch.zeros(1, device=dev, dtype=torch.int64)
+        if visual_rows and not 0 <= image_start <= tokens - visual_rows:
+            raise ValueError("visual rows do not fit in the bucket")
+        self.nv, self.image_start = visual_rows, image_start
+        self.visual = e(visual_rows, H) if visual_rows else None
+        self.deep = [e(visual_rows, H) for _ in range(deep_layers)] if visual_rows else []
+        self.inv_freq = rope_inv_freq(cfg.theta, D).to(dev)
+        # activations
+        self.cos, self.sin = e(T, D), e(T, D)
+        self.h = [e(T, H), e(T, H)]
+        self.res = e(T, H)
+        self.logits = torch.zeros(weights.head.shape[0], device=dev, dtype=torch.float32)
+        if self.path == "fused":
+            self.xq, self.xs = e(T, H, dt=E4M3), e(T, dt=torch.float32)
+            self.qkv = e(T, cfg.qkv_out)
+            self.yq, self.yk, self.vt = e(HQ, T, D), e(HK, T, D), e(HK, D, self.Tp)
+            self.attn = e(T, HQ * D)
+            self.aq, self.as_ = e(T, HQ * D, dt=E4M3), e(T, dt=torch.float32)
+            self.o = e(T, H)
+            self.pq, self.ps = e(T, H, dt=E4M3), e(T, dt=torch.float32)
+            self.gu = e(T, 2 * I)
+            self.mq, self.ms = e(T, I, dt=E4M3), e(T, dt=torch.float32)
+            self.dn = e(T, H)
+            self.hp = e(1, H)
+        self.graph = None
+        self.graph_out = None
+
+    # ------------------------------------------------------------ inputs
+
+    def set_inputs(self, ids, pos, pick, visual=None, deep=None):
+        """Refill the static inputs (graph replay reads them in place)."""
+        ids = torch.as_tensor(ids, dtype=torch.int64)
+        n = ids.numel()
+        if not 0 < n <= self.T:
+            raise ValueError(f"{n} tokens do not fit the {self.T}-token bucket")
+        if not 0 <= int(pick) < n:
+            raise ValueError("pick must index a real token")
+        if int(ids.min()) < 0 or int(ids.max()) >= self.cfg.vocab:
+            raise ValueError("token id outside the vocabulary")
+        pos = torch.as_tensor(pos, dtype=torch.int64)
+        if pos.shape != (3, self.T):
+            raise ValueError(f"positions must be (3, {self.T})")
+        self.ids.zero_()
+        self.ids[:n].copy_(ids, non_blocking=True)
+        self.pos.copy_(pos, non_blocking=True)
+        self.pick.fill_(int(pick))
+        if visual is not None:
+            self.visual.copy_(visual)
+        for d, src in zip(self.deep, deep or []):
+            d.copy_(src)
+
+    # ------------------------------------------------------------ step bodies
+
+    def _prologue(self):
+        cfg, s = self.cfg, stream()
+        T, H, D = self.T, cfg.hidden, cfg.head_dim
+        h = self.h[0]
+        call("ff_embed", ptr(self.ids), ptr(self.w.embed), ptr(h), T, H, cfg.vocab, s)
+        if self.visual is not None:
+            call("ff_scatter_rows", ptr(self.visual), ptr(h), self.image_start, self.nv, H, s)
+        call("ff_mrope_cos_sin", ptr(self.pos), ptr(self.inv_freq), ptr(self.cos), ptr(self.sin), T, D,
+             cfg.sections[1], cfg.sections[2], s)
+        return h
+
+    def _step_fused(self):
+        cfg, w, s = self.cfg, self.w, stream()
+        T, Tp, H, D = self.T, self.Tp, cfg.hidden, cfg.head_dim
+        HQ, HK, I, eps = cfg.heads, cfg.kv_heads, cfg.inter, cfg.eps
+        h = self._prologue()
+        L = w.layers
+        call("ff_fast_norm_quant", ptr(h), ptr(L[0].input_norm.weight), None, ptr(self.xq), ptr(self.xs), T, H,
+             float(L[0].input_norm.variance_epsilon), s)
+        cur = 0
+        for j in range(cfg.layers - 1):
+            lw = L[j]
+            h = self.h[cur]
+            self._attention_fused(lw, s)
+            call("ff_gemm_fp8", ptr(self.aq), ptr(self.as_), 1, ptr(lw.o.weight), ptr(lw.o.scale), 1, ptr(self.o), H,
+                 T, H, HQ * D, s)
+            call("ff_add_rms_quant", ptr(h), ptr(self.o), None, ptr(lw.post_norm.weight), ptr(self.res), None,
+                 ptr(self.pq), ptr(self.ps), T, H, float(lw.post_norm.variance_epsilon), 0, 0, s)
+            self._mlp_fused(lw, self.pq, self.ps, T, self.dn, s)
+            nxt = self.h[cur ^ 1]
+            deep = self.deep[j] if j < len(self.deep) else None
+            nn = L[j + 1].input_norm
+            call("ff_add_rms_quant", ptr(self.res), ptr(self.dn), ptr(deep), ptr(nn.weight), ptr(nxt), None,
+                 ptr(self.xq), ptr(self.xs), T, H, float(nn.variance_epsilon), self.image_start,
+                 self.nv if deep is not None else 0, s)
+            cur ^= 1
+        # pick-only tail (_family/night_runtime.py:92-105)
+        lw = L[-1]
+        h = self.h[cur]
+        self._attention_fused(lw, s, tail=True)
+        call("ff_gemm_fp8", ptr(self.aq), ptr(self.as_), 1, ptr(lw.o.weight), ptr(lw.o.scale), 1, ptr(self.o), H,
+             1, H, HQ * D, s)
+        call("ff_gather_rows", ptr(h), H, ptr(self.pick), ptr(self.hp), H, 1, H, T, s)
+        call("ff_add_rms_quant", ptr(self.hp), ptr(self.o), None, ptr(lw.post_norm.weight), ptr(self.res), None,
+             ptr(self.pq), ptr(self.ps), 1, H, float(lw.post_norm.variance_epsilon), 0, 0, s)
+        self._mlp_fused(lw, self.pq, self.ps, 1, self.dn, s)
+        call("ff_lm_readout", ptr(self.res), ptr(self.dn), ptr(w.norm.weight), ptr(w.head), ptr(self.logits), H,
+             w.head.shape[0], float(w.norm.variance_epsilon), s)
+        return self.logits
+
+    def _attention_fused(self, lw, s, tail=False):
+        cfg = self.cfg
+        T, Tp, H, D = self.T, self.Tp, cfg.hidden, cfg.head_dim
+        HQ, HK = cfg.heads, cfg.kv_heads
+        n3 = cfg.qkv_out
+        call("ff_gemm_fp8", ptr(self.xq), ptr(self.xs), 1, ptr(lw.qkv.weight), ptr(lw.qkv.scale), 1, ptr(self.qkv),
+             n3, T, n3, H, s)
+        base = self.qkv.data_ptr()
+        esz = 2
+        call("ff_qkv_post", base, base + HQ * D * esz, base + (HQ + HK) * D * esz, n3,
+             ptr(lw.q_norm.weight), ptr(lw.k_norm.weight), float(lw.q_norm.variance_epsilon),
+             float(lw.k_norm.variance_epsilon), ptr(self.cos), ptr(self.sin), ptr(self.yq), ptr(self.yk),
+             ptr(self.vt), T, Tp, HQ, HK, D, s)
+        if tail:
+            call("ff_attention_vt", ptr(self.yq), ptr(self.yk), ptr(self.vt), ptr(self.pick), 1, ptr(self.attn),
+                 1, T, Tp, HQ, HK, D, float(cfg.scaling), s)
+            call("ff_quant_rows_fp8", ptr(self.attn), HQ * D, ptr(self.aq), ptr(self.as_), 1, HQ * D, s)
+        else:
+            call("ff_attention_vt", ptr(self.yq), ptr(self.yk), ptr(self.vt), None, 0, ptr(self.attn), T, T, Tp,
+                 HQ, HK, D, float(cfg.scaling), s)
+            call("ff_quant_rows_fp8", ptr(self.attn), HQ * D, ptr(self.aq), ptr(self.as_), T, HQ * D, s)
+
+    def _mlp_fused(self, lw, q, sc, m, out, s):
+        I, H = self.cfg.inter, self.cfg.hidden
+        call("ff_gemm_fp8", ptr(q), ptr(sc), 1, ptr(lw.gateup.weight), ptr(lw.gateup.scale), 1, ptr(self.gu),
+             2 * I, m, 2 * I, H, s)
+        base = self.gu.data_ptr()
+        call("ff_swiglu_quant", base, base + I * 2, 2 * I, None, ptr(self.mq), ptr(self.ms), m, I, s)
+        call("ff_gemm_fp8", ptr(self.mq), ptr(self.ms), 1, ptr(lw.down.weight), ptr(lw.down.scale), 1, ptr(out), H,
+             m, H, I, s)
+
+    def _step_generic(self):
+        """The reference's op sequence (scaled_qwen_runtime.py:143-176,
+        _family/night_runtime.py:92-105) through the drop-in ops."""
+        cfg, w = self.cfg, self.w
+        HQ, HK, D = cfg.heads, cfg.kv_heads, cfg.head_dim
+        h = self._prologue()[None]
+        cos, sin = self.cos[None], self.sin[None]
+        L = w.layers
+        normalized = ops.fast_norm(h, L[0].input_norm)
+        for j in range(cfg.layers - 1):
+            lw = L[j]
+            attn = self._attention_generic(lw, normalized, cos, sin)
+            residual, post = ops.add_rms(h, attn, None, lw.post_norm)
+            g, u = Linear.apply(post, lw.gateup).chunk(2, -1)
+            value = Linear.apply(ops.swiglu(g, u), lw.down)
+            deep = self.deep[j] if j < len(self.deep) else None
+            h, normalized = ops.add_rms(residual, value, deep, L[j + 1].input_norm, self.image_start,
+                                        self.nv if deep is not None else 0)
+        lw = L[-1]
+        x = ops.fast_norm(h, lw.input_norm)
+        q, k, v = Linear.apply(x, lw.qkv).split([HQ * D, HK * D, HK * D], -1)
+        shape = (*x.shape[:-1], -1, D)
+        q, k = ops.qk_pair(q.view(shape), k.view(shape), lw.q_norm, lw.k_norm, cos, sin)
+        v = v.view(shape).transpose(1, 2)
+        query = self._index_rows(q[0], self.pick)[None]            # q.index_select(2, pick)
+        out = ops.attention_direct(query, k, v, cfg.scaling, positions=self.pick)
+        value = Linear.apply(out.reshape(1, 1, -1), lw.o)
+        hp = self._index_rows(h[0], self.pick, dim1=True)           # h.index_select(1, pick)
+        residual, post = ops.add_rms(hp, value, None, lw.post_norm)
+        g, u = Linear.apply(post[0], lw.gateup).chunk(2, -1)
+        mlp = Linear.apply(ops.swiglu(g, u), lw.down)
+        y = torch.empty((1, w.head.shape[0]), device=self.dev, dtype=torch.float32)
+        call("ff_lm_readout", ptr(residual), ptr(mlp), ptr(w.norm.weight), ptr(w.head), ptr(y), cfg.hidden,
+             w.head.shape[0], float(w.norm.variance_epsilon), stream())
+        self.logits.copy_(y[0])
+        return self.logits
+
+    def _attention_generic(self, lw, x, cos, sin):
+        cfg = self.cfg
+        HQ, HK, D = cfg.heads, cfg.kv_heads, cfg.head_dim
+        q, k, v = Linear.apply(x, lw.qkv).split([HQ * D, HK * D, HK * D], -1)
+        shape = (*x.shape[:-1], -1, D)
+        q, k = ops.qk_pair(q.view(shape), k.view(shape), lw.q_norm, lw.k_norm, cos, sin)
+        v = v.view(shape).transpose(1, 2)
+        out = ops.attention_direct(q, k, v, cfg.scaling)
+        return Linear.apply(out.reshape(*x.shape[:-1], -1), lw.o)
+
+    def _index_rows(self, x, idx, dim1=False):
+        """Rows ``idx`` of x along its token axis on the device (index_select);
+        x is (heads, T, D) or, with dim1, (1, T, H) -> (1, n, H)."""
+        if dim1:
+            x2 = x.reshape(-1, x.shape[-1])
+            out = torch.empty((1, idx.numel(), x2.shape[-1]), device=x.device, dtype=x.dtype)
+            call("ff_gather_rows", ptr(x2), x2.stride(0), ptr(idx), ptr(out), x2.shape[-1], idx.numel(),
+                 x2.shape[-1], x2.shape[0], stream())
+            return out
+        heads, t, d = x.shape
+        out = torch.empty((heads, idx.numel(), d), device=x.device, dtype=x.dtype)
+        for hh in range(heads):
+            call("ff_gather_rows", x[hh].data_ptr(), d, ptr(idx), out[hh].data_ptr(), d, idx.numel(), d, t,
+                 stream())
+        return out
+
+    def step(self):
+        """Run the step eagerly on the current stream; returns the logits buffer."""
+        return self._step_fused() if self.path == "fused" else self._step_generic()
+
+    # ------------------------------------------------------------ hipGraph
+
+    def capture(self, warmup=2):
+        """Capture the whole step into one hipGraph (torch.cuda.CUDAGraph is a
+        hipGraph on ROCm). The inputs of the last ``set_inputs`` are used for the
+        warmup runs; replays read the static input buffers in place."""
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                self.step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = self.step()
+        self.graph, self.graph_out = g, out
+        return g
+
+    def replay(self):
+        if self.graph is None:
+            self.capture()
+        self.graph.replay()
+        return self.graph_out

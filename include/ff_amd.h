@@ -1,0 +1,186 @@
+/*
+ * ff_amd.h — C ABI of the MI355X (gfx950) Qwen3-VL LM-step kernels.
+ *
+ * Every entry point takes raw device pointers, sizes, strides and scalars plus an
+ * explicit HIP stream (ff_stream_t, a hipStream_t; NULL = the null stream). None
+ * of them allocates device memory, synchronises the host or picks a grid size
+ * from device data, so all of them may be captured into a hipGraph. Tensors are
+ * bf16 (raw 16-bit), e4m3fn (raw 8-bit) or fp32 unless stated. Returns FF_OK or a
+ * negative status; ff_last_error() then holds a message for the calling thread.
+ *
+ * Reference paths are relative to FastForward's src/fastforward_accel/.
+ */
+#ifndef FF_AMD_H
+#define FF_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* ff_stream_t;
+
+#define FF_OK 0
+#define FF_EINVAL (-1)   /* bad shape, stride, alignment or argument */
+#define FF_ELAUNCH (-2)  /* kernel launch failed */
+#define FF_EDEVICE (-3)  /* no usable gfx950 device */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int ff_version(void);
+/* Message for the last failing call on this thread ("" if none). */
+const char* ff_last_error(void);
+/* FF_OK if the current HIP device is a gfx950 (MI355X). */
+int ff_device_check(void);
+
+/* fast_norm(x, module): out = bf16(bf16(x*rsqrt(sum(x^2)/h + eps)) * w), one row
+ * per token. Replaces _legacy/sub10_runtime.py:37 (fast_norm / rms_one :31-36).
+ * x, out: (rows, h) contiguous, h % 8 == 0, h <= 16384. */
+int ff_fast_norm(const void* x, const void* w, void* out, int64_t rows, int64_t h, float eps,
+                 ff_stream_t stream);
+
+/* add_rms(a, b, deep, module, start, nv) -> (residual, out): x = bf16(a+b); rows
+ * r in [start, start+nv) add bf16(x + deep[r-start]) when deep != NULL; residual
+ * = x; out = bf16(bf16(x*rsqrt(mean(x^2)+eps))*w). Replaces
+ * _legacy/lower_kernels.py:24 (kernel :7-21) and _legacy/broad_kernels.py:9. */
+int ff_add_rms(const void* a, const void* b, const void* deep, const void* w, void* residual,
+               void* out, int64_t rows, int64_t h, float eps, int64_t start, int64_t nv,
+               ff_stream_t stream);
+
+/* Fused producer variants (no reference counterpart as separate ops; same
+ * arithmetic as ff_add_rms / ff_fast_norm followed by ff_quant_rows_fp8 on
+ * `out`): additionally write the per-token e4m3 codes q (rows, h) and fp32
+ * scales (rows) of the normalised output. `out` may be NULL to skip the bf16
+ * normalised output. */
+int ff_add_rms_quant(const void* a, const void* b, const void* deep, const void* w, void* residual,
+                     void* out, void* q, float* scales, int64_t rows, int64_t h, float eps,
+                     int64_t start, int64_t nv, ff_stream_t stream);
+int ff_fast_norm_quant(const void* x, const void* w, void* out, void* q, float* scales,
+                       int64_t rows, int64_t h, float eps, ff_stream_t stream);
+
+/* qk_pair(q, k, qn, kn, cos, sin): per (token, head) RMSNorm over d with weight
+ * wq / wk, then rotate-half M-RoPE: y = bf16(bf16(x*cos) + bf16(rot(x)*sin)).
+ * q (t, hq, d) and k (t, hk, d) are strided views with token stride `row_stride`
+ * elements (e.g. the packed QKV output); cos/sin (t, d) with strides
+ * (cos_ts, cos_ds). Writes yq (hq, t, d), yk (hk, t, d) contiguous.
+ * Replaces _legacy/broad_kernels.py:63 (kernel _legacy/lower_kernels.py:66-98).
+ * d == 128. */
+int ff_qk_pair(const void* q, const void* k, int64_t row_stride, const void* wq, const void* wk,
+               float eps_q, float eps_k, const void* cos, const void* sin, int64_t cos_ts,
+               int64_t cos_ds, int64_t sin_ts, int64_t sin_ds, void* yq, void* yk, int64_t t,
+               int64_t hq, int64_t hk, int64_t d, ff_stream_t stream);
+
+/* Fused q/k/v post-processing for the layer loop: ff_qk_pair plus a transposed
+ * copy of v (hk, d, t_pad) with keys contiguous and zeros for keys in [t, t_pad),
+ * the layout ff_attention_vt consumes. v is the strided view (t, hk, d) with the
+ * same token stride. t_pad % 64 == 0, t_pad >= t. */
+int ff_qkv_post(const void* q, const void* k, const void* v, int64_t row_stride, const void* wq,
+                const void* wk, float eps_q, float eps_k, const void* cos, const void* sin,
+                void* yq, void* yk, void* vt, int64_t t, int64_t t_pad, int64_t hq, int64_t hk,
+                int64_t d, ff_stream_t stream);
+
+/* Transposed copy of v (t, hk, d) [token stride v_ts, head stride v_hs] into
+ * vt (hk, d, t_pad), zero-filling keys >= t. */
+int ff_v_transpose(const void* v, int64_t v_ts, int64_t v_hs, void* vt, int64_t t, int64_t t_pad,
+                   int64_t hk, int64_t d, ff_stream_t stream);
+
+/* swiglu(gate, up): y = bf16(bf16(g/(1+exp(-g))) * u). g, u: (rows, i) views with
+ * row stride `row_stride` elements; y (rows, i) contiguous. Replaces
+ * _legacy/search_kernels.py:18 (kernel :8-15). i % 8 == 0. */
+int ff_swiglu(const void* g, const void* u, int64_t row_stride, void* y, int64_t rows, int64_t i,
+              ff_stream_t stream);
+/* swiglu followed by per-token e4m3 quant of y (codes q (rows, i), scales (rows)).
+ * y may be NULL. */
+int ff_swiglu_quant(const void* g, const void* u, int64_t row_stride, void* y, void* q,
+                    float* scales, int64_t rows, int64_t i, ff_stream_t stream);
+
+/* attention_direct(q, k, v, scale, positions=None, triangular=True): causal GQA
+ * attention with fp32 scores/softmax statistics, P rounded to bf16 before P.V,
+ * fp32 accumulation. q (hq, s, d) contiguous, k (hk, t, d) contiguous, vt the
+ * transposed v (hk, d, t_pad) from ff_qkv_post / ff_v_transpose. positions
+ * (int64, s) gives each query's position (SELECTED mode) or NULL for row i at
+ * position i. With gather_q != 0, q is (hq, t, d) and query i reads q row
+ * positions[i] (the tail's q.index_select(2, pick) fused in). y (s, hq, d).
+ * Replaces _legacy/limit_kernels.py:36 (kernel :8-33). d == 128, hq % hk == 0. */
+int ff_attention_vt(const void* q, const void* k, const void* vt, const int64_t* positions,
+                    int gather_q, void* y, int64_t s, int64_t t, int64_t t_pad, int64_t hq,
+                    int64_t hk, int64_t d, float scale, ff_stream_t stream);
+
+/* lm_readout(x, norm, weight): x_hat = bf16(bf16(x*rsqrt(mean(x^2)+eps))*w);
+ * y[c] = bf16(sum_k x_hat_k * head[c,k]) stored as fp32. If x2 != NULL the
+ * input row is bf16(x + x2) (the tail's `residual + mlp` add). x (h), head
+ * (n_opt, h) contiguous, h <= 8192; y (n_opt) fp32. Replaces _legacy/limit_kernels.py:60
+ * (kernel :48-57). */
+int ff_lm_readout(const void* x, const void* x2, const void* norm_w, const void* head, float* y,
+                  int64_t h, int64_t n_opt, float eps, ff_stream_t stream);
+
+/* Per-token dynamic activation quant: scale[m] = max(amax_k|x[m,k]|, 1e-12)/448,
+ * q = e4m3(clamp(x/scale, +-448)). x (rows, k) with row stride x_rs elements.
+ * Replaces quantize_rows, _legacy/fp8_private.py:11-18. */
+int ff_quant_rows_fp8(const void* x, int64_t x_rs, void* q, float* scales, int64_t rows, int64_t k,
+                      ff_stream_t stream);
+
+/* Static per-tensor activation quant: q = e4m3(clamp(x*inv, +-448)) for the first
+ * `rows` rows; rows in [rows, rows_pad) are written as zero codes. Replaces
+ * _runtime_scale / quantize_runtime, _family/depth_fp8.py:8-19. */
+int ff_quant_static_fp8(const void* x, void* q, int64_t rows, int64_t rows_pad, int64_t k,
+                        float inv, ff_stream_t stream);
+
+/* Setup-time weight quant. per_channel != 0: scale[n] = max(amax_k|W[n,k]|,
+ * 1e-12)/448 (FP8Linear.__init__, _legacy/fp8_private.py:22-27); else one scale
+ * for the tensor (StaticFP8Linear.__init__, _legacy/limit_kernels.py:122-127),
+ * which needs a caller-provided fp32 workspace of n floats (row amax).
+ * q = e4m3(clamp(W/scale, +-448)). w (n, k) bf16 contiguous. */
+int ff_quant_weight_fp8(const void* w, void* q, float* scale, float* workspace, int64_t n,
+                        int64_t k, int per_channel, ff_stream_t stream);
+
+/* FP8 GEMM: y (m, n) bf16 = bf16(sum_k qa[m,k]*qw[n,k] * sa * sw) with fp32
+ * accumulation (torch._scaled_mm as called at _legacy/fp8_private.py:36 and
+ * _family/depth_fp8.py:25). qa (m, k) and qw (n, k) e4m3 row-major; sa is per-row
+ * (m floats) if sa_rows else one float; sw is per-column (n floats) if sw_cols
+ * else one float. y row stride ldy elements. k % 128 == 0. */
+int ff_gemm_fp8(const void* qa, const float* sa, int sa_rows, const void* qw, const float* sw,
+                int sw_cols, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
+                ff_stream_t stream);
+
+/* Setup-time int4 quant of w (n, k) bf16 into packed nibbles (n, k/2) (even k in
+ * the high nibble) and scales [k/group, n, 2] bf16 (scale, zero).
+ * symmetric != 0: s = bf16(max(amax|w|,1e-6)/7), q = clamp(rint(w/s)+8, 0, 15),
+ * zero = 0. symmetric == 0: the reference's asymmetric min/max form
+ * (Int4.__init__, _family/night_runtime.py:16-26). */
+int ff_quant_weight_int4(const void* w, void* packed, void* scales, int64_t n, int64_t k,
+                         int64_t group, int symmetric, ff_stream_t stream);
+
+/* W4A16 GEMM: y (m, n) bf16 = x (m, k) bf16 @ dequant(W)^T with dequant
+ * w = (q-8)*s + z fused into the B-operand load, fp32 accumulation (Int4.__call__,
+ * _family/night_runtime.py:31-42). x row stride ldx; k % 128 == 0,
+ * group % 32 == 0. */
+int ff_gemm_w4a16(const void* x, int64_t ldx, const void* packed, const void* scales,
+                  int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
+                  ff_stream_t stream);
+
+/* Embedding gather h[t] = table[ids[t]] (scaled_qwen_runtime.py:145
+ * embed_tokens). Ids outside [0, vocab) read row 0 (the host validates ids). */
+int ff_embed(const int64_t* ids, const void* table, void* out, int64_t t, int64_t h,
+             int64_t vocab, ff_stream_t stream);
+
+/* Copy rows: out[i] = src[idx[i]] for i < n (index_copy / index_select of the
+ * layer loop, scaled_qwen_runtime.py:145, _family/night_runtime.py:100,103).
+ * Row width `width` elements of 2 bytes; src/out row strides in elements. */
+int ff_gather_rows(const void* src, int64_t src_rs, const int64_t* idx, void* out, int64_t out_rs,
+                   int64_t n, int64_t width, int64_t src_rows, ff_stream_t stream);
+/* out[start + i] = src[i] for i < n (visual rows into the embedding). */
+int ff_scatter_rows(const void* src, void* out, int64_t start, int64_t n, int64_t width,
+                    ff_stream_t stream);
+
+/* M-RoPE cos/sin (lm.rotary_emb, scaled_qwen_runtime.py:145): pos (3, t) int64,
+ * inv_freq (d/2) fp32; slot i of the half uses the H position if i%3==1 and
+ * i < 3*sec_h, W if i%3==2 and i < 3*sec_w, else T; emb = cat(f, f);
+ * cos/sin (t, d) bf16. */
+int ff_mrope_cos_sin(const int64_t* pos, const float* inv_freq, void* cos, void* sin, int64_t t,
+                     int64_t d, int sec_h, int sec_w, ff_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FF_AMD_H */

@@ -1,0 +1,56 @@
+"""CPU checks of the C ABI: the library loads without a GPU, exports every
+function include/ff_amd.h declares, and the ctypes binding agrees with the
+header on names and parameter counts. No compute call is made."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ff_amd.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"(?:int|const char\*)\s+(ff_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = m.group(2).strip()
+        n = 0 if params in ("", "void") else len(params.split(","))
+        decls[m.group(1)] = n
+    return decls
+
+
+@pytest.fixture(scope="module")
+def lib_path():
+    from fastforward_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        from fastforward_amd import build
+        build.build(verbose=False)
+    return _lib.LIB_PATH
+
+
+def test_header_declares_entry_points():
+    d = _declared()
+    assert len(d) >= 24
+    for name in ("ff_gemm_fp8", "ff_gemm_w4a16", "ff_attention_vt", "ff_add_rms", "ff_qk_pair",
+                 "ff_swiglu", "ff_fast_norm", "ff_lm_readout"):
+        assert name in d
+
+
+def test_library_exports_every_declared_symbol(lib_path):
+    lib = ctypes.CDLL(lib_path)
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_binding_matches_header(lib_path):
+    from fastforward_amd import _lib
+    d = _declared()
+    assert set(d) == set(_lib.SIGNATURES)
+    for name, n in d.items():
+        assert len(_lib.SIGNATURES[name]) == n, name
+    lib = _lib.load()
+    assert lib.ff_version() >= 100
+    assert lib.ff_last_error() == b""

@@ -1,0 +1,373 @@
+"""Per-op parity of the gfx950 kernels against the CPU oracle on seeded inputs.
+
+Tolerances (stated per op):
+* bit-exact: add_rms residual, e4m3 activation / weight quantization codes and
+  scales given the same bf16 input, int4 codes and scale indexing, embedding
+  gather, fused-vs-unfused producers, V^T transposition.
+* <= 1 bf16 ulp, exact for all but a small fraction: RMSNorm outputs, q/k norm
+  + rotary, SwiGLU, FP8 GEMM (the exact product is the same; only the fp32
+  summation order differs), readout, M-RoPE tables.
+* attention: |gpu - oracle| <= 1/64 absolute (values are O(1)) and relative RMS
+  <= 0.5% (the block-online softmax rounds P to bf16 at different running maxima).
+* W4A16 GEMM: relative RMS <= 0.5% vs the fp32-dequant product (the reference's own
+  operator bar is 1%), bit-exact dequantized weights through one-hot rows.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import ops as O
+from tests.helpers import assert_bf16_close, bf16_ulps
+
+pytestmark = pytest.mark.gpu
+
+BF16 = torch.bfloat16
+DEV = "cuda"
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _norm_module(h, seed, jitter=0.1):
+    from fastforward_amd.ops import RMSNorm
+    w = (1 + jitter * torch.randn(h, generator=_g(seed))).to(BF16)
+    return RMSNorm(w.to(DEV), 1e-6), w
+
+
+# ------------------------------------------------------------------ norms
+
+@pytest.mark.parametrize("t,h", [(320, 2048), (576, 4096), (37, 5120)])
+def test_fast_norm(gpu, t, h):
+    from fastforward_amd import ops
+    x = (torch.randn(1, t, h, generator=_g(1)) * 3).to(BF16)
+    mod, w = _norm_module(h, 2)
+    got = ops.fast_norm(x.to(DEV), mod).cpu()
+    want = O.fast_norm(x, w, 1e-6)
+    assert_bf16_close(got, want, 1, 2e-3, "fast_norm")
+
+
+@pytest.mark.parametrize("deep", [False, True])
+@pytest.mark.parametrize("t,h", [(576, 4096), (320, 2048), (17, 5120)])
+def test_add_rms(gpu, t, h, deep):
+    from fastforward_amd import ops
+    a = torch.randn(1, t, h, generator=_g(3)).to(BF16)
+    b = torch.randn(1, t, h, generator=_g(4)).to(BF16)
+    mod, w = _norm_module(h, 5)
+    start, nv = (2, min(10, t - 2)) if deep else (0, 0)
+    dp = torch.randn(nv, h, generator=_g(6)).to(BF16) if deep else None
+    res, out = ops.add_rms(a.to(DEV), b.to(DEV), dp.to(DEV) if deep else None, mod, start, nv)
+    rw, ow = O.add_rms(a, b, dp, w, 1e-6, start, nv)
+    assert torch.equal(res.cpu(), rw), "residual must be bit-exact"
+    assert_bf16_close(out.cpu(), ow, 1, 2e-3, "add_rms out")
+
+
+def test_add_rms_quant_equals_unfused(gpu):
+    from fastforward_amd import ops, _lib
+    from fastforward_amd._lib import call, ptr, stream
+    t, h = 576, 4096
+    a = torch.randn(t, h, generator=_g(7)).to(BF16).to(DEV)
+    b = torch.randn(t, h, generator=_g(8)).to(BF16).to(DEV)
+    b[3] *= 50                                                   # an outlier row
+    mod, _ = _norm_module(h, 9)
+    dp = torch.randn(20, h, generator=_g(10)).to(BF16).to(DEV)
+    res0, out0 = ops.add_rms(a, b, dp, mod, 5, 20)
+    res = torch.empty_like(a)
+    out = torch.empty_like(a)
+    q = torch.empty(t, h, device=DEV, dtype=torch.float8_e4m3fn)
+    s = torch.empty(t, device=DEV)
+    call("ff_add_rms_quant", ptr(a), ptr(b), ptr(dp), ptr(mod.weight), ptr(res), ptr(out), ptr(q), ptr(s),
+         t, h, 1e-6, 5, 20, stream())
+    assert torch.equal(res, res0) and torch.equal(out, out0)
+    qw, sw = O.quant_rows_dynamic(out0.cpu())
+    assert torch.equal(q.view(torch.uint8).cpu(), qw.view(torch.uint8))
+    assert torch.equal(s.cpu(), sw)
+    # fast_norm_quant without the bf16 output
+    q2 = torch.empty_like(q)
+    s2 = torch.empty_like(s)
+    call("ff_fast_norm_quant", ptr(res0), ptr(mod.weight), None, ptr(q2), ptr(s2), t, h, 1e-6, stream())
+    qn, sn = O.quant_rows_dynamic(ops.fast_norm(res0, mod).cpu())
+    assert torch.equal(q2.view(torch.uint8).cpu(), qn.view(torch.uint8)) and torch.equal(s2.cpu(), sn)
+    _ = _lib
+
+
+# ------------------------------------------------------------------ rotary
+
+def _packed_qkv(t, hq, hk, d, seed):
+    return (torch.randn(1, t, (hq + 2 * hk) * d, generator=_g(seed)) * 2).to(BF16)
+
+
+@pytest.mark.parametrize("t,hq,hk", [(576, 32, 8), (320, 16, 8), (33, 64, 8)])
+def test_qk_pair(gpu, t, hq, hk):
+    from fastforward_amd import ops
+    d = 128
+    packed = _packed_qkv(t, hq, hk, d, 11)
+    qn, wq = _norm_module(d, 12, 0.3)
+    kn, wk = _norm_module(d, 13, 0.3)
+    pos = O.mrope_positions(4, 4, 6, t) if t >= 28 else torch.arange(t).expand(3, t).clone()
+    cos, sin = O.mrope_cos_sin(pos, 5e6, d)
+    pg = packed.to(DEV)
+    q = pg[..., : hq * d].view(1, t, hq, d)
+    k = pg[..., hq * d:(hq + hk) * d].view(1, t, hk, d)
+    yq, yk = ops.qk_pair(q, k, qn, kn, cos.to(DEV), sin.to(DEV))
+    wq_, wk_ = O.qk_pair(packed[..., : hq * d].view(1, t, hq, d), packed[..., hq * d:(hq + hk) * d].view(1, t, hk, d),
+                         wq, wk, 1e-6, 1e-6, cos, sin)
+    assert_bf16_close(yq.cpu(), wq_, 1, 2e-3, "qk_pair q")
+    assert_bf16_close(yk.cpu(), wk_, 1, 2e-3, "qk_pair k")
+
+
+def test_qkv_post_matches_qk_pair_and_transposes_v(gpu):
+    from fastforward_amd import ops
+    from fastforward_amd._lib import call, ptr, stream
+    t, hq, hk, d = 300, 32, 8, 128
+    tp = 320
+    packed = _packed_qkv(t, hq, hk, d, 14).to(DEV)[0]
+    qn, _ = _norm_module(d, 15, 0.3)
+    kn, _ = _norm_module(d, 16, 0.3)
+    cos, sin = O.mrope_cos_sin(O.mrope_positions(4, 8, 8, t), 5e6, d)
+    cos, sin = cos[0].to(DEV), sin[0].to(DEV)
+    yq = torch.empty(hq, t, d, device=DEV, dtype=BF16)
+    yk = torch.empty(hk, t, d, device=DEV, dtype=BF16)
+    vt = torch.full((hk, d, tp), float("nan"), device=DEV, dtype=BF16)
+    base, n3 = packed.data_ptr(), (hq + 2 * hk) * d
+    call("ff_qkv_post", base, base + hq * d * 2, base + (hq + hk) * d * 2, n3, ptr(qn.weight), ptr(kn.weight),
+         1e-6, 1e-6, ptr(cos), ptr(sin), ptr(yq), ptr(yk), ptr(vt), t, tp, hq, hk, d, stream())
+    q = packed[:, : hq * d].view(1, t, hq, d)
+    k = packed[:, hq * d:(hq + hk) * d].view(1, t, hk, d)
+    rq, rk = ops.qk_pair(q, k, qn, kn, cos[None], sin[None])
+    assert torch.equal(yq, rq[0]) and torch.equal(yk, rk[0])
+    v = packed[:, (hq + hk) * d:].view(t, hk, d)
+    assert torch.equal(vt[:, :, :t], v.permute(1, 2, 0))
+    assert torch.all(vt[:, :, t:] == 0)
+
+
+# ------------------------------------------------------------------ swiglu
+
+@pytest.mark.parametrize("t,i", [(576, 12288), (1, 12288), (320, 6144)])
+def test_swiglu(gpu, t, i):
+    from fastforward_amd import ops
+    gu = (torch.randn(t, 2 * i, generator=_g(17)) * 3).to(BF16)
+    g, u = gu.to(DEV).chunk(2, -1)
+    got = ops.swiglu(g, u).cpu()
+    want = O.swiglu(*gu.chunk(2, -1))
+    assert_bf16_close(got, want, 1, 5e-3, "swiglu")
+
+
+def test_swiglu_quant_equals_unfused(gpu):
+    from fastforward_amd import ops
+    from fastforward_amd._lib import call, ptr, stream
+    t, i = 200, 12288
+    gu = (torch.randn(t, 2 * i, generator=_g(18)) * 3).to(BF16).to(DEV)
+    g, u = gu.chunk(2, -1)
+    y0 = ops.swiglu(g, u)
+    y = torch.empty_like(y0)
+    q = torch.empty(t, i, device=DEV, dtype=torch.float8_e4m3fn)
+    s = torch.empty(t, device=DEV)
+    call("ff_swiglu_quant", ptr(g), ptr(u), 2 * i, ptr(y), ptr(q), ptr(s), t, i, stream())
+    assert torch.equal(y, y0)
+    qw, sw = O.quant_rows_dynamic(y0.cpu())
+    assert torch.equal(q.view(torch.uint8).cpu(), qw.view(torch.uint8)) and torch.equal(s.cpu(), sw)
+
+
+# ------------------------------------------------------------------ quantization
+
+@pytest.mark.parametrize("m,k", [(576, 4096), (576, 12288), (33, 25600), (5, 40960), (1, 2048)])
+def test_quant_rows_fp8_bit_exact(gpu, m, k):
+    from fastforward_amd.linear import FP8Linear
+    x = torch.randn(m, k, generator=_g(19))
+    x[torch.rand(m, k, generator=_g(20)) < 0.001] *= 20
+    if m > 3:
+        x[2] = 0
+    x = x.to(BF16)
+    op = FP8Linear.__new__(FP8Linear)
+    q, s = op.quantize(x.to(DEV))
+    qw, sw = O.quant_rows_dynamic(x)
+    assert torch.equal(q.view(torch.uint8).cpu(), qw.view(torch.uint8))
+    assert torch.equal(s.cpu(), sw)
+
+
+def test_quant_static_bit_exact(gpu):
+    from fastforward_amd._lib import call, ptr, stream
+    m, k = 300, 4096
+    x = (torch.randn(m, k, generator=_g(21)) * 40).to(BF16)
+    inv = 448 / 37.5
+    q = torch.full((304, k), 7, device=DEV, dtype=torch.uint8)
+    call("ff_quant_static_fp8", ptr(x.to(DEV)), ptr(q), m, 304, k, inv, stream())
+    qw = O.quant_static(x, inv)
+    assert torch.equal(q[:m].cpu(), qw.view(torch.uint8))
+    assert torch.all(q[m:] == 0)
+
+
+@pytest.mark.parametrize("per_channel", [True, False])
+def test_weight_quant_fp8_bit_exact(gpu, per_channel):
+    from fastforward_amd.linear import FP8Linear, StaticFP8Linear
+    w = (torch.randn(6144, 4096, generator=_g(22)) * 0.02).to(BF16)
+    w[5, 7] = 0.5                                               # a channel outlier
+    qw, sw = O.fp8_weight_quant(w, per_channel)
+    if per_channel:
+        op = FP8Linear(w.to(DEV))
+        assert torch.equal(op.scale.reshape(-1).cpu(), sw)
+    else:
+        op = StaticFP8Linear(w.to(DEV), 448 / 8.0)
+        assert torch.equal(op.weight_scale.cpu(), sw)
+    assert torch.equal(op.weight.view(torch.uint8).cpu(), qw.view(torch.uint8))
+
+
+@pytest.mark.parametrize("sym,group", [(True, 128), (False, 32), (False, 128)])
+def test_int4_quant_bit_exact(gpu, sym, group):
+    from fastforward_amd.linear import Int4
+    w = (torch.randn(512, 1024, generator=_g(23)) * 0.02).to(BF16)
+    quant = O.int4_quantize_sym if sym else O.int4_quantize_asym
+    _, packed, scales = quant(w, group)
+    op = Int4(w.to(DEV), group=group, symmetric=sym)
+    assert torch.equal(op.packed.cpu(), packed)
+    assert torch.equal(op.scales.cpu(), scales)
+
+
+# ------------------------------------------------------------------ GEMMs
+
+FP8_SHAPES = [(320, 2048, 6144), (320, 6144, 2048), (576, 4096, 12288), (576, 12288, 4096),
+              (1024, 5120, 25600), (1, 4096, 24576), (17, 256, 384), (130, 1024, 200)]
+
+
+@pytest.mark.parametrize("m,k,n", FP8_SHAPES)
+def test_gemm_fp8_dynamic(gpu, m, k, n):
+    """Codes and scales come from the oracle's quantizers (pinned bit-exact above);
+    the GEMM then differs from the oracle only by fp32 summation order."""
+    from fastforward_amd._lib import call, ptr, stream
+    x = torch.randn(m, k, generator=_g(24))
+    x[torch.rand(m, k, generator=_g(25)) < 0.001] *= 20
+    x = x.to(BF16)
+    w = (torch.randn(n, k, generator=_g(26)) * 0.02).to(BF16)
+    qa, sa = O.quant_rows_dynamic(x)
+    qw, sw = O.fp8_weight_quant(w)
+    want = O.fp8_gemm(qa, sa, qw, sw)
+    y = torch.empty(m, n, device=DEV, dtype=BF16)
+    call("ff_gemm_fp8", ptr(qa.to(DEV)), ptr(sa.to(DEV)), 1, ptr(qw.to(DEV)), ptr(sw.to(DEV)), 1, ptr(y), n,
+         m, n, k, stream())
+    assert_bf16_close(y.cpu(), want, 1, 1e-2, f"gemm_fp8 {m}x{k}x{n}")
+
+
+def test_gemm_fp8_static_scalars(gpu):
+    from fastforward_amd.linear import StaticFP8Linear
+    m, k, n = 576, 4096, 4096
+    x = (torch.randn(m, k, generator=_g(27)) * 3).to(BF16)
+    w = (torch.randn(n, k, generator=_g(28)) * 0.02).to(BF16)
+    op = StaticFP8Linear(w.to(DEV), 448 / 12.0)
+    y = op(x.to(DEV)).cpu()
+    want = O.fp8_linear_static(x, op.weight.cpu(), op.weight_scale.cpu(), op.inverse_scale, op.input_scale.cpu())
+    assert_bf16_close(y, want, 1, 1e-2, "static fp8 linear")
+
+
+@pytest.mark.parametrize("sym,group", [(True, 128), (False, 32)])
+@pytest.mark.parametrize("m,k,n", [(576, 4096, 6144), (1, 12288, 4096), (100, 1024, 384)])
+def test_gemm_w4a16(gpu, m, k, n, sym, group):
+    from fastforward_amd.linear import Int4
+    x = torch.randn(m, k, generator=_g(29)).to(BF16)
+    w = (torch.randn(n, k, generator=_g(30)) * 0.02).to(BF16)
+    op = Int4(w.to(DEV), group=group, symmetric=sym)
+    y = op(x.to(DEV)).cpu().double()
+    want = O.w4a16_linear(x, op.packed.cpu(), op.scales.cpu(), group).double()
+    exact = x.double() @ O.int4_dequant(op.packed.cpu(), op.scales.cpu(), group).double().T
+    rel = float((y - exact).pow(2).mean().sqrt() / exact.pow(2).mean().sqrt())
+    assert rel <= 5e-3, rel
+    assert float((want - exact).pow(2).mean().sqrt() / exact.pow(2).mean().sqrt()) <= 5e-3
+
+
+def test_w4a16_dequant_bit_exact_via_one_hot(gpu):
+    """x = rows of the identity: y[r, n] = bf16((q-8)*s + z) for k = r exactly."""
+    from fastforward_amd.linear import Int4
+    k, n = 256, 128
+    w = (torch.randn(n, k, generator=_g(31)) * 0.02).to(BF16)
+    for sym, group in ((True, 128), (False, 32)):
+        op = Int4(w.to(DEV), group=group, symmetric=sym)
+        eye = torch.eye(k, dtype=BF16, device=DEV)
+        y = op(eye).cpu()
+        dq = O.int4_dequant(op.packed.cpu(), op.scales.cpu(), group).to(BF16)
+        assert torch.equal(y, dq.T.contiguous())
+
+
+# ------------------------------------------------------------------ attention
+
+@pytest.mark.parametrize("t,hq,hk", [(576, 32, 8), (320, 16, 8), (70, 64, 8)])
+def test_attention_causal(gpu, t, hq, hk):
+    from fastforward_amd import ops
+    d = 128
+    q = torch.randn(1, hq, t, d, generator=_g(32)).to(BF16)
+    k = torch.randn(1, hk, t, d, generator=_g(33)).to(BF16)
+    v = torch.randn(1, hk, t, d, generator=_g(34)).to(BF16)
+    v[:, 1] += 2                                                 # distinguishes kv heads
+    got = ops.attention_direct(q.to(DEV), k.to(DEV), v.to(DEV), d ** -0.5).cpu().float()
+    want = O.attention_direct(q, k, v, d ** -0.5).float()
+    diff = (got - want).abs()
+    assert float(diff.max()) <= 1 / 64, float(diff.max())
+    assert float((got - want).pow(2).mean().sqrt() / want.pow(2).mean().sqrt()) <= 5e-3
+
+
+def test_attention_selected_positions_and_strided_v(gpu):
+    from fastforward_amd import ops
+    t, hq, hk, d = 576, 32, 8, 128
+    packed = torch.randn(1, t, (hq + 2 * hk) * d, generator=_g(35)).to(BF16)
+    q = torch.randn(1, hq, 3, d, generator=_g(36)).to(BF16)
+    k = torch.randn(1, hk, t, d, generator=_g(37)).to(BF16)
+    pick = torch.tensor([575, 100, 0])
+    pg = packed.to(DEV)
+    v = pg[..., (hq + hk) * d:].view(1, t, hk, d).transpose(1, 2)        # strided view, as the reference passes it
+    got = ops.attention_direct(q.to(DEV), k.to(DEV), v, d ** -0.5, positions=pick.to(DEV)).cpu().float()
+    want = O.attention_direct(q, k, packed[..., (hq + hk) * d:].view(1, t, hk, d).transpose(1, 2), d ** -0.5,
+                              positions=pick).float()
+    assert float((got - want).abs().max()) <= 1 / 64
+
+
+# ------------------------------------------------------------------ readout, gathers, rope
+
+def test_lm_readout(gpu):
+    from fastforward_amd import ops
+    h = 4096
+    x = (torch.randn(1, h, generator=_g(38)) * 4).to(BF16)
+    mod, w = _norm_module(h, 39)
+    head = (torch.randn(8, h, generator=_g(40)) * 0.02).to(BF16)
+    got = ops.lm_readout(x.to(DEV), mod, head.to(DEV)).cpu()
+    want = O.lm_readout(x, w, 1e-6, head)
+    assert got.shape == (1, 8) and got.dtype == torch.float32
+    assert_bf16_close(got.to(BF16), want.to(BF16), 1, 0.25, "lm_readout")
+
+
+def test_embed_and_gather_exact(gpu):
+    from fastforward_amd._lib import call, ptr, stream
+    vocab, h, t = 1000, 4096, 100
+    table = torch.randn(vocab, h, generator=_g(41)).to(BF16).to(DEV)
+    ids = torch.randint(0, vocab, (t,), generator=_g(42))
+    out = torch.empty(t, h, device=DEV, dtype=BF16)
+    call("ff_embed", ptr(ids.to(DEV)), ptr(table), ptr(out), t, h, vocab, stream())
+    assert torch.equal(out.cpu(), table.cpu()[ids])
+    idx = torch.tensor([99, 3], device=DEV)
+    g = torch.empty(2, h, device=DEV, dtype=BF16)
+    call("ff_gather_rows", ptr(out), h, ptr(idx), ptr(g), h, 2, h, t, stream())
+    assert torch.equal(g, out[[99, 3]])
+
+
+@pytest.mark.parametrize("s0,gh,gw,t", [(4, 16, 32, 576), (4, 30, 32, 1024), (4, 16, 16, 320)])
+def test_mrope_cos_sin(gpu, s0, gh, gw, t):
+    from fastforward_amd._lib import call, ptr, stream
+    from fastforward_amd.runtime import mrope_positions, rope_inv_freq
+    pos = torch.from_numpy(mrope_positions(s0, gh, gw, t))
+    assert torch.equal(pos, O.mrope_positions(s0, gh, gw, t))
+    cos = torch.empty(t, 128, device=DEV, dtype=BF16)
+    sin = torch.empty(t, 128, device=DEV, dtype=BF16)
+    call("ff_mrope_cos_sin", ptr(pos.to(DEV)), ptr(rope_inv_freq(5e6, 128).to(DEV)), ptr(cos), ptr(sin), t, 128,
+         20, 20, stream())
+    wc, ws = O.mrope_cos_sin(pos, 5e6, 128)
+    assert_bf16_close(cos.cpu(), wc[0], 1, 1e-2, "cos")
+    assert_bf16_close(sin.cpu(), ws[0], 1, 1e-2, "sin")
+
+
+def test_bad_arguments_raise(gpu):
+    from fastforward_amd import ops
+    from fastforward_amd._lib import call, ptr, stream
+    x = torch.zeros(4, 4096, device=DEV, dtype=BF16)
+    with pytest.raises(RuntimeError, match="multiple of"):
+        call("ff_gemm_fp8", ptr(x), ptr(x), 1, ptr(x), ptr(x), 1, ptr(x), 4096, 4, 4096, 100, stream())
+    with pytest.raises(AssertionError):
+        ops.add_rms(x, x[:2], None, ops.RMSNorm(torch.ones(4096, device=DEV, dtype=BF16)))
+    _ = np, bf16_ulps
