@@ -1,0 +1,244 @@
+"""Benchmark: Qwen3-VL-8B-shaped FP8 prefill + choice-score step on one MI355X.
+
+Workload (the headline metric): 36 decoder layers, hidden 4096, GQA 32/8,
+head_dim 128, MLP 12288, vocab 151936; FP8 e4m3 linears (per-token activation /
+per-channel weight scales), bf16 elsewhere; 576 tokens (4 text + 16x32 image
+grid + 60 text), pick-only final layer, 8 answer choices; the whole step is one
+hipGraph. Weights are random-init N(0, 0.02) and token ids uniform (seeded):
+there is no checkpoint. A step = one graph replay with inputs resident in HBM.
+
+Prints ONE JSON line. ``roofline`` covers the dominant kernel, the FP8 GEMM,
+timed live with HIP events on the step's own shapes; ``cpu_baseline`` times the
+CPU oracle on a bounded sample of the same step (a few layers + the tail),
+scaled to the full step.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+METRIC = "ms per prefill+choice-score step (8B-shape FP8, 576 tok); FP8 GEMM % MFMA peak"
+PEAK_FP8_TFLOPS = 5000.0      # MI355X dense fp8 MFMA
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+MICRO_SHAPES = [(320, 2048, 6144), (320, 6144, 2048), (576, 4096, 12288), (576, 12288, 4096),
+                (1024, 5120, 25600)]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_graph(rt, steps, warmup):
+    for _ in range(warmup):
+        rt.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        rt.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def gemm_launches(cfg, T):
+    """(role, m, count) of every FP8 GEMM launch in one step: full layers run all
+    four linears on T rows; the pick-only final layer runs qkv on T rows and
+    o / gateup / down on one row."""
+    full = cfg.layers - 1
+    return [("qkv", T, full + 1), ("o", T, full), ("gateup", T, full), ("down", T, full),
+            ("o", 1, 1), ("gateup", 1, 1), ("down", 1, 1)]
+
+
+def time_gemm(q, s, op, m, reps=20):
+    """Average duration (ms) of one ff_gemm_fp8 launch, HIP events on the launch stream."""
+    out = torch.empty((m, op.weight.shape[0]), device=q.device, dtype=torch.bfloat16)
+    for _ in range(3):
+        op.gemm(q[:m], s[:m], out)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        op.gemm(q[:m], s[:m], out)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def gemm_roofline(cfg, w, T):
+    """Live FP8 GEMM timing on the step's shapes (layer 0's weights): algorithmic
+    FLOPs per launch over the average launch duration, weighted as in the step."""
+    lw = w.layers[0]
+    total_flop = total_ms = 0.0
+    launches = 0
+    per_shape = {}
+    for role, m, count in gemm_launches(cfg, T):
+        op = getattr(lw, role)
+        n, k = op.weight.shape
+        x = torch.randn(T, k, device="cuda").to(torch.bfloat16)
+        q, s = op.quantize(x)
+        ms = time_gemm(q, s, op, m)
+        flop = 2.0 * m * n * k
+        per_shape[f"{role} {m}x{k}x{n}"] = dict(us=round(ms * 1e3, 2), tflops=round(flop / ms / 1e9, 1))
+        total_flop += flop * count
+        total_ms += ms * count
+        launches += count
+    avg_ms = total_ms / launches
+    achieved = total_flop / launches / (avg_ms * 1e-3) / 1e12
+    return dict(bound="mfma", achieved=round(achieved, 1), peak=PEAK_FP8_TFLOPS, unit="TFLOP/s",
+                frac=round(achieved / PEAK_FP8_TFLOPS, 4), traffic=_traffic(),
+                kernel="gemm_fp8_kernel", avg_launch_us=round(avg_ms * 1e3, 2), launches_per_step=launches,
+                gemm_ms_per_step=round(total_ms, 3), by_shape=per_shape)
+
+
+def _traffic():
+    """HBM bytes per GEMM launch from the committed rocprofv3 PMC summary, if any."""
+    path = os.path.join(HERE, "profiles", "gemm_fp8_traffic.json")
+    if os.path.exists(path):
+        with open(path) as f:
+            return json.load(f).get("bytes_per_launch")
+    return None
+
+
+def micro_gemms():
+    """The FP8 linear microbench shapes (M,K,N): TFLOP/s of one GEMM launch."""
+    from fastforward_amd.linear import FP8Linear
+    out = {}
+    for m, k, n in MICRO_SHAPES:
+        w = (torch.randn(n, k, device="cuda") * 0.02).to(torch.bfloat16)
+        op = FP8Linear(w)
+        del w
+        x = torch.randn(m, k, device="cuda").to(torch.bfloat16)
+        q, s = op.quantize(x)
+        ms = time_gemm(q, s, op, m)
+        flop = 2.0 * m * n * k
+        byt = m * k + n * k + 4 * (m + n) + 2 * m * n
+        out[f"{m}x{k}x{n}"] = dict(us=round(ms * 1e3, 2), tflops=round(flop / ms / 1e9, 1),
+                                   frac_fp8_peak=round(flop / ms / 1e9 / PEAK_FP8_TFLOPS, 4),
+                                   gbs=round(byt / ms / 1e6, 1))
+        del op
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(cfg, w, ids, pos, pick, T, layers_sample):
+    """The CPU oracle on ``layers_sample`` decoder layers + the pick-only tail of the
+    same step, on this host's cores; scaled to the full depth."""
+    from oracle import model as omodel
+    from oracle import ops as O
+    from tests.helpers import linear_to_oracle
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    shape = omodel.Shape(layers=cfg.layers, hidden=cfg.hidden, heads=cfg.heads, kv_heads=cfg.kv_heads,
+                         head_dim=cfg.head_dim, inter=cfg.inter, vocab=cfg.vocab)
+    keep = list(range(layers_sample)) + [cfg.layers - 1]
+    L = {}
+    for j in keep:
+        lw = w.layers[j]
+        L[j] = omodel.Layer(input_norm=lw.input_norm.weight.cpu(), post_norm=lw.post_norm.weight.cpu(),
+                            q_norm=lw.q_norm.weight.cpu(), k_norm=lw.k_norm.weight.cpu(),
+                            qkv=linear_to_oracle(lw.qkv), o=linear_to_oracle(lw.o),
+                            gateup=linear_to_oracle(lw.gateup), down=linear_to_oracle(lw.down))
+    ow = omodel.Weights(embed=None, layers=[], norm=w.norm.weight.cpu(), head=w.head.cpu())
+    h = w.embed[torch.as_tensor(ids).cuda()].cpu()[None]
+    t0 = time.perf_counter()
+    cos, sin = O.mrope_cos_sin(pos, shape.theta, shape.head_dim, shape.sections)
+    x = O.fast_norm(h, L[0].input_norm, shape.eps)
+    for j in range(layers_sample):
+        attn = omodel.attention_block(shape, L[j], x, cos, sin)
+        res, post = O.add_rms(h, attn, None, L[j].post_norm, shape.eps)
+        val = omodel.mlp(L[j], post)
+        nxt = L[j + 1] if j + 1 < layers_sample else L[cfg.layers - 1]
+        h, x = O.add_rms(res, val, None, nxt.input_norm, shape.eps)
+    t1 = time.perf_counter()
+    omodel.tail(shape, L[cfg.layers - 1], ow, h, cos, sin, pick)
+    t2 = time.perf_counter()
+    per_layer = (t1 - t0) / layers_sample
+    full_ms = (per_layer * (cfg.layers - 1) + (t2 - t1)) * 1e3
+    return dict(value=round(full_ms, 1), unit="ms per step (scaled)", cores=torch.get_num_threads(),
+                kind="port",
+                sample=f"{layers_sample} of {cfg.layers - 1} full decoder layers + the pick-only tail of the "
+                       f"same 8B-shape FP8 {T}-token step, timed on the host with the oracle "
+                       f"(torch CPU, fp32 with e4m3/bf16 rounding points), scaled to the full depth; "
+                       f"sample wall time {t2 - t0:.1f} s")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--preset", default="qwen3vl-8b")
+    ap.add_argument("--tokens", type=int, default=576)
+    ap.add_argument("--cpu-layers", type=int, default=35, help="decoder layers in the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip the W4A16 step and the GEMM microbench")
+    ap.add_argument("--profile", action="store_true", help="only replay the graph (for rocprofv3 runs)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build's step runs on a single MI355X and has no "
+              "multi-GPU path (request-level replicas would scale it; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    from fastforward_amd import _lib
+    from fastforward_amd.runtime import PRESETS, Runtime
+    from fastforward_amd.synthetic import make_model, make_request
+    _lib.check_device()
+    cfg = PRESETS[args.preset]
+    T = args.tokens
+    grid = (16, 32) if T >= 576 else (16, 16)
+    log(f"building {cfg.name} fp8 (random init, seed 0)")
+    w = make_model(cfg, mode="fp8", seed=0, n_options=8)
+    ids, pos, pick = make_request(cfg, T, *grid, seed=0)
+    rt = Runtime(cfg, w, T)
+    rt.set_inputs(ids, pos, pick)
+    rt.capture()
+    torch.cuda.synchronize()
+    log("graph captured")
+    ms = time_graph(rt, args.steps, args.warmup)
+    log(f"step {ms:.3f} ms")
+    if args.profile:
+        print(json.dumps(dict(metric=METRIC, value=round(ms, 4), unit="ms", profile_run=True)))
+        return
+    roof = gemm_roofline(cfg, w, T)
+    log(f"gemm {roof['achieved']} TFLOP/s ({roof['frac']:.3f} of fp8 peak)")
+    extras = {}
+    if not args.no_extras:
+        extras["gemm_fp8_microbench"] = micro_gemms()
+        log("microbench done")
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline")
+        cpu = cpu_baseline(cfg, w, ids, pos, pick, T, args.cpu_layers)
+    del rt
+    if not args.no_extras:
+        del w
+        torch.cuda.empty_cache()
+        w4 = make_model(cfg, mode="w4a16", seed=0, n_options=8)
+        rt4 = Runtime(cfg, w4, T)
+        rt4.set_inputs(ids, pos, pick)
+        rt4.capture()
+        extras["w4a16_g128_step_ms"] = round(time_graph(rt4, args.steps, args.warmup), 4)
+        del rt4, w4
+    line = dict(
+        metric=METRIC, value=round(ms, 4), unit="ms", n_gpus=1, steps=args.steps, warmup=args.warmup,
+        ms_per_step=round(ms, 4), higher_is_better=False, scaling="weak", vs_baseline=None,
+        dtype="fp8_e4m3 GEMM (fp32 acc) / bf16",
+        data="synthetic: random-init N(0,0.02) weights, seeded uniform token ids, no checkpoint",
+        config=dict(workload=f"{cfg.name} FP8 prefill + choice-score step, hipGraph replay",
+                    layers=cfg.layers, hidden=cfg.hidden, heads=f"{cfg.heads}/{cfg.kv_heads}",
+                    mlp=cfg.inter, vocab=cfg.vocab, tokens=T, image_grid=f"{grid[0]}x{grid[1]}", choices=8,
+                    linear="e4m3 per-token activation / per-channel weight scales"),
+        roofline=roof, cpu_baseline=cpu, **extras)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

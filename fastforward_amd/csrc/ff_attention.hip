@@ -120,11 +120,37 @@ __global__ __launch_bounds__(kThreads) void qkv_post_kernel(
 
 // ---------------------------------------------------------------- attention
 
-// Grid (ceil(s/64), hq); 4 waves, each owns 16 queries of one head.
+// S^T tile pair for one 32-key chunk starting at kc: lane (r16, g) gets the
+// scaled scores of keys kc + 8g + jj (jj = 0..7) for its query, with keys past
+// the query's position (or past t) at -inf. A-row i of tile tt is key
+// kc + 8*(i/4) + 4*tt + (i%4), so both products see the same key order.
+__device__ __forceinline__ void score_chunk(const bf16_t* __restrict__ kp, const u32x4* qf, int kc, int t,
+                                            int pos, float scale, int r16, int g, float* sc) {
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    int key = kc + 8 * (r16 >> 2) + 4 * tt + (r16 & 3);
+    key = min(key, t - 1);
+    const bf16_t* kr = kp + (int64_t)key * D;
+    f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 4; ++st) a = mfma_bf16(*reinterpret_cast<const u32x4*>(kr + 32 * st + 8 * g), qf[st], a);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int kk = kc + 8 * g + 4 * tt + r;
+      sc[4 * tt + r] = (kk > pos || kk >= t) ? -INFINITY : a[r] * scale;
+    }
+  }
+}
+
+// Grid (ceil(s/64), hq); 4 waves, each owns 16 queries of one head. Keys are
+// consumed in 64-key blocks aligned at key 0 with one running-max update per
+// block, as the reference kernel does (BN = 64): s = (q.k)*scale in fp32,
+// p = exp(s - max), den = den*alpha + sum(p), acc = acc*alpha + bf16(p).V,
+// out = acc/den.
 __global__ __launch_bounds__(kThreads) void attention_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ vt,
     const int64_t* __restrict__ positions, int gather_q, bf16_t* __restrict__ y, int s_len, int t,
-    int t_pad, int hq, int hk, float scale_log2) {
+    int t_pad, int hq, int hk, float scale) {
   const int head = blockIdx.y;
   const int kvh = head / (hq / hk);
   const int qblock = gridDim.x - 1 - blockIdx.x;  // heaviest (latest) query blocks first
@@ -155,66 +181,58 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(
   for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, den = 0.f;
 
-  for (int kc = 0; kc < kend; kc += 32) {
-    // S^T tiles: A-row i of tile tt is key kc + 8*(i/4) + 4*tt + (i%4).
-    f32x4 sacc[2];
+  for (int kb = 0; kb < kend; kb += 64) {
+    const bool two = kb + 32 < kend;  // wave-uniform: second chunk has a visible key
+    float sc[16];
+    score_chunk(kp, qf, kb, t, pos, scale, r16, g, sc);
+    if (two) {
+      score_chunk(kp, qf, kb + 32, t, pos, scale, r16, g, sc + 8);
+    } else {
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      int key = kc + 8 * (r16 >> 2) + 4 * tt + (r16 & 3);
-      key = min(key, t - 1);
-      const bf16_t* kr = kp + (int64_t)key * D;
-      f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int st = 0; st < 4; ++st) a = mfma_bf16(*reinterpret_cast<const u32x4*>(kr + 32 * st + 8 * g), qf[st], a);
-      sacc[tt] = a;
+      for (int jj = 8; jj < 16; ++jj) sc[jj] = -INFINITY;
     }
-    // lane holds keys kc + 8g + jj (jj = 4*tt + r) for query qi
-    float sc[8];
-    float cmax = -INFINITY;
+    float bmax = sc[0];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+    for (int jj = 1; jj < 16; ++jj) bmax = fmaxf(bmax, sc[jj]);
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+    const float mnew = fmaxf(m, bmax);
+    const float alpha = expf(m - mnew);
+    float p[16], psum = 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = kc + 8 * g + 4 * tt + r;
-        float v = sacc[tt][r] * scale_log2;
-        if (key > pos || key >= t) v = -INFINITY;
-        sc[4 * tt + r] = v;
-        cmax = fmaxf(cmax, v);
-      }
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
-    const float mnew = fmaxf(m, cmax);
-    const float alpha = exp2f(m - mnew);
-    float p[8], psum = 0.f;
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      p[jj] = exp2f(sc[jj] - mnew);
+    for (int jj = 0; jj < 16; ++jj) {
+      p[jj] = expf(sc[jj] - mnew);
       psum += p[jj];
     }
     psum += __shfl_xor(psum, 16, 64);
     psum += __shfl_xor(psum, 32, 64);
     den = den * alpha + psum;
     m = mnew;
-    u32x4 pf;
-    pf.x = pack_bf16x2(p[0], p[1]);
-    pf.y = pack_bf16x2(p[2], p[3]);
-    pf.z = pack_bf16x2(p[4], p[5]);
-    pf.w = pack_bf16x2(p[6], p[7]);
+    u32x4 pf0, pf1;
+    pf0.x = pack_bf16x2(p[0], p[1]);
+    pf0.y = pack_bf16x2(p[2], p[3]);
+    pf0.z = pack_bf16x2(p[4], p[5]);
+    pf0.w = pack_bf16x2(p[6], p[7]);
+    pf1.x = pack_bf16x2(p[8], p[9]);
+    pf1.y = pack_bf16x2(p[10], p[11]);
+    pf1.z = pack_bf16x2(p[12], p[13]);
+    pf1.w = pack_bf16x2(p[14], p[15]);
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      const u32x4 va = *reinterpret_cast<const u32x4*>(vp + (int64_t)(16 * dt + r16) * t_pad + kc + 8 * g);
+      const bf16_t* vr = vp + (int64_t)(16 * dt + r16) * t_pad + kb + 8 * g;
       f32x4 acc = o[dt] * alpha;
-      o[dt] = mfma_bf16(va, pf, acc);
+      acc = mfma_bf16(*reinterpret_cast<const u32x4*>(vr), pf0, acc);
+      if (two) acc = mfma_bf16(*reinterpret_cast<const u32x4*>(vr + 32), pf1, acc);
+      o[dt] = acc;
     }
   }
   if (!qvalid) return;
-  const float rden = 1.0f / den;
   bf16_t* yp = y + ((int64_t)qi * hq + head) * D;
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) {
     u32x2 w2;
-    w2.x = pack_bf16x2(o[dt][0] * rden, o[dt][1] * rden);
-    w2.y = pack_bf16x2(o[dt][2] * rden, o[dt][3] * rden);
+    w2.x = pack_bf16x2(o[dt][0] / den, o[dt][1] / den);
+    w2.y = pack_bf16x2(o[dt][2] / den, o[dt][3] / den);
     *reinterpret_cast<u32x2*>(yp + 16 * dt + 4 * g) = w2;
   }
 }
@@ -293,10 +311,9 @@ extern "C" int ff_attention_vt(const void* q, const void* k, const void* vt, con
   FF_REQUIRE(!gather_q || positions, "ff_attention_vt: gather_q needs positions");
   FF_REQUIRE(ff_aligned(q, 16) && ff_aligned(k, 16) && ff_aligned(vt, 16) && ff_aligned(y, 8),
              "ff_attention_vt: alignment");
-  const float scale_log2 = scale * 1.4426950408889634f;
   hipLaunchKernelGGL(attention_kernel, dim3((unsigned)((s + 63) / 64), (unsigned)hq), dim3(kThreads), 0,
                      (hipStream_t)stream, (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)vt, positions,
-                     gather_q, (bf16_t*)y, (int)s, (int)t, (int)t_pad, (int)hq, (int)hk, scale_log2);
+                     gather_q, (bf16_t*)y, (int)s, (int)t, (int)t_pad, (int)hq, (int)hk, scale);
   FF_LAUNCH_CHECK("ff_attention_vt");
   return FF_OK;
 }

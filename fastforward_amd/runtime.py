@@ -192,7 +192,7 @@ class Runtime:
              cfg.sections[1], cfg.sections[2], s)
         return h
 
-    def _step_fused(self):
+    def _step_fused(self, trace=None):
         cfg, w, s = self.cfg, self.w, stream()
         T, Tp, H, D = self.T, self.Tp, cfg.hidden, cfg.head_dim
         HQ, HK, I, eps = cfg.heads, cfg.kv_heads, cfg.inter, cfg.eps
@@ -217,6 +217,8 @@ class Runtime:
                  ptr(self.xq), ptr(self.xs), T, H, float(nn.variance_epsilon), self.image_start,
                  self.nv if deep is not None else 0, s)
             cur ^= 1
+            if trace is not None:
+                trace.append(nxt.clone())
         # pick-only tail (_family/night_runtime.py:92-105)
         lw = L[-1]
         h = self.h[cur]
@@ -262,7 +264,7 @@ class Runtime:
         call("ff_gemm_fp8", ptr(self.mq), ptr(self.ms), 1, ptr(lw.down.weight), ptr(lw.down.scale), 1, ptr(out), H,
              m, H, I, s)
 
-    def _step_generic(self):
+    def _step_generic(self, trace=None):
         """The reference's op sequence (scaled_qwen_runtime.py:143-176,
         _family/night_runtime.py:92-105) through the drop-in ops."""
         cfg, w = self.cfg, self.w
@@ -280,6 +282,8 @@ class Runtime:
             deep = self.deep[j] if j < len(self.deep) else None
             h, normalized = ops.add_rms(residual, value, deep, L[j + 1].input_norm, self.image_start,
                                         self.nv if deep is not None else 0)
+            if trace is not None:
+                trace.append(h[0].clone())
         lw = L[-1]
         x = ops.fast_norm(h, lw.input_norm)
         q, k, v = Linear.apply(x, lw.qkv).split([HQ * D, HK * D, HK * D], -1)
@@ -325,9 +329,11 @@ class Runtime:
                  stream())
         return out
 
-    def step(self):
-        """Run the step eagerly on the current stream; returns the logits buffer."""
-        return self._step_fused() if self.path == "fused" else self._step_generic()
+    def step(self, trace=None):
+        """Run the step eagerly on the current stream; returns the logits buffer.
+        ``trace`` (a list) receives a copy of the residual stream after every
+        full layer (eager runs only)."""
+        return self._step_fused(trace) if self.path == "fused" else self._step_generic(trace)
 
     # ------------------------------------------------------------ hipGraph
 
