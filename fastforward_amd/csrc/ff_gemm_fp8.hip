@@ -1,46 +1,85 @@
-// FP8 (e4m3fn) GEMM for gfx950: y = bf16(sum_k qa[m,k] qw[n,k] * sa * sw).
+// FP8 (e4m3fn) GEMM for gfx950: y = bf16((sum_k qa[m,k] qw[n,k]) * sa * sw).
 //
 // Both operands are K-contiguous ("TN"): activations qa (M,K) and weights qw
-// (N,K), as the reference stores FP8 weights (N,K) row-major. A workgroup of
-// 256 threads (4 waves, 2x2) computes a BM x BN = 128 x 128 tile; each wave owns
-// 64 x 64 = 4 x 4 tiles of v_mfma_f32_16x16x128_f8f6f4 (fp32 accumulate). K is
-// consumed in 128-byte steps staged through LDS with double buffering; 16-byte
-// chunks are XOR-swizzled by row so the fragment reads of 16 consecutive rows
-// spread over the LDS banks.
+// (N,K), as the reference stores FP8 weights (N,K) row-major. A workgroup of 4
+// waves (2 x 2) owns a BM x BN tile; each wave owns (BM/2) x (BN/2) as 16 x 16
+// tiles of v_mfma_f32_16x16x128_f8f6f4 with fp32 accumulators.
 //
-// MFMA operand layout used (any K permutation is valid as long as A and B use
-// the same one): lane l supplies row (l % 16) of its 16-row A (or B) tile and
-// the 32 bytes k in [32*(l/16), 32*(l/16)+32) of the 128-byte K step. The
-// accumulator of lane l holds D[4*(l/16) + r][l % 16], r = 0..3.
+// K is consumed KS x 128 bytes per stage. Stages are filled with
+// global_load_lds_dwordx4 (gfx950 direct-to-LDS loads: lane l's 16 bytes land at
+// base + 16*l, no staging registers). Each load instruction covers 8 rows x 128
+// bytes -- whole cache lines, which doubles the bytes per memory request over a
+// 16-row pattern -- with the 16-byte chunk of row r stored at slot
+// 8*(r%8) + (chunk ^ (r/2)) of its 1 KB block (r in 0..15 within a 16-row group;
+// rows 0-7 in block 0, rows 8-15 in block 1). An MFMA operand for lane l
+// (row l%16, g = l/16) is chunks 2g and 2g+1 of its row: the XOR places the 16
+// rows a wave reads per ds_read_b128 pass in 16 distinct bank groups, and the
+// operand is k in [32g, 32g+32), the same for A and B.
+// S stages rotate through LDS with S-1 in flight; one barrier per stage.
+//
+// The accumulator of lane l holds D[4*(l/16) + r][l % 16]. The epilogue applies
+// the scales, rounds to bf16 and stages the tile through LDS so global stores
+// are 16-byte row chunks.
 //
 // Tiles are ordered XCD-aware: consecutive workgroups are dealt round-robin to
 // the 8 XCDs, so the logical tile id gives each XCD a contiguous range of tiles
-// walked M-fastest; the few M-tiles that share a weight tile then hit the same
-// L2, and the weights stream from HBM about once.
+// walked M-fastest; tiles that share a weight slab then share an L2.
+#include <stdio.h>
+#include <stdlib.h>
+
 #include "ff_common.h"
 
 using namespace ff;
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 128;
+constexpr int BK = 128;
 constexpr int kThreads = 256;
 constexpr int kXcds = 8;
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glb_void;
 
 __device__ __forceinline__ f32x4 mfma_fp8(const i32x8& a, const i32x8& b, const f32x4& c) {
   // scale operands 0 select the unscaled v_mfma_f32_16x16x128_f8f6f4; format 0 = e4m3.
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ (row & 7)) << 4); }
+__device__ __forceinline__ void load_lds16(const void* g, uint8_t* lds) {
+  __builtin_amdgcn_global_load_lds((glb_void*)g, (lds_void*)lds, 16, 0, 0);
+}
 
-__global__ __launch_bounds__(kThreads, 2) void gemm_fp8_kernel(
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int BM, int BN, int KS, int S>
+struct Cfg {
+  static constexpr int RA = BM / 16, RB = BN / 16;     // 16-row groups
+  static constexpr int SUB = 2 * (RA + RB);            // 1 KB blocks per 128-byte k-substep
+  static constexpr int BLOCKS = SUB * KS;              // 1 KB blocks per stage
+  static constexpr int STAGE = BLOCKS * 1024;
+  static constexpr int WI = RA / 2, WJ = RB / 2;       // MFMA tiles per wave (rows, cols)
+  static constexpr int EPI_LD = BN + 8;                // bf16 row pitch of the epilogue tile
+  static constexpr int SMEM = S * STAGE > BM * EPI_LD * 2 ? S * STAGE : BM * EPI_LD * 2;
+  static_assert(SMEM <= 160 * 1024, "LDS budget");
+  static_assert(RA % 2 == 0 && RB % 2 == 0, "tile must split over 2 x 2 waves");
+  static_assert(BLOCKS % 4 == 0, "stage blocks must split over 4 waves");
+};
+
+// KS = 128-byte k-substeps per stage; S = LDS stages, S-1 in flight.
+template <int BM, int BN, int KS, int S>
+__global__ __launch_bounds__(kThreads, 1) void gemm_fp8_kernel(
     const uint8_t* __restrict__ qa, const float* __restrict__ sa, int sa_rows,
     const uint8_t* __restrict__ qw, const float* __restrict__ sw, int sw_cols,
     bf16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int tiles_m, int tiles_n) {
-  __shared__ __align__(16) uint8_t smem[2][(BM + BN) * BK];
+  using C = Cfg<BM, BN, KS, S>;
+  __shared__ __align__(16) uint8_t smem[C::SMEM];
 
-  // XCD-aware logical tile id.
   const int nblk = tiles_m * tiles_n;
   const int b = blockIdx.x;
   int logical = b;
@@ -52,87 +91,116 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_fp8_kernel(
   const int wm = wave >> 1, wn = wave & 1;
   const int r16 = lane & 15, g = lane >> 4;
 
-  // global -> register staging: 4 chunks of A and 4 of B per thread.
-  u32x4 ra[4], rb[4];
-  auto gload = [&](int k0) {
+  // Source pointers of this lane for every block this wave loads (k offset 0).
+  // Rows past M / N are clamped to the last row (in bounds; masked at the store).
+  constexpr int PER_WAVE = C::BLOCKS / 4;
+  const uint8_t* src[PER_WAVE];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int q = tid + i * kThreads, row = q >> 3, c = q & 7;
-      const int m = m0 + row;
-      if (m < M) ra[i] = *reinterpret_cast<const u32x4*>(qa + (size_t)m * K + k0 + c * 16);
-      else ra[i] = u32x4{0, 0, 0, 0};
-      const int n = n0 + row;
-      if (n < N) rb[i] = *reinterpret_cast<const u32x4*>(qw + (size_t)n * K + k0 + c * 16);
-      else rb[i] = u32x4{0, 0, 0, 0};
+  for (int i = 0; i < PER_WAVE; ++i) {
+    const int blk = wave + 4 * i;
+    const int ks = blk / C::SUB, rem = blk % C::SUB, h = rem & 1;
+    const int rr = 8 * h + (lane >> 3);             // row within the 16-row group
+    const int ch = (lane & 7) ^ (rr >> 1);          // 16-byte chunk of the row
+    if (rem < 2 * C::RA) {
+      const int row = min(m0 + (rem >> 1) * 16 + rr, M - 1);
+      src[i] = qa + (size_t)row * K + ks * 128 + 16 * ch;
+    } else {
+      const int row = min(n0 + ((rem - 2 * C::RA) >> 1) * 16 + rr, N - 1);
+      src[i] = qw + (size_t)row * K + ks * 128 + 16 * ch;
     }
-  };
-  auto lstore = [&](int buf) {
-    uint8_t* As = smem[buf];
-    uint8_t* Bs = smem[buf] + BM * BK;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int q = tid + i * kThreads, row = q >> 3, c = q & 7;
-      *reinterpret_cast<u32x4*>(As + swz(row, c)) = ra[i];
-      *reinterpret_cast<u32x4*>(Bs + swz(row, c)) = rb[i];
-    }
-  };
-
-  f32x4 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int KT = K / BK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < KT) gload((kt + 1) * BK);
-    const uint8_t* As = smem[buf];
-    const uint8_t* Bs = smem[buf] + BM * BK;
-    i32x8 af[4], bfr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = wm * 64 + i * 16 + r16;
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(As + swz(row, 2 * g));
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(As + swz(row, 2 * g + 1));
-      af[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = wn * 64 + j * 16 + r16;
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(Bs + swz(row, 2 * g));
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(Bs + swz(row, 2 * g + 1));
-      bfr[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma_fp8(af[i], bfr[j], acc[i][j]);
-    if (kt + 1 < KT) lstore(buf ^ 1);
-    __syncthreads();
   }
+  auto issue = [&](int k0, int buf) {
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) load_lds16(src[i] + k0, smem + buf * C::STAGE + (wave + 4 * i) * 1024);
+  };
 
-  // epilogue: y = bf16((acc * sa) * sw)
+  f32x4 acc[C::WI][C::WJ];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int n = n0 + wn * 64 + j * 16 + r16;
-    if (n >= N) continue;
-    const float swv = sw[sw_cols ? n : 0];
+  for (int i = 0; i < C::WI; ++i)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int j = 0; j < C::WJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = K / (BK * KS);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * 64 + i * 16 + 4 * g + r;
-        if (m < M) {
-          const float sav = sa[sa_rows ? m : 0];
-          y[(size_t)m * ldy + n] = (bf16_t)f32_to_bf16((acc[i][j][r] * sav) * swv);
-        }
+  for (int st = 0; st < S - 1; ++st)
+    if (st < KT) issue(st * BK * KS, st);
+  // fragment read offsets (within a k-substep): rows r16 of block pair blk, chunks 2g, 2g+1
+  const int frag = 128 * (r16 & 7) + 1024 * (r16 >> 3);
+  const int c0 = 16 * ((2 * g) ^ (r16 >> 1)), c1 = 16 * ((2 * g + 1) ^ (r16 >> 1));
+  for (int kt = 0; kt < KT; ++kt) {
+    // stage kt has landed once at most (stages issued after it) x PER_WAVE loads remain
+    if (kt + S - 2 < KT) wait_vmcnt<(S - 2) * PER_WAVE>();
+    else wait_vmcnt<0>();
+    __syncthreads();  // every wave's loads for stage kt landed; stage kt-1 fully consumed
+    if (kt + S - 1 < KT) issue((kt + S - 1) * BK * KS, (kt + S - 1) % S);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const uint8_t* st = smem + (kt % S) * C::STAGE + ks * C::SUB * 1024 + frag;
+      i32x8 af[C::WI];
+#pragma unroll
+      for (int i = 0; i < C::WI; ++i) {
+        const uint8_t* p = st + 2 * (wm * C::WI + i) * 1024;
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(p + c0);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(p + c1);
+        af[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      }
+#pragma unroll
+      for (int j = 0; j < C::WJ; ++j) {
+        const uint8_t* p = st + (2 * C::RA + 2 * (wn * C::WJ + j)) * 1024;
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(p + c0);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(p + c1);
+        const i32x8 bfr = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+#pragma unroll
+        for (int i = 0; i < C::WI; ++i) acc[i][j] = mfma_fp8(af[i], bfr, acc[i][j]);
       }
     }
   }
+  __syncthreads();  // all stages consumed before the epilogue reuses the LDS
+
+  // epilogue: y = bf16((acc * sa) * sw), staged through LDS as a row-major tile.
+  bf16_t* tile = reinterpret_cast<bf16_t*>(smem);
+#pragma unroll
+  for (int j = 0; j < C::WJ; ++j) {
+    const int cl = wn * (BN / 2) + j * 16 + r16;
+    const int n = min(n0 + cl, N - 1);
+    const float swv = sw[sw_cols ? n : 0];
+#pragma unroll
+    for (int i = 0; i < C::WI; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int rl = wm * (BM / 2) + i * 16 + 4 * g + r;
+        const int m = min(m0 + rl, M - 1);
+        const float sav = sa[sa_rows ? m : 0];
+        tile[rl * C::EPI_LD + cl] = (bf16_t)f32_to_bf16((acc[i][j][r] * sav) * swv);
+      }
+  }
+  __syncthreads();
+  constexpr int CHUNKS = BM * BN / 8;
+#pragma unroll
+  for (int c = tid; c < CHUNKS; c += kThreads) {
+    const int rl = c / (BN / 8), cl = (c % (BN / 8)) * 8;
+    const int m = m0 + rl, n = n0 + cl;
+    if (m < M && n < N)
+      *reinterpret_cast<u32x4*>(y + (size_t)m * ldy + n) = *reinterpret_cast<const u32x4*>(tile + rl * C::EPI_LD + cl);
+  }
+}
+
+template <int BM, int BN, int KS, int S>
+int launch(const void* qa, const float* sa, int sa_rows, const void* qw, const float* sw, int sw_cols,
+           void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, hipStream_t s) {
+  const int tiles_m = (int)((m + BM - 1) / BM), tiles_n = (int)((n + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_fp8_kernel<BM, BN, KS, S>), dim3(tiles_m * tiles_n), dim3(kThreads), 0, s,
+                     (const uint8_t*)qa, sa, sa_rows, (const uint8_t*)qw, sw, sw_cols, (bf16_t*)y, ldy, (int)m,
+                     (int)n, (int)k, tiles_m, tiles_n);
+  return FF_OK;
+}
+
+// Tile choice (measured on the Qwen3-VL shapes at M = 320..1024): 128 x 256 when
+// the N dimension alone gives at least two full waves of workgroups, else
+// 128 x 128 with two 128-byte k-substeps per stage.
+int pick_tile(int64_t m, int64_t n) {
+  const int64_t tiles_256 = ((m + 127) / 128) * ((n + 255) / 256);
+  return tiles_256 >= 2 * 256 - 64 ? 128256 : 128128;
 }
 
 }  // namespace
@@ -143,13 +211,22 @@ extern "C" int ff_gemm_fp8(const void* qa, const float* sa, int sa_rows, const v
   FF_REQUIRE(qa && sa && qw && sw && y, "ff_gemm_fp8: null pointer");
   FF_REQUIRE(m >= 0 && n > 0 && k > 0 && k % BK == 0, "ff_gemm_fp8: k=%lld must be a multiple of %d",
              (long long)k, BK);
-  FF_REQUIRE(ldy >= n && m < (1 << 30) && n < (1 << 30) && k < (1 << 30), "ff_gemm_fp8: bad sizes");
-  FF_REQUIRE(ff_aligned(qa, 16) && ff_aligned(qw, 16), "ff_gemm_fp8: operands must be 16-byte aligned");
+  FF_REQUIRE(n % 8 == 0 && ldy >= n && ldy % 8 == 0 && m < (1 << 30) && n < (1 << 30) && k < (1 << 30),
+             "ff_gemm_fp8: bad sizes (n and ldy must be multiples of 8)");
+  FF_REQUIRE(ff_aligned(qa, 16) && ff_aligned(qw, 16) && ff_aligned(y, 16),
+             "ff_gemm_fp8: operands must be 16-byte aligned");
   if (m == 0) return FF_OK;
-  const int tiles_m = (int)((m + BM - 1) / BM), tiles_n = (int)((n + BN - 1) / BN);
-  hipLaunchKernelGGL(gemm_fp8_kernel, dim3(tiles_m * tiles_n), dim3(kThreads), 0, (hipStream_t)stream,
-                     (const uint8_t*)qa, sa, sa_rows, (const uint8_t*)qw, sw, sw_cols, (bf16_t*)y, ldy,
-                     (int)m, (int)n, (int)k, tiles_m, tiles_n);
+  hipStream_t s = (hipStream_t)stream;
+  // FF_GEMM_FP8_TILE=<bm>x<bn> forces a tile (tuning sweeps); unset = the model's choice.
+  static const int forced = [] {
+    const char* e = getenv("FF_GEMM_FP8_TILE");
+    int bm = 0, bn = 0;
+    return (e && sscanf(e, "%dx%d", &bm, &bn) == 2) ? bm * 1000 + bn : 0;
+  }();
+  const int tile = forced ? forced : pick_tile(m, n);
+  if (tile == 128256) launch<128, 256, 1, 3>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
+  else if (k % (2 * BK) == 0) launch<128, 128, 2, 2>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
+  else launch<128, 128, 1, 4>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
   FF_LAUNCH_CHECK("ff_gemm_fp8");
   return FF_OK;
 }
