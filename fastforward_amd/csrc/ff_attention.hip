@@ -9,6 +9,8 @@
 // inside each 32-key chunk is chosen so that lane group g = l/16 owns keys
 // 8g..8g+7 in both products; V^T (keys contiguous per d) is produced once per
 // layer by the q/k/v post-processing kernel.
+#include <stdlib.h>
+
 #include "ff_common.h"
 
 using namespace ff;
@@ -119,13 +121,99 @@ __global__ __launch_bounds__(kThreads) void qkv_post_kernel(
 }
 
 // ---------------------------------------------------------------- attention
+//
+// Both attention kernels keep the reference kernel's schedule (BN = 64): keys
+// are consumed in 64-key blocks aligned at key 0 with one running-max update
+// per block; s = q.k * scale in fp32, p = exp(s - max), den = den*alpha +
+// sum(p), acc = acc*alpha + bf16(p).V, out = acc/den. exp is the hardware
+// exp2 of (s - max) * log2(e), as tl.exp lowers on the reference's GPUs.
+// Both kernels share the per-block softmax below, so they produce identical
+// bits for the same query.
 
-// S^T tile pair for one 32-key chunk starting at kc: lane (r16, g) gets the
-// scaled scores of keys kc + 8g + jj (jj = 0..7) for its query, with keys past
-// the query's position (or past t) at -inf. A-row i of tile tt is key
-// kc + 8*(i/4) + 4*tt + (i%4), so both products see the same key order.
+// Reductions over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48)
+// with the gfx950 row-swap permutes; every lane receives the result.
+__device__ __forceinline__ float max_rows(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_rows(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// One 64-key block of the online softmax for a 16-query tile held as S^T
+// accumulators: s[2c + tt][r] = q.k of key kb + 32c + 8g + 4tt + r for the
+// lane's query (lane (r16, g) = (query, key group)). Keys whose offset
+// 32c + 4tt + r exceeds lim = min(position, t-1) - kb - 8g are masked when
+// `masked` (blocks entirely visible to the tile skip it). Returns alpha and P^T
+// as bf16 B-operand fragments (keys kb + 32c + 8g .. +7 in pf[c]); den is this
+// lane's partial denominator over its key groups (reduced with sum_rows at the
+// end); m is the running max of q.k (the scale is positive, so max commutes
+// with it).
+__device__ __forceinline__ float softmax_block(f32x4 (&s)[4], bool masked, int lim, float c2, float& m,
+                                               float& den, u32x4 (&pf)[2]) {
+  if (masked) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (32 * (i >> 1) + 4 * (i & 1) + r > lim) s[i][r] = -INFINITY;
+  }
+  float bmax = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+#pragma unroll
+  for (int i = 1; i < 4; ++i) bmax = fmaxf(bmax, fmaxf(fmaxf(s[i][0], s[i][1]), fmaxf(s[i][2], s[i][3])));
+  const float mnew = fmaxf(m, max_rows(bmax));
+  const float mref = mnew == -INFINITY ? 0.f : mnew;  // a fully masked query keeps p = 0, alpha = 0
+  const float alpha = __builtin_amdgcn_exp2f((m - mref) * c2);
+  float p[16], psum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float e = __builtin_amdgcn_exp2f((s[i][r] - mref) * c2);
+      p[4 * i + r] = e;
+      psum += e;
+    }
+  den = den * alpha + psum;
+  m = mnew;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    pf[c].x = pack_bf16x2(p[8 * c + 0], p[8 * c + 1]);
+    pf[c].y = pack_bf16x2(p[8 * c + 2], p[8 * c + 3]);
+    pf[c].z = pack_bf16x2(p[8 * c + 4], p[8 * c + 5]);
+    pf[c].w = pack_bf16x2(p[8 * c + 6], p[8 * c + 7]);
+  }
+  return alpha;
+}
+
+// acc *= alpha, skipped when no query of the wave changed its max (alpha == 1
+// exactly leaves acc unchanged).
+__device__ __forceinline__ void rescale(f32x4 (&o)[8], float alpha) {
+  if (__ballot(alpha != 1.f)) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[dt] = o[dt] * alpha;
+  }
+}
+
+__device__ __forceinline__ void store_rows(bf16_t* __restrict__ yp, const f32x4 (&o)[8], float den, int g) {
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    u32x2 w2;
+    w2.x = pack_bf16x2(o[dt][0] / den, o[dt][1] / den);
+    w2.y = pack_bf16x2(o[dt][2] / den, o[dt][3] / den);
+    *reinterpret_cast<u32x2*>(yp + 16 * dt + 4 * g) = w2;
+  }
+}
+
+// S^T tiles of one 32-key chunk starting at kc read straight from global
+// memory: A-row i of tile tt is key kc + 8*(i/4) + 4*tt + (i%4), so lane group
+// g of the result holds keys kc + 8g + 4tt + r.
 __device__ __forceinline__ void score_chunk(const bf16_t* __restrict__ kp, const u32x4* qf, int kc, int t,
-                                            int pos, float scale, int r16, int g, float* sc) {
+                                            int r16, int g, f32x4& s0, f32x4& s1) {
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     int key = kc + 8 * (r16 >> 2) + 4 * tt + (r16 & 3);
@@ -134,23 +222,18 @@ __device__ __forceinline__ void score_chunk(const bf16_t* __restrict__ kp, const
     f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < 4; ++st) a = mfma_bf16(*reinterpret_cast<const u32x4*>(kr + 32 * st + 8 * g), qf[st], a);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int kk = kc + 8 * g + 4 * tt + r;
-      sc[4 * tt + r] = (kk > pos || kk >= t) ? -INFINITY : a[r] * scale;
-    }
+    (tt ? s1 : s0) = a;
   }
 }
 
-// Grid (ceil(s/64), hq); 4 waves, each owns 16 queries of one head. Keys are
-// consumed in 64-key blocks aligned at key 0 with one running-max update per
-// block, as the reference kernel does (BN = 64): s = (q.k)*scale in fp32,
-// p = exp(s - max), den = den*alpha + sum(p), acc = acc*alpha + bf16(p).V,
-// out = acc/den.
+// Per-head kernel, used for selected query positions (the pick-only tail) and
+// head groups the grouped kernel does not cover. Grid (ceil(s/64), hq);
+// 4 waves, each owns 16 queries of one head; K and V^T are read from global
+// memory (L2) directly.
 __global__ __launch_bounds__(kThreads) void attention_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ vt,
     const int64_t* __restrict__ positions, int gather_q, bf16_t* __restrict__ y, int s_len, int t,
-    int t_pad, int hq, int hk, float scale) {
+    int t_pad, int hq, int hk, float c2) {
   const int head = blockIdx.y;
   const int kvh = head / (hq / hk);
   const int qblock = gridDim.x - 1 - blockIdx.x;  // heaviest (latest) query blocks first
@@ -180,60 +263,187 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, den = 0.f;
+  const int plim = min(pos, t - 1);
 
   for (int kb = 0; kb < kend; kb += 64) {
-    const bool two = kb + 32 < kend;  // wave-uniform: second chunk has a visible key
-    float sc[16];
-    score_chunk(kp, qf, kb, t, pos, scale, r16, g, sc);
+    const bool two = kb + 32 < kend;  // wave-uniform: the second chunk has a visible key
+    f32x4 sc[4];
+    score_chunk(kp, qf, kb, t, r16, g, sc[0], sc[1]);
     if (two) {
-      score_chunk(kp, qf, kb + 32, t, pos, scale, r16, g, sc + 8);
+      score_chunk(kp, qf, kb + 32, t, r16, g, sc[2], sc[3]);
     } else {
-#pragma unroll
-      for (int jj = 8; jj < 16; ++jj) sc[jj] = -INFINITY;
+      sc[2] = sc[3] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     }
-    float bmax = sc[0];
-#pragma unroll
-    for (int jj = 1; jj < 16; ++jj) bmax = fmaxf(bmax, sc[jj]);
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-    const float mnew = fmaxf(m, bmax);
-    const float alpha = expf(m - mnew);
-    float p[16], psum = 0.f;
-#pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      p[jj] = expf(sc[jj] - mnew);
-      psum += p[jj];
-    }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
-    den = den * alpha + psum;
-    m = mnew;
-    u32x4 pf0, pf1;
-    pf0.x = pack_bf16x2(p[0], p[1]);
-    pf0.y = pack_bf16x2(p[2], p[3]);
-    pf0.z = pack_bf16x2(p[4], p[5]);
-    pf0.w = pack_bf16x2(p[6], p[7]);
-    pf1.x = pack_bf16x2(p[8], p[9]);
-    pf1.y = pack_bf16x2(p[10], p[11]);
-    pf1.z = pack_bf16x2(p[12], p[13]);
-    pf1.w = pack_bf16x2(p[14], p[15]);
+    u32x4 pf[2];
+    const float alpha = softmax_block(sc, true, plim - kb - 8 * g, c2, m, den, pf);
+    rescale(o, alpha);
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const bf16_t* vr = vp + (int64_t)(16 * dt + r16) * t_pad + kb + 8 * g;
-      f32x4 acc = o[dt] * alpha;
-      acc = mfma_bf16(*reinterpret_cast<const u32x4*>(vr), pf0, acc);
-      if (two) acc = mfma_bf16(*reinterpret_cast<const u32x4*>(vr + 32), pf1, acc);
-      o[dt] = acc;
+      o[dt] = mfma_bf16(*reinterpret_cast<const u32x4*>(vr), pf[0], o[dt]);
+      if (two) o[dt] = mfma_bf16(*reinterpret_cast<const u32x4*>(vr + 32), pf[1], o[dt]);
     }
   }
+  den = sum_rows(den);
   if (!qvalid) return;
-  bf16_t* yp = y + ((int64_t)qi * hq + head) * D;
+  store_rows(y + ((int64_t)qi * hq + head) * D, o, den, g);
+}
+
+// ---------------------------------------------------------------- grouped prefill attention
+//
+// A workgroup owns one 64-key-block walk for HPW query heads that share a kv
+// head (HPW = 4, 2 or 1 for GQA groups that are multiples of 4, 2 or 1) and
+// QB = 16*QT*(4/HPW) consecutive queries: wave w takes head w % HPW and QT
+// tiles of 16 queries from row set w / HPW. Each 64-key block of K
+// (64 x 256 B) and V^T (128 x 128 B) is fetched once per workgroup into LDS
+// with global_load_lds_dwordx4 (one 1 KB instruction = 8 rows x 128 B, whole
+// cache lines), three stages deep with two in flight, and every fragment read
+// from LDS feeds QT MFMAs.
+//
+// LDS stage layout (32 KB): K at [0, 16 KB), V^T at [16 KB, 32 KB), each as
+// sixteen 1 KB blocks of 8 rows x 128 B. K row `key` (0..63 within the block)
+// half h sits in block 2*(key/8) + h, row key%8; V^T row d in block d/8, row
+// d%8. Inside a 128 B row the 16 B chunk c is stored at slot c ^ swz with
+// swz = ((key>>1)&1) | ((key>>2)&6) for K and (d>>1)&7 for V^T, which makes
+// every MFMA fragment read (16 lanes per LDS cycle) hit 16 distinct bank
+// groups.
+//
+// Grid: one dimension, heaviest query blocks first across all groups; the
+// group is blockIdx % (hq/HPW), so with 8 XCDs taking workgroups round-robin
+// the groups of one kv head stay on one XCD (and its L2).
+template <int QT, int HPW>
+__global__ __launch_bounds__(kThreads, 1) void attention_prefill_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ vt,
+    bf16_t* __restrict__ y, int s_len, int t, int t_pad, int hq, int hk, float c2, int nqb) {
+  constexpr int QB = 16 * QT * (4 / HPW);
+  constexpr int STAGE = 32 * 1024;
+  constexpr int NS = 3;
+  __shared__ __align__(1024) uint8_t smem[NS * STAGE];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int ngroups = hq / HPW;
+  const int grp = (int)blockIdx.x % ngroups;
+  const int qb = nqb - 1 - (int)blockIdx.x / ngroups;
+  const int head = grp * HPW + wave % HPW;
+  const int kvh = head / (hq / hk);
+  const int q0 = qb * QB;
+  const int wq0 = q0 + (wave / HPW) * 16 * QT;  // first query of this wave
+  const int kend = min(t, min(s_len, q0 + QB));  // keys [0, kend) are visible to some query
+  const int nblocks = (kend + 63) / 64;
+
+  // Load sources of this lane: blocks wave + 4i, i = 0..7 (0..15 K, 16..31 V^T).
+  const bf16_t* kbase = k + (int64_t)kvh * t * D;
+  const bf16_t* vbase = vt + (int64_t)kvh * D * t_pad;
+  int k_key[4], k_col[4];
+  int64_t v_off[4];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) {
-    u32x2 w2;
-    w2.x = pack_bf16x2(o[dt][0] / den, o[dt][1] / den);
-    w2.y = pack_bf16x2(o[dt][2] / den, o[dt][3] / den);
-    *reinterpret_cast<u32x2*>(yp + 16 * dt + 4 * g) = w2;
+  for (int i = 0; i < 4; ++i) {
+    const int bi = wave + 4 * i;  // K block
+    const int key = 8 * (bi >> 1) + (lane >> 3);
+    const int swz = ((key >> 1) & 1) | ((key >> 2) & 6);
+    k_key[i] = key;
+    k_col[i] = 64 * (bi & 1) + 8 * ((lane & 7) ^ swz);
+    const int d = 8 * bi + (lane >> 3);  // V^T block bi
+    v_off[i] = (int64_t)d * t_pad + 8 * ((lane & 7) ^ ((d >> 1) & 7));
+  }
+  const uint32_t lds0 = lds_addr(smem) + (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 1024;
+  auto issue = [&](int kb, int buf) {
+    const uint32_t st = lds0 + buf * STAGE;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = min(kb + k_key[i], t - 1);
+      lds_dma16(kbase + (int64_t)key * D + k_col[i], st + 4 * i * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lds_dma16(vbase + v_off[i] + kb, st + 16 * 1024 + 4 * i * 1024);
+  };
+
+  // Fragment read offsets (bytes within a stage). K fragment (c, tt, st):
+  // key = 32c + 8(r16>>2) + 4tt + (r16&3), d chunk 4st + g, swz = r16>>1.
+  // V^T fragment (dt, c): d = 16dt + r16, key chunk 4c + g, swz = (r16>>1)&7.
+  const int sw = r16 >> 1;
+  auto koff = [&](int c, int tt, int st) {
+    return ((4 * c + (r16 >> 2)) * 2 + (st >> 1)) * 1024 + (4 * tt + (r16 & 3)) * 128 +
+           16 * ((4 * (st & 1) + g) ^ sw);
+  };
+  auto voff = [&](int dt, int c) {
+    return 16 * 1024 + (2 * dt + (r16 >> 3)) * 1024 + (r16 & 7) * 128 + 16 * ((4 * c + g) ^ sw);
+  };
+
+  f32x4 o[QT][8];
+  float m[QT], den[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    m[qt] = -INFINITY;
+    den[qt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // The first two key blocks and the queries load together. The queries are
+  // waited for before the loop: a compiler-placed wait for them inside the
+  // loop would also wait for the prefetches issued there.
+  issue(0, 0);
+  if (nblocks > 1) issue(64, 1);
+  u32x4 qf[QT][4];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qrow = min(wq0 + 16 * qt + r16, s_len - 1);
+    const bf16_t* qp = q + ((int64_t)head * s_len + qrow) * D;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) qf[qt][st] = *reinterpret_cast<const u32x4*>(qp + 32 * st + 8 * g);
+  }
+  // consuming the registers here makes the compiler wait for the loads now
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+      asm volatile("" : : "v"(qf[qt][st].x), "v"(qf[qt][st].y), "v"(qf[qt][st].z), "v"(qf[qt][st].w));
+  for (int ib = 0; ib < nblocks; ++ib) {
+    if (ib + 1 < nblocks) wait_vmcnt<8>();
+    else wait_vmcnt<0>();
+    barrier_lds();  // block ib landed for every wave; block ib-1 fully consumed
+    if (ib + 2 < nblocks) issue((ib + 2) * 64, (ib + 2) % NS);
+    const int kb = ib * 64;
+    if (kb >= s_len || kb > wq0 + 16 * QT - 1) continue;  // wave-uniform: no query of the wave sees it
+    const uint8_t* st_base = smem + (ib % NS) * STAGE;
+
+    f32x4 sc[QT][4];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc[qt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(st_base + koff(i >> 1, i & 1, st));
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) sc[qt][i] = mfma_bf16(kf, qf[qt][st], sc[qt][i]);
+      }
+    u32x4 pf[QT][2];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int tq0 = wq0 + 16 * qt;  // first query of the tile
+      const bool masked = kb + 63 > tq0 || kb + 63 >= t;
+      const int lim = min(tq0 + r16, t - 1) - kb - 8 * g;
+      const float alpha = softmax_block(sc[qt], masked, lim, c2, m[qt], den[qt], pf[qt]);
+      rescale(o[qt], alpha);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const u32x4 vf = *reinterpret_cast<const u32x4*>(st_base + voff(dt, c));
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) o[qt][dt] = mfma_bf16(vf, pf[qt][c], o[qt][dt]);
+      }
+  }
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const float dsum = sum_rows(den[qt]);
+    const int qi = wq0 + 16 * qt + r16;
+    if (qi < s_len) store_rows(y + ((int64_t)qi * hq + head) * D, o[qt], dsum, g);
   }
 }
 
@@ -311,9 +521,35 @@ extern "C" int ff_attention_vt(const void* q, const void* k, const void* vt, con
   FF_REQUIRE(!gather_q || positions, "ff_attention_vt: gather_q needs positions");
   FF_REQUIRE(ff_aligned(q, 16) && ff_aligned(k, 16) && ff_aligned(vt, 16) && ff_aligned(y, 8),
              "ff_attention_vt: alignment");
-  hipLaunchKernelGGL(attention_kernel, dim3((unsigned)((s + 63) / 64), (unsigned)hq), dim3(kThreads), 0,
-                     (hipStream_t)stream, (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)vt, positions,
-                     gather_q, (bf16_t*)y, (int)s, (int)t, (int)t_pad, (int)hq, (int)hk, scale);
+  const float c2 = (float)((double)scale * 1.4426950408889634);  // scale * log2(e)
+  const int group = (int)(hq / hk);
+  const int hpw = group % 4 == 0 ? 4 : (group == 2 ? 2 : (group == 1 ? 1 : 0));
+  hipStream_t st = (hipStream_t)stream;
+  if (!positions && s == t && hpw) {
+    // FF_ATTN_QT=<1|2|4> overrides the query tiles per wave (tuning).
+    static const int qt_env = [] {
+      const char* e = getenv("FF_ATTN_QT");
+      return e ? atoi(e) : 0;
+    }();
+    const int qt = (qt_env == 1 || qt_env == 2 || qt_env == 4) ? qt_env : (s <= 1024 ? 1 : (s <= 2048 ? 2 : 4));
+    const int qb = 16 * qt * (4 / hpw);
+    const int nqb = (int)((s + qb - 1) / qb);
+    const dim3 grid((unsigned)(nqb * (hq / hpw))), block(kThreads);
+#define FF_PREFILL(QT, HPW)                                                                                  \
+  if (qt == QT && hpw == HPW)                                                                                \
+    hipLaunchKernelGGL((attention_prefill_kernel<QT, HPW>), grid, block, 0, st, (const bf16_t*)q,            \
+                       (const bf16_t*)k, (const bf16_t*)vt, (bf16_t*)y, (int)s, (int)t, (int)t_pad, (int)hq, \
+                       (int)hk, c2, nqb);
+    FF_PREFILL(1, 4) FF_PREFILL(2, 4) FF_PREFILL(4, 4)
+    FF_PREFILL(1, 2) FF_PREFILL(2, 2) FF_PREFILL(4, 2)
+    FF_PREFILL(1, 1) FF_PREFILL(2, 1) FF_PREFILL(4, 1)
+#undef FF_PREFILL
+    FF_LAUNCH_CHECK("ff_attention_vt");
+    return FF_OK;
+  }
+  hipLaunchKernelGGL(attention_kernel, dim3((unsigned)((s + 63) / 64), (unsigned)hq), dim3(kThreads), 0, st,
+                     (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)vt, positions, gather_q, (bf16_t*)y,
+                     (int)s, (int)t, (int)t_pad, (int)hq, (int)hk, c2);
   FF_LAUNCH_CHECK("ff_attention_vt");
   return FF_OK;
 }

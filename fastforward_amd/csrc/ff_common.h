@@ -19,6 +19,38 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+// ------------------------------------------------------------------ LDS DMA pipelines
+//
+// global_load_lds_dwordx4 copies 16 bytes per lane from global memory into LDS
+// at M0 + 16*lane with no register round trip. It is issued from inline asm so
+// that the compiler's wait-count pass does not track it: that pass otherwise
+// waits for every such load before the next LDS read it cannot prove disjoint,
+// and __syncthreads() (a workgroup fence) waits for all of them as well, which
+// collapses a multi-stage pipeline to one stage. Kernels that use lds_dma16
+// wait for their own loads with wait_vmcnt<N>() (loads complete in issue
+// order) and synchronise with barrier_lds().
+
+// 32-bit LDS address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// lds (wave-uniform) receives 16 bytes from src of every lane, lane l at lds + 16*l.
+__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds)
+               : "memory", "m0");
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier without a memory fence; this wave's LDS reads complete first.
+__device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
+
 // ------------------------------------------------------------------ bf16
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }

@@ -336,6 +336,22 @@ def test_attention_causal(gpu, t, hq, hk):
     assert float((got - want).pow(2).mean().sqrt() / want.pow(2).mean().sqrt()) <= 5e-3
 
 
+@pytest.mark.parametrize("t,hq,hk", [(576, 32, 8), (1000, 64, 8), (129, 16, 4), (17, 8, 2)])
+def test_attention_prefill_matches_per_head_kernel(gpu, t, hq, hk):
+    """The grouped prefill kernel (>= 4 query heads per kv head, K/V staged in
+    LDS) and the per-head kernel (taken when positions are given) run the same
+    64-key-block online softmax in the same order: results are bit-identical."""
+    from fastforward_amd import ops
+    d = 128
+    q = torch.randn(1, hq, t, d, generator=_g(40)).to(BF16).to(DEV)
+    k = torch.randn(1, hk, t, d, generator=_g(41)).to(BF16).to(DEV)
+    v = (torch.randn(1, hk, t, d, generator=_g(42)) * 3).to(BF16).to(DEV)
+    pos = torch.arange(t, device=DEV)
+    grouped = ops.attention_direct(q, k, v, d ** -0.5)
+    per_head = ops.attention_direct(q, k, v, d ** -0.5, positions=pos)
+    assert torch.equal(grouped, per_head)
+
+
 def test_attention_selected_positions_and_strided_v(gpu):
     from fastforward_amd import ops
     t, hq, hk, d = 576, 32, 8, 128
