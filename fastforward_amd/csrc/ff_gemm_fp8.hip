@@ -37,24 +37,9 @@ constexpr int BK = 128;
 constexpr int kThreads = 256;
 constexpr int kXcds = 8;
 
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(1))) void glb_void;
-
 __device__ __forceinline__ f32x4 mfma_fp8(const i32x8& a, const i32x8& b, const f32x4& c) {
   // scale operands 0 select the unscaled v_mfma_f32_16x16x128_f8f6f4; format 0 = e4m3.
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
-}
-
-__device__ __forceinline__ void load_lds16(const void* g, uint8_t* lds) {
-  __builtin_amdgcn_global_load_lds((glb_void*)g, (lds_void*)lds, 16, 0, 0);
-}
-
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
-// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
 template <int BM, int BN, int KS, int S>
@@ -109,9 +94,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_kernel(
       src[i] = qw + (size_t)row * K + ks * 128 + 16 * ch;
     }
   }
+  const uint32_t lds0 = lds_addr(smem) + (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 1024;
   auto issue = [&](int k0, int buf) {
 #pragma unroll
-    for (int i = 0; i < PER_WAVE; ++i) load_lds16(src[i] + k0, smem + buf * C::STAGE + (wave + 4 * i) * 1024);
+    for (int i = 0; i < PER_WAVE; ++i) lds_dma16(src[i] + k0, lds0 + buf * C::STAGE + 4 * i * 1024);
   };
 
   f32x4 acc[C::WI][C::WJ];
@@ -131,7 +117,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_kernel(
     // stage kt has landed once at most (stages issued after it) x PER_WAVE loads remain
     if (kt + S - 2 < KT) wait_vmcnt<(S - 2) * PER_WAVE>();
     else wait_vmcnt<0>();
-    __syncthreads();  // every wave's loads for stage kt landed; stage kt-1 fully consumed
+    barrier_lds();  // every wave's loads for stage kt landed; stage kt-1 fully consumed
     if (kt + S - 1 < KT) issue((kt + S - 1) * BK * KS, (kt + S - 1) % S);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
