@@ -107,6 +107,28 @@ def _traffic():
     return None
 
 
+def kernel_pass(cfg, w, T, reps=5):
+    """Counter-collection workload: each FP8 GEMM shape of the step (layer 0's
+    weights) ``reps`` times, then a 256 MiB bf16 scale-by-one (read 256 MiB,
+    write 256 MiB) as the copy kernel that calibrates FETCH_SIZE / WRITE_SIZE."""
+    lw = w.layers[0]
+    for role, m, _ in gemm_launches(cfg, T):
+        op = getattr(lw, role)
+        n, k = op.weight.shape
+        q, s = op.quantize(torch.randn(T, k, device="cuda").to(torch.bfloat16))
+        out = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+        for _ in range(reps):
+            op.gemm(q[:m], s[:m], out)
+        torch.cuda.synchronize()
+        log(f"gemm {role} {m}x{k}x{n} x{reps}")
+    x = torch.ones(128 << 20, device="cuda", dtype=torch.bfloat16)
+    for _ in range(reps):
+        y = x * 1.0
+    torch.cuda.synchronize()
+    del x, y
+    log("copy 256 MiB done")
+
+
 def micro_gemms():
     """The FP8 linear microbench shapes (M,K,N): TFLOP/s of one GEMM launch."""
     from fastforward_amd.linear import FP8Linear
@@ -181,10 +203,12 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the W4A16 step and the GEMM microbench")
     ap.add_argument("--profile", action="store_true", help="only replay the graph (for rocprofv3 runs)")
+    ap.add_argument("--kernels", action="store_true",
+                    help="only run the step's GEMM shapes and a calibration copy (rocprofv3 --pmc runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build's step runs on a single MI355X and has no "
-              "multi-GPU path (request-level replicas would scale it; see DESIGN.md)", file=sys.stderr)
+        print("bench.py measures one GPU: the step runs on a single MI355X and has no multi-GPU "
+              "path (independent request-level replicas would scale it)", file=sys.stderr)
         sys.exit(2)
 
     from fastforward_amd import _lib
@@ -197,6 +221,9 @@ def main():
     log(f"building {cfg.name} fp8 (random init, seed 0)")
     w = make_model(cfg, mode="fp8", seed=0, n_options=8)
     ids, pos, pick = make_request(cfg, T, *grid, seed=0)
+    if args.kernels:
+        kernel_pass(cfg, w, T)
+        return
     rt = Runtime(cfg, w, T)
     rt.set_inputs(ids, pos, pick)
     rt.capture()
