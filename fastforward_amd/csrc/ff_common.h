@@ -115,6 +115,37 @@ __device__ __forceinline__ float clamp448(float v) {
   return v != v ? v : fminf(448.0f, fmaxf(-448.0f, v));
 }
 
+// x / d correctly rounded for d > 0, from r = 1/d correctly rounded: the
+// product x*r is within an ulp of the quotient and one FMA residual step rounds
+// it exactly (Markstein). The sign is taken from x, which keeps -0 / d = -0
+// (the residual step would return +0). Quantisation divides a whole row by one
+// scale, so the division is done once per row and this per element.
+__device__ __forceinline__ float div_rcp(float x, float d, float r) {
+  const float y = x * r;
+  const float e = __builtin_fmaf(-y, d, x);
+  return __builtin_copysignf(__builtin_fmaf(e, r, y), x);
+}
+
+// e4m3 codes of four values already clamped to [-448, 448], packed low to high,
+// with v_cvt_pk_fp8_f32 (round to nearest even; the same codes as f32_to_e4m3
+// for every fp32 value of that range).
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+
+// Per-token quantisation of 8 values: clamp(x / scale, +-448) -> e4m3, r = 1/scale.
+__device__ __forceinline__ u32x2 quant8(const float* x, float scale, float r) {
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = clamp448(div_rcp(x[i], scale, r));
+  u32x2 p;
+  p.x = e4m3x4(v[0], v[1], v[2], v[3]);
+  p.y = e4m3x4(v[4], v[5], v[6], v[7]);
+  return p;
+}
+
+
 // ------------------------------------------------------------------ reductions
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -154,6 +185,38 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 #pragma unroll
   for (int i = 1; i < NW; ++i) s = fmaxf(s, red[i]);
   return s;
+}
+
+// Block-wide sum / max for a runtime block of blockDim.x threads (a multiple of 64).
+__device__ __forceinline__ float block_sum_rt(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float s = 0.f;
+  for (int i = 0; i < nw; ++i) s += red[i];
+  return s;
+}
+
+__device__ __forceinline__ float block_max_rt(float v, float* red) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float s = red[0];
+  for (int i = 1; i < nw; ++i) s = fmaxf(s, red[i]);
+  return s;
+}
+
+// Threads per row and 16-byte chunks per thread for a row of nchunk chunks:
+// up to 1024 threads (16 waves) per row, chunks spread evenly.
+inline void row_shape(int64_t nchunk, int* threads, int* cpt) {
+  const int c = (int)((nchunk + 1023) / 1024);
+  const int64_t t = (nchunk + c - 1) / c;
+  *cpt = c;
+  *threads = (int)((t + 63) / 64 * 64);
 }
 
 // 1/sqrt with correctly rounded sqrt and divide (matches 1/std::sqrt on the host).

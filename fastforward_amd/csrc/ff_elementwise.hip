@@ -78,19 +78,20 @@ __global__ __launch_bounds__(kThreads) void swiglu_kernel(const bf16_t* __restri
   }
 }
 
-// One workgroup per row: swiglu, then per-token e4m3 quant of the bf16 result.
+// One workgroup per row (blockDim.x threads, CPT chunks each): swiglu, then
+// per-token e4m3 quant of the bf16 result.
 template <int CPT>
-__global__ __launch_bounds__(kThreads) void swiglu_quant_kernel(
+__global__ __launch_bounds__(1024) void swiglu_quant_kernel(
     const bf16_t* __restrict__ g, const bf16_t* __restrict__ u, int64_t row_stride,
     bf16_t* __restrict__ y, uint8_t* __restrict__ q, float* __restrict__ scales, int i) {
-  __shared__ float red[kWaves];
-  const int row = blockIdx.x;
+  __shared__ float red[16];
+  const int row = blockIdx.x, nt = blockDim.x;
   const int nchunk = i >> 3;
   float o[CPT][8];
   u32x4 vg[CPT], vu[CPT];
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
-    const int idx = threadIdx.x + c * kThreads;
+    const int idx = threadIdx.x + c * nt;
     if (idx < nchunk) {
       vg[c] = *reinterpret_cast<const u32x4*>(g + row * row_stride + idx * 8);
       vu[c] = *reinterpret_cast<const u32x4*>(u + row * row_stride + idx * 8);
@@ -99,7 +100,7 @@ __global__ __launch_bounds__(kThreads) void swiglu_quant_kernel(
   float amax = 0.f;
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
-    const int idx = threadIdx.x + c * kThreads;
+    const int idx = threadIdx.x + c * nt;
     if (idx < nchunk) {
       float gv[8], uv[8];
       unpack8(vg[c], gv);
@@ -112,20 +113,13 @@ __global__ __launch_bounds__(kThreads) void swiglu_quant_kernel(
       if (y) *reinterpret_cast<u32x4*>(y + (size_t)row * i + idx * 8) = pack8(o[c]);
     }
   }
-  amax = block_max<kWaves>(amax, red);
+  amax = block_max_rt(amax, red);
   const float scale = fmaxf(amax, 1e-12f) / 448.0f;
+  const float r = 1.0f / scale;
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
-    const int idx = threadIdx.x + c * kThreads;
-    if (idx < nchunk) {
-      float v[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = clamp448(o[c][k] / scale);
-      u32x2 p;
-      p.x = pack_e4m3x4(v);
-      p.y = pack_e4m3x4(v + 4);
-      *reinterpret_cast<u32x2*>(q + (size_t)row * i + idx * 8) = p;
-    }
+    const int idx = threadIdx.x + c * nt;
+    if (idx < nchunk) *reinterpret_cast<u32x2*>(q + (size_t)row * i + idx * 8) = quant8(o[c], scale, r);
   }
   if (threadIdx.x == 0) scales[row] = scale;
 }
@@ -133,37 +127,30 @@ __global__ __launch_bounds__(kThreads) void swiglu_quant_kernel(
 // ---------------------------------------------------------------- activation quant
 
 template <int CPT>
-__global__ __launch_bounds__(kThreads) void quant_rows_kernel(const bf16_t* __restrict__ x,
-                                                              int64_t x_rs, uint8_t* __restrict__ q,
-                                                              float* __restrict__ scales, int k) {
-  __shared__ float red[kWaves];
-  const int row = blockIdx.x;
+__global__ __launch_bounds__(1024) void quant_rows_kernel(const bf16_t* __restrict__ x, int64_t x_rs,
+                                                         uint8_t* __restrict__ q, float* __restrict__ scales,
+                                                         int k) {
+  __shared__ float red[16];
+  const int row = blockIdx.x, nt = blockDim.x;
   const int nchunk = k >> 3;
   float v[CPT][8];
   float amax = 0.f;
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
-    const int idx = threadIdx.x + c * kThreads;
+    const int idx = threadIdx.x + c * nt;
     if (idx < nchunk) {
       unpack8(*reinterpret_cast<const u32x4*>(x + row * x_rs + idx * 8), v[c]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[c][e]));
     }
   }
-  amax = block_max<kWaves>(amax, red);
+  amax = block_max_rt(amax, red);
   const float scale = fmaxf(amax, 1e-12f) / 448.0f;
+  const float r = 1.0f / scale;
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
-    const int idx = threadIdx.x + c * kThreads;
-    if (idx < nchunk) {
-      float t[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) t[e] = clamp448(v[c][e] / scale);
-      u32x2 p;
-      p.x = pack_e4m3x4(t);
-      p.y = pack_e4m3x4(t + 4);
-      *reinterpret_cast<u32x2*>(q + (size_t)row * k + idx * 8) = p;
-    }
+    const int idx = threadIdx.x + c * nt;
+    if (idx < nchunk) *reinterpret_cast<u32x2*>(q + (size_t)row * k + idx * 8) = quant8(v[c], scale, r);
   }
   if (threadIdx.x == 0) scales[row] = scale;
 }
@@ -365,17 +352,17 @@ extern "C" int ff_swiglu_quant(const void* g, const void* u, int64_t row_stride,
   FF_REQUIRE(ff_aligned(g, 16) && ff_aligned(u, 16) && ff_aligned(q, 8) && (!y || ff_aligned(y, 16)),
              "ff_swiglu_quant: alignment");
   if (rows == 0) return FF_OK;
-  const int cpt = (int)((i / 8 + kThreads - 1) / kThreads);
+  int threads, cpt;
+  row_shape(i / 8, &threads, &cpt);
   hipStream_t s = (hipStream_t)stream;
-#define FF_SWQ(N)                                                                              \
-  case N:                                                                                      \
-    hipLaunchKernelGGL(swiglu_quant_kernel<N>, dim3((unsigned)rows), dim3(kThreads), 0, s,     \
-                       (const bf16_t*)g, (const bf16_t*)u, row_stride, (bf16_t*)y, (uint8_t*)q, \
-                       scales, (int)i);                                                        \
+#define FF_SWQ(N)                                                                                      \
+  case N:                                                                                              \
+    hipLaunchKernelGGL(swiglu_quant_kernel<N>, dim3((unsigned)rows), dim3((unsigned)threads), 0, s,    \
+                       (const bf16_t*)g, (const bf16_t*)u, row_stride, (bf16_t*)y, (uint8_t*)q, scales, \
+                       (int)i);                                                                        \
     break;
   switch (cpt) {
-    FF_SWQ(1) FF_SWQ(2) FF_SWQ(3) FF_SWQ(4) FF_SWQ(5) FF_SWQ(6) FF_SWQ(7) FF_SWQ(8)
-    FF_SWQ(9) FF_SWQ(10) FF_SWQ(11) FF_SWQ(12) FF_SWQ(13) FF_SWQ(14) FF_SWQ(15) FF_SWQ(16)
+    FF_SWQ(1) FF_SWQ(2) FF_SWQ(3) FF_SWQ(4)
     default:
       ff_set_error("ff_swiglu_quant: i=%lld too large", (long long)i);
       return FF_EINVAL;
@@ -392,16 +379,16 @@ extern "C" int ff_quant_rows_fp8(const void* x, int64_t x_rs, void* q, float* sc
              "ff_quant_rows_fp8: bad sizes k=%lld", (long long)k);
   FF_REQUIRE(ff_aligned(x, 16) && ff_aligned(q, 8), "ff_quant_rows_fp8: alignment");
   if (rows == 0) return FF_OK;
-  const int cpt = (int)((k / 8 + kThreads - 1) / kThreads);
   hipStream_t s = (hipStream_t)stream;
-#define FF_QR(N)                                                                                  \
-  case N:                                                                                         \
-    hipLaunchKernelGGL(quant_rows_kernel<N>, dim3((unsigned)rows), dim3(kThreads), 0, s,          \
-                       (const bf16_t*)x, x_rs, (uint8_t*)q, scales, (int)k);                      \
+  int threads, cpt;
+  row_shape(k / 8, &threads, &cpt);
+#define FF_QR(N)                                                                                   \
+  case N:                                                                                          \
+    hipLaunchKernelGGL(quant_rows_kernel<N>, dim3((unsigned)rows), dim3((unsigned)threads), 0, s,  \
+                       (const bf16_t*)x, x_rs, (uint8_t*)q, scales, (int)k);                       \
     break;
   switch (cpt) {
-    FF_QR(1) FF_QR(2) FF_QR(3) FF_QR(4) FF_QR(5) FF_QR(6) FF_QR(7) FF_QR(8)
-    FF_QR(9) FF_QR(10) FF_QR(11) FF_QR(12) FF_QR(13) FF_QR(14) FF_QR(15) FF_QR(16)
+    FF_QR(1) FF_QR(2) FF_QR(3) FF_QR(4)
     default:
       hipLaunchKernelGGL(quant_rows_long_kernel, dim3((unsigned)rows), dim3(kThreads), 0, s,
                          (const bf16_t*)x, x_rs, (uint8_t*)q, scales, (int)k);

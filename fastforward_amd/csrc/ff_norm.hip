@@ -1,44 +1,45 @@
 // Row-wise RMSNorm kernels: fast_norm, add_rms (+ DeepStack rows), their fused
 // per-token e4m3 quant variants, and the choice readout.
 //
-// One workgroup of 256 threads owns one token row. Each thread loads its 16-byte
-// chunks (8 bf16) up front, so a row's whole HBM traffic is in flight before the
-// reduction; rows are independent, and the grid (one workgroup per row) keeps all
-// rows resident at the prefill sizes (<= 2048 rows).
+// One workgroup owns one token row, with up to 1024 threads so that a row's
+// arithmetic spreads over 16 waves. Each thread loads its 16-byte chunks (8
+// bf16) up front, so a row's whole traffic is in flight before the reduction;
+// rows are independent.
 #include "ff_common.h"
 
 using namespace ff;
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
 
-// CPT = 16-byte chunks per thread (h <= CPT * 8 * 256).
+// One workgroup per row, blockDim.x threads (a multiple of 64, <= 1024) with
+// CPT 16-byte chunks each (row_shape picks both from h).
 template <int CPT, bool ADD, bool DEEP, bool WRITE_RES, bool WRITE_OUT, bool QUANT>
-__global__ __launch_bounds__(kThreads) void row_norm_kernel(
+__global__ __launch_bounds__(1024) void row_norm_kernel(
     const bf16_t* __restrict__ a, const bf16_t* __restrict__ b, const bf16_t* __restrict__ deep,
     const bf16_t* __restrict__ w, bf16_t* __restrict__ residual, bf16_t* __restrict__ out,
     uint8_t* __restrict__ q, float* __restrict__ scales, int h, float eps, int start, int nv) {
-  __shared__ float red[kWaves];
+  __shared__ float red[16];
   const int row = blockIdx.x;
   const int nchunk = h >> 3;
+  const int nt = blockDim.x;
   const size_t base = (size_t)row * h;
   float x[CPT][8];
-  u32x4 va[CPT], vb[CPT];
+  u32x4 va[CPT], vb[CPT], vw[CPT];
   const bool in_deep = DEEP && row >= start && row < start + nv;
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
-    const int idx = threadIdx.x + c * kThreads;
+    const int idx = threadIdx.x + c * nt;
     if (idx < nchunk) {
       va[c] = *reinterpret_cast<const u32x4*>(a + base + (size_t)idx * 8);
       if (ADD) vb[c] = *reinterpret_cast<const u32x4*>(b + base + (size_t)idx * 8);
+      vw[c] = *reinterpret_cast<const u32x4*>(w + (size_t)idx * 8);
     }
   }
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
-    const int idx = threadIdx.x + c * kThreads;
+    const int idx = threadIdx.x + c * nt;
     if (idx < nchunk) {
       unpack8(va[c], x[c]);
       if (ADD) {
@@ -58,15 +59,15 @@ __global__ __launch_bounds__(kThreads) void row_norm_kernel(
       for (int i = 0; i < 8; ++i) ss += x[c][i] * x[c][i];
     }
   }
-  const float var = block_sum<kWaves>(ss, red) / (float)h;
+  const float var = block_sum_rt(ss, red) / (float)h;
   const float inv = rsqrt_rn(var + eps);
   float amax = 0.f;
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
-    const int idx = threadIdx.x + c * kThreads;
+    const int idx = threadIdx.x + c * nt;
     if (idx < nchunk) {
       float wv[8];
-      unpack8(*reinterpret_cast<const u32x4*>(w + (size_t)idx * 8), wv);
+      unpack8(vw[c], wv);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         x[c][i] = round_bf16(round_bf16(x[c][i] * inv) * wv[i]);
@@ -76,20 +77,13 @@ __global__ __launch_bounds__(kThreads) void row_norm_kernel(
     }
   }
   if (QUANT) {
-    amax = block_max<kWaves>(amax, red);
+    amax = block_max_rt(amax, red);
     const float scale = fmaxf(amax, 1e-12f) / 448.0f;
+    const float r = 1.0f / scale;
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
-      const int idx = threadIdx.x + c * kThreads;
-      if (idx < nchunk) {
-        u32x2 p;
-        uint32_t e[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) e[i] = f32_to_e4m3(clamp448(x[c][i] / scale));
-        p.x = e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24);
-        p.y = e[4] | (e[5] << 8) | (e[6] << 16) | (e[7] << 24);
-        *reinterpret_cast<u32x2*>(q + base + (size_t)idx * 8) = p;
-      }
+      const int idx = threadIdx.x + c * nt;
+      if (idx < nchunk) *reinterpret_cast<u32x2*>(q + base + (size_t)idx * 8) = quant8(x[c], scale, r);
     }
     if (threadIdx.x == 0) scales[row] = scale;
   }
@@ -99,8 +93,9 @@ template <bool ADD, bool DEEP, bool WRITE_RES, bool WRITE_OUT, bool QUANT>
 int launch_row_norm(const void* a, const void* b, const void* deep, const void* w, void* residual,
                     void* out, void* q, float* scales, int64_t rows, int64_t h, float eps,
                     int64_t start, int64_t nv, hipStream_t s, const char* name) {
-  const int cpt = (int)((h / 8 + kThreads - 1) / kThreads);
-  dim3 grid((unsigned)rows), block(kThreads);
+  int threads, cpt;
+  row_shape(h / 8, &threads, &cpt);
+  dim3 grid((unsigned)rows), block((unsigned)threads);
 #define FF_ROWNORM_CASE(N)                                                                       \
   case N:                                                                                        \
     hipLaunchKernelGGL((row_norm_kernel<N, ADD, DEEP, WRITE_RES, WRITE_OUT, QUANT>), grid, block, \
@@ -111,12 +106,6 @@ int launch_row_norm(const void* a, const void* b, const void* deep, const void* 
   switch (cpt) {
     FF_ROWNORM_CASE(1)
     FF_ROWNORM_CASE(2)
-    FF_ROWNORM_CASE(3)
-    FF_ROWNORM_CASE(4)
-    FF_ROWNORM_CASE(5)
-    FF_ROWNORM_CASE(6)
-    FF_ROWNORM_CASE(7)
-    FF_ROWNORM_CASE(8)
     default:
       ff_set_error("%s: h=%lld too large", name, (long long)h);
       return FF_EINVAL;
@@ -137,34 +126,60 @@ int check_rows(const char* name, const void* x, int64_t rows, int64_t h) {
 
 // ---------------------------------------------------------------- readout
 
-// One workgroup: normalise the (optionally summed) row once, then each wave
-// computes dot products for options w, w+4, ...
-__global__ __launch_bounds__(kThreads) void readout_kernel(const bf16_t* __restrict__ x,
-                                                           const bf16_t* __restrict__ x2,
-                                                           const bf16_t* __restrict__ w,
-                                                           const bf16_t* __restrict__ head,
-                                                           float* __restrict__ y, int h, int n_opt,
-                                                           float eps) {
-  extern __shared__ float xs[];  // h floats (normalised row)
-  __shared__ float red[kWaves];
+// One workgroup per answer option c: normalise the (optionally summed) row,
+// then z_c = bf16(sum_k x_hat_k * head[c, k]). Each workgroup recomputes the
+// row norm (h values), so the options run in parallel with no second pass.
+template <int CPT>
+__global__ __launch_bounds__(1024) void readout_kernel(const bf16_t* __restrict__ x,
+                                                      const bf16_t* __restrict__ x2,
+                                                      const bf16_t* __restrict__ w,
+                                                      const bf16_t* __restrict__ head,
+                                                      float* __restrict__ y, int h, float eps) {
+  __shared__ float red[16];
+  const int c = blockIdx.x, nt = blockDim.x, nchunk = h >> 3;
+  float v[CPT][8];
+  u32x4 vx[CPT], vx2[CPT], vw[CPT], vh[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int idx = threadIdx.x + k * nt;
+    if (idx < nchunk) {
+      vx[k] = *reinterpret_cast<const u32x4*>(x + (size_t)idx * 8);
+      if (x2) vx2[k] = *reinterpret_cast<const u32x4*>(x2 + (size_t)idx * 8);
+      vw[k] = *reinterpret_cast<const u32x4*>(w + (size_t)idx * 8);
+      vh[k] = *reinterpret_cast<const u32x4*>(head + (size_t)c * h + (size_t)idx * 8);
+    }
+  }
   float ss = 0.f;
-  for (int i = threadIdx.x; i < h; i += kThreads) {
-    float v = bf16_to_f32(x[i]);
-    if (x2) v = round_bf16(v + bf16_to_f32(x2[i]));
-    xs[i] = v;
-    ss += v * v;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int idx = threadIdx.x + k * nt;
+    if (idx < nchunk) {
+      unpack8(vx[k], v[k]);
+      if (x2) {
+        float t[8];
+        unpack8(vx2[k], t);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[k][i] = round_bf16(v[k][i] + t[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += v[k][i] * v[k][i];
+    }
   }
-  const float inv = rsqrt_rn(block_sum<kWaves>(ss, red) / (float)h + eps);
-  for (int i = threadIdx.x; i < h; i += kThreads)
-    xs[i] = round_bf16(round_bf16(xs[i] * inv) * bf16_to_f32(w[i]));
-  __syncthreads();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int c = wave; c < n_opt; c += kWaves) {
-    float acc = 0.f;
-    for (int i = lane; i < h; i += 64) acc += xs[i] * bf16_to_f32(head[(size_t)c * h + i]);
-    acc = wave_sum(acc);
-    if (lane == 0) y[c] = round_bf16(acc);
+  const float inv = rsqrt_rn(block_sum_rt(ss, red) / (float)h + eps);
+  float acc = 0.f;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int idx = threadIdx.x + k * nt;
+    if (idx < nchunk) {
+      float wv[8], hv[8];
+      unpack8(vw[k], wv);
+      unpack8(vh[k], hv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc += round_bf16(round_bf16(v[k][i] * inv) * wv[i]) * hv[i];
+    }
   }
+  acc = block_sum_rt(acc, red);
+  if (threadIdx.x == 0) y[c] = round_bf16(acc);
 }
 
 }  // namespace
@@ -248,11 +263,20 @@ extern "C" int ff_add_rms_quant(const void* a, const void* b, const void* deep, 
 extern "C" int ff_lm_readout(const void* x, const void* x2, const void* norm_w, const void* head,
                              float* y, int64_t h, int64_t n_opt, float eps, ff_stream_t stream) {
   FF_REQUIRE(x && norm_w && head && y, "ff_lm_readout: null pointer");
-  FF_REQUIRE(h > 0 && h <= 8192 && n_opt > 0 && n_opt <= 64, "ff_lm_readout: bad h=%lld n_opt=%lld",
-             (long long)h, (long long)n_opt);
-  hipLaunchKernelGGL(readout_kernel, dim3(1), dim3(kThreads), (size_t)h * sizeof(float),
-                     (hipStream_t)stream, (const bf16_t*)x, (const bf16_t*)x2, (const bf16_t*)norm_w,
-                     (const bf16_t*)head, y, (int)h, (int)n_opt, eps);
+  FF_REQUIRE(h > 0 && h % 8 == 0 && h <= 16384 && n_opt > 0 && n_opt <= 65535,
+             "ff_lm_readout: bad h=%lld n_opt=%lld", (long long)h, (long long)n_opt);
+  FF_REQUIRE(ff_aligned(x, 16) && (!x2 || ff_aligned(x2, 16)) && ff_aligned(norm_w, 16) && ff_aligned(head, 16),
+             "ff_lm_readout: x, x2, norm_w and head must be 16-byte aligned");
+  int threads, cpt;
+  row_shape(h / 8, &threads, &cpt);
+  if (cpt == 1)
+    hipLaunchKernelGGL(readout_kernel<1>, dim3((unsigned)n_opt), dim3((unsigned)threads), 0, (hipStream_t)stream,
+                       (const bf16_t*)x, (const bf16_t*)x2, (const bf16_t*)norm_w, (const bf16_t*)head, y, (int)h,
+                       eps);
+  else
+    hipLaunchKernelGGL(readout_kernel<2>, dim3((unsigned)n_opt), dim3((unsigned)threads), 0, (hipStream_t)stream,
+                       (const bf16_t*)x, (const bf16_t*)x2, (const bf16_t*)norm_w, (const bf16_t*)head, y, (int)h,
+                       eps);
   FF_LAUNCH_CHECK("ff_lm_readout");
   return FF_OK;
 }

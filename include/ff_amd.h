@@ -109,7 +109,8 @@ int ff_attention_vt(const void* q, const void* k, const void* vt, const int64_t*
 /* lm_readout(x, norm, weight): x_hat = bf16(bf16(x*rsqrt(mean(x^2)+eps))*w);
  * y[c] = bf16(sum_k x_hat_k * head[c,k]) stored as fp32. If x2 != NULL the
  * input row is bf16(x + x2) (the tail's `residual + mlp` add). x (h), head
- * (n_opt, h) contiguous, h <= 8192; y (n_opt) fp32. Replaces _legacy/limit_kernels.py:60
+ * (n_opt, h) contiguous, h % 8 == 0, h <= 16384, x / x2 / norm_w / head
+ * 16-byte aligned; y (n_opt) fp32. Replaces _legacy/limit_kernels.py:60
  * (kernel :48-57). */
 int ff_lm_readout(const void* x, const void* x2, const void* norm_w, const void* head, float* y,
                   int64_t h, int64_t n_opt, float eps, ff_stream_t stream);
