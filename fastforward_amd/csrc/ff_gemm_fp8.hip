@@ -56,9 +56,10 @@ struct Cfg {
   static_assert(BLOCKS % 4 == 0, "stage blocks must split over 4 waves");
 };
 
-// KS = 128-byte k-substeps per stage; S = LDS stages, S-1 in flight.
-template <int BM, int BN, int KS, int S>
-__global__ __launch_bounds__(kThreads, 1) void gemm_fp8_kernel(
+// KS = 128-byte k-substeps per stage; S = LDS stages, S-1 in flight; OCC =
+// workgroups per CU the register budget is sized for.
+template <int BM, int BN, int KS, int S, int OCC>
+__global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
     const uint8_t* __restrict__ qa, const float* __restrict__ sa, int sa_rows,
     const uint8_t* __restrict__ qw, const float* __restrict__ sw, int sw_cols,
     bf16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int tiles_m, int tiles_n) {
@@ -171,22 +172,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_kernel(
   }
 }
 
-template <int BM, int BN, int KS, int S>
+template <int BM, int BN, int KS, int S, int OCC>
 int launch(const void* qa, const float* sa, int sa_rows, const void* qw, const float* sw, int sw_cols,
            void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, hipStream_t s) {
+  static_assert(OCC * Cfg<BM, BN, KS, S>::SMEM <= 160 * 1024, "LDS budget for the occupancy");
   const int tiles_m = (int)((m + BM - 1) / BM), tiles_n = (int)((n + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_fp8_kernel<BM, BN, KS, S>), dim3(tiles_m * tiles_n), dim3(kThreads), 0, s,
+  hipLaunchKernelGGL((gemm_fp8_kernel<BM, BN, KS, S, OCC>), dim3(tiles_m * tiles_n), dim3(kThreads), 0, s,
                      (const uint8_t*)qa, sa, sa_rows, (const uint8_t*)qw, sw, sw_cols, (bf16_t*)y, ldy, (int)m,
                      (int)n, (int)k, tiles_m, tiles_n);
   return FF_OK;
 }
 
-// Tile choice (measured on the Qwen3-VL shapes at M = 320..1024): 128 x 256 when
-// the N dimension alone gives at least two full waves of workgroups, else
-// 128 x 128 with two 128-byte k-substeps per stage.
+// Tile choice (measured on the Qwen3-VL shapes at M = 576, two workgroups per
+// CU): 128 x 128 tiles (two stages) when they give at least two workgroups per
+// CU, else 64 x 128 tiles (three stages), which halve the rows per tile to
+// double the workgroups; the extra operand traffic costs less than idle CUs.
 int pick_tile(int64_t m, int64_t n) {
-  const int64_t tiles_256 = ((m + 127) / 128) * ((n + 255) / 256);
-  return tiles_256 >= 2 * 256 - 64 ? 128256 : 128128;
+  const int64_t tiles_128 = ((m + 127) / 128) * ((n + 127) / 128);
+  return tiles_128 >= 2 * 256 ? 128128 : 64128;
 }
 
 }  // namespace
@@ -210,9 +213,9 @@ extern "C" int ff_gemm_fp8(const void* qa, const float* sa, int sa_rows, const v
     return (e && sscanf(e, "%dx%d", &bm, &bn) == 2) ? bm * 1000 + bn : 0;
   }();
   const int tile = forced ? forced : pick_tile(m, n);
-  if (tile == 128256) launch<128, 256, 1, 3>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
-  else if (k % (2 * BK) == 0) launch<128, 128, 2, 2>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
-  else launch<128, 128, 1, 4>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
+  if (tile == 128256) launch<128, 256, 1, 3, 1>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
+  else if (tile == 128128) launch<128, 128, 1, 2, 2>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
+  else launch<64, 128, 1, 3, 2>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
   FF_LAUNCH_CHECK("ff_gemm_fp8");
   return FF_OK;
 }
