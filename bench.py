@@ -57,34 +57,38 @@ def gemm_launches(cfg, T):
             ("o", 1, 1), ("gateup", 1, 1), ("down", 1, 1)]
 
 
-def time_gemm(q, s, op, m, reps=20):
-    """Average duration (ms) of one ff_gemm_fp8 launch, HIP events on the launch stream."""
-    out = torch.empty((m, op.weight.shape[0]), device=q.device, dtype=torch.bfloat16)
-    for _ in range(3):
+def time_gemm(q, s, ops, m, reps=3):
+    """Average duration (ms) of one ff_gemm_fp8 launch: the launch sequence walks
+    every layer's weights in turn, as the step does, so weights come from HBM
+    rather than from a cache warmed by the previous launch. HIP events on the
+    launch stream bracket reps x len(ops) launches."""
+    out = torch.empty((m, ops[0].weight.shape[0]), device=q.device, dtype=torch.bfloat16)
+    for op in ops:
         op.gemm(q[:m], s[:m], out)
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(reps):
-        op.gemm(q[:m], s[:m], out)
+        for op in ops:
+            op.gemm(q[:m], s[:m], out)
     b.record()
     torch.cuda.synchronize()
-    return a.elapsed_time(b) / reps
+    return a.elapsed_time(b) / (reps * len(ops))
 
 
 def gemm_roofline(cfg, w, T):
-    """Live FP8 GEMM timing on the step's shapes (layer 0's weights): algorithmic
-    FLOPs per launch over the average launch duration, weighted as in the step."""
-    lw = w.layers[0]
+    """Live FP8 GEMM timing on the step's shapes over all layers' weights:
+    algorithmic FLOPs per launch over the average launch duration, weighted by
+    the step's launch counts."""
     total_flop = total_ms = 0.0
     launches = 0
     per_shape = {}
     for role, m, count in gemm_launches(cfg, T):
-        op = getattr(lw, role)
-        n, k = op.weight.shape
+        ops = [getattr(lw, role) for lw in w.layers]
+        n, k = ops[0].weight.shape
         x = torch.randn(T, k, device="cuda").to(torch.bfloat16)
-        q, s = op.quantize(x)
-        ms = time_gemm(q, s, op, m)
+        q, s = ops[0].quantize(x)
+        ms = time_gemm(q, s, ops, m)
         flop = 2.0 * m * n * k
         per_shape[f"{role} {m}x{k}x{n}"] = dict(us=round(ms * 1e3, 2), tflops=round(flop / ms / 1e9, 1))
         total_flop += flop * count
@@ -139,7 +143,7 @@ def micro_gemms():
         del w
         x = torch.randn(m, k, device="cuda").to(torch.bfloat16)
         q, s = op.quantize(x)
-        ms = time_gemm(q, s, op, m)
+        ms = time_gemm(q, s, [op], m, reps=20)
         flop = 2.0 * m * n * k
         byt = m * k + n * k + 4 * (m + n) + 2 * m * n
         out[f"{m}x{k}x{n}"] = dict(us=round(ms * 1e3, 2), tflops=round(flop / ms / 1e9, 1),

@@ -1,0 +1,86 @@
+"""Request-API contract: the reference's tests/test_contract.py cases
+(test_request, test_response) on this build's api module, plus bundle
+validation and, on the GPU, predict_tokens against an eager step."""
+import json
+
+import pytest
+
+from fastforward_amd.api import Accelerator, read_bundle, response, validate_request
+
+
+def test_request(tmp_path):
+    image = tmp_path / "input.png"
+    image.touch()
+    validate_request(image, "Question", ["A", "B"])
+    for choices in (["A"], ["A", ""], ["A"] * 9, "AB", ["A", 3]):
+        with pytest.raises(ValueError):
+            validate_request(image, "Question", choices)
+    with pytest.raises(ValueError):
+        validate_request(image, "  ", ["A", "B"])
+    with pytest.raises(FileNotFoundError):
+        validate_request(tmp_path / "missing.png", "Question", ["A", "B"])
+
+
+def test_response():
+    r = response([1.0, 1.0], ["a", "b"], "x")
+    assert r["answer"] == {"letter": "A", "text": "a"} and r["id"] == "x"
+    assert abs(sum(r["probabilities"]) - 1.0) < 1e-12
+    with pytest.raises(RuntimeError):
+        response([float("nan"), 0.0], ["a", "b"], "x")
+    with pytest.raises(RuntimeError):
+        response([0.0], ["a", "b"], "x")
+    r = response([0.5, 2.0, 2.0, -1.0], ["a", "b", "c", "d"], "y")   # ties -> first index
+    assert r["answer"]["letter"] == "B" and r["probabilities"][1] == r["probabilities"][2]
+
+
+def _bundle(tmp_path, **kw):
+    c = dict(schema_version=1, task="visual_choice", architecture="qwen3_vl_lm", preset="qwen3vl-2b",
+             linear="fp8", seed=3, tokens=320, image_grid=[16, 16], prefix_tokens=4)
+    c.update(kw)
+    p = tmp_path / "bundle.json"
+    p.write_text(json.dumps(c))
+    return p
+
+
+@pytest.mark.parametrize("bad", [dict(schema_version=2), dict(task="caption"), dict(architecture="llama"),
+                                 dict(preset="qwen3vl-70b"), dict(linear="int8"), dict(tokens=100)])
+def test_bundle_rejected(tmp_path, bad):
+    with pytest.raises(ValueError):
+        read_bundle(_bundle(tmp_path, **bad))
+
+
+def test_bundle_checkpoint_and_backend(tmp_path):
+    with pytest.raises(FileNotFoundError):
+        read_bundle(_bundle(tmp_path, checkpoint=str(tmp_path / "absent.pt")))
+    ck = tmp_path / "ck.pt"
+    ck.write_bytes(b"weights")
+    with pytest.raises(ValueError):
+        read_bundle(_bundle(tmp_path, checkpoint=str(ck), checkpoint_sha256="0" * 64))
+    assert read_bundle(_bundle(tmp_path))["preset"] == "qwen3vl-2b"
+    with pytest.raises(ValueError):
+        Accelerator(_bundle(tmp_path), backend="turbo")
+    with pytest.raises(RuntimeError):
+        Accelerator(_bundle(tmp_path), backend="native")
+
+
+@pytest.mark.gpu
+def test_predict_tokens_matches_eager_step(gpu, tmp_path):
+    import torch
+    from fastforward_amd.runtime import Runtime
+    from fastforward_amd.synthetic import make_request
+    acc = Accelerator(_bundle(tmp_path))
+    image = tmp_path / "input.png"
+    image.touch()
+    with pytest.raises(RuntimeError):
+        acc.predict(image, "Which?", ["yes", "no"])
+    eager = Runtime(acc.cfg, acc.weights, acc.tokens)
+    for seed, n_choices in ((1, 4), (2, 2)):
+        ids, pos, pick = make_request(acc.cfg, 320, 16, 16, seed=seed, real_tokens=300)
+        cands = [f"c{i}" for i in range(n_choices)]
+        r = acc.predict_tokens(ids, cands, item_id=f"r{seed}")
+        eager.set_inputs(ids, pos, pick)
+        z = eager.step().cpu().tolist()[:n_choices]
+        assert r["logits"] == z and r["id"] == f"r{seed}"
+        assert r["answer"] == response(z, cands, "r")["answer"]
+    with pytest.raises(ValueError):
+        acc.predict_tokens(torch.zeros(10, dtype=torch.int64), ["a", "b"])
