@@ -15,7 +15,7 @@ def _declared():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     decls = {}
-    for m in re.finditer(r"(?:int|const char\*)\s+(ff_\w+)\s*\(([^)]*)\)\s*;", text):
+    for m in re.finditer(r"(?:int64_t|int|const char\*)\s+(ff_\w+)\s*\(([^)]*)\)\s*;", text):
         params = m.group(2).strip()
         n = 0 if params in ("", "void") else len(params.split(","))
         decls[m.group(1)] = n
