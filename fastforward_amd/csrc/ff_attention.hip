@@ -130,21 +130,6 @@ __global__ __launch_bounds__(kThreads) void qkv_post_kernel(
 // Both kernels share the per-block softmax below, so they produce identical
 // bits for the same query.
 
-// Reductions over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48)
-// with the gfx950 row-swap permutes; every lane receives the result.
-__device__ __forceinline__ float max_rows(float x) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float sum_rows(float x) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
 // One 64-key block of the online softmax for a 16-query tile held as S^T
 // accumulators: s[2c + tt][r] = q.k of key kb + 32c + 8g + 4tt + r for the
 // lane's query (lane (r16, g) = (query, key group)). Keys whose offset

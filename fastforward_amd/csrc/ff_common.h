@@ -134,6 +134,9 @@ __device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
 }
 
+// SiLU as the reference writes it: g / (1 + exp(-g)), correctly rounded divide.
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
 // Per-token quantisation of 8 values: clamp(x / scale, +-448) -> e4m3, r = 1/scale.
 __device__ __forceinline__ u32x2 quant8(const float* x, float scale, float r) {
   float v[8];
@@ -148,16 +151,48 @@ __device__ __forceinline__ u32x2 quant8(const float* x, float scale, float r) {
 
 // ------------------------------------------------------------------ reductions
 
+// Reductions over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48)
+// with the gfx950 row-swap permutes; every lane receives the result.
+__device__ __forceinline__ float max_rows(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_rows(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Value of the lane selected by a DPP control within each 16-lane row.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(x), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppRowMirror = 0x140;  // lane i <- 15 - i
+constexpr int kDppHalfMirror = 0x141; // lane i <- 7 - i within each 8
+
+// Wave-wide sum / max on DPP within rows and row swaps across them. Every step
+// adds a lane's value to its partner's (a commutative pair), so all 64 lanes
+// end with the same bits.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppRowMirror>(v);
+  return sum_rows(v);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppRowMirror>(v));
+  return max_rows(v);
 }
 
 // Block-wide sum / max over NW waves; every thread gets the result.

@@ -54,8 +54,6 @@ __device__ __forceinline__ uint32_t pack_e4m3x4(const float* v) {
 
 // ---------------------------------------------------------------- swiglu
 
-// SiLU as the reference writes it: g / (1 + exp(-g)), correctly rounded divide.
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
 // Elementwise over (rows, i): each thread handles one 8-wide chunk.
 __global__ __launch_bounds__(kThreads) void swiglu_kernel(const bf16_t* __restrict__ g,
@@ -151,6 +149,40 @@ __global__ __launch_bounds__(1024) void quant_rows_kernel(const bf16_t* __restri
   for (int c = 0; c < CPT; ++c) {
     const int idx = threadIdx.x + c * nt;
     if (idx < nchunk) *reinterpret_cast<u32x2*>(q + (size_t)row * k + idx * 8) = quant8(v[c], scale, r);
+  }
+  if (threadIdx.x == 0) scales[row] = scale;
+}
+
+// Per-token quantisation whose row amax comes from npart partial maxima
+// (pmax[row * npart + j], written by the producer of x): the same codes and
+// scales as quant_rows_kernel on x, without a reduction over the row.
+template <int CPT>
+__global__ __launch_bounds__(1024) void quant_rows_pmax_kernel(const bf16_t* __restrict__ x, int64_t x_rs,
+                                                              const float* __restrict__ pmax, int npart,
+                                                              uint8_t* __restrict__ q,
+                                                              float* __restrict__ scales, int k) {
+  __shared__ float red[16];
+  const int row = blockIdx.x, nt = blockDim.x;
+  const int nchunk = k >> 3;
+  u32x4 v[CPT];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int idx = threadIdx.x + c * nt;
+    if (idx < nchunk) v[c] = *reinterpret_cast<const u32x4*>(x + row * x_rs + idx * 8);
+  }
+  float amax = 0.f;
+  for (int j = threadIdx.x; j < npart; j += nt) amax = fmaxf(amax, pmax[(size_t)row * npart + j]);
+  amax = block_max_rt(amax, red);
+  const float scale = fmaxf(amax, 1e-12f) / 448.0f;
+  const float r = 1.0f / scale;
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int idx = threadIdx.x + c * nt;
+    if (idx < nchunk) {
+      float f[8];
+      unpack8(v[c], f);
+      *reinterpret_cast<u32x2*>(q + (size_t)row * k + idx * 8) = quant8(f, scale, r);
+    }
   }
   if (threadIdx.x == 0) scales[row] = scale;
 }
@@ -490,5 +522,31 @@ extern "C" int ff_mrope_cos_sin(const int64_t* pos, const float* inv_freq, void*
                      (hipStream_t)stream, pos, inv_freq, (bf16_t*)cos, (bf16_t*)sin, t, (int)d, sec_h,
                      sec_w);
   FF_LAUNCH_CHECK("ff_mrope_cos_sin");
+  return FF_OK;
+}
+
+extern "C" int ff_quant_rows_pmax(const void* x, int64_t x_rs, const float* pmax, int64_t npart, void* q,
+                                  float* scales, int64_t rows, int64_t k, ff_stream_t stream) {
+  FF_REQUIRE(x && pmax && q && scales, "ff_quant_rows_pmax: null pointer");
+  FF_REQUIRE(k > 0 && k % 8 == 0 && x_rs >= k && x_rs % 8 == 0 && rows >= 0 && npart > 0 && npart < (1 << 20),
+             "ff_quant_rows_pmax: bad sizes k=%lld npart=%lld", (long long)k, (long long)npart);
+  FF_REQUIRE(ff_aligned(x, 16) && ff_aligned(q, 8), "ff_quant_rows_pmax: alignment");
+  if (rows == 0) return FF_OK;
+  int threads, cpt;
+  row_shape(k / 8, &threads, &cpt);
+  hipStream_t s = (hipStream_t)stream;
+#define FF_QP(N)                                                                                      \
+  case N:                                                                                             \
+    hipLaunchKernelGGL(quant_rows_pmax_kernel<N>, dim3((unsigned)rows), dim3((unsigned)threads), 0, s, \
+                       (const bf16_t*)x, x_rs, pmax, (int)npart, (uint8_t*)q, scales, (int)k);         \
+    break;
+  switch (cpt) {
+    FF_QP(1) FF_QP(2) FF_QP(3) FF_QP(4)
+    default:
+      ff_set_error("ff_quant_rows_pmax: k=%lld too large", (long long)k);
+      return FF_EINVAL;
+  }
+#undef FF_QP
+  FF_LAUNCH_CHECK("ff_quant_rows_pmax");
   return FF_OK;
 }

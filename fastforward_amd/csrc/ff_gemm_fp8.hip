@@ -42,6 +42,12 @@ __device__ __forceinline__ f32x4 mfma_fp8(const i32x8& a, const i32x8& b, const 
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
+// Weight row of tile column r for the gate/up pairing: tile tn covers channels
+// [64 tn, 64 tn + 64) of the gate rows [0, half) and of the up rows [half, 2 half).
+__device__ __forceinline__ int weight_row_swiglu(int r, int tn, int half) {
+  return r < 64 ? tn * 64 + r : half + tn * 64 + (r - 64);
+}
+
 template <int BM, int BN, int KS, int S>
 struct Cfg {
   static constexpr int RA = BM / 16, RB = BN / 16;     // 16-row groups
@@ -58,11 +64,19 @@ struct Cfg {
 
 // KS = 128-byte k-substeps per stage; S = LDS stages, S-1 in flight; OCC =
 // workgroups per CU the register budget is sized for.
-template <int BM, int BN, int KS, int S, int OCC>
+// EPI selects the epilogue: kPlain stores y (M, N); kSwiglu reads the weight as
+// [gate (half rows); up (half rows)] and gives each workgroup BN/2 channels of
+// both halves (gate in tile columns [0, BN/2), up in [BN/2, BN)), then stores
+// y = bf16(bf16(silu(gate)) * up) (M, half) and the per-row max |y| of its
+// channels in pmax[m * tiles_n + tile].
+constexpr int kPlain = 0, kSwiglu = 1;
+
+template <int BM, int BN, int KS, int S, int OCC, int EPI>
 __global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
     const uint8_t* __restrict__ qa, const float* __restrict__ sa, int sa_rows,
     const uint8_t* __restrict__ qw, const float* __restrict__ sw, int sw_cols,
-    bf16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int tiles_m, int tiles_n) {
+    bf16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int tiles_m, int tiles_n, int half,
+    float* __restrict__ pmax) {
   using C = Cfg<BM, BN, KS, S>;
   __shared__ __align__(16) uint8_t smem[C::SMEM];
 
@@ -91,7 +105,8 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
       const int row = min(m0 + (rem >> 1) * 16 + rr, M - 1);
       src[i] = qa + (size_t)row * K + ks * 128 + 16 * ch;
     } else {
-      const int row = min(n0 + ((rem - 2 * C::RA) >> 1) * 16 + rr, N - 1);
+      const int r = ((rem - 2 * C::RA) >> 1) * 16 + rr;  // B row within the tile
+      const int row = EPI == kSwiglu ? weight_row_swiglu(r, tn, half) : min(n0 + r, N - 1);
       src[i] = qw + (size_t)row * K + ks * 128 + 16 * ch;
     }
   }
@@ -149,7 +164,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
 #pragma unroll
   for (int j = 0; j < C::WJ; ++j) {
     const int cl = wn * (BN / 2) + j * 16 + r16;
-    const int n = min(n0 + cl, N - 1);
+    const int n = EPI == kSwiglu ? weight_row_swiglu(cl, tn, half) : min(n0 + cl, N - 1);
     const float swv = sw[sw_cols ? n : 0];
 #pragma unroll
     for (int i = 0; i < C::WI; ++i)
@@ -162,6 +177,34 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
       }
   }
   __syncthreads();
+  if constexpr (EPI == kSwiglu) {
+    // 8 channels per thread; the 8 threads of one row are 8 consecutive lanes.
+    constexpr int CH = BN / 2, CPR = CH / 8;
+    static_assert(CPR == 8, "row max reduces over 8 lanes");
+    const int g0 = tn * CH;
+#pragma unroll
+    for (int c = tid; c < BM * CPR; c += kThreads) {
+      const int rl = c / CPR, cc = (c % CPR) * 8;
+      float gv[8], uv[8], hv[8];
+      unpack8(*reinterpret_cast<const u32x4*>(tile + rl * C::EPI_LD + cc), gv);
+      unpack8(*reinterpret_cast<const u32x4*>(tile + rl * C::EPI_LD + CH + cc), uv);
+      float mx = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        hv[e] = round_bf16(round_bf16(silu(gv[e])) * uv[e]);
+        mx = fmaxf(mx, fabsf(hv[e]));
+      }
+      mx = fmaxf(mx, dpp<kDppXor1>(mx));
+      mx = fmaxf(mx, dpp<kDppXor2>(mx));
+      mx = fmaxf(mx, dpp<kDppHalfMirror>(mx));
+      const int m = m0 + rl;
+      if (m < M) {
+        *reinterpret_cast<u32x4*>(y + (size_t)m * ldy + g0 + cc) = pack8(hv);
+        if (cc == 0) pmax[(size_t)m * tiles_n + tn] = mx;
+      }
+    }
+    return;
+  }
   constexpr int CHUNKS = BM * BN / 8;
 #pragma unroll
   for (int c = tid; c < CHUNKS; c += kThreads) {
@@ -172,14 +215,16 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
   }
 }
 
-template <int BM, int BN, int KS, int S, int OCC>
+template <int BM, int BN, int KS, int S, int OCC, int EPI = kPlain>
 int launch(const void* qa, const float* sa, int sa_rows, const void* qw, const float* sw, int sw_cols,
-           void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, hipStream_t s) {
+           void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, hipStream_t s, float* pmax = nullptr) {
   static_assert(OCC * Cfg<BM, BN, KS, S>::SMEM <= 160 * 1024, "LDS budget for the occupancy");
-  const int tiles_m = (int)((m + BM - 1) / BM), tiles_n = (int)((n + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_fp8_kernel<BM, BN, KS, S, OCC>), dim3(tiles_m * tiles_n), dim3(kThreads), 0, s,
+  // kSwiglu: n = 2 * half weight rows, BN/2 channels of each half per tile
+  const int tiles_m = (int)((m + BM - 1) / BM);
+  const int tiles_n = EPI == kSwiglu ? (int)(n / BN) : (int)((n + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_fp8_kernel<BM, BN, KS, S, OCC, EPI>), dim3(tiles_m * tiles_n), dim3(kThreads), 0, s,
                      (const uint8_t*)qa, sa, sa_rows, (const uint8_t*)qw, sw, sw_cols, (bf16_t*)y, ldy, (int)m,
-                     (int)n, (int)k, tiles_m, tiles_n);
+                     (int)n, (int)k, tiles_m, tiles_n, (int)(n / 2), pmax);
   return FF_OK;
 }
 
@@ -217,5 +262,19 @@ extern "C" int ff_gemm_fp8(const void* qa, const float* sa, int sa_rows, const v
   else if (tile == 128128) launch<128, 128, 1, 2, 2>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
   else launch<64, 128, 1, 3, 2>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
   FF_LAUNCH_CHECK("ff_gemm_fp8");
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_fp8_swiglu(const void* qa, const float* sa, const void* qw, const float* sw, void* h,
+                                  int64_t ldh, float* pmax, int64_t m, int64_t i, int64_t k, ff_stream_t stream) {
+  FF_REQUIRE(qa && sa && qw && sw && h && pmax, "ff_gemm_fp8_swiglu: null pointer");
+  FF_REQUIRE(m >= 0 && i > 0 && i % 64 == 0 && k > 0 && k % BK == 0 && ldh >= i && ldh % 8 == 0 &&
+                 m < (1 << 30) && i < (1 << 29) && k < (1 << 30),
+             "ff_gemm_fp8_swiglu: bad sizes (i %% 64, k %% 128, ldh %% 8)");
+  FF_REQUIRE(ff_aligned(qa, 16) && ff_aligned(qw, 16) && ff_aligned(h, 16),
+             "ff_gemm_fp8_swiglu: operands must be 16-byte aligned");
+  if (m == 0) return FF_OK;
+  launch<128, 128, 1, 2, 2, kSwiglu>(qa, sa, 1, qw, sw, 1, h, ldh, m, 2 * i, k, (hipStream_t)stream, pmax);
+  FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu");
   return FF_OK;
 }

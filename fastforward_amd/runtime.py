@@ -148,7 +148,8 @@ class Runtime:
             self.aq, self.as_ = e(T, HQ * D, dt=E4M3), e(T, dt=torch.float32)
             self.o = e(T, H)
             self.pq, self.ps = e(T, H, dt=E4M3), e(T, dt=torch.float32)
-            self.gu = e(T, 2 * I)
+            self.hm = e(T, I)                                    # swiglu output (bf16)
+            self.pmax = e(T, I // 64, dt=torch.float32)          # its row maxima per 64 channels
             self.mq, self.ms = e(T, I, dt=E4M3), e(T, dt=torch.float32)
             self.dn = e(T, H)
             self.hp = e(1, H)
@@ -257,10 +258,10 @@ class Runtime:
 
     def _mlp_fused(self, lw, q, sc, m, out, s):
         I, H = self.cfg.inter, self.cfg.hidden
-        call("ff_gemm_fp8", ptr(q), ptr(sc), 1, ptr(lw.gateup.weight), ptr(lw.gateup.scale), 1, ptr(self.gu),
-             2 * I, m, 2 * I, H, s)
-        base = self.gu.data_ptr()
-        call("ff_swiglu_quant", base, base + I * 2, 2 * I, None, ptr(self.mq), ptr(self.ms), m, I, s)
+        # gate/up GEMM with SwiGLU in its epilogue, then per-token quant from its row maxima
+        call("ff_gemm_fp8_swiglu", ptr(q), ptr(sc), ptr(lw.gateup.weight), ptr(lw.gateup.scale), ptr(self.hm), I,
+             ptr(self.pmax), m, I, H, s)
+        call("ff_quant_rows_pmax", ptr(self.hm), I, ptr(self.pmax), I // 64, ptr(self.mq), ptr(self.ms), m, I, s)
         call("ff_gemm_fp8", ptr(self.mq), ptr(self.ms), 1, ptr(lw.down.weight), ptr(lw.down.scale), 1, ptr(out), H,
              m, H, I, s)
 

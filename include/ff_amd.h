@@ -144,6 +144,22 @@ int ff_gemm_fp8(const void* qa, const float* sa, int sa_rows, const void* qw, co
                 int sw_cols, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
                 ff_stream_t stream);
 
+/* Fused gate/up GEMM + SwiGLU (no reference counterpart as one op; the same
+ * arithmetic as ff_gemm_fp8 on the packed gate/up weight followed by ff_swiglu):
+ * qw (2i, k) e4m3 = [gate rows; up rows] with per-row scales sw (2i); qa (m, k)
+ * with per-token scales sa (m). Writes h (m, i) bf16 (row stride ldh) =
+ * bf16(bf16(silu(g)) * u) for g, u the bf16 GEMM outputs, and pmax (m, i/64)
+ * fp32, the max |h| of each row over each 64-channel block, for
+ * ff_quant_rows_pmax. i % 64 == 0, k % 128 == 0. */
+int ff_gemm_fp8_swiglu(const void* qa, const float* sa, const void* qw, const float* sw, void* h,
+                       int64_t ldh, float* pmax, int64_t m, int64_t i, int64_t k, ff_stream_t stream);
+
+/* ff_quant_rows_fp8 with the row amax given as npart partial maxima per row
+ * (pmax (rows, npart), as ff_gemm_fp8_swiglu writes them): identical codes and
+ * scales, no reduction over x. */
+int ff_quant_rows_pmax(const void* x, int64_t x_rs, const float* pmax, int64_t npart, void* q,
+                       float* scales, int64_t rows, int64_t k, ff_stream_t stream);
+
 /* Setup-time int4 quant of w (n, k) bf16 into packed nibbles (n, k/2) (even k in
  * the high nibble) and scales [k/group, n, 2] bf16 (scale, zero).
  * symmetric != 0: s = bf16(max(amax|w|,1e-6)/7), q = clamp(rint(w/s)+8, 0, 15),

@@ -283,6 +283,33 @@ def test_gemm_fp8_dynamic(gpu, m, k, n):
     _assert_fp8_gemm(y.cpu(), qa, sa, qw, sw, want, f"gemm_fp8 {m}x{k}x{n}")
 
 
+@pytest.mark.parametrize("m,i,k", [(576, 12288, 4096), (1, 12288, 4096), (130, 6144, 2048), (33, 640, 256)])
+def test_gemm_fp8_swiglu_equals_unfused(gpu, m, i, k):
+    """The gate/up GEMM with the SwiGLU epilogue equals ff_gemm_fp8 on the packed
+    weight followed by swiglu, bit for bit; its row maxima equal max |h|; the
+    quantisation from them equals ff_quant_rows_fp8 on h."""
+    from fastforward_amd import ops
+    from fastforward_amd._lib import call, ptr, stream
+    x = (torch.randn(m, k, generator=_g(34)) * 2).to(BF16)
+    w = (torch.randn(2 * i, k, generator=_g(35)) * 0.05).to(BF16)
+    qa, sa = O.quant_rows_dynamic(x)
+    qw, sw = O.fp8_weight_quant(w)
+    qa_d, sa_d, qw_d, sw_d = qa.to(DEV), sa.to(DEV), qw.to(DEV), sw.to(DEV)
+    gu = torch.empty(m, 2 * i, device=DEV, dtype=BF16)
+    call("ff_gemm_fp8", ptr(qa_d), ptr(sa_d), 1, ptr(qw_d), ptr(sw_d), 1, ptr(gu), 2 * i, m, 2 * i, k, stream())
+    want = ops.swiglu(*gu.chunk(2, -1))
+    h = torch.full((m, i), float("nan"), device=DEV, dtype=BF16)
+    pmax = torch.full((m, i // 64), float("nan"), device=DEV)
+    call("ff_gemm_fp8_swiglu", ptr(qa_d), ptr(sa_d), ptr(qw_d), ptr(sw_d), ptr(h), i, ptr(pmax), m, i, k, stream())
+    assert torch.equal(h, want)
+    assert torch.equal(pmax, h.float().abs().view(m, i // 64, 64).amax(-1))
+    q1, s1 = torch.empty(m, i, device=DEV, dtype=torch.uint8), torch.empty(m, device=DEV)
+    q2, s2 = torch.empty_like(q1), torch.empty_like(s1)
+    call("ff_quant_rows_pmax", ptr(h), i, ptr(pmax), i // 64, ptr(q1), ptr(s1), m, i, stream())
+    call("ff_quant_rows_fp8", ptr(h), i, ptr(q2), ptr(s2), m, i, stream())
+    assert torch.equal(q1, q2) and torch.equal(s1, s2)
+
+
 def test_gemm_fp8_static_scalars(gpu):
     from fastforward_amd.linear import StaticFP8Linear
     m, k, n = 576, 4096, 4096
