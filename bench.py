@@ -205,7 +205,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=576)
     ap.add_argument("--cpu-layers", type=int, default=35, help="decoder layers in the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-extras", action="store_true", help="skip the W4A16 step and the GEMM microbench")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the GEMM microbench and the W4A16 / 2B / 32B steps")
     ap.add_argument("--profile", action="store_true", help="only replay the graph (for rocprofv3 runs)")
     ap.add_argument("--kernels", action="store_true",
                     help="only run the step's GEMM shapes and a calibration copy (rocprofv3 --pmc runs)")
@@ -252,12 +253,21 @@ def main():
     if not args.no_extras:
         del w
         torch.cuda.empty_cache()
-        w4 = make_model(cfg, mode="w4a16", seed=0, n_options=8)
-        rt4 = Runtime(cfg, w4, T)
-        rt4.set_inputs(ids, pos, pick)
-        rt4.capture()
-        extras["w4a16_g128_step_ms"] = round(time_graph(rt4, args.steps, args.warmup), 4)
-        del rt4, w4
+        # the other LM configurations, each one hipGraph replay per step
+        for key, preset, mode, tokens, grid, n_opt in (
+                ("w4a16_g128_8b_576_step_ms", args.preset, "w4a16", T, grid, 8),
+                ("fp8_2b_320_step_ms", "qwen3vl-2b", "fp8", 320, (16, 16), 4),
+                ("fp8_32b_1024_step_ms", "qwen3vl-32b", "fp8", 1024, (30, 32), 2)):
+            c = PRESETS[preset]
+            wx = make_model(c, mode=mode, seed=0, n_options=n_opt)
+            ix, px, kx = make_request(c, tokens, *grid, seed=0)
+            rx = Runtime(c, wx, tokens)
+            rx.set_inputs(ix, px, kx)
+            rx.capture()
+            extras[key] = round(time_graph(rx, args.steps, args.warmup), 4)
+            log(f"{key} {extras[key]}")
+            del rx, wx
+            torch.cuda.empty_cache()
     line = dict(
         metric=METRIC, value=round(ms, 4), unit="ms", n_gpus=1, steps=args.steps, warmup=args.warmup,
         ms_per_step=round(ms, 4), higher_is_better=False, scaling="weak", vs_baseline=None,

@@ -26,6 +26,7 @@
 // walked M-fastest; tiles that share a weight slab then share an L2.
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include "ff_common.h"
 
@@ -228,13 +229,32 @@ int launch(const void* qa, const float* sa, int sa_rows, const void* qw, const f
   return FF_OK;
 }
 
-// Tile choice (measured on the Qwen3-VL shapes at M = 576, two workgroups per
-// CU): 128 x 128 tiles (two stages) when they give at least two workgroups per
-// CU, else 64 x 128 tiles (three stages), which halve the rows per tile to
-// double the workgroups; the extra operand traffic costs less than idle CUs.
-int pick_tile(int64_t m, int64_t n) {
+// Tile choice, measured at M = 576 with the weights streamed from HBM as in the
+// step (each launch on a different weight matrix): 128 x 128 tiles with two
+// stages and two workgroups per CU when there are at least two such tiles per
+// CU; 128 x 128 tiles with four stages (three in flight), one workgroup per CU,
+// when the tiles about fill the CUs once; otherwise 64 x 128 tiles (three
+// stages, two per CU), which double the workgroups at the price of more
+// operand traffic.
+enum Tile { k64x128, k128x128, k128x128Deep, k128x256 };
+
+Tile pick_tile(int64_t m, int64_t n) {
   const int64_t tiles_128 = ((m + 127) / 128) * ((n + 127) / 128);
-  return tiles_128 >= 2 * 256 ? 128128 : 64128;
+  if (tiles_128 >= 2 * 256) return k128x128;
+  if (tiles_128 >= 192 && tiles_128 <= 256) return k128x128Deep;
+  return k64x128;
+}
+
+// FF_GEMM_FP8_TILE=64x128 | 128x128 | 128x128s4 | 128x256 forces a tile (tuning
+// sweeps); unset or unknown = the choice above.
+int forced_tile() {
+  const char* e = getenv("FF_GEMM_FP8_TILE");
+  if (!e) return -1;
+  if (!strcmp(e, "64x128")) return k64x128;
+  if (!strcmp(e, "128x128")) return k128x128;
+  if (!strcmp(e, "128x128s4")) return k128x128Deep;
+  if (!strcmp(e, "128x256")) return k128x256;
+  return -1;
 }
 
 }  // namespace
@@ -251,15 +271,11 @@ extern "C" int ff_gemm_fp8(const void* qa, const float* sa, int sa_rows, const v
              "ff_gemm_fp8: operands must be 16-byte aligned");
   if (m == 0) return FF_OK;
   hipStream_t s = (hipStream_t)stream;
-  // FF_GEMM_FP8_TILE=<bm>x<bn> forces a tile (tuning sweeps); unset = the model's choice.
-  static const int forced = [] {
-    const char* e = getenv("FF_GEMM_FP8_TILE");
-    int bm = 0, bn = 0;
-    return (e && sscanf(e, "%dx%d", &bm, &bn) == 2) ? bm * 1000 + bn : 0;
-  }();
-  const int tile = forced ? forced : pick_tile(m, n);
-  if (tile == 128256) launch<128, 256, 1, 3, 1>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
-  else if (tile == 128128) launch<128, 128, 1, 2, 2>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
+  static const int forced = forced_tile();
+  const int tile = forced >= 0 ? forced : pick_tile(m, n);
+  if (tile == k128x256) launch<128, 256, 1, 3, 1>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
+  else if (tile == k128x128) launch<128, 128, 1, 2, 2>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
+  else if (tile == k128x128Deep) launch<128, 128, 1, 4, 1>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
   else launch<64, 128, 1, 3, 2>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
   FF_LAUNCH_CHECK("ff_gemm_fp8");
   return FF_OK;

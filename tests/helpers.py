@@ -36,18 +36,21 @@ def linear_to_oracle(op):
     raise TypeError(type(op))
 
 
-def to_oracle(cfg, w, layers=None):
-    """(oracle Shape, oracle Weights) holding CPU copies of the product's weights."""
+def to_oracle(cfg, w, layers=None, only=None):
+    """(oracle Shape, oracle Weights) holding CPU copies of the product's weights.
+    ``only``: indices of the layers whose linears are copied (the others keep
+    their norms and None linears), for shapes too large to copy whole."""
     shape = omodel.Shape(layers=cfg.layers, hidden=cfg.hidden, heads=cfg.heads, kv_heads=cfg.kv_heads,
                          head_dim=cfg.head_dim, inter=cfg.inter, vocab=cfg.vocab, eps=cfg.eps,
                          theta=cfg.theta, sections=tuple(cfg.sections))
     out = []
-    for lw in w.layers[: layers or len(w.layers)]:
+    for j, lw in enumerate(w.layers[: layers or len(w.layers)]):
+        lin = only is None or j in only
         out.append(omodel.Layer(
             input_norm=lw.input_norm.weight.cpu(), post_norm=lw.post_norm.weight.cpu(),
             q_norm=lw.q_norm.weight.cpu(), k_norm=lw.k_norm.weight.cpu(),
-            qkv=linear_to_oracle(lw.qkv), o=linear_to_oracle(lw.o),
-            gateup=linear_to_oracle(lw.gateup), down=linear_to_oracle(lw.down)))
+            qkv=linear_to_oracle(lw.qkv) if lin else None, o=linear_to_oracle(lw.o) if lin else None,
+            gateup=linear_to_oracle(lw.gateup) if lin else None, down=linear_to_oracle(lw.down) if lin else None))
     return shape, omodel.Weights(embed=w.embed.cpu(), layers=out, norm=w.norm.weight.cpu(), head=w.head.cpu())
 
 

@@ -89,7 +89,7 @@ def _exact_gemm(qa, sa, qw, sw):
     return (acc * sa.double().reshape(-1, 1) * sw.double().reshape(1, -1)).to(torch.bfloat16)
 
 
-def _check_teacher_forced(cfg, w, mode, ids, pos, pick, layers, what):
+def _check_teacher_forced(cfg, w, mode, ids, pos, pick, layers, what, copy_all=True):
     """Run the GPU step with a residual trace, then check the chosen layers and the
     tail against the oracle fed with the GPU's own layer inputs."""
     from fastforward_amd.runtime import Runtime
@@ -98,7 +98,7 @@ def _check_teacher_forced(cfg, w, mode, ids, pos, pick, layers, what):
     trace = []
     z = rt.step(trace=trace).clone().cpu()
     trace = [t.cpu() for t in trace]
-    shape, ow = to_oracle(cfg, w)
+    shape, ow = to_oracle(cfg, w, only=None if copy_all else set(layers) | {cfg.layers - 1})
     del rt
     cos, sin = O.mrope_cos_sin(pos, shape.theta, shape.head_dim, shape.sections)
     full = torch.zeros(pos.shape[1], dtype=torch.int64)
@@ -241,3 +241,29 @@ def test_full_model_vs_oracle(gpu, preset, tokens, grid, choices, mode):
           f"gpu-vs-oracle {rel_err(z, ze):.4f}, oracle(exact acc)-vs-oracle {rel_err(zx, ze):.4f}", flush=True)
     assert rel_err(z, ze) <= 1.0, "gross end-to-end disagreement"
     sys.stdout.flush()
+
+
+@pytest.mark.timeout(1200)
+def test_32b_shape_on_one_gpu(gpu):
+    """The 32B shape (64 layers, hidden 5120, 64/8 heads with HQ*D = 8192 != H,
+    MLP 25600, 1024 tokens on a 30x32 image grid, 2 choices, FP8): graph replay
+    equals the eager step; first, second and second-to-last layers and the tail
+    teacher-forced against the oracle (only those layers are copied to the host)."""
+    from fastforward_amd.runtime import PRESETS, Runtime
+    from fastforward_amd.synthetic import make_model, make_request
+    cfg = PRESETS["qwen3vl-32b"]
+    print("building qwen3vl-32b fp8", flush=True)
+    w = make_model(cfg, mode="fp8", seed=9, n_options=2)
+    ids, pos, pick = make_request(cfg, 1024, 30, 32, seed=9)
+    rt = Runtime(cfg, w, 1024)
+    rt.set_inputs(ids, pos, pick)
+    z_eager = rt.step().clone()
+    rt.capture()
+    z_graph = rt.replay().clone()
+    torch.cuda.synchronize()
+    assert torch.equal(z_graph, z_eager)
+    del rt
+    torch.cuda.empty_cache()
+    z, _, _ = _check_teacher_forced(cfg, w, "fp8", ids, pos, pick, (0, 1, cfg.layers - 2), "qwen3vl-32b fp8",
+                                    copy_all=False)
+    assert torch.equal(z, z_eager.cpu())
