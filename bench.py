@@ -57,20 +57,34 @@ def gemm_launches(cfg, T):
             ("o", 1, 1), ("gateup", 1, 1), ("down", 1, 1)]
 
 
-def time_gemm(q, s, ops, m, reps=3):
-    """Average duration (ms) of one ff_gemm_fp8 launch: the launch sequence walks
+def launch_gemm(role, op, q, s, m, out, pmax):
+    """One FP8 GEMM launch as the step issues it: the gate/up projection with its
+    SwiGLU epilogue (ff_gemm_fp8_swiglu), every other role a plain ff_gemm_fp8."""
+    from fastforward_amd._lib import call, ptr, stream
+    if role == "gateup":
+        n, k = op.weight.shape
+        call("ff_gemm_fp8_swiglu", ptr(q), ptr(s), ptr(op.weight), ptr(op.scale), ptr(out), n // 2, ptr(pmax),
+             m, n // 2, k, stream())
+    else:
+        op.gemm(q[:m], s[:m], out)
+
+
+def time_gemm(role, q, s, ops, m, reps=3):
+    """Average duration (ms) of one launch of ``role``: the launch sequence walks
     every layer's weights in turn, as the step does, so weights come from HBM
     rather than from a cache warmed by the previous launch. HIP events on the
     launch stream bracket reps x len(ops) launches."""
-    out = torch.empty((m, ops[0].weight.shape[0]), device=q.device, dtype=torch.bfloat16)
+    n = ops[0].weight.shape[0]
+    out = torch.empty((m, n // 2 if role == "gateup" else n), device=q.device, dtype=torch.bfloat16)
+    pmax = torch.empty((m, max(1, n // 128)), device=q.device, dtype=torch.float32)
     for op in ops:
-        op.gemm(q[:m], s[:m], out)
+        launch_gemm(role, op, q, s, m, out, pmax)
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(reps):
         for op in ops:
-            op.gemm(q[:m], s[:m], out)
+            launch_gemm(role, op, q, s, m, out, pmax)
     b.record()
     torch.cuda.synchronize()
     return a.elapsed_time(b) / (reps * len(ops))
@@ -88,7 +102,7 @@ def gemm_roofline(cfg, w, T):
         n, k = ops[0].weight.shape
         x = torch.randn(T, k, device="cuda").to(torch.bfloat16)
         q, s = ops[0].quantize(x)
-        ms = time_gemm(q, s, ops, m)
+        ms = time_gemm(role, q, s, ops, m)
         flop = 2.0 * m * n * k
         per_shape[f"{role} {m}x{k}x{n}"] = dict(us=round(ms * 1e3, 2), tflops=round(flop / ms / 1e9, 1))
         total_flop += flop * count
@@ -120,9 +134,10 @@ def kernel_pass(cfg, w, T, reps=5):
         op = getattr(lw, role)
         n, k = op.weight.shape
         q, s = op.quantize(torch.randn(T, k, device="cuda").to(torch.bfloat16))
-        out = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+        out = torch.empty((m, n // 2 if role == "gateup" else n), device="cuda", dtype=torch.bfloat16)
+        pmax = torch.empty((m, max(1, n // 128)), device="cuda", dtype=torch.float32)
         for _ in range(reps):
-            op.gemm(q[:m], s[:m], out)
+            launch_gemm(role, op, q, s, m, out, pmax)
         torch.cuda.synchronize()
         log(f"gemm {role} {m}x{k}x{n} x{reps}")
     x = torch.ones(128 << 20, device="cuda", dtype=torch.bfloat16)
@@ -143,7 +158,7 @@ def micro_gemms():
         del w
         x = torch.randn(m, k, device="cuda").to(torch.bfloat16)
         q, s = op.quantize(x)
-        ms = time_gemm(q, s, [op], m, reps=20)
+        ms = time_gemm("micro", q, s, [op], m, reps=20)
         flop = 2.0 * m * n * k
         byt = m * k + n * k + 4 * (m + n) + 2 * m * n
         out[f"{m}x{k}x{n}"] = dict(us=round(ms * 1e3, 2), tflops=round(flop / ms / 1e9, 1),
