@@ -274,6 +274,97 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(
   store_rows(y + ((int64_t)qi * hq + head) * D, o, den, g);
 }
 
+// Selected rows, split over keys: for at most 16 queries (the pick-only tail
+// scores one), one workgroup per head runs 8 waves over interleaved 64-key
+// blocks (wave w takes blocks w, w + 8, ...), each with its own online softmax
+// (the routine above), and the waves' partial results are merged in LDS:
+// M = max_w m_w, den = sum_w den_w 2^((m_w - M) log2e scale), acc likewise,
+// out = acc / den. P is rounded to bf16 relative to each wave's running max
+// rather than the global one, so the result can differ from the one-pass
+// kernels in the last bits of P (well inside the attention tolerance).
+constexpr int kDecodeWaves = 8;
+
+__global__ __launch_bounds__(kDecodeWaves * 64) void attention_decode_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ vt,
+    const int64_t* __restrict__ positions, int gather_q, bf16_t* __restrict__ y, int s_len, int t, int t_pad,
+    int hq, int hk, float c2) {
+  __shared__ float sm[kDecodeWaves][16];
+  __shared__ float sden[kDecodeWaves][16];
+  __shared__ float so[kDecodeWaves][16][D + 1];
+  const int head = blockIdx.x;
+  const int kvh = head / (hq / hk);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const bool qvalid = r16 < s_len;
+  const int qrow = qvalid ? r16 : s_len - 1;
+  const int pos = (int)positions[qrow];
+  int kend = pos + 1;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) kend = max(kend, __shfl_xor(kend, o, 64));
+  kend = min(kend, t);
+  const int64_t qsrc = gather_q ? min(max(pos, 0), t - 1) : qrow;
+  const bf16_t* qp = q + ((int64_t)head * (gather_q ? t : s_len) + qsrc) * D;
+  u32x4 qf[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) qf[st] = *reinterpret_cast<const u32x4*>(qp + 32 * st + 8 * g);
+  const bf16_t* kp = k + (int64_t)kvh * t * D;
+  const bf16_t* vp = vt + (int64_t)kvh * D * t_pad;
+  f32x4 o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, den = 0.f;
+  const int plim = min(pos, t - 1);
+  for (int kb = wave * 64; kb < kend; kb += kDecodeWaves * 64) {
+    const bool two = kb + 32 < kend;
+    f32x4 sc[4];
+    score_chunk(kp, qf, kb, t, r16, g, sc[0], sc[1]);
+    if (two) {
+      score_chunk(kp, qf, kb + 32, t, r16, g, sc[2], sc[3]);
+    } else {
+      sc[2] = sc[3] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    }
+    u32x4 pf[2];
+    const float alpha = softmax_block(sc, true, plim - kb - 8 * g, c2, m, den, pf);
+    rescale(o, alpha);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const bf16_t* vr = vp + (int64_t)(16 * dt + r16) * t_pad + kb + 8 * g;
+      o[dt] = mfma_bf16(*reinterpret_cast<const u32x4*>(vr), pf[0], o[dt]);
+      if (two) o[dt] = mfma_bf16(*reinterpret_cast<const u32x4*>(vr + 32), pf[1], o[dt]);
+    }
+  }
+  den = sum_rows(den);
+  if (g == 0) {
+    sm[wave][r16] = m;
+    sden[wave][r16] = den;
+  }
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) so[wave][r16][16 * dt + 4 * g + r] = o[dt][r];
+  __syncthreads();
+  // merge: thread -> (query, 4 consecutive d)
+  for (int e = threadIdx.x; e < 16 * (D / 4); e += kDecodeWaves * 64) {
+    const int qi = e / (D / 4), d0 = (e % (D / 4)) * 4;
+    if (qi >= s_len) continue;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; ++w) mx = fmaxf(mx, sm[w][qi]);
+    float dsum = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; ++w) {
+      const float wt = sm[w][qi] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((sm[w][qi] - mx) * c2);
+      dsum += sden[w][qi] * wt;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] += so[w][qi][d0 + r] * wt;
+    }
+    u32x2 w2;
+    w2.x = pack_bf16x2(acc[0] / dsum, acc[1] / dsum);
+    w2.y = pack_bf16x2(acc[2] / dsum, acc[3] / dsum);
+    *reinterpret_cast<u32x2*>(y + ((int64_t)qi * hq + head) * D + d0) = w2;
+  }
+}
+
 // ---------------------------------------------------------------- grouped prefill attention
 //
 // A workgroup owns one 64-key-block walk for HPW query heads that share a kv
@@ -529,6 +620,13 @@ extern "C" int ff_attention_vt(const void* q, const void* k, const void* vt, con
     FF_PREFILL(1, 2) FF_PREFILL(2, 2) FF_PREFILL(4, 2)
     FF_PREFILL(1, 1) FF_PREFILL(2, 1) FF_PREFILL(4, 1)
 #undef FF_PREFILL
+    FF_LAUNCH_CHECK("ff_attention_vt");
+    return FF_OK;
+  }
+  if (positions && s <= 16) {
+    hipLaunchKernelGGL(attention_decode_kernel, dim3((unsigned)hq), dim3(kDecodeWaves * 64), 0, st,
+                       (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)vt, positions, gather_q, (bf16_t*)y,
+                       (int)s, (int)t, (int)t_pad, (int)hq, (int)hk, c2);
     FF_LAUNCH_CHECK("ff_attention_vt");
     return FF_OK;
   }

@@ -216,6 +216,162 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
   }
 }
 
+// ---------------------------------------------------------------- GEMV (m <= 4)
+//
+// For a handful of rows (the pick-only tail runs its linears on one token) the
+// tile kernel leaves most of the machine idle; these kernels stream each weight
+// row once instead: one wave per output row (or per gate/up channel pair),
+// every lane 16-byte chunks of it, e4m3 decoded with v_cvt_pk_f32_fp8 and the
+// exact products summed with fp32 FMAs, then a wave reduction. The sum is more
+// accurate than the matrix-unit path (it does not truncate 32-product blocks).
+
+constexpr int kGemvMaxM = 4;
+
+__device__ __forceinline__ void decode_e4m3x16(const u32x4 v, float* f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[q], false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[q], true);
+    f[4 * q + 0] = lo[0];
+    f[4 * q + 1] = lo[1];
+    f[4 * q + 2] = hi[0];
+    f[4 * q + 3] = hi[1];
+  }
+}
+
+// acc[m] += sum over this lane's chunks of a[m, k] * w[row, k] for NR weight rows;
+// chunks c = lane + 64 j, B chunks per lane in flight per row.
+template <int MM, int NR, int B>
+__device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ qa, const uint8_t* const* wrow, int K,
+                                          int lane, float (&acc)[NR][MM]) {
+  const int nchunk = K / 16;
+#pragma unroll
+  for (int r = 0; r < NR; ++r)
+#pragma unroll
+    for (int m = 0; m < MM; ++m) acc[r][m] = 0.f;
+  for (int c0 = lane; c0 < nchunk; c0 += 64 * B) {
+    u32x4 wv[NR][B];
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const int c = c0 + 64 * u;
+        wv[r][u] = c < nchunk ? *reinterpret_cast<const u32x4*>(wrow[r] + (size_t)c * 16) : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int c = c0 + 64 * u;
+      if (c >= nchunk) break;
+      float af[MM][16];
+#pragma unroll
+      for (int m = 0; m < MM; ++m) decode_e4m3x16(*reinterpret_cast<const u32x4*>(qa + (size_t)m * K + (size_t)c * 16), af[m]);
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        float wf[16];
+        decode_e4m3x16(wv[r][u], wf);
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[r][m] = __builtin_fmaf(af[m][e], wf[e], acc[r][m]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; ++r)
+#pragma unroll
+    for (int m = 0; m < MM; ++m) acc[r][m] = wave_sum(acc[r][m]);
+}
+
+// y[m, n] = bf16((dot * sa) * sw): one wave per output row n, 4 rows per workgroup.
+template <int MM>
+__global__ __launch_bounds__(256) void gemv_fp8_kernel(const uint8_t* __restrict__ qa, const float* __restrict__ sa,
+                                                       int sa_rows, const uint8_t* __restrict__ qw,
+                                                       const float* __restrict__ sw, int sw_cols,
+                                                       bf16_t* __restrict__ y, int64_t ldy, int N, int K) {
+  const int lane = threadIdx.x & 63;
+  const int n = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;  // wave-uniform
+  const uint8_t* wrow[1] = {qw + (size_t)n * K};
+  float acc[1][MM];
+  gemv_rows<MM, 1, 8>(qa, wrow, K, lane, acc);
+  if (lane == 0) {
+    const float swv = sw[sw_cols ? n : 0];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) y[(size_t)m * ldy + n] = (bf16_t)f32_to_bf16((acc[0][m] * sa[sa_rows ? m : 0]) * swv);
+  }
+}
+
+// SwiGLU GEMV: workgroup = 16 waves = 64 channels, 4 per wave; gate row c and
+// up row half + c per channel; h = bf16(bf16(silu(g)) * u); pmax[m, block] = the
+// block's max |h| (the 64-channel blocks of ff_gemm_fp8_swiglu).
+template <int MM>
+__global__ __launch_bounds__(1024) void gemv_fp8_swiglu_kernel(const uint8_t* __restrict__ qa,
+                                                              const float* __restrict__ sa,
+                                                              const uint8_t* __restrict__ qw,
+                                                              const float* __restrict__ sw, bf16_t* __restrict__ h,
+                                                              int64_t ldh, float* __restrict__ pmax, int half,
+                                                              int K) {
+  __shared__ float red[16][kGemvMaxM];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c0 = (int)blockIdx.x * 64 + wave * 4;
+  const uint8_t* wrow[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    wrow[2 * j] = qw + (size_t)(c0 + j) * K;
+    wrow[2 * j + 1] = qw + (size_t)(half + c0 + j) * K;
+  }
+  float acc[8][MM];
+  gemv_rows<MM, 8, 2>(qa, wrow, K, lane, acc);
+  float mx[MM];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    mx[m] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float sav = sa[m];
+      const float g = round_bf16((acc[2 * j][m] * sav) * sw[c0 + j]);
+      const float u = round_bf16((acc[2 * j + 1][m] * sav) * sw[half + c0 + j]);
+      const float hv = round_bf16(round_bf16(silu(g)) * u);
+      mx[m] = fmaxf(mx[m], fabsf(hv));
+      if (lane == 0) h[(size_t)m * ldh + c0 + j] = (bf16_t)f32_to_bf16(hv);
+    }
+    if (lane == 0) red[wave][m] = mx[m];
+  }
+  __syncthreads();
+  if (threadIdx.x < MM) {
+    float v = 0.f;
+    for (int w = 0; w < 16; ++w) v = fmaxf(v, red[w][threadIdx.x]);
+    pmax[(size_t)threadIdx.x * (half / 64) + blockIdx.x] = v;
+  }
+}
+
+int launch_gemv(const void* qa, const float* sa, int sa_rows, const void* qw, const float* sw, int sw_cols,
+                void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, hipStream_t s) {
+  const dim3 grid((unsigned)((n + 3) / 4)), block(256);
+#define FF_GEMV(MM)                                                                                       \
+  case MM:                                                                                                \
+    hipLaunchKernelGGL(gemv_fp8_kernel<MM>, grid, block, 0, s, (const uint8_t*)qa, sa, sa_rows,            \
+                       (const uint8_t*)qw, sw, sw_cols, (bf16_t*)y, ldy, (int)n, (int)k);                  \
+    break;
+  switch (m) { FF_GEMV(1) FF_GEMV(2) FF_GEMV(3) FF_GEMV(4) }
+#undef FF_GEMV
+  return FF_OK;
+}
+
+int launch_gemv_swiglu(const void* qa, const float* sa, const void* qw, const float* sw, void* h, int64_t ldh,
+                       float* pmax, int64_t m, int64_t i, int64_t k, hipStream_t s) {
+  const dim3 grid((unsigned)(i / 64)), block(1024);
+#define FF_GEMVS(MM)                                                                                      \
+  case MM:                                                                                                \
+    hipLaunchKernelGGL(gemv_fp8_swiglu_kernel<MM>, grid, block, 0, s, (const uint8_t*)qa, sa,              \
+                       (const uint8_t*)qw, sw, (bf16_t*)h, ldh, pmax, (int)i, (int)k);                     \
+    break;
+  switch (m) { FF_GEMVS(1) FF_GEMVS(2) FF_GEMVS(3) FF_GEMVS(4) }
+#undef FF_GEMVS
+  return FF_OK;
+}
+
 template <int BM, int BN, int KS, int S, int OCC, int EPI = kPlain>
 int launch(const void* qa, const float* sa, int sa_rows, const void* qw, const float* sw, int sw_cols,
            void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, hipStream_t s, float* pmax = nullptr) {
@@ -271,6 +427,11 @@ extern "C" int ff_gemm_fp8(const void* qa, const float* sa, int sa_rows, const v
              "ff_gemm_fp8: operands must be 16-byte aligned");
   if (m == 0) return FF_OK;
   hipStream_t s = (hipStream_t)stream;
+  if (m <= kGemvMaxM) {
+    launch_gemv(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
+    FF_LAUNCH_CHECK("ff_gemm_fp8");
+    return FF_OK;
+  }
   static const int forced = forced_tile();
   const int tile = forced >= 0 ? forced : pick_tile(m, n);
   if (tile == k128x256) launch<128, 256, 1, 3, 1>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
@@ -290,7 +451,10 @@ extern "C" int ff_gemm_fp8_swiglu(const void* qa, const float* sa, const void* q
   FF_REQUIRE(ff_aligned(qa, 16) && ff_aligned(qw, 16) && ff_aligned(h, 16),
              "ff_gemm_fp8_swiglu: operands must be 16-byte aligned");
   if (m == 0) return FF_OK;
-  launch<128, 128, 1, 2, 2, kSwiglu>(qa, sa, 1, qw, sw, 1, h, ldh, m, 2 * i, k, (hipStream_t)stream, pmax);
+  if (m <= kGemvMaxM)
+    launch_gemv_swiglu(qa, sa, qw, sw, h, ldh, pmax, m, i, k, (hipStream_t)stream);
+  else
+    launch<128, 128, 1, 2, 2, kSwiglu>(qa, sa, 1, qw, sw, 1, h, ldh, m, 2 * i, k, (hipStream_t)stream, pmax);
   FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu");
   return FF_OK;
 }
