@@ -38,6 +38,7 @@ SIGNATURES = {
     "ff_gemm_fp8": [P, P, I32, P, P, I32, P, I64, I64, I64, I64, P],
     "ff_gemm_fp8_swiglu": [P, P, P, P, P, I64, P, I64, I64, I64, P],
     "ff_quant_rows_pmax": [P, I64, P, I64, P, P, I64, I64, P],
+    "ff_gemm_fp8_qkv": [P, P, P, P, I64, I64, I64, I64, P, P, F32, F32, P, P, P, P, P, I64, P],
     "ff_quant_weight_int4": [P, P, P, I64, I64, I64, I32, P],
     "ff_gemm_w4a16": [P, I64, P, P, I64, P, I64, I64, I64, I64, P],
     "ff_embed": [P, P, P, I64, I64, I64, P],

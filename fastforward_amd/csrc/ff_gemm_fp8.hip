@@ -29,6 +29,7 @@
 #include <string.h>
 
 #include "ff_common.h"
+#include "ff_rope.h"
 
 using namespace ff;
 
@@ -70,14 +71,30 @@ struct Cfg {
 // both halves (gate in tile columns [0, BN/2), up in [BN/2, BN)), then stores
 // y = bf16(bf16(silu(gate)) * up) (M, half) and the per-row max |y| of its
 // channels in pmax[m * tiles_n + tile].
-constexpr int kPlain = 0, kSwiglu = 1;
+// kQkv: N = (hq + 2 hk) * 128 and BN = 128, so tile column block tn is one head
+// of the packed QKV output: q/k heads get the per-head RMSNorm + rotary of
+// qk_pair and are stored head-major (heads, M, 128); v heads are stored
+// transposed, vt (hk, 128, t_pad), with zeros for tokens in [M, t_pad).
+constexpr int kPlain = 0, kSwiglu = 1, kQkv = 2;
+
+struct QkvEpilogue {
+  const bf16_t* qn;  // q_norm weight (128)
+  const bf16_t* kn;  // k_norm weight (128)
+  float eps_q, eps_k;
+  const bf16_t* cos;  // (M, 128)
+  const bf16_t* sin;
+  bf16_t* yq;  // (hq, M, 128)
+  bf16_t* yk;  // (hk, M, 128)
+  bf16_t* vt;  // (hk, 128, t_pad)
+  int hq, hk, t_pad;
+};
 
 template <int BM, int BN, int KS, int S, int OCC, int EPI>
 __global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
     const uint8_t* __restrict__ qa, const float* __restrict__ sa, int sa_rows,
     const uint8_t* __restrict__ qw, const float* __restrict__ sw, int sw_cols,
     bf16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int tiles_m, int tiles_n, int half,
-    float* __restrict__ pmax) {
+    float* __restrict__ pmax, QkvEpilogue qe) {
   using C = Cfg<BM, BN, KS, S>;
   __shared__ __align__(16) uint8_t smem[C::SMEM];
 
@@ -202,6 +219,39 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
       if (m < M) {
         *reinterpret_cast<u32x4*>(y + (size_t)m * ldy + g0 + cc) = pack8(hv);
         if (cc == 0) pmax[(size_t)m * tiles_n + tn] = mx;
+      }
+    }
+    return;
+  }
+  if constexpr (EPI == kQkv) {
+    static_assert(BN == kHeadDim, "one head per tile column block");
+    const int head = tn;
+    if (head < qe.hq + qe.hk) {
+      // q or k head: one 16-lane group per token row, as the qkv_post kernel does
+      const bool isq = head < qe.hq;
+      const int hh = isq ? head : head - qe.hq;
+      const bf16_t* wn = isq ? qe.qn : qe.kn;
+      const float eps = isq ? qe.eps_q : qe.eps_k;
+      bf16_t* dst = (isq ? qe.yq : qe.yk) + (size_t)hh * M * kHeadDim;
+      const int grp = tid >> 4, j = tid & 15;
+      for (int rl = grp; rl < BM; rl += kThreads / 16) {
+        const int m = m0 + rl;
+        const bool valid = m < M;
+        const int mm = valid ? m : M - 1;
+        rope_row(tile + rl * C::EPI_LD, wn, eps, qe.cos + (size_t)mm * kHeadDim, qe.sin + (size_t)mm * kHeadDim,
+                 dst + (size_t)mm * kHeadDim, j, valid);
+      }
+    } else {
+      // v head: 8 consecutive tokens of one d row per thread (16-byte stores)
+      const int hv = head - qe.hq - qe.hk;
+      for (int c = tid; c < kHeadDim * (BM / 8); c += kThreads) {
+        const int d = c / (BM / 8), t0 = (c % (BM / 8)) * 8;
+        const int tok = m0 + t0;
+        if (tok >= qe.t_pad) continue;
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = (tok + e < M) ? bf16_to_f32(tile[(t0 + e) * C::EPI_LD + d]) : 0.f;
+        *reinterpret_cast<u32x4*>(qe.vt + ((size_t)hv * kHeadDim + d) * qe.t_pad + tok) = pack8(f);
       }
     }
     return;
@@ -374,14 +424,15 @@ int launch_gemv_swiglu(const void* qa, const float* sa, const void* qw, const fl
 
 template <int BM, int BN, int KS, int S, int OCC, int EPI = kPlain>
 int launch(const void* qa, const float* sa, int sa_rows, const void* qw, const float* sw, int sw_cols,
-           void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, hipStream_t s, float* pmax = nullptr) {
+           void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, hipStream_t s, float* pmax = nullptr,
+           QkvEpilogue qe = QkvEpilogue{}) {
   static_assert(OCC * Cfg<BM, BN, KS, S>::SMEM <= 160 * 1024, "LDS budget for the occupancy");
   // kSwiglu: n = 2 * half weight rows, BN/2 channels of each half per tile
   const int tiles_m = (int)((m + BM - 1) / BM);
   const int tiles_n = EPI == kSwiglu ? (int)(n / BN) : (int)((n + BN - 1) / BN);
   hipLaunchKernelGGL((gemm_fp8_kernel<BM, BN, KS, S, OCC, EPI>), dim3(tiles_m * tiles_n), dim3(kThreads), 0, s,
                      (const uint8_t*)qa, sa, sa_rows, (const uint8_t*)qw, sw, sw_cols, (bf16_t*)y, ldy, (int)m,
-                     (int)n, (int)k, tiles_m, tiles_n, (int)(n / 2), pmax);
+                     (int)n, (int)k, tiles_m, tiles_n, (int)(n / 2), pmax, qe);
   return FF_OK;
 }
 
@@ -456,5 +507,34 @@ extern "C" int ff_gemm_fp8_swiglu(const void* qa, const float* sa, const void* q
   else
     launch<128, 128, 1, 2, 2, kSwiglu>(qa, sa, 1, qw, sw, 1, h, ldh, m, 2 * i, k, (hipStream_t)stream, pmax);
   FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu");
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_fp8_qkv(const void* qa, const float* sa, const void* qw, const float* sw, int64_t m,
+                               int64_t k, int64_t hq, int64_t hk, const void* q_norm, const void* k_norm, float eps_q,
+                               float eps_k, const void* cos, const void* sin, void* yq, void* yk, void* vt,
+                               int64_t t_pad, ff_stream_t stream) {
+  FF_REQUIRE(qa && sa && qw && sw && q_norm && k_norm && cos && sin && yq && yk && vt,
+             "ff_gemm_fp8_qkv: null pointer");
+  FF_REQUIRE(m > 0 && k > 0 && k % BK == 0 && hq > 0 && hk > 0 && hq % hk == 0 && t_pad >= m && t_pad % 64 == 0 &&
+                 m < (1 << 30) && k < (1 << 30) && (hq + 2 * hk) * kHeadDim < (1 << 30),
+             "ff_gemm_fp8_qkv: bad sizes m=%lld k=%lld hq=%lld hk=%lld t_pad=%lld", (long long)m, (long long)k,
+             (long long)hq, (long long)hk, (long long)t_pad);
+  FF_REQUIRE(ff_aligned(qa, 16) && ff_aligned(qw, 16) && ff_aligned(cos, 16) && ff_aligned(sin, 16) &&
+                 ff_aligned(q_norm, 16) && ff_aligned(k_norm, 16) && ff_aligned(yq, 16) && ff_aligned(yk, 16) &&
+                 ff_aligned(vt, 16),
+             "ff_gemm_fp8_qkv: operands must be 16-byte aligned");
+  const int64_t n = (hq + 2 * hk) * kHeadDim;
+  QkvEpilogue qe{(const bf16_t*)q_norm, (const bf16_t*)k_norm, eps_q, eps_k, (const bf16_t*)cos,
+                 (const bf16_t*)sin, (bf16_t*)yq, (bf16_t*)yk, (bf16_t*)vt, (int)hq, (int)hk, (int)t_pad};
+  hipStream_t s = (hipStream_t)stream;
+  const int tile = pick_tile(m, n);
+  if (tile == k128x128)
+    launch<128, 128, 1, 2, 2, kQkv>(qa, sa, 1, qw, sw, 1, nullptr, 0, m, n, k, s, nullptr, qe);
+  else if (tile == k128x128Deep)
+    launch<128, 128, 1, 4, 1, kQkv>(qa, sa, 1, qw, sw, 1, nullptr, 0, m, n, k, s, nullptr, qe);
+  else
+    launch<64, 128, 1, 3, 2, kQkv>(qa, sa, 1, qw, sw, 1, nullptr, 0, m, n, k, s, nullptr, qe);
+  FF_LAUNCH_CHECK("ff_gemm_fp8_qkv");
   return FF_OK;
 }

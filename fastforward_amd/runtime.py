@@ -142,7 +142,6 @@ class Runtime:
         self.logits = torch.zeros(weights.head.shape[0], device=dev, dtype=torch.float32)
         if self.path == "fused":
             self.xq, self.xs = e(T, H, dt=E4M3), e(T, dt=torch.float32)
-            self.qkv = e(T, cfg.qkv_out)
             self.yq, self.yk, self.vt = e(HQ, T, D), e(HK, T, D), e(HK, D, self.Tp)
             self.attn = e(T, HQ * D)
             self.aq, self.as_ = e(T, HQ * D, dt=E4M3), e(T, dt=torch.float32)
@@ -238,15 +237,11 @@ class Runtime:
         cfg = self.cfg
         T, Tp, H, D = self.T, self.Tp, cfg.hidden, cfg.head_dim
         HQ, HK = cfg.heads, cfg.kv_heads
-        n3 = cfg.qkv_out
-        call("ff_gemm_fp8", ptr(self.xq), ptr(self.xs), 1, ptr(lw.qkv.weight), ptr(lw.qkv.scale), 1, ptr(self.qkv),
-             n3, T, n3, H, s)
-        base = self.qkv.data_ptr()
-        esz = 2
-        call("ff_qkv_post", base, base + HQ * D * esz, base + (HQ + HK) * D * esz, n3,
+        # QKV GEMM with q/k norm + rotary and the V transpose in its epilogue
+        call("ff_gemm_fp8_qkv", ptr(self.xq), ptr(self.xs), ptr(lw.qkv.weight), ptr(lw.qkv.scale), T, H, HQ, HK,
              ptr(lw.q_norm.weight), ptr(lw.k_norm.weight), float(lw.q_norm.variance_epsilon),
              float(lw.k_norm.variance_epsilon), ptr(self.cos), ptr(self.sin), ptr(self.yq), ptr(self.yk),
-             ptr(self.vt), T, Tp, HQ, HK, D, s)
+             ptr(self.vt), Tp, s)
         if tail:
             call("ff_attention_vt", ptr(self.yq), ptr(self.yk), ptr(self.vt), ptr(self.pick), 1, ptr(self.attn),
                  1, T, Tp, HQ, HK, D, float(cfg.scaling), s)

@@ -154,6 +154,18 @@ int ff_gemm_fp8(const void* qa, const float* sa, int sa_rows, const void* qw, co
 int ff_gemm_fp8_swiglu(const void* qa, const float* sa, const void* qw, const float* sw, void* h,
                        int64_t ldh, float* pmax, int64_t m, int64_t i, int64_t k, ff_stream_t stream);
 
+/* Fused QKV GEMM + q/k norm + rotary + V transpose (no reference counterpart as
+ * one op; the same arithmetic as ff_gemm_fp8 on the packed QKV weight followed
+ * by ff_qkv_post): qw ((hq + 2 hk) * 128, k) e4m3 with per-row scales sw, qa (m, k)
+ * with per-token scales sa. Writes yq (hq, m, 128), yk (hk, m, 128) (per-head
+ * RMSNorm with q_norm / k_norm, then rotary with cos / sin (m, 128)) and vt
+ * (hk, 128, t_pad) with zeros for tokens in [m, t_pad). Head dim 128. Replaces
+ * the qkv linear + qk_pair of scaled_qwen_runtime.py:150-155. */
+int ff_gemm_fp8_qkv(const void* qa, const float* sa, const void* qw, const float* sw, int64_t m, int64_t k,
+                    int64_t hq, int64_t hk, const void* q_norm, const void* k_norm, float eps_q, float eps_k,
+                    const void* cos, const void* sin, void* yq, void* yk, void* vt, int64_t t_pad,
+                    ff_stream_t stream);
+
 /* ff_quant_rows_fp8 with the row amax given as npart partial maxima per row
  * (pmax (rows, npart), as ff_gemm_fp8_swiglu writes them): identical codes and
  * scales, no reduction over x. */

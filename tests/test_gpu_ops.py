@@ -451,3 +451,38 @@ def test_bad_arguments_raise(gpu):
     with pytest.raises(AssertionError):
         ops.add_rms(x, x[:2], None, ops.RMSNorm(torch.ones(4096, device=DEV, dtype=BF16)))
     _ = np, bf16_ulps
+
+
+@pytest.mark.parametrize("t,k,hq,hk", [(576, 4096, 32, 8), (300, 2048, 16, 8), (100, 1024, 8, 2), (1024, 5120, 64, 8)])
+def test_gemm_fp8_qkv_equals_unfused(gpu, t, k, hq, hk):
+    """The QKV GEMM with the norm + rotary + V^T epilogue equals ff_gemm_fp8 on the
+    packed weight followed by ff_qkv_post, bit for bit (including the zero
+    padding of V^T)."""
+    from fastforward_amd._lib import call, ptr, stream
+    d = 128
+    tp = (t + 63) // 64 * 64
+    n = (hq + 2 * hk) * d
+    x = torch.randn(t, k, generator=_g(36)).to(BF16)
+    w = (torch.randn(n, k, generator=_g(37)) * 0.03).to(BF16)
+    qa, sa = O.quant_rows_dynamic(x)
+    qw, sw = O.fp8_weight_quant(w)
+    qa_d, sa_d, qw_d, sw_d = qa.to(DEV), sa.to(DEV), qw.to(DEV), sw.to(DEV)
+    qn, _ = _norm_module(d, 38, 0.3)
+    kn, _ = _norm_module(d, 39, 0.3)
+    cos, sin = O.mrope_cos_sin(O.mrope_positions(4, 8, 8, t), 5e6, d)
+    cos, sin = cos[0].to(DEV), sin[0].to(DEV)
+    packed = torch.empty(t, n, device=DEV, dtype=BF16)
+    call("ff_gemm_fp8", ptr(qa_d), ptr(sa_d), 1, ptr(qw_d), ptr(sw_d), 1, ptr(packed), n, t, n, k, stream())
+    rq = torch.empty(hq, t, d, device=DEV, dtype=BF16)
+    rk = torch.empty(hk, t, d, device=DEV, dtype=BF16)
+    rv = torch.full((hk, d, tp), float("nan"), device=DEV, dtype=BF16)
+    base = packed.data_ptr()
+    call("ff_qkv_post", base, base + hq * d * 2, base + (hq + hk) * d * 2, n, ptr(qn.weight), ptr(kn.weight),
+         1e-6, 1e-6, ptr(cos), ptr(sin), ptr(rq), ptr(rk), ptr(rv), t, tp, hq, hk, d, stream())
+    yq = torch.full_like(rq, float("nan"))
+    yk = torch.full_like(rk, float("nan"))
+    vt = torch.full_like(rv, float("nan"))
+    call("ff_gemm_fp8_qkv", ptr(qa_d), ptr(sa_d), ptr(qw_d), ptr(sw_d), t, k, hq, hk, ptr(qn.weight), ptr(kn.weight),
+         1e-6, 1e-6, ptr(cos), ptr(sin), ptr(yq), ptr(yk), ptr(vt), tp, stream())
+    assert torch.equal(yq, rq) and torch.equal(yk, rk)
+    assert torch.equal(vt, rv)
