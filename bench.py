@@ -223,6 +223,8 @@ def main():
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the GEMM microbench and the W4A16 / 2B / 32B steps")
     ap.add_argument("--profile", action="store_true", help="only replay the graph (for rocprofv3 runs)")
+    ap.add_argument("--linear", default="fp8", choices=("fp8", "fp8_static", "w4a16"),
+                    help="linear format of the --profile step (the benchmark line is always FP8)")
     ap.add_argument("--kernels", action="store_true",
                     help="only run the step's GEMM shapes and a calibration copy (rocprofv3 --pmc runs)")
     args = ap.parse_args()
@@ -239,7 +241,7 @@ def main():
     T = args.tokens
     grid = (16, 32) if T >= 576 else (16, 16)
     log(f"building {cfg.name} fp8 (random init, seed 0)")
-    w = make_model(cfg, mode="fp8", seed=0, n_options=8)
+    w = make_model(cfg, mode=args.linear if args.profile else "fp8", seed=0, n_options=8)
     ids, pos, pick = make_request(cfg, T, *grid, seed=0)
     if args.kernels:
         kernel_pass(cfg, w, T)
