@@ -182,8 +182,9 @@ int ff_quant_weight_int4(const void* w, void* packed, void* scales, int64_t n, i
 
 /* W4A16 GEMM: y (m, n) bf16 = x (m, k) bf16 @ dequant(W)^T with dequant
  * w = (q-8)*s + z fused into the B-operand load, fp32 accumulation (Int4.__call__,
- * _family/night_runtime.py:31-42). x row stride ldx; k % 128 == 0,
- * group % 32 == 0. */
+ * _family/night_runtime.py:31-42). x row stride ldx; k % 128 == 0, group 32 or
+ * a multiple of 64 dividing k; n, ldx, ldy multiples of 8; x, packed, scales and
+ * y 16-byte aligned. */
 int ff_gemm_w4a16(const void* x, int64_t ldx, const void* packed, const void* scales,
                   int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
                   ff_stream_t stream);

@@ -337,13 +337,44 @@ def test_gemm_w4a16(gpu, m, k, n, sym, group):
     assert float((want - exact).pow(2).mean().sqrt() / exact.pow(2).mean().sqrt()) <= 5e-3
 
 
-def test_w4a16_dequant_bit_exact_via_one_hot(gpu):
-    """x = rows of the identity: y[r, n] = bf16((q-8)*s + z) for k = r exactly."""
+@pytest.mark.parametrize("tile", ["64x256", "192x192"])
+@pytest.mark.parametrize("m,k,n", [(576, 4096, 6144), (200, 1024, 392)])
+def test_gemm_w4a16_both_tiles(gpu, monkeypatch, m, k, n, tile):
+    """Each tile shape of the W4A16 GEMM (chosen by size in production) against
+    the fp64 product with the exactly dequantised weight, asymmetric group 32 and
+    ragged M / N edges included."""
     from fastforward_amd.linear import Int4
-    k, n = 256, 128
-    w = (torch.randn(n, k, generator=_g(31)) * 0.02).to(BF16)
+    monkeypatch.setenv("FF_W4A16_TILE", tile)
+    x = torch.randn(m, k, generator=_g(36)).to(BF16)
+    w = (torch.randn(n, k, generator=_g(37)) * 0.02).to(BF16)
     for sym, group in ((True, 128), (False, 32)):
         op = Int4(w.to(DEV), group=group, symmetric=sym)
+        y = op(x.to(DEV)).cpu().double()
+        exact = x.double() @ O.int4_dequant(op.packed.cpu(), op.scales.cpu(), group).double().T
+        rel = float((y - exact).pow(2).mean().sqrt() / exact.pow(2).mean().sqrt())
+        assert rel <= 5e-3, (tile, sym, rel)
+        # worst element against the output scale: bf16 operand and output rounding only
+        worst = float((y - exact).abs().max() / exact.pow(2).mean().sqrt())
+        assert worst <= 0.05, (tile, sym, worst)
+
+
+@pytest.mark.parametrize("tile", ["64x256", "192x192"])
+def test_w4a16_dequant_bit_exact_via_one_hot(gpu, monkeypatch, tile):
+    """x = rows of the identity: y[r, n] = bf16((q-8)*s + z) for k = r exactly.
+    Columns 0-39 hold a constant 64.0 in their first 32 k: the asymmetric
+    quantizer then stores s = bf16(1e-6), z = 64, for which z - 8s is not exact
+    in fp32, so those stages take the kernel's exact (q-8, then fma) form."""
+    from fastforward_amd.linear import Int4
+    monkeypatch.setenv("FF_W4A16_TILE", tile)
+    k, n = 256, 128
+    w = (torch.randn(n, k, generator=_g(31)) * 0.02).to(BF16)
+    w[:40, :32] = 64.0
+    for sym, group in ((True, 128), (False, 32)):
+        op = Int4(w.to(DEV), group=group, symmetric=sym)
+        if not sym:
+            s, z = op.scales[0, 0].double().cpu().tolist()          # exact in float64
+            z8_f32 = float(torch.tensor(z - 8 * s, dtype=torch.float64).float())
+            assert z == 64.0 and z8_f32 != z - 8 * s                  # z8 inexact in fp32
         eye = torch.eye(k, dtype=BF16, device=DEV)
         y = op(eye).cpu()
         dq = O.int4_dequant(op.packed.cpu(), op.scales.cpu(), group).to(BF16)
