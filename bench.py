@@ -17,6 +17,7 @@ import json
 import os
 import sys
 import time
+import types
 
 import torch
 
@@ -57,37 +58,61 @@ def gemm_launches(cfg, T):
             ("o", 1, 1), ("gateup", 1, 1), ("down", 1, 1)]
 
 
-def launch_gemm(role, op, q, s, m, out, pmax):
-    """One FP8 GEMM launch as the step issues it: the gate/up projection with its
-    SwiGLU epilogue (ff_gemm_fp8_swiglu), every other role a plain ff_gemm_fp8."""
-    from fastforward_amd._lib import call, ptr, stream
+def gemm_buffers(cfg, role, n, m, T):
+    """Output buffers of one launch of ``role`` as the step allocates them."""
+    dev, bf = "cuda", torch.bfloat16
+    if role == "qkv":
+        D, Tp = cfg.head_dim, (T + 63) // 64 * 64
+        b = dict(yq=torch.empty(cfg.heads, T, D, device=dev, dtype=bf),
+                 yk=torch.empty(cfg.kv_heads, T, D, device=dev, dtype=bf),
+                 vt=torch.empty(cfg.kv_heads, D, Tp, device=dev, dtype=bf),
+                 cos=torch.ones(T, D, device=dev, dtype=bf), sin=torch.zeros(T, D, device=dev, dtype=bf),
+                 Tp=Tp)
+        return b
     if role == "gateup":
-        n, k = op.weight.shape
-        call("ff_gemm_fp8_swiglu", ptr(q), ptr(s), ptr(op.weight), ptr(op.scale), ptr(out), n // 2, ptr(pmax),
-             m, n // 2, k, stream())
+        return dict(out=torch.empty((m, n // 2), device=dev, dtype=bf),
+                    pmax=torch.empty((m, max(1, n // 128)), device=dev, dtype=torch.float32))
+    return dict(out=torch.empty((m, n), device=dev, dtype=bf))
+
+
+def launch_gemm(cfg, role, lw, q, s, m, b):
+    """One FP8 GEMM launch as the step issues it: the QKV projection with its
+    q/k norm + rotary + V^T epilogue (ff_gemm_fp8_qkv), the gate/up projection
+    with its SwiGLU epilogue (ff_gemm_fp8_swiglu), o and down plain ff_gemm_fp8
+    (which takes the GEMV kernels for the tail's single row)."""
+    from fastforward_amd._lib import call, ptr, stream
+    op = getattr(lw, role)
+    n, k = op.weight.shape
+    if role == "qkv":
+        call("ff_gemm_fp8_qkv", ptr(q), ptr(s), ptr(op.weight), ptr(op.scale), m, k, cfg.heads, cfg.kv_heads,
+             ptr(lw.q_norm.weight), ptr(lw.k_norm.weight), float(lw.q_norm.variance_epsilon),
+             float(lw.k_norm.variance_epsilon), ptr(b["cos"]), ptr(b["sin"]), ptr(b["yq"]), ptr(b["yk"]),
+             ptr(b["vt"]), b["Tp"], stream())
+    elif role == "gateup":
+        call("ff_gemm_fp8_swiglu", ptr(q), ptr(s), ptr(op.weight), ptr(op.scale), ptr(b["out"]), n // 2,
+             ptr(b["pmax"]), m, n // 2, k, stream())
     else:
-        op.gemm(q[:m], s[:m], out)
+        op.gemm(q[:m], s[:m], b["out"])
 
 
-def time_gemm(role, q, s, ops, m, reps=3):
+def time_gemm(cfg, role, q, s, layers, m, T, reps=3):
     """Average duration (ms) of one launch of ``role``: the launch sequence walks
     every layer's weights in turn, as the step does, so weights come from HBM
     rather than from a cache warmed by the previous launch. HIP events on the
-    launch stream bracket reps x len(ops) launches."""
-    n = ops[0].weight.shape[0]
-    out = torch.empty((m, n // 2 if role == "gateup" else n), device=q.device, dtype=torch.bfloat16)
-    pmax = torch.empty((m, max(1, n // 128)), device=q.device, dtype=torch.float32)
-    for op in ops:
-        launch_gemm(role, op, q, s, m, out, pmax)
+    launch stream bracket reps x len(layers) launches."""
+    n = getattr(layers[0], role).weight.shape[0]
+    b = gemm_buffers(cfg, role, n, m, T)
+    for lw in layers:
+        launch_gemm(cfg, role, lw, q, s, m, b)
     torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(reps):
-        for op in ops:
-            launch_gemm(role, op, q, s, m, out, pmax)
-    b.record()
+        for lw in layers:
+            launch_gemm(cfg, role, lw, q, s, m, b)
+    e.record()
     torch.cuda.synchronize()
-    return a.elapsed_time(b) / (reps * len(ops))
+    return a.elapsed_time(e) / (reps * len(layers))
 
 
 def gemm_roofline(cfg, w, T):
@@ -98,11 +123,11 @@ def gemm_roofline(cfg, w, T):
     launches = 0
     per_shape = {}
     for role, m, count in gemm_launches(cfg, T):
-        ops = [getattr(lw, role) for lw in w.layers]
-        n, k = ops[0].weight.shape
+        op0 = getattr(w.layers[0], role)
+        n, k = op0.weight.shape
         x = torch.randn(T, k, device="cuda").to(torch.bfloat16)
-        q, s = ops[0].quantize(x)
-        ms = time_gemm(role, q, s, ops, m)
+        q, s = op0.quantize(x)
+        ms = time_gemm(cfg, role, q, s, w.layers, m, T)
         flop = 2.0 * m * n * k
         per_shape[f"{role} {m}x{k}x{n}"] = dict(us=round(ms * 1e3, 2), tflops=round(flop / ms / 1e9, 1))
         total_flop += flop * count
@@ -125,19 +150,39 @@ def _traffic():
     return None
 
 
+def algorithmic_bytes(cfg, role, m, n, k, T):
+    """Bytes one launch must move at least: the e4m3 operands and fp32 scales,
+    plus what its epilogue reads and writes (QKV: q/k norm weights and cos/sin
+    in, head-major q/k and V^T out; gate/up: the SwiGLU product (m, n/2) and
+    the fp32 row maxima per 64 channels; o/down: the bf16 (m, n) output)."""
+    base = m * k + n * k + 4 * (m + n)
+    if role == "qkv":
+        D = cfg.head_dim
+        return base + 2 * 2 * D + 2 * 2 * T * D + 2 * m * n
+    if role == "gateup":
+        return base + 2 * m * (n // 2) + 4 * m * (n // 128)
+    return base + 2 * m * n
+
+
 def kernel_pass(cfg, w, T, reps=5):
-    """Counter-collection workload: each FP8 GEMM shape of the step (layer 0's
+    """Counter-collection workload: each FP8 GEMM launch of the step (layer 0's
     weights) ``reps`` times, then a 256 MiB bf16 scale-by-one (read 256 MiB,
-    write 256 MiB) as the copy kernel that calibrates FETCH_SIZE / WRITE_SIZE."""
+    write 256 MiB) as the copy kernel that calibrates FETCH_SIZE / WRITE_SIZE.
+    Prints the launch manifest (shape, launches per step, algorithmic bytes,
+    reps) as one JSON line for ``rocprof_summary traffic``."""
     lw = w.layers[0]
+    manifest = []
+    for role, m, count in gemm_launches(cfg, T):
+        n, k = getattr(lw, role).weight.shape
+        manifest.append(dict(shape=f"{role} {m}x{k}x{n}", launches_per_step=count,
+                             algorithmic_bytes=algorithmic_bytes(cfg, role, m, n, k, T), reps=reps))
     for role, m, _ in gemm_launches(cfg, T):
         op = getattr(lw, role)
         n, k = op.weight.shape
         q, s = op.quantize(torch.randn(T, k, device="cuda").to(torch.bfloat16))
-        out = torch.empty((m, n // 2 if role == "gateup" else n), device="cuda", dtype=torch.bfloat16)
-        pmax = torch.empty((m, max(1, n // 128)), device="cuda", dtype=torch.float32)
+        b = gemm_buffers(cfg, role, n, m, T)
         for _ in range(reps):
-            launch_gemm(role, op, q, s, m, out, pmax)
+            launch_gemm(cfg, role, lw, q, s, m, b)
         torch.cuda.synchronize()
         log(f"gemm {role} {m}x{k}x{n} x{reps}")
     x = torch.ones(128 << 20, device="cuda", dtype=torch.bfloat16)
@@ -146,6 +191,7 @@ def kernel_pass(cfg, w, T, reps=5):
     torch.cuda.synchronize()
     del x, y
     log("copy 256 MiB done")
+    print(json.dumps(dict(gemm_launches=manifest, copy_bytes=256 << 20, copy_reps=reps)))
 
 
 def micro_gemms():
@@ -158,7 +204,7 @@ def micro_gemms():
         del w
         x = torch.randn(m, k, device="cuda").to(torch.bfloat16)
         q, s = op.quantize(x)
-        ms = time_gemm("micro", q, s, [op], m, reps=20)
+        ms = time_gemm(None, "micro", q, s, [types.SimpleNamespace(micro=op)], m, m, reps=20)
         flop = 2.0 * m * n * k
         byt = m * k + n * k + 4 * (m + n) + 2 * m * n
         out[f"{m}x{k}x{n}"] = dict(us=round(ms * 1e3, 2), tflops=round(flop / ms / 1e9, 1),
@@ -271,13 +317,13 @@ def main():
         del w
         torch.cuda.empty_cache()
         # the other LM configurations, each one hipGraph replay per step
-        for key, preset, mode, tokens, grid, n_opt in (
+        for key, preset, mode, tokens, gx, n_opt in (
                 ("w4a16_g128_8b_576_step_ms", args.preset, "w4a16", T, grid, 8),
                 ("fp8_2b_320_step_ms", "qwen3vl-2b", "fp8", 320, (16, 16), 4),
                 ("fp8_32b_1024_step_ms", "qwen3vl-32b", "fp8", 1024, (30, 32), 2)):
             c = PRESETS[preset]
             wx = make_model(c, mode=mode, seed=0, n_options=n_opt)
-            ix, px, kx = make_request(c, tokens, *grid, seed=0)
+            ix, px, kx = make_request(c, tokens, *gx, seed=0)
             rx = Runtime(c, wx, tokens)
             rx.set_inputs(ix, px, kx)
             rx.capture()

@@ -5,8 +5,17 @@ kernel name the dispatch count, total and average duration and share of the
 total (``--kernel-trace`` rocpd database). ``python -m
 fastforward_amd.rocprof_summary pmc <counter_collection.csv> [...]`` prints the
 average counter value per dispatch for every kernel name and counter found in
-``--pmc`` CSV output.
+``--pmc`` CSV output. ``python -m fastforward_amd.rocprof_summary steptrace
+<results.db>`` prints per-step kernel time (model-construction kernels left
+out; a step is one readout launch) and ``step <results.db> <fetch.csv>
+<write.csv> <mfma.csv> <fetch_factor> <write_factor>`` adds bytes per call and
+MFMA busy % from the three counter runs. ``traffic <fetch.csv> <write.csv>
+<manifest.json>`` turns the two counter runs of ``bench.py --kernels`` (and the
+launch manifest that command prints) into HBM bytes per GEMM launch, scaled by
+what the counters read for its 256 MiB calibration copy, and writes the JSON
+summary to stdout after the table.
 """
+import json
 import collections
 import csv
 import re
@@ -67,7 +76,8 @@ def _by_grid(path, counters=None):
 
 
 def step_table(db, fetch_csv, write_csv, mfma_csv, fetch_factor, write_factor, xcds=8, simds=1024,
-               skip=("at::native", "__amd_rocclr", "weight_quant_kernel", "row_amax_kernel", "channel_scale_kernel")):
+               skip=("at::native", "__amd_rocclr", "weight_quant_kernel", "row_amax_kernel", "channel_scale_kernel",
+                     "int4_quant_kernel")):
     con = sqlite3.connect(db)
     dur = collections.defaultdict(list)
     for name, gx, gy, gz, wx, start, end in con.execute(
@@ -76,7 +86,7 @@ def step_table(db, fetch_csv, write_csv, mfma_csv, fetch_factor, write_factor, x
         if k.startswith(skip):
             continue
         dur[(k, gx * gy * gz)].append((end - start) / 1e3)
-    fe, wr, mf = _by_grid(fetch_csv), _by_grid(write_csv), _by_grid(mfma_csv)
+    fe, wr, mf = (_by_grid(p) if p else {} for p in (fetch_csv, write_csv, mfma_csv))
     steps = max(len(v) for k, v in dur.items() if k[0].startswith("readout_kernel")) if any(
         k[0].startswith("readout_kernel") for k in dur) else 1
     rows = []
@@ -93,7 +103,13 @@ def step_table(db, fetch_csv, write_csv, mfma_csv, fetch_factor, write_factor, x
     return rows
 
 
-def format_step_table(rows, hbm_peak_gbs=8000.0):
+def format_step_table(rows, hbm_peak_gbs=8000.0, counters=True):
+    if not counters:
+        lines = [f"{'kernel':44s} {'threads':>8s} {'calls/step':>10s} {'avg_us':>8s} {'us/step':>9s}"]
+        for k, g, calls, us, tot, *_ in rows:
+            lines.append(f"{k[:44]:44s} {g:8d} {calls:10.1f} {us:8.2f} {tot:9.1f}")
+        lines.append(f"{'total':44s} {'':8s} {'':10s} {'':8s} {sum(r[4] for r in rows):9.1f}")
+        return "\n".join(lines)
     lines = [f"{'kernel':44s} {'threads':>8s} {'calls/step':>10s} {'avg_us':>8s} {'us/step':>9s} "
              f"{'MB/call':>8s} {'GB/s':>7s} {'%HBM':>6s} {'MFMA%':>6s}"]
     for k, g, calls, us, tot, byt, gbs, util in rows:
@@ -103,9 +119,70 @@ def format_step_table(rows, hbm_peak_gbs=8000.0):
     return "\n".join(lines)
 
 
+def _dispatches(path):
+    """[(dispatch id, kernel, {counter: value})] in dispatch order from one --pmc CSV."""
+    rows = collections.OrderedDict()
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            d = rows.setdefault(int(r["Dispatch_Id"]), [short_name(r["Kernel_Name"]), {}])
+            d[1][r["Counter_Name"]] = d[1].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    return [(i, k, c) for i, (k, c) in sorted(rows.items())]
+
+
+def traffic(fetch_csv, write_csv, manifest):
+    """GEMM launches of ``bench.py --kernels`` in manifest order (``reps`` each),
+    then the calibration copy (the last ``copy_reps`` dispatches)."""
+    fe, wr = _dispatches(fetch_csv), _dispatches(write_csv)
+    reps = manifest["copy_reps"]
+    f_copy = sum(c["FETCH_SIZE"] for _, _, c in fe[-reps:]) / reps
+    w_copy = sum(c["WRITE_SIZE"] for _, _, c in wr[-reps:]) / reps
+    ff = manifest["copy_bytes"] / (f_copy * 1024)
+    wf = manifest["copy_bytes"] / (w_copy * 1024)
+    gf = [d for d in fe[:-reps] if d[1].startswith(("gemm_fp8", "gemv_fp8"))]
+    gw = [d for d in wr[:-reps] if d[1].startswith(("gemm_fp8", "gemv_fp8"))]
+    out, pos, tot_b, tot_n = [], 0, 0.0, 0
+    for e in manifest["gemm_launches"]:
+        n = e["reps"]
+        fk = sum(c["FETCH_SIZE"] for _, _, c in gf[pos:pos + n]) / n
+        wk = sum(c["WRITE_SIZE"] for _, _, c in gw[pos:pos + n]) / n
+        kern = gf[pos][1]
+        pos += n
+        hbm = fk * 1024 * ff + wk * 1024 * wf
+        out.append(dict(shape=e["shape"], kernel=kern, launches_per_step=e["launches_per_step"],
+                        fetch_kib=round(fk, 1), write_kib=round(wk, 1), hbm_bytes=int(hbm),
+                        algorithmic_bytes=e["algorithmic_bytes"], ratio=round(hbm / e["algorithmic_bytes"], 2)))
+        tot_b += hbm * e["launches_per_step"]
+        tot_n += e["launches_per_step"]
+    return dict(kernel="gemm_fp8_kernel", bytes_per_launch=int(tot_b / tot_n), launches_per_step=tot_n,
+                calibration=dict(copy_bytes=manifest["copy_bytes"], fetch_kib=round(f_copy, 1),
+                                 write_kib=round(w_copy, 1), fetch_factor=round(ff, 4), write_factor=round(wf, 4)),
+                by_shape=out)
+
+
+def format_traffic(t):
+    lines = ["| shape (M x K x N) | kernel | launches/step | FETCH KiB | WRITE KiB | HBM bytes | algorithmic bytes | ratio |",
+             "|---|---|---|---|---|---|---|---|"]
+    for r in t["by_shape"]:
+        lines.append(f"| {r['shape']} | `{r['kernel']}` | {r['launches_per_step']} | {r['fetch_kib']} | "
+                     f"{r['write_kib']} | {r['hbm_bytes'] / 1e6:.1f} MB | {r['algorithmic_bytes'] / 1e6:.1f} MB | "
+                     f"{r['ratio']} |")
+    lines.append(f"\nStep-weighted bytes per launch: {t['bytes_per_launch'] / 1e6:.1f} MB "
+                 f"({t['launches_per_step']} launches per step); calibration factors FETCH "
+                 f"{t['calibration']['fetch_factor']}, WRITE {t['calibration']['write_factor']}.")
+    return "\n".join(lines)
+
+
 def main(argv):
     if len(argv) >= 2 and argv[0] == "kernels":
         print(format_kernel_stats(kernel_stats(argv[1])))
+    elif len(argv) == 4 and argv[0] == "traffic":
+        with open(argv[3]) as f:
+            man = json.loads([ln for ln in f if ln.startswith("{")][-1])
+        t = traffic(argv[1], argv[2], man)
+        print(format_traffic(t))
+        print(json.dumps(t, indent=1))
+    elif len(argv) == 2 and argv[0] == "steptrace":
+        print(format_step_table(step_table(argv[1], None, None, None, 1.0, 1.0), counters=False))
     elif len(argv) == 7 and argv[0] == "step":
         print(format_step_table(step_table(argv[1], argv[2], argv[3], argv[4], float(argv[5]), float(argv[6]))))
     elif len(argv) >= 2 and argv[0] == "pmc":
