@@ -15,6 +15,7 @@ P = ctypes.c_void_p
 I64 = ctypes.c_int64
 I32 = ctypes.c_int
 F32 = ctypes.c_float
+PI64 = ctypes.POINTER(ctypes.c_int64)
 
 # name -> argtypes (restype int unless noted); mirrors include/ff_amd.h
 SIGNATURES = {
@@ -41,6 +42,8 @@ SIGNATURES = {
     "ff_gemm_fp8_qkv": [P, P, P, P, I64, I64, I64, I64, P, P, F32, F32, P, P, P, P, P, I64, P],
     "ff_quant_weight_int4": [P, P, P, I64, I64, I64, I32, P],
     "ff_gemm_w4a16": [P, I64, P, P, I64, P, I64, I64, I64, I64, P],
+    "ff_gemm_w4a16_workspace": [I64, I64, I64, PI64],
+    "ff_gemm_w4a16_ws": [P, I64, P, P, I64, P, I64, I64, I64, I64, P, I64, P],
     "ff_embed": [P, P, P, I64, I64, I64, P],
     "ff_gather_rows": [P, I64, P, P, I64, I64, I64, I64, P],
     "ff_scatter_rows": [P, P, I64, I64, I64, P],

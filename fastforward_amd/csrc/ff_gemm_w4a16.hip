@@ -42,6 +42,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "ff_common.h"
@@ -108,7 +109,9 @@ struct W4Cfg {
   static constexpr int STAGE = A_BYTES + 4 * (B_WAVE + SC_WAVE);
   static constexpr int ND = NDA + NDB + 1;           // DMA instructions per wave per stage
   static constexpr int EPI_LD = BN + 8;              // bf16 row pitch of the epilogue tile
+  static constexpr int EPI32_LD = BN + 4;            // fp32 row pitch of a split-K partial tile
   static constexpr int SMEM = S * STAGE > BM * EPI_LD * 2 ? S * STAGE : BM * EPI_LD * 2;
+  static constexpr bool kSplitK = BM * EPI32_LD * 4 <= SMEM;  // the fp32 partial tile fits the LDS
   static_assert(BM % 32 == 0 && CW % 16 == 0 && CW <= 64, "tile shape");
   static_assert(SMEM <= 160 * 1024, "LDS budget");
   static_assert((S - 1) * ND < 64 && S >= 3, "vmcnt range; two stages resident");
@@ -118,15 +121,20 @@ template <int BM, int CW, int S, int OCC>
 __global__ __launch_bounds__(kThreads, OCC) void gemm_w4a16_kernel(
     const bf16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ packed,
     const bf16_t* __restrict__ scales, int group, bf16_t* __restrict__ y, int64_t ldy, int M, int N, int K,
-    int tiles_m, int tiles_n) {
+    int tiles_m, int tiles_n, int splits, float* __restrict__ ws) {
   using C = W4Cfg<BM, CW, S>;
   __shared__ __align__(16) uint8_t smem[C::SMEM];
 
   const int nblk = tiles_m * tiles_n;
-  const int b = blockIdx.x;
+  const int split = blockIdx.x / nblk;
+  const int b = blockIdx.x % nblk;
   int logical = b;
   if (nblk % kXcds == 0) logical = (b % kXcds) * (nblk / kXcds) + b / kXcds;
   const int tm = logical / tiles_n, tn = logical % tiles_n;
+  // Split-K: this workgroup's k range, in whole pairs of stages (the loop runs two per trip).
+  const int kp = K / (2 * KSTAGE);
+  const int kp0 = (int)((int64_t)kp * split / splits), kp1 = (int)((int64_t)kp * (split + 1) / splits);
+  const int kbase = kp0 * 2 * KSTAGE;
   const int m0 = tm * BM, n0 = tn * C::BN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -163,7 +171,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_w4a16_kernel(
   const uint32_t ldsB = lds0 + C::A_BYTES + (uint32_t)__builtin_amdgcn_readfirstlane(wave) * C::B_WAVE;
   const uint32_t ldsS = lds0 + C::A_BYTES + 4 * C::B_WAVE + (uint32_t)__builtin_amdgcn_readfirstlane(wave) * C::SC_WAVE;
   auto issue = [&](int kt, int buf) {
-    const int k0 = kt * KSTAGE;
+    const int k0 = kbase + kt * KSTAGE;
     const uint32_t off = buf * C::STAGE;
 #pragma unroll
     for (int i = 0; i < C::NDA; ++i) lds_dma16(srcA[i] + 2 * k0, ldsA + off + 4 * i * 1024);
@@ -179,7 +187,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_w4a16_kernel(
 #pragma unroll
     for (int j = 0; j < C::TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int KT = K / KSTAGE;
+  const int KT = 2 * (kp1 - kp0);  // stages of this workgroup
 #pragma unroll
   for (int st = 0; st < S - 1; ++st)
     if (st < KT) issue(st, st);
@@ -282,6 +290,32 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_w4a16_kernel(
   }
   __syncthreads();  // all stages consumed before the epilogue reuses the LDS
 
+  if constexpr (C::kSplitK) {
+   if (splits > 1) {
+    // fp32 partial tile of this split, row-major (M, N) at ws + split * M * N
+    float* tile32 = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (int j = 0; j < C::TJ; ++j) {
+      const int cl = wave * CW + j * 16 + r16;
+#pragma unroll
+      for (int i = 0; i < C::RA; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) tile32[(i * 16 + 4 * g + r) * C::EPI32_LD + cl] = acc[i][j][r];
+    }
+    __syncthreads();
+    float* part = ws + (size_t)split * M * N;
+    constexpr int CH4 = BM * C::BN / 4;
+#pragma unroll
+    for (int c = tid; c < CH4; c += kThreads) {
+      const int rl = c / (C::BN / 4), cl = (c % (C::BN / 4)) * 4;
+      const int m = m0 + rl, n = n0 + cl;
+      if (m < M && n < N)
+        *reinterpret_cast<f32x4*>(part + (size_t)m * N + n) = *reinterpret_cast<const f32x4*>(tile32 + rl * C::EPI32_LD + cl);
+    }
+    return;
+   }
+  }
+
   bf16_t* tile = reinterpret_cast<bf16_t*>(smem);
 #pragma unroll
   for (int j = 0; j < C::TJ; ++j) {
@@ -302,15 +336,39 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_w4a16_kernel(
   }
 }
 
+// y = bf16(sum over splits of the fp32 partials, in split order); 8 outputs per thread.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int splits, int M, int N,
+                                                            bf16_t* __restrict__ y, int64_t ldy) {
+  const int64_t per_row = N / 8;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)M * per_row) return;
+  const int m = (int)(i / per_row), n = (int)(i % per_row) * 8;
+  const size_t off = (size_t)m * N + n;
+  f32x4 a = *reinterpret_cast<const f32x4*>(ws + off), b = *reinterpret_cast<const f32x4*>(ws + off + 4);
+  for (int s = 1; s < splits; ++s) {
+    a += *reinterpret_cast<const f32x4*>(ws + (size_t)s * M * N + off);
+    b += *reinterpret_cast<const f32x4*>(ws + (size_t)s * M * N + off + 4);
+  }
+  u32x4 o;
+  o.x = pack_bf16x2(a[0], a[1]); o.y = pack_bf16x2(a[2], a[3]);
+  o.z = pack_bf16x2(b[0], b[1]); o.w = pack_bf16x2(b[2], b[3]);
+  *reinterpret_cast<u32x4*>(y + (size_t)m * ldy + n) = o;
+}
+
 enum W4Tile { kW64x256, kW192x192 };
 
 template <int BM, int CW, int S, int OCC>
 void launch_w4(const void* x, int64_t ldx, const void* packed, const void* scales, int group, void* y, int64_t ldy,
-               int m, int n, int k, hipStream_t stream) {
+               int m, int n, int k, int splits, float* ws, hipStream_t stream) {
   const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + 4 * CW - 1) / (4 * CW);
-  hipLaunchKernelGGL((gemm_w4a16_kernel<BM, CW, S, OCC>), dim3(tiles_m * tiles_n), dim3(kThreads), 0, stream,
-                     (const bf16_t*)x, ldx, (const uint8_t*)packed, (const bf16_t*)scales, group, (bf16_t*)y, ldy,
-                     m, n, k, tiles_m, tiles_n);
+  hipLaunchKernelGGL((gemm_w4a16_kernel<BM, CW, S, OCC>), dim3(tiles_m * tiles_n * splits), dim3(kThreads), 0,
+                     stream, (const bf16_t*)x, ldx, (const uint8_t*)packed, (const bf16_t*)scales, group,
+                     (bf16_t*)y, ldy, m, n, k, tiles_m, tiles_n, splits, ws);
+  if (splits > 1) {
+    const int64_t items = (int64_t)m * (n / 8);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, stream, ws, splits,
+                       m, n, (bf16_t*)y, ldy);
+  }
 }
 
 // 192 x 192 tiles dequantise each weight for 192 rows (a third of the VALU work
@@ -326,11 +384,27 @@ W4Tile pick_w4_tile(int64_t m, int64_t n) {
   return (m > 64 && tiles192 >= 256) ? kW192x192 : kW64x256;
 }
 
-}  // namespace
+// Split-K factor of the 64 x 256 tiles: grids below 256 workgroups leave CUs
+// idle, so the k range is split until about two workgroups per CU (at most 8
+// ways, at least one pair of stages each); the fp32 partials cost 8 bytes per
+// output per split (written once, read once by the reduction).
+// FF_W4A16_SPLITS overrides the choice.
+int pick_w4_splits(W4Tile t, int64_t m, int64_t n, int64_t k) {
+  static_assert(W4Cfg<64, 64, 4>::kSplitK, "the 64 x 256 tile stages its fp32 partials in LDS");
+  if (t != kW64x256) return 1;
+  const int64_t pairs = k / (2 * KSTAGE);
+  int64_t s;
+  if (const char* e = getenv("FF_W4A16_SPLITS")) {
+    s = atoi(e);
+  } else {
+    const int64_t tiles = ((m + 63) / 64) * ((n + 255) / 256);
+    s = tiles >= 256 ? 1 : 512 / tiles;
+  }
+  return (int)std::max<int64_t>(1, std::min<int64_t>({s, 8, pairs}));
+}
 
-extern "C" int ff_gemm_w4a16(const void* x, int64_t ldx, const void* packed, const void* scales,
-                             int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
-                             ff_stream_t stream) {
+static int gemm_w4a16(const void* x, int64_t ldx, const void* packed, const void* scales, int64_t group, void* y,
+                      int64_t ldy, int64_t m, int64_t n, int64_t k, void* ws, int64_t ws_bytes, ff_stream_t stream) {
   FF_REQUIRE(x && packed && scales && y, "ff_gemm_w4a16: null pointer");
   FF_REQUIRE(k > 0 && k % (2 * KSTAGE) == 0 && (group == 32 || group % 64 == 0) && k % group == 0,
              "ff_gemm_w4a16: k=%lld must be a multiple of %d and of group=%lld (group 32 or a multiple of 64)",
@@ -339,12 +413,43 @@ extern "C" int ff_gemm_w4a16(const void* x, int64_t ldx, const void* packed, con
              "ff_gemm_w4a16: bad sizes (n %% 8 == 0, ldx and ldy multiples of 8)");
   FF_REQUIRE(ff_aligned(x, 16) && ff_aligned(packed, 16) && ff_aligned(scales, 16) && ff_aligned(y, 16),
              "ff_gemm_w4a16: x, packed, scales and y must be 16-byte aligned");
+  FF_REQUIRE(ws_bytes >= 0 && (ws_bytes == 0 || (ws && ff_aligned(ws, 16))),
+             "ff_gemm_w4a16_ws: workspace must be 16-byte aligned");
   if (m == 0) return FF_OK;
   const hipStream_t s = (hipStream_t)stream;
-  switch (pick_w4_tile(m, n)) {
-    case kW64x256: launch_w4<64, 64, 4, 2>(x, ldx, packed, scales, (int)group, y, ldy, (int)m, (int)n, (int)k, s); break;
-    case kW192x192: launch_w4<192, 48, 4, 1>(x, ldx, packed, scales, (int)group, y, ldy, (int)m, (int)n, (int)k, s); break;
+  const W4Tile t = pick_w4_tile(m, n);
+  int splits = pick_w4_splits(t, m, n, k);
+  while (splits > 1 && (int64_t)splits * m * n * 4 > ws_bytes) --splits;
+  switch (t) {
+    case kW64x256:
+      launch_w4<64, 64, 4, 2>(x, ldx, packed, scales, (int)group, y, ldy, (int)m, (int)n, (int)k, splits,
+                              (float*)ws, s);
+      break;
+    case kW192x192:
+      launch_w4<192, 48, 4, 1>(x, ldx, packed, scales, (int)group, y, ldy, (int)m, (int)n, (int)k, 1, nullptr, s);
+      break;
   }
   FF_LAUNCH_CHECK("ff_gemm_w4a16");
   return FF_OK;
+}
+
+}  // namespace
+
+extern "C" int ff_gemm_w4a16(const void* x, int64_t ldx, const void* packed, const void* scales,
+                             int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
+                             ff_stream_t stream) {
+  return gemm_w4a16(x, ldx, packed, scales, group, y, ldy, m, n, k, nullptr, 0, stream);
+}
+
+extern "C" int ff_gemm_w4a16_workspace(int64_t m, int64_t n, int64_t k, int64_t* bytes) {
+  FF_REQUIRE(bytes && m >= 0 && n > 0 && k > 0, "ff_gemm_w4a16_workspace: bad arguments");
+  const int splits = k % (2 * KSTAGE) == 0 ? pick_w4_splits(pick_w4_tile(m, n), m, n, k) : 1;
+  *bytes = splits > 1 ? (int64_t)splits * m * n * 4 : 0;
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_w4a16_ws(const void* x, int64_t ldx, const void* packed, const void* scales, int64_t group,
+                                void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, void* workspace,
+                                int64_t workspace_bytes, ff_stream_t stream) {
+  return gemm_w4a16(x, ldx, packed, scales, group, y, ldy, m, n, k, workspace, workspace_bytes, stream);
 }

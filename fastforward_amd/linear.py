@@ -17,6 +17,7 @@ attributes:
 Weight quantization runs once on the GPU at construction. All calls allocate
 their outputs with torch.empty and launch on the current stream.
 """
+import ctypes
 import types
 
 import torch
@@ -139,6 +140,9 @@ class Int4:
         m, k = flat.shape
         n = self.weight.shape[0]
         y = torch.empty((m, n), device=x.device, dtype=BF16) if out is None else out
-        call("ff_gemm_w4a16", ptr(flat), flat.stride(0), ptr(self.packed), ptr(self.scales), self.group,
-             ptr(y), y.stride(0), m, n, k, stream())
+        need = ctypes.c_int64(0)
+        call("ff_gemm_w4a16_workspace", m, n, k, ctypes.byref(need))
+        ws = torch.empty(need.value, device=x.device, dtype=torch.uint8) if need.value else None
+        call("ff_gemm_w4a16_ws", ptr(flat), flat.stride(0), ptr(self.packed), ptr(self.scales), self.group,
+             ptr(y), y.stride(0), m, n, k, ptr(ws), need.value, stream())
         return y

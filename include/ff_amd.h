@@ -189,6 +189,19 @@ int ff_gemm_w4a16(const void* x, int64_t ldx, const void* packed, const void* sc
                   int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
                   ff_stream_t stream);
 
+/* The same product with a caller-provided device workspace (the reference's
+ * _weight_int4pack_mm call at _family/night_runtime.py:33 allocates inside its
+ * library; here the caller allocates, so the call stays graph-capturable). Shapes
+ * whose tile grid would leave CUs idle split K; the fp32 partial sums go to the
+ * workspace and a second launch adds them in split order (deterministic) and
+ * rounds to bf16. ff_gemm_w4a16_workspace stores the bytes the split wants (0:
+ * none); a smaller workspace lowers the split, and 0 bytes is ff_gemm_w4a16.
+ * workspace must be 16-byte aligned. */
+int ff_gemm_w4a16_workspace(int64_t m, int64_t n, int64_t k, int64_t* bytes);
+int ff_gemm_w4a16_ws(const void* x, int64_t ldx, const void* packed, const void* scales,
+                     int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
+                     void* workspace, int64_t workspace_bytes, ff_stream_t stream);
+
 /* Embedding gather h[t] = table[ids[t]] (scaled_qwen_runtime.py:145
  * embed_tokens). Ids outside [0, vocab) read row 0 (the host validates ids). */
 int ff_embed(const int64_t* ids, const void* table, void* out, int64_t t, int64_t h,

@@ -337,14 +337,17 @@ def test_gemm_w4a16(gpu, m, k, n, sym, group):
     assert float((want - exact).pow(2).mean().sqrt() / exact.pow(2).mean().sqrt()) <= 5e-3
 
 
-@pytest.mark.parametrize("tile", ["64x256", "192x192"])
-@pytest.mark.parametrize("m,k,n", [(576, 4096, 6144), (200, 1024, 392)])
-def test_gemm_w4a16_both_tiles(gpu, monkeypatch, m, k, n, tile):
-    """Each tile shape of the W4A16 GEMM (chosen by size in production) against
-    the fp64 product with the exactly dequantised weight, asymmetric group 32 and
+@pytest.mark.parametrize("tile,splits", [("64x256", None), ("64x256", "1"), ("64x256", "3"), ("192x192", None)])
+@pytest.mark.parametrize("m,k,n", [(576, 4096, 6144), (200, 1024, 392), (1, 12288, 4096)])
+def test_gemm_w4a16_both_tiles(gpu, monkeypatch, m, k, n, tile, splits):
+    """Each tile shape of the W4A16 GEMM (chosen by size in production) and the
+    split-K form of the 64 x 256 tile (automatic, off, forced to 3) against the
+    fp64 product with the exactly dequantised weight, asymmetric group 32 and
     ragged M / N edges included."""
     from fastforward_amd.linear import Int4
     monkeypatch.setenv("FF_W4A16_TILE", tile)
+    if splits is not None:
+        monkeypatch.setenv("FF_W4A16_SPLITS", splits)
     x = torch.randn(m, k, generator=_g(36)).to(BF16)
     w = (torch.randn(n, k, generator=_g(37)) * 0.02).to(BF16)
     for sym, group in ((True, 128), (False, 32)):
