@@ -175,6 +175,7 @@ constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppRowMirror = 0x140;  // lane i <- 15 - i
 constexpr int kDppHalfMirror = 0x141; // lane i <- 7 - i within each 8
+constexpr int kDppRowRor8 = 0x128;    // lane i <- lane (i + 8) mod 16 of its row
 
 // Wave-wide sum / max on DPP within rows and row swaps across them. Every step
 // adds a lane's value to its partner's (a commutative pair), so all 64 lanes

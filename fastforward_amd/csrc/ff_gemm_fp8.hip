@@ -177,6 +177,24 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
   }
   __syncthreads();  // all stages consumed before the epilogue reuses the LDS
 
+  // QKV epilogue of a q/k head: issue its global loads (norm weights, the cos /
+  // sin rows of this thread's tokens) now, so they land while the tile is staged.
+  constexpr int kRopeRows = BM / (kThreads / 16);
+  float rope_w[8];
+  u32x4 rope_c[kRopeRows], rope_s[kRopeRows];
+  if constexpr (EPI == kQkv) {
+    if (tn < qe.hq + qe.hk) {
+      const int j = tid & 15, grp = tid >> 4;
+      unpack8(*reinterpret_cast<const u32x4*>((tn < qe.hq ? qe.qn : qe.kn) + 8 * j), rope_w);
+#pragma unroll
+      for (int p = 0; p < kRopeRows; ++p) {
+        const int mm = min(m0 + grp + p * (kThreads / 16), M - 1);
+        rope_c[p] = *reinterpret_cast<const u32x4*>(qe.cos + (size_t)mm * kHeadDim + 8 * j);
+        rope_s[p] = *reinterpret_cast<const u32x4*>(qe.sin + (size_t)mm * kHeadDim + 8 * j);
+      }
+    }
+  }
+
   // epilogue: y = bf16((acc * sa) * sw), staged through LDS as a row-major tile.
   bf16_t* tile = reinterpret_cast<bf16_t*>(smem);
 #pragma unroll
@@ -230,16 +248,16 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
       // q or k head: one 16-lane group per token row, as the qkv_post kernel does
       const bool isq = head < qe.hq;
       const int hh = isq ? head : head - qe.hq;
-      const bf16_t* wn = isq ? qe.qn : qe.kn;
       const float eps = isq ? qe.eps_q : qe.eps_k;
       bf16_t* dst = (isq ? qe.yq : qe.yk) + (size_t)hh * M * kHeadDim;
       const int grp = tid >> 4, j = tid & 15;
-      for (int rl = grp; rl < BM; rl += kThreads / 16) {
+#pragma unroll
+      for (int p = 0; p < kRopeRows; ++p) {
+        const int rl = grp + p * (kThreads / 16);
         const int m = m0 + rl;
         const bool valid = m < M;
         const int mm = valid ? m : M - 1;
-        rope_row(tile + rl * C::EPI_LD, wn, eps, qe.cos + (size_t)mm * kHeadDim, qe.sin + (size_t)mm * kHeadDim,
-                 dst + (size_t)mm * kHeadDim, j, valid);
+        rope_row_pre(tile + rl * C::EPI_LD, rope_w, eps, rope_c[p], rope_s[p], dst + (size_t)mm * kHeadDim, j, valid);
       }
     } else {
       // v head: 8 consecutive tokens of one d row per thread (16-byte stores)
