@@ -260,10 +260,12 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
         rope_row_pre(tile + rl * C::EPI_LD, rope_w, eps, rope_c[p], rope_s[p], dst + (size_t)mm * kHeadDim, j, valid);
       }
     } else {
-      // v head: 8 consecutive tokens of one d row per thread (16-byte stores)
+      // v head: 8 consecutive tokens of one d row per thread (16-byte stores);
+      // consecutive lanes take consecutive d, so each LDS read of a wave is one
+      // 128-byte row segment (no bank conflicts)
       const int hv = head - qe.hq - qe.hk;
       for (int c = tid; c < kHeadDim * (BM / 8); c += kThreads) {
-        const int d = c / (BM / 8), t0 = (c % (BM / 8)) * 8;
+        const int d = c % kHeadDim, t0 = (c / kHeadDim) * 8;
         const int tok = m0 + t0;
         if (tok >= qe.t_pad) continue;
         float f[8];
