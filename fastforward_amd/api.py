@@ -12,7 +12,9 @@ question into tokens is outside this build.
 Bundle (JSON): ``{"schema_version": 1, "task": "visual_choice",
 "architecture": "qwen3_vl_lm", "preset": "qwen3vl-8b", "linear": "fp8" |
 "fp8_static" | "w4a16", "seed": 0, "tokens": 576, "image_grid": [16, 32],
-"prefix_tokens": 4}``.
+"prefix_tokens": 4, "buckets": [576]}``; ``buckets`` (token buckets, each a
+captured graph, as the reference's ``buckets`` config) defaults to
+``[tokens]``.
 """
 import hashlib
 import json
@@ -81,6 +83,10 @@ def read_bundle(bundle):
     prefix = int(c.get("prefix_tokens", 4))
     if tokens <= 0 or gh < 0 or gw < 0 or prefix < 0 or prefix + gh * gw > tokens:
         raise ValueError("tokens must hold the prefix and the image grid")
+    buckets = c.get("buckets", [tokens])
+    if (not isinstance(buckets, list) or not buckets or any(not isinstance(b, int) for b in buckets)
+            or min(buckets) < prefix + gh * gw):
+        raise ValueError("buckets must be token counts that hold the prefix and the image grid")
     if "checkpoint" in c:
         if not Path(c["checkpoint"]).exists():
             raise FileNotFoundError(c["checkpoint"])
@@ -106,7 +112,8 @@ class Accelerator:
             raise RuntimeError(f"The {backend!r} backend is not part of this build; use 'fast'")
         from . import _lib
         _lib.check_device()      # exactly the gfx950 path; there is no CPU fallback
-        from .runtime import PRESETS, Runtime
+        from .graphs import StepGraphs
+        from .runtime import PRESETS
         from .synthetic import OPTION_IDS, make_model
         self.config = c
         self.backend = backend
@@ -117,8 +124,8 @@ class Accelerator:
         self.prefix_tokens = int(c.get("prefix_tokens", 4))
         self.weights = make_model(self.cfg, mode=c.get("linear", "fp8"), seed=int(c.get("seed", 0)),
                                   n_options=len(OPTION_IDS))
-        self.runtime = Runtime(self.cfg, self.weights, self.tokens)
-        self.captured = False
+        self.buckets = sorted(set(c.get("buckets", [self.tokens])))
+        self.graphs = StepGraphs(self.cfg, self.weights, self.buckets, self.grid, self.prefix_tokens)
 
     def predict(self, image, question, candidates, item_id="request", *, backend=None):
         """The reference's entry point: validated as there, then refused --
@@ -133,30 +140,21 @@ class Accelerator:
 
     def predict_tokens(self, ids, candidates, item_id="request", *, pick=None):
         """Score ``candidates`` (2..8 strings, answer letters A.. in order) for a
-        prompt of token ids (1-D int, at most ``tokens`` long) whose image block
-        sits after ``prefix_tokens`` tokens on the bundle's grid. ``pick`` is
-        the scored row (default: the last token). Returns the response dict."""
+        prompt of token ids (1-D int, at most the largest bucket long) whose
+        image block sits after ``prefix_tokens`` tokens on the bundle's grid.
+        ``pick`` is the scored row (default: the last token). The request runs
+        in the smallest bucket that holds it; the bucket's first request
+        captures its graph. Returns the response dict."""
         import torch
-        from .runtime import mrope_positions
         validate_candidates(candidates)
         ids = torch.as_tensor(ids, dtype=torch.int64).reshape(-1)
         n = ids.numel()
-        gh, gw = self.grid
-        if not self.prefix_tokens + gh * gw <= n <= self.tokens:
-            raise ValueError(f"expected {self.prefix_tokens + gh * gw}..{self.tokens} token ids, got {n}")
-        if int(ids.min()) < 0 or int(ids.max()) >= self.cfg.vocab:
-            raise ValueError("token id outside the vocabulary")
+        if n > self.buckets[-1]:
+            raise ValueError(f"expected at most {self.buckets[-1]} token ids, got {n}")
         pick = n - 1 if pick is None else int(pick)
-        if not 0 <= pick < n:
-            raise ValueError("pick must index a real token")
-        pos = torch.from_numpy(mrope_positions(self.prefix_tokens, gh, gw, self.tokens))
         with self.lock, torch.no_grad():
-            self.runtime.set_inputs(ids, pos, pick)
-            if not self.captured:
-                self.runtime.capture()
-                self.captured = True
-            z = self.runtime.replay()
-            logits = z.cpu().tolist()[: len(candidates)]
+            z, _ = self.graphs.run(ids, pick, len(candidates))
+            logits = z.cpu().tolist()
         return response(logits, list(candidates), item_id)
 
     def warmup(self, requests):

@@ -43,7 +43,8 @@ def _bundle(tmp_path, **kw):
 
 
 @pytest.mark.parametrize("bad", [dict(schema_version=2), dict(task="caption"), dict(architecture="llama"),
-                                 dict(preset="qwen3vl-70b"), dict(linear="int8"), dict(tokens=100)])
+                                 dict(preset="qwen3vl-70b"), dict(linear="int8"), dict(tokens=100),
+                                 dict(buckets=[200, 320]), dict(buckets=[]), dict(buckets="320")])
 def test_bundle_rejected(tmp_path, bad):
     with pytest.raises(ValueError):
         read_bundle(_bundle(tmp_path, **bad))
@@ -84,3 +85,51 @@ def test_predict_tokens_matches_eager_step(gpu, tmp_path):
         assert r["answer"] == response(z, cands, "r")["answer"]
     with pytest.raises(ValueError):
         acc.predict_tokens(torch.zeros(10, dtype=torch.int64), ["a", "b"])
+
+
+def test_step_graphs_buckets_and_position_templates():
+    """Bucket choice (smallest bucket that holds the request) and the
+    per-bucket M-RoPE template: on a prompt's real tokens it equals the
+    positions of the prompt alone (the reference's template check)."""
+    import numpy as np
+    from fastforward_amd.graphs import StepGraphs
+    from fastforward_amd.runtime import PRESETS, mrope_positions
+    g = StepGraphs(PRESETS["qwen3vl-2b"], None, [320, 288], (16, 16), 4)
+    assert g.buckets == [288, 320]
+    assert g.bucket_for(260) == 288 and g.bucket_for(288) == 288 and g.bucket_for(289) == 320
+    with pytest.raises(ValueError):
+        g.bucket_for(321)
+    for n in (260, 275, 288):
+        t = g.positions(g.bucket_for(n)).numpy()
+        assert np.array_equal(t[:, :n], mrope_positions(4, 16, 16, n))
+    with pytest.raises(ValueError):
+        StepGraphs(PRESETS["qwen3vl-2b"], None, [200], (16, 16), 4)
+
+
+@pytest.mark.gpu
+def test_bucketed_graphs_match_eager_and_isolate_padding(gpu, tmp_path):
+    """Requests of 270, 300 and 280 tokens over buckets (288, 320): each bucket
+    captures on its first request only, every replay equals an eager step of
+    its bucket bit for bit, and the gate (position template, graph == eager,
+    padding ids set to 42 leave the answer's bits unchanged) passes."""
+    import torch
+    from fastforward_amd.runtime import Runtime
+    from fastforward_amd.synthetic import make_request
+    acc = Accelerator(_bundle(tmp_path, buckets=[288, 320]))
+    seen = []
+    for seed, n in ((1, 270), (2, 300), (3, 280)):
+        ids, _, _ = make_request(acc.cfg, n, 16, 16, seed=seed, real_tokens=n)
+        ids = torch.as_tensor(ids)[:n]
+        z, captured = acc.graphs.run(ids, n - 1, 4)
+        b = acc.graphs.bucket_for(n)
+        assert captured == (b not in seen)
+        seen.append(b)
+        eager = Runtime(acc.cfg, acc.weights, b)
+        eager.set_inputs(ids, acc.graphs.positions(b), n - 1)
+        assert torch.equal(z.cpu(), eager.step()[:4].cpu())
+        report = acc.graphs.gate(ids, n - 1, 4)
+        assert report["passed"] and report["bucket"] == b
+        r = acc.predict_tokens(ids, ["a", "b", "c", "d"], item_id=f"r{seed}")
+        assert r["logits"] == z.cpu().tolist()
+    src, pin, _ = acc.graphs.staging[288]
+    assert src.is_pinned() and pin.is_pinned()
