@@ -14,7 +14,9 @@ Bundle (JSON): ``{"schema_version": 1, "task": "visual_choice",
 "fp8_static" | "w4a16", "seed": 0, "tokens": 576, "image_grid": [16, 32],
 "prefix_tokens": 4, "buckets": [576]}``; ``buckets`` (token buckets, each a
 captured graph, as the reference's ``buckets`` config) defaults to
-``[tokens]``.
+``[tokens]``. With ``linear: "fp8_static"`` a bundle may name a calibration
+profile (``profile_path``, ``profile_sha256``, ``variant``), selected at
+construction.
 """
 import hashlib
 import json
@@ -87,6 +89,13 @@ def read_bundle(bundle):
     if (not isinstance(buckets, list) or not buckets or any(not isinstance(b, int) for b in buckets)
             or min(buckets) < prefix + gh * gw):
         raise ValueError("buckets must be token counts that hold the prefix and the image grid")
+    if "profile_path" in c:
+        from .profiles import read_profiles
+        if c.get("linear") != "fp8_static":
+            raise ValueError("a calibration profile needs static FP8 linears (linear: fp8_static)")
+        profiles = read_profiles(c["profile_path"], c.get("profile_sha256"))
+        if c.get("variant") not in profiles:
+            raise ValueError(f"Unknown calibration variant {c.get('variant')!r}")
     if "checkpoint" in c:
         if not Path(c["checkpoint"]).exists():
             raise FileNotFoundError(c["checkpoint"])
@@ -126,6 +135,20 @@ class Accelerator:
                                   n_options=len(OPTION_IDS))
         self.buckets = sorted(set(c.get("buckets", [self.tokens])))
         self.graphs = StepGraphs(self.cfg, self.weights, self.buckets, self.grid, self.prefix_tokens)
+        self.variant = None
+        if "profile_path" in c:
+            from .profiles import read_profiles
+            self.profiles = read_profiles(c["profile_path"], c.get("profile_sha256"))
+            self.select(c["variant"])
+
+    def select(self, variant):
+        """Switch the static FP8 activation bounds to calibration ``variant``
+        (the reference's ``select``); graphs re-capture on their next request."""
+        if variant not in getattr(self, "profiles", {}):
+            raise ValueError(f"Unknown calibration variant {variant!r}")
+        with self.lock:
+            self.graphs.select(self.profiles[variant])
+            self.variant = variant
 
     def predict(self, image, question, candidates, item_id="request", *, backend=None):
         """The reference's entry point: validated as there, then refused --

@@ -37,6 +37,17 @@ class StepGraphs:
         self.cache = {}     # bucket -> captured Runtime
         self.staging = {}   # bucket -> (pinned ids (bucket,), pinned pick (1,), event)
 
+    def select(self, bounds):
+        """Apply a calibration profile ({"j:role": bound}) to the static FP8
+        linears and drop the captured graphs: the activation multiplier is a
+        kernel argument recorded at capture, so each bucket re-captures on its
+        next request (the reference selects before it captures)."""
+        from .profiles import apply_profile
+        torch.cuda.synchronize()
+        apply_profile(self.w, bounds)
+        self.cache.clear()
+        self.staging.clear()
+
     def bucket_for(self, n):
         b = next((b for b in self.buckets if b >= n), None)
         if b is None:

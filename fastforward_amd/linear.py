@@ -96,6 +96,14 @@ class StaticFP8Linear:
         self.input_scale = torch.tensor([1. / inverse_scale], device=w.device, dtype=torch.float32)
         self.fast_accum = True
 
+    def set_bound(self, bound):
+        """Calibrate to activation bound ``bound`` as the reference's ``select``
+        does per op (_family/night_runtime.py:52-54): ``inverse_scale = 448/bound``
+        and ``input_scale`` refilled in place with ``bound/448``. A graph captured
+        before this call keeps the old multiplier; the graph runners re-capture."""
+        self.inverse_scale = 448. / bound
+        self.input_scale.fill_(bound / 448.)
+
     def __call__(self, x):
         flat = _rows(x)
         if not flat.is_contiguous():

@@ -133,3 +133,86 @@ def test_bucketed_graphs_match_eager_and_isolate_padding(gpu, tmp_path):
         assert r["logits"] == z.cpu().tolist()
     src, pin, _ = acc.graphs.staging[288]
     assert src.is_pinned() and pin.is_pinned()
+
+
+def _profile(tmp_path, variants, layers=28):
+    roles = ("qkv", "output", "gateup", "down")
+    p = tmp_path / "profile.json"
+    p.write_text(json.dumps({"profiles": {v: {f"{j}:{r}": b for j in range(layers) for r in roles}
+                                          for v, b in variants.items()}}))
+    from fastforward_amd.api import sha256
+    return p, sha256(p)
+
+
+def test_calibration_profiles_read_and_bundle_checks(tmp_path):
+    """Profile files as activate_fast reads them (digest checked), and the
+    bundle rules: a profile needs static FP8 linears and a known variant."""
+    from fastforward_amd.profiles import read_profiles
+    p, digest = _profile(tmp_path, {"square256": 8.0, "tall": 12.0})
+    assert set(read_profiles(p, digest)) == {"square256", "tall"}
+    with pytest.raises(ValueError):
+        read_profiles(p, "0" * 64)
+    with pytest.raises(FileNotFoundError):
+        read_profiles(tmp_path / "none.json")
+    bad = tmp_path / "bad.json"
+    bad.write_text(json.dumps({"profiles": {"v": {"0:qkv": -1}}}))
+    with pytest.raises(ValueError):
+        read_profiles(bad)
+    kw = dict(profile_path=str(p), profile_sha256=digest, variant="tall")
+    assert read_bundle(_bundle(tmp_path, linear="fp8_static", **kw))["variant"] == "tall"
+    with pytest.raises(ValueError):
+        read_bundle(_bundle(tmp_path, linear="fp8", **kw))
+    with pytest.raises(ValueError):
+        read_bundle(_bundle(tmp_path, linear="fp8_static", **dict(kw, variant="wide")))
+
+
+def test_set_bound_matches_reference_select():
+    """select's per-op update (_family/night_runtime.py:52-54) on a host-side
+    op: inverse_scale = 448/bound, input_scale refilled in place with bound/448;
+    apply_profile names the first missing entry."""
+    import types
+    import torch
+    from fastforward_amd.linear import StaticFP8Linear
+    from fastforward_amd.profiles import apply_profile
+    op = object.__new__(StaticFP8Linear)
+    op.input_scale = torch.zeros(1)
+    buf = op.input_scale
+    op.set_bound(7.0)
+    assert op.inverse_scale == 448.0 / 7.0 and op.input_scale is buf
+    assert float(op.input_scale[0]) == float(torch.tensor(7.0 / 448.0))
+    layer = types.SimpleNamespace(qkv=op, o=op, gateup=op, down=op)
+    w = types.SimpleNamespace(layers=[layer])
+    assert apply_profile(w, {"0:qkv": 2.0, "0:output": 3.0, "0:gateup": 4.0, "0:down": 5.0}) == 4
+    assert op.inverse_scale == 448.0 / 5.0
+    with pytest.raises(KeyError):
+        apply_profile(w, {"0:qkv": 2.0})
+
+
+@pytest.mark.gpu
+def test_select_switches_static_fp8_variants(gpu, tmp_path):
+    """A static-FP8 bundle with two calibration variants: each select gives the
+    eager step of that calibration bit for bit through a re-captured graph,
+    and selecting the first variant again restores its logits exactly."""
+    import torch
+    from fastforward_amd.profiles import apply_profile
+    from fastforward_amd.runtime import Runtime
+    from fastforward_amd.synthetic import make_request
+    p, digest = _profile(tmp_path, {"a": 6.0, "b": 14.0})
+    acc = Accelerator(_bundle(tmp_path, linear="fp8_static", profile_path=str(p), profile_sha256=digest,
+                              variant="a"))
+    ids, _, _ = make_request(acc.cfg, 300, 16, 16, seed=5, real_tokens=300)
+    ids = torch.as_tensor(ids)[:300]
+    za, cap = acc.graphs.run(ids, 299, 4)
+    za = za.cpu()
+    assert cap
+    acc.select("b")
+    zb, cap = acc.graphs.run(ids, 299, 4)
+    zb = zb.cpu()
+    assert cap and not torch.equal(za, zb)
+    eager = Runtime(acc.cfg, acc.weights, 320)
+    eager.set_inputs(ids, acc.graphs.positions(320), 299)
+    assert torch.equal(eager.step()[:4].cpu(), zb)
+    acc.select("a")
+    assert torch.equal(acc.graphs.run(ids, 299, 4)[0].cpu(), za)
+    with pytest.raises(ValueError):
+        acc.select("c")
