@@ -337,7 +337,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void attention_decode_kernel(
 // tiles of 16 queries from row set w / HPW. Each 64-key block of K
 // (64 x 256 B) and V^T (128 x 128 B) is fetched once per workgroup into LDS
 // with global_load_lds_dwordx4 (one 1 KB instruction = 8 rows x 128 B, whole
-// cache lines), three stages deep with two in flight, and every fragment read
+// cache lines), NS stages deep with NS-1 in flight (NS = 3: one workgroup per
+// CU, 96 KB LDS; NS = 2: two per CU, 64 KB each), and every fragment read
 // from LDS feeds QT MFMAs.
 //
 // LDS stage layout (32 KB): K at [0, 16 KB), V^T at [16 KB, 32 KB), each as
@@ -351,13 +352,13 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void attention_decode_kernel(
 // Grid: one dimension, heaviest query blocks first across all groups; the
 // group is blockIdx % (hq/HPW), so with 8 XCDs taking workgroups round-robin
 // the groups of one kv head stay on one XCD (and its L2).
-template <int QT, int HPW>
-__global__ __launch_bounds__(kThreads, 1) void attention_prefill_kernel(
+template <int QT, int HPW, int NS>
+__global__ __launch_bounds__(kThreads, NS == 2 ? 2 : 1) void attention_prefill_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ vt,
     bf16_t* __restrict__ y, int s_len, int t, int t_pad, int hq, int hk, float c2, int nqb) {
   constexpr int QB = 16 * QT * (4 / HPW);
   constexpr int STAGE = 32 * 1024;
-  constexpr int NS = 3;
+  static_assert(NS == 2 || NS == 3, "two or three K/V stages");
   __shared__ __align__(1024) uint8_t smem[NS * STAGE];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r16 = lane & 15, g = lane >> 4;
@@ -420,11 +421,11 @@ __global__ __launch_bounds__(kThreads, 1) void attention_prefill_kernel(
     for (int dt = 0; dt < 8; ++dt) o[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // The first two key blocks and the queries load together. The queries are
+  // The first NS-1 key blocks and the queries load together. The queries are
   // waited for before the loop: a compiler-placed wait for them inside the
   // loop would also wait for the prefetches issued there.
   issue(0, 0);
-  if (nblocks > 1) issue(64, 1);
+  if (NS == 3 && nblocks > 1) issue(64, 1);
   u32x4 qf[QT][4];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
@@ -440,10 +441,10 @@ __global__ __launch_bounds__(kThreads, 1) void attention_prefill_kernel(
     for (int st = 0; st < 4; ++st)
       asm volatile("" : : "v"(qf[qt][st].x), "v"(qf[qt][st].y), "v"(qf[qt][st].z), "v"(qf[qt][st].w));
   for (int ib = 0; ib < nblocks; ++ib) {
-    if (ib + 1 < nblocks) wait_vmcnt<8>();
+    if (NS == 3 && ib + 1 < nblocks) wait_vmcnt<8>();
     else wait_vmcnt<0>();
     barrier_lds();  // block ib landed for every wave; block ib-1 fully consumed
-    if (ib + 2 < nblocks) issue((ib + 2) * 64, (ib + 2) % NS);
+    if (ib + NS - 1 < nblocks) issue((ib + NS - 1) * 64, (ib + NS - 1) % NS);
     const int kb = ib * 64;
     if (kb >= s_len || kb > wq0 + 16 * QT - 1) continue;  // wave-uniform: no query of the wave sees it
     const uint8_t* st_base = smem + (ib % NS) * STAGE;
@@ -572,17 +573,28 @@ extern "C" int ff_attention_vt(const void* q, const void* k, const void* vt, con
       return e ? atoi(e) : 0;
     }();
     const int qt = (qt_env == 1 || qt_env == 2 || qt_env == 4) ? qt_env : (s <= 1024 ? 1 : (s <= 2048 ? 2 : 4));
+    // FF_ATTN_NS=<2|3> overrides the number of K/V LDS stages (tuning).
+    static const int ns_env = [] {
+      const char* e = getenv("FF_ATTN_NS");
+      return e ? atoi(e) : 0;
+    }();
+    // Two stages run at two workgroups per CU, which fits the registers of
+    // QT <= 2 only (QT = 4 would spill); at QT = 1 the 8B prefill (576 tokens,
+    // 32/8 heads) takes 12.9 us with two stages and 15.2 us with three.
+    const int ns = qt <= 2 && ns_env != 3 ? 2 : 3;
     const int qb = 16 * qt * (4 / hpw);
     const int nqb = (int)((s + qb - 1) / qb);
     const dim3 grid((unsigned)(nqb * (hq / hpw))), block(kThreads);
-#define FF_PREFILL(QT, HPW)                                                                                  \
-  if (qt == QT && hpw == HPW)                                                                                \
-    hipLaunchKernelGGL((attention_prefill_kernel<QT, HPW>), grid, block, 0, st, (const bf16_t*)q,            \
+#define FF_PREFILL(QT, HPW, NS)                                                                              \
+  if (qt == QT && hpw == HPW && ns == NS)                                                                    \
+    hipLaunchKernelGGL((attention_prefill_kernel<QT, HPW, NS>), grid, block, 0, st, (const bf16_t*)q,        \
                        (const bf16_t*)k, (const bf16_t*)vt, (bf16_t*)y, (int)s, (int)t, (int)t_pad, (int)hq, \
                        (int)hk, c2, nqb);
-    FF_PREFILL(1, 4) FF_PREFILL(2, 4) FF_PREFILL(4, 4)
-    FF_PREFILL(1, 2) FF_PREFILL(2, 2) FF_PREFILL(4, 2)
-    FF_PREFILL(1, 1) FF_PREFILL(2, 1) FF_PREFILL(4, 1)
+#define FF_PREFILL_NS(QT, HPW) FF_PREFILL(QT, HPW, 2) FF_PREFILL(QT, HPW, 3)
+    FF_PREFILL_NS(1, 4) FF_PREFILL_NS(2, 4) FF_PREFILL(4, 4, 3)
+    FF_PREFILL_NS(1, 2) FF_PREFILL_NS(2, 2) FF_PREFILL(4, 2, 3)
+    FF_PREFILL_NS(1, 1) FF_PREFILL_NS(2, 1) FF_PREFILL(4, 1, 3)
+#undef FF_PREFILL_NS
 #undef FF_PREFILL
     FF_LAUNCH_CHECK("ff_attention_vt");
     return FF_OK;
