@@ -78,7 +78,7 @@ def gemm_buffers(cfg, role, n, m, T):
 def launch_gemm(cfg, role, lw, q, s, m, b):
     """One FP8 GEMM launch as the step issues it: the QKV projection with its
     q/k norm + rotary + V^T epilogue (ff_gemm_fp8_qkv), the gate/up projection
-    with its SwiGLU epilogue (ff_gemm_fp8_swiglu), o and down plain ff_gemm_fp8
+    with its SwiGLU epilogue (ff_gemm_fp8_swiglu_pk: packed weights), o and down plain ff_gemm_fp8
     (which takes the GEMV kernels for the tail's single row)."""
     from fastforward_amd._lib import call, ptr, stream
     op = getattr(lw, role)
@@ -89,8 +89,8 @@ def launch_gemm(cfg, role, lw, q, s, m, b):
              float(lw.k_norm.variance_epsilon), ptr(b["cos"]), ptr(b["sin"]), ptr(b["yq"]), ptr(b["yk"]),
              ptr(b["vt"]), b["Tp"], stream())
     elif role == "gateup":
-        call("ff_gemm_fp8_swiglu", ptr(q), ptr(s), ptr(op.weight), ptr(op.scale), ptr(b["out"]), n // 2,
-             ptr(b["pmax"]), m, n // 2, k, stream())
+        call("ff_gemm_fp8_swiglu_pk", ptr(q), ptr(s), ptr(op.weight), ptr(op.packed), ptr(op.scale), ptr(b["out"]),
+             n // 2, ptr(b["pmax"]), m, n // 2, k, stream())
     else:
         op.gemm(q[:m], s[:m], b["out"])
 
@@ -288,6 +288,9 @@ def main():
     grid = (16, 32) if T >= 576 else (16, 16)
     log(f"building {cfg.name} fp8 (random init, seed 0)")
     w = make_model(cfg, mode=args.linear if args.profile else "fp8", seed=0, n_options=8)
+    for L in w.layers:
+        if hasattr(L.gateup, "pack"):
+            L.gateup.pack()  # as Runtime does: the gate/up tile kernel reads the packed copy
     ids, pos, pick = make_request(cfg, T, *grid, seed=0)
     if args.kernels:
         kernel_pass(cfg, w, T)

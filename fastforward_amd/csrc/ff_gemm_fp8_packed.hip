@@ -1,0 +1,335 @@
+// FP8 (e4m3fn) gate/up GEMM + SwiGLU on fragment-packed weights, for gfx950.
+//
+// Same arithmetic as ff_gemm_fp8_swiglu (one v_mfma_f32_16x16x128_f8f6f4 per
+// 128-byte k step into the same fp32 accumulator, k steps in order, then
+// bf16((acc * sa) * sw) and bf16(bf16(silu(g)) * u)), so the two produce
+// identical bits. What differs is how the operands reach the matrix cores:
+//
+// * Weights are repacked once at setup (ff_pack_weight_fp8) so that the MFMA
+//   operand of one 16-row x 128-byte fragment is 2 KB contiguous, lane l's 32
+//   bytes at 32 l. Each wave loads its weight fragments with buffer loads
+//   straight into the operand registers: every load instruction moves 1 KB of
+//   whole cache lines, and no LDS traffic or barrier is spent on the weights.
+// * A workgroup of 4 waves owns BM tokens x BN = 4 CW weight rows; wave w owns
+//   all BM tokens x CW rows, so each A fragment read from LDS feeds CW/16 MFMAs
+//   (0.33 KB of LDS reads per MFMA at 144 x 96, a third of a 64 x 64 wave tile).
+//   For the SwiGLU pairing waves 0-1 take BN/2 gate rows and waves 2-3 the
+//   matching up rows.
+// * Activations go global -> registers -> LDS (D steps of register staging,
+//   2G LDS stages, one barrier per G steps). Every load is an ordinary
+//   compiler-visible buffer load, so the compiler's wait counts are exact
+//   partial waits; the prologue issues its loads in the loop's own order so the
+//   loop entry needs no full drain.
+// * Inside a k step the MFMAs run weight fragment by weight fragment, and each
+//   weight fragment is refilled for step k + P as soon as its last MFMA has
+//   been issued.
+// * The MFMA is issued from inline asm with the accumulator tied ("+a"): the
+//   compiler otherwise gives this gfx950 instruction distinct source and
+//   destination AGPRs in an unrolled loop and copies every accumulator back at
+//   the loop edge. The hazards the compiler no longer sees are covered by
+//   s_nop: after the accumulators are zeroed, and after the last MFMA before
+//   the epilogue reads them (ACC_NOPS).
+//
+// Packed layout (ff_pack_weight_fp8): fragment (f, kt) of rows [16 f, 16 f + 16)
+// and k bytes [128 kt, 128 kt + 128) is the 2048 bytes at (f * K/128 + kt) * 2048;
+// lane l = 16 g + r holds row 16 f + r, k bytes [128 kt + 32 g, +32) at 32 l.
+// That is the operand layout of the MFMA for both A and B (the row-major
+// kernels feed the same k range to the same lane).
+#include <stdio.h>
+#include <type_traits>
+
+#include "ff_common.h"
+
+using namespace ff;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kXcds = 8;
+
+typedef int i32x4v __attribute__((ext_vector_type(4)));
+
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+constexpr int lcm3(int a, int b, int c) {
+  int l = a;
+  while (l % b || l % c) l += a;
+  return l;
+}
+
+// Raw buffer resource over `bytes` bytes (stride 0, 32-bit data format).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ i32x4v bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+}
+
+// acc += A . B^T for one 16 x 16 x 128 e4m3 tile, accumulator tied in place.
+__device__ __forceinline__ void mfma_acc(f32x4& acc, const i32x8& a, const i32x8& b) {
+  asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+__global__ __launch_bounds__(kThreads) void pack_fp8_kernel(const uint8_t* __restrict__ w, uint8_t* __restrict__ p,
+                                                            int64_t n, int64_t k) {
+  const int64_t kt_n = k / 128;
+  const int64_t lanes = (n / 16) * kt_n * 64;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < lanes; i += (int64_t)gridDim.x * blockDim.x) {
+    const int l = (int)(i & 63);
+    const int64_t f = i >> 6;  // fragment index f16 * kt_n + kt
+    const int64_t kt = f % kt_n, f16 = f / kt_n;
+    const int64_t row = f16 * 16 + (l & 15);
+    const u32x4* src = reinterpret_cast<const u32x4*>(w + row * k + kt * 128 + 32 * (l >> 4));
+    u32x4* dst = reinterpret_cast<u32x4*>(p + f * 2048 + 32 * l);
+    dst[0] = src[0];
+    dst[1] = src[1];
+  }
+}
+
+// BM tokens x (BN/2 gate + BN/2 up channels), BN = 4 CW; P = weight register
+// stages, D = activation register stages, G = k steps per barrier.
+template <int BM, int CW, int P, int D, int G>
+__global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
+    const uint8_t* __restrict__ qa, const float* __restrict__ sa, const uint8_t* __restrict__ qwp,
+    const float* __restrict__ sw, bf16_t* __restrict__ h, int64_t ldh, float* __restrict__ pmax, int M, int half,
+    int K, int tiles_m, int tiles_n) {
+  constexpr int BN = 4 * CW, CH = BN / 2;
+  constexpr int RA = BM / 16, TJ = CW / 16;
+  constexpr int A_CHUNKS = BM * 8;  // 16-byte chunks of one A stage
+  constexpr int FULL = A_CHUNKS / kThreads, REM = A_CHUNKS % kThreads;
+  constexpr int NA = FULL + (REM ? 1 : 0);
+  constexpr int STAGE = BM * 128;
+  constexpr int NB = 2 * G;
+  constexpr int EPI_LD = BN + 8;  // bf16 pitch of the epilogue tile
+  constexpr int SMEM = NB * STAGE > BM * EPI_LD * 2 ? NB * STAGE : BM * EPI_LD * 2;
+  constexpr int U = lcm3(P, D, NB);  // k steps per unrolled loop iteration
+  constexpr int CPR = CH / 8;        // 8-channel chunks per row in the SwiGLU pass
+  static_assert(SMEM <= 160 * 1024, "LDS budget");
+  static_assert(A_CHUNKS >= kThreads, "at least one full activation round");
+  static_assert(CH == 2 * CW, "waves 0-1 take the gate rows, waves 2-3 the up rows");
+  static_assert(CH % 64 == 0 && (BM * CPR) % 64 == 0, "64-channel row maxima over whole waves");
+  __shared__ __align__(1024) uint8_t smem[SMEM];
+
+  const int nblk = tiles_m * tiles_n;
+  const int b = blockIdx.x;
+  int logical = b;
+  if (nblk % kXcds == 0) logical = (b % kXcds) * (nblk / kXcds) + b / kXcds;  // one XCD walks a tile range
+  const int tm = logical % tiles_m, tn = logical / tiles_m;                    // M fastest: L2 shares weights
+  const int m0 = tm * BM;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int KT = K / 128;
+
+  // Activations: chunk c = tid + 256 i is row c / 8, 16-byte chunk c % 8; a
+  // partial last round is moved back over the last 256 chunks (the overlap is
+  // loaded and stored twice with the same bytes), so nothing is predicated.
+  // LDS stage layout as the row-major kernel: 1 KB blocks of 8 rows x 128 B,
+  // chunk c of row r at slot c ^ ((r % 16) / 2).
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(qa, (uint32_t)M * (uint32_t)K);
+  uint32_t voffA[NA];
+  int dstA[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int c = i < FULL ? tid + kThreads * i : A_CHUNKS - kThreads + tid;
+    const int row = c >> 3, ch = c & 7;
+    voffA[i] = (uint32_t)min(m0 + row, M - 1) * (uint32_t)K + 16 * ch;
+    dstA[i] = (row >> 3) * 1024 + 128 * (row & 7) + 16 * (ch ^ ((row & 15) >> 1));
+  }
+  i32x4v ast[D][NA];  // ext-vector elements: an array of structs would be kept in scratch
+  auto loadA = [&](int kt, auto SLOT) {
+    constexpr int slot = decltype(SLOT)::value;
+    static_for<0, NA>([&](auto I_) {
+      constexpr int i = decltype(I_)::value;
+      ast[slot][i] = bload16(rA, voffA[i], (uint32_t)kt * 128);
+    });
+  };
+  auto writeA = [&](auto SLOT, auto BUF) {
+    constexpr int slot = decltype(SLOT)::value, buf = decltype(BUF)::value;
+    static_for<0, NA>([&](auto I_) {
+      constexpr int i = decltype(I_)::value;
+      *reinterpret_cast<i32x4v*>(smem + buf * STAGE + dstA[i]) = ast[slot][i];
+    });
+  };
+
+  // Weights: fragment j of this wave is the 16-row group of weight row
+  // (gate half for waves 0-1, up half for waves 2-3) + channel.
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(qwp, (uint32_t)(2 * half) * (uint32_t)K);
+  const uint32_t voffB = 32u * (uint32_t)lane;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  uint32_t sB[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int cl = wave_s * CW + 16 * j;  // tile column
+    const int row = cl < CH ? tn * CH + cl : half + tn * CH + (cl - CH);
+    sB[j] = (uint32_t)(row / 16) * (uint32_t)KT * 2048u;
+  }
+  i32x8 bq[P][TJ];
+  auto loadB = [&](int kt, auto SLOT) {
+    constexpr int slot = decltype(SLOT)::value;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const i32x4v lo = bload16(rB, voffB, sB[j] + (uint32_t)kt * 2048u);
+      const i32x4v hi = bload16(rB, voffB + 16u, sB[j] + (uint32_t)kt * 2048u);
+      bq[slot][j] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    }
+  };
+
+  f32x4 acc[RA][TJ];
+#pragma unroll
+  for (int i = 0; i < RA; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // ACC_PIN: every accumulator through an asm barrier (each is zeroed before it).
+  // ACC_NOPS: wait states between VALU writes / MFMA results and their readers.
+#define ACC_PIN()                                     \
+  do {                                                \
+    _Pragma("unroll") for (int i_ = 0; i_ < RA; ++i_) \
+    _Pragma("unroll") for (int j_ = 0; j_ < TJ; ++j_) \
+      asm volatile("" : "+a"(acc[i_][j_]));           \
+  } while (0)
+#define ACC_NOPS() asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(acc[RA - 1][TJ - 1]))
+  ACC_PIN();
+  ACC_NOPS();
+
+  // Prologue: LDS stages 0..G-1 = steps 0..G-1, staging slots = steps G..G+D-1,
+  // weight stages = steps 0..P-1, issued in the loop's order (A, then B).
+  using I0 = std::integral_constant<int, 0>;
+  static_for<0, G>([&](auto S_) {
+    constexpr int s = decltype(S_)::value;
+    loadA(min(s, KT - 1), I0{});
+    writeA(I0{}, std::integral_constant<int, s>{});
+  });
+  static_for<0, (D > P ? D : P)>([&](auto S_) {
+    constexpr int s = decltype(S_)::value;
+    if constexpr (s < D) loadA(min(G + s, KT - 1), std::integral_constant<int, (G + s) % D>{});
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (s < P) loadB(min(s, KT - 1), std::integral_constant<int, s>{});
+    __builtin_amdgcn_sched_barrier(0);
+  });
+
+  const int frag = 128 * (r16 & 7) + 1024 * (r16 >> 3);
+  const int c0 = 16 * ((2 * g) ^ (r16 >> 1)), c1 = 16 * ((2 * g + 1) ^ (r16 >> 1));
+  for (int kb = 0; kb < KT; kb += U) {
+    static_for<0, U>([&](auto U_) {
+      constexpr int u = decltype(U_)::value;
+      const int kt = kb + u;
+      // One barrier per G steps: this group's stages (written during the previous
+      // group) are visible, and the previous group's stages, overwritten below
+      // with steps kt + G.., are no longer read.
+      if constexpr (u % G == 0) __syncthreads();
+      writeA(std::integral_constant<int, (u + G) % D>{}, std::integral_constant<int, (u + G) % NB>{});
+      loadA(min(kt + G + D, KT - 1), std::integral_constant<int, (u + G) % D>{});
+      const uint8_t* st = smem + (u % NB) * STAGE + frag;
+      i32x8 af[RA];
+#pragma unroll
+      for (int i = 0; i < RA; ++i) {
+        const i32x4v lo = *reinterpret_cast<const i32x4v*>(st + 2 * i * 1024 + c0);
+        const i32x4v hi = *reinterpret_cast<const i32x4v*>(st + 2 * i * 1024 + c1);
+        af[i] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      }
+      const uint32_t ktn = (uint32_t)min(kt + P, KT - 1);
+      static_for<0, TJ>([&](auto J_) {
+        constexpr int j = decltype(J_)::value;
+#pragma unroll
+        for (int i = 0; i < RA; ++i) mfma_acc(acc[i][j], af[i], bq[u % P][j]);
+        const i32x4v lo = bload16(rB, voffB, sB[j] + ktn * 2048u);
+        const i32x4v hi = bload16(rB, voffB + 16u, sB[j] + ktn * 2048u);
+        bq[u % P][j] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      });
+    });
+  }
+  ACC_NOPS();
+  ACC_PIN();
+#undef ACC_PIN
+#undef ACC_NOPS
+  __syncthreads();  // every wave is done with the stages; the tile reuses the LDS
+
+  // y = bf16((acc * sa) * sw) as a row-major tile: gate channels in columns
+  // [0, CH), the matching up channels in [CH, BN).
+  bf16_t* tile = reinterpret_cast<bf16_t*>(smem);
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int cl = wave * CW + 16 * j + r16;
+    const int row = cl < CH ? tn * CH + cl : half + tn * CH + (cl - CH);
+    const float swv = sw[row];
+#pragma unroll
+    for (int i = 0; i < RA; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int rl = 16 * i + 4 * g + r;
+        const float sav = sa[min(m0 + rl, M - 1)];
+        tile[rl * EPI_LD + cl] = (bf16_t)f32_to_bf16((acc[i][j][r] * sav) * swv);
+      }
+  }
+  __syncthreads();
+  // SwiGLU, 8 channels per thread; the 8 lanes of one row's 64-channel block are
+  // 8 consecutive lanes, which reduce its max |h| for ff_quant_rows_pmax.
+  const int c_base = tn * CH;
+  const int64_t npart = half / 64;
+  for (int c = tid; c < BM * CPR; c += kThreads) {
+    const int rl = c / CPR, cc = (c % CPR) * 8;
+    float gv[8], uv[8], hv[8];
+    unpack8(*reinterpret_cast<const u32x4*>(tile + rl * EPI_LD + cc), gv);
+    unpack8(*reinterpret_cast<const u32x4*>(tile + rl * EPI_LD + CH + cc), uv);
+    float mx = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      hv[e] = round_bf16(round_bf16(silu(gv[e])) * uv[e]);
+      mx = fmaxf(mx, fabsf(hv[e]));
+    }
+    mx = fmaxf(mx, dpp<kDppXor1>(mx));
+    mx = fmaxf(mx, dpp<kDppXor2>(mx));
+    mx = fmaxf(mx, dpp<kDppHalfMirror>(mx));
+    const int m = m0 + rl;
+    if (m < M) {
+      *reinterpret_cast<u32x4*>(h + (int64_t)m * ldh + c_base + cc) = pack8(hv);
+      if (cc % 64 == 0) pmax[(int64_t)m * npart + (c_base + cc) / 64] = mx;
+    }
+  }
+}
+
+// The configuration measured for the 8B gate/up shape (576 x 4096 x 2 x 12288):
+// 144 x 384 tiles, one workgroup per CU (4 x 64 = 256 workgroups).
+constexpr int kPkBM = 144, kPkCW = 96, kPkP = 2, kPkD = 2, kPkG = 2;
+constexpr int kPkCH = 2 * kPkCW;
+constexpr int kPkKAlign = 128 * lcm3(kPkP, kPkD, 2 * kPkG);  // k multiple of the unrolled k steps
+
+}  // namespace
+
+extern "C" int ff_pack_weight_fp8(const void* w, void* packed, int64_t n, int64_t k, ff_stream_t stream) {
+  FF_REQUIRE(w && packed, "ff_pack_weight_fp8: null pointer");
+  FF_REQUIRE(n > 0 && n % 16 == 0 && k > 0 && k % 128 == 0 && n * k < (int64_t(1) << 40),
+             "ff_pack_weight_fp8: bad sizes (n %% 16, k %% 128)");
+  FF_REQUIRE(ff_aligned(w, 16) && ff_aligned(packed, 16), "ff_pack_weight_fp8: alignment");
+  const int64_t lanes = (n / 16) * (k / 128) * 64;
+  const int64_t blocks = (lanes + kThreads - 1) / kThreads;
+  hipLaunchKernelGGL(pack_fp8_kernel, dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const uint8_t*)w, (uint8_t*)packed, n, k);
+  FF_LAUNCH_CHECK("ff_pack_weight_fp8");
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_fp8_swiglu_pk(const void* qa, const float* sa, const void* qw, const void* qw_packed,
+                                     const float* sw, void* h, int64_t ldh, float* pmax, int64_t m, int64_t i,
+                                     int64_t k, ff_stream_t stream) {
+  FF_REQUIRE(qa && sa && qw && sw && h && pmax, "ff_gemm_fp8_swiglu_pk: null pointer");
+  const int64_t tiles_m = (m + kPkBM - 1) / kPkBM, tiles_n = i / kPkCH;
+  const bool packed_fits = qw_packed && m > 4 && i % kPkCH == 0 && k % kPkKAlign == 0 && ldh % 8 == 0 &&
+                           ldh >= i && m * k < (int64_t(1) << 31) && 2 * i * k < (int64_t(1) << 31) &&
+                           tiles_m * tiles_n >= 192 && ff_aligned(qa, 16) && ff_aligned(qw_packed, 16) &&
+                           ff_aligned(h, 16);
+  if (!packed_fits) return ff_gemm_fp8_swiglu(qa, sa, qw, sw, h, ldh, pmax, m, i, k, stream);
+  hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<kPkBM, kPkCW, kPkP, kPkD, kPkG>),
+                     dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads), 0, (hipStream_t)stream,
+                     (const uint8_t*)qa, sa, (const uint8_t*)qw_packed, sw, (bf16_t*)h, ldh, pmax, (int)m, (int)i,
+                     (int)k, (int)tiles_m, (int)tiles_n);
+  FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu_pk");
+  return FF_OK;
+}

@@ -51,6 +51,16 @@ class FP8Linear:
         scale = torch.empty((n,), device=w.device, dtype=torch.float32)
         call("ff_quant_weight_fp8", ptr(w), ptr(self.weight), ptr(scale), None, n, k, 1, stream())
         self.scale = scale.reshape(1, n)
+        self.packed = None
+
+    def pack(self):
+        """Add the MFMA-fragment copy of the weight (ff_pack_weight_fp8) that the
+        gate/up tile kernel reads; ``weight`` stays row-major for every other path."""
+        n, k = self.weight.shape
+        if self.packed is None and n % 16 == 0 and k % 128 == 0:
+            self.packed = torch.empty_like(self.weight)
+            call("ff_pack_weight_fp8", ptr(self.weight), ptr(self.packed), n, k, stream())
+        return self
 
     def quantize(self, x):
         """Per-token e4m3 codes and scales of x (2-D view, bf16)."""

@@ -122,6 +122,9 @@ class Runtime:
         self.path = path or ("fused" if fp8 else "generic")
         if self.path == "fused" and not fp8:
             raise ValueError("the fused path needs FP8Linear (per-token / per-channel) weights")
+        if self.path == "fused":
+            for L in weights.layers:
+                L.gateup.pack()  # MFMA-fragment copy for the gate/up tile kernel (once per weight)
         T, H, D = tokens, cfg.hidden, cfg.head_dim
         HQ, HK, I = cfg.heads, cfg.kv_heads, cfg.inter
         e = lambda *s, dt=BF16: torch.empty(s, device=dev, dtype=dt)  # noqa: E731
@@ -254,8 +257,8 @@ class Runtime:
     def _mlp_fused(self, lw, q, sc, m, out, s):
         I, H = self.cfg.inter, self.cfg.hidden
         # gate/up GEMM with SwiGLU in its epilogue, then per-token quant from its row maxima
-        call("ff_gemm_fp8_swiglu", ptr(q), ptr(sc), ptr(lw.gateup.weight), ptr(lw.gateup.scale), ptr(self.hm), I,
-             ptr(self.pmax), m, I, H, s)
+        call("ff_gemm_fp8_swiglu_pk", ptr(q), ptr(sc), ptr(lw.gateup.weight), ptr(lw.gateup.packed),
+             ptr(lw.gateup.scale), ptr(self.hm), I, ptr(self.pmax), m, I, H, s)
         call("ff_quant_rows_pmax", ptr(self.hm), I, ptr(self.pmax), I // 64, ptr(self.mq), ptr(self.ms), m, I, s)
         call("ff_gemm_fp8", ptr(self.mq), ptr(self.ms), 1, ptr(lw.down.weight), ptr(lw.down.scale), 1, ptr(out), H,
              m, H, I, s)

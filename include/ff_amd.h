@@ -154,6 +154,24 @@ int ff_gemm_fp8(const void* qa, const float* sa, int sa_rows, const void* qw, co
 int ff_gemm_fp8_swiglu(const void* qa, const float* sa, const void* qw, const float* sw, void* h,
                        int64_t ldh, float* pmax, int64_t m, int64_t i, int64_t k, ff_stream_t stream);
 
+/* Setup-time repack of e4m3 weights w (n, k) row-major into the MFMA fragment
+ * layout read by ff_gemm_fp8_swiglu_pk (no reference counterpart: a storage
+ * layout of this library): fragment (f, kt), rows [16 f, 16 f + 16) x k bytes
+ * [128 kt, 128 kt + 128), is the 2048 bytes at (f * k/128 + kt) * 2048; lane
+ * l = 16 g + r holds row 16 f + r, k bytes [128 kt + 32 g, +32) at 32 l.
+ * packed holds n * k bytes. n % 16 == 0, k % 128 == 0. */
+int ff_pack_weight_fp8(const void* w, void* packed, int64_t n, int64_t k, ff_stream_t stream);
+
+/* ff_gemm_fp8_swiglu with an optional packed copy of the same weight
+ * (ff_pack_weight_fp8 of qw): identical results (same products and summation
+ * order); when qw_packed is given and the shape suits it (i % 192 == 0,
+ * k % 512 == 0, m > 4, enough 144 x 384 tiles to fill the GPU) the weights are
+ * read from the packed copy straight into the matrix-core operands, otherwise
+ * this is ff_gemm_fp8_swiglu on qw. */
+int ff_gemm_fp8_swiglu_pk(const void* qa, const float* sa, const void* qw, const void* qw_packed,
+                          const float* sw, void* h, int64_t ldh, float* pmax, int64_t m, int64_t i, int64_t k,
+                          ff_stream_t stream);
+
 /* Fused QKV GEMM + q/k norm + rotary + V transpose (no reference counterpart as
  * one op; the same arithmetic as ff_gemm_fp8 on the packed QKV weight followed
  * by ff_qkv_post): qw ((hq + 2 hk) * 128, k) e4m3 with per-row scales sw, qa (m, k)

@@ -310,6 +310,49 @@ def test_gemm_fp8_swiglu_equals_unfused(gpu, m, i, k):
     assert torch.equal(q1, q2) and torch.equal(s1, s2)
 
 
+def test_pack_weight_fp8_layout(gpu):
+    """ff_pack_weight_fp8 stores fragment (f, kt) at (f * k/128 + kt) * 2048 with
+    lane l = 16 g + r holding row 16 f + r, k bytes [128 kt + 32 g, +32) at 32 l."""
+    from fastforward_amd._lib import call, ptr, stream
+    n, k = 48, 384
+    w = torch.randint(0, 256, (n, k), generator=_g(50), dtype=torch.uint8)
+    p = torch.empty(n * k, device=DEV, dtype=torch.uint8)
+    w_d = w.to(DEV)
+    call("ff_pack_weight_fp8", ptr(w_d), ptr(p), n, k, stream())
+    got = p.cpu().numpy().reshape(n // 16, k // 128, 64, 32)
+    wn = w.numpy()
+    for f in range(n // 16):
+        for kt in range(k // 128):
+            for lane in range(64):
+                r, g = lane % 16, lane // 16
+                assert np.array_equal(got[f, kt, lane], wn[16 * f + r, 128 * kt + 32 * g: 128 * kt + 32 * g + 32])
+
+
+@pytest.mark.parametrize("m,i,k", [(576, 12288, 4096), (300, 12288, 2048), (433, 6144, 4096), (3, 12288, 4096),
+                                   (576, 4096, 4096)])
+def test_gemm_fp8_swiglu_packed_equals_rowmajor(gpu, m, i, k):
+    """The gate/up GEMM on the packed weight copy (144 x 384 tiles, weights
+    straight into the MFMA operands) gives the same bits as ff_gemm_fp8_swiglu on
+    the row-major weight, SwiGLU output and row maxima, including a ragged last
+    token tile; shapes it does not take (3 rows, i % 192 != 0, too few tiles)
+    go to the row-major kernels."""
+    from fastforward_amd._lib import call, ptr, stream
+    from fastforward_amd.linear import FP8Linear
+    x = (torch.randn(m, k, generator=_g(51)) * 2).to(BF16).to(DEV)
+    op = FP8Linear((torch.randn(2 * i, k, generator=_g(52)) * 0.05).to(BF16).to(DEV)).pack()
+    qa, sa = op.quantize(x)
+    outs = []
+    for entry in ("ff_gemm_fp8_swiglu", "ff_gemm_fp8_swiglu_pk"):
+        h = torch.full((m, i), float("nan"), device=DEV, dtype=BF16)
+        pmax = torch.full((m, i // 64), float("nan"), device=DEV)
+        args = [ptr(qa), ptr(sa), ptr(op.weight)] + ([ptr(op.packed)] if entry.endswith("pk") else [])
+        call(entry, *args, ptr(op.scale), ptr(h), i, ptr(pmax), m, i, k, stream())
+        outs.append((h, pmax))
+    (h0, p0), (h1, p1) = outs
+    assert not torch.isnan(h0.float()).any()
+    assert torch.equal(h0, h1) and torch.equal(p0, p1)
+
+
 def test_gemm_fp8_static_scalars(gpu):
     from fastforward_amd.linear import StaticFP8Linear
     m, k, n = 576, 4096, 4096
