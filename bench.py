@@ -288,9 +288,10 @@ def main():
     grid = (16, 32) if T >= 576 else (16, 16)
     log(f"building {cfg.name} fp8 (random init, seed 0)")
     w = make_model(cfg, mode=args.linear if args.profile else "fp8", seed=0, n_options=8)
-    for L in w.layers:
-        if hasattr(L.gateup, "pack"):
-            L.gateup.pack()  # as Runtime does: the gate/up tile kernel reads the packed copy
+    for L in w.layers:  # as Runtime does: the packed tile kernels read these copies
+        for op in (L.o, L.gateup, L.down):
+            if hasattr(op, "pack"):
+                op.pack()
     ids, pos, pick = make_request(cfg, T, *grid, seed=0)
     if args.kernels:
         kernel_pass(cfg, w, T)

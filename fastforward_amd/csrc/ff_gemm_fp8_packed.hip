@@ -93,39 +93,27 @@ __global__ __launch_bounds__(kThreads) void pack_fp8_kernel(const uint8_t* __res
   }
 }
 
-// BM tokens x (BN/2 gate + BN/2 up channels), BN = 4 CW; P = weight register
-// stages, D = activation register stages, G = k steps per barrier.
+// Main loop shared by the kernels below: acc (BM x 4 CW tile of this
+// workgroup, wave w owning all BM rows x CW weight rows) = sum over k steps
+// [kt0, kt0 + nk) of A . B^T. sB[j] is the byte offset of this wave's weight
+// fragment row j at k step 0. P = weight register stages, D = activation
+// register stages, G = k steps per barrier; nk % lcm(P, D, 2G) == 0.
 template <int BM, int CW, int P, int D, int G>
-__global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
-    const uint8_t* __restrict__ qa, const float* __restrict__ sa, const uint8_t* __restrict__ qwp,
-    const float* __restrict__ sw, bf16_t* __restrict__ h, int64_t ldh, float* __restrict__ pmax, int M, int half,
-    int K, int tiles_m, int tiles_n) {
-  constexpr int BN = 4 * CW, CH = BN / 2;
+__device__ __forceinline__ void pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], uint8_t* smem,
+                                            const uint8_t* __restrict__ qa, int M, int K, int m0,
+                                            const uint8_t* __restrict__ qwp, uint32_t wbytes,
+                                            const uint32_t (&sB)[CW / 16], int kt0, int nk) {
   constexpr int RA = BM / 16, TJ = CW / 16;
   constexpr int A_CHUNKS = BM * 8;  // 16-byte chunks of one A stage
   constexpr int FULL = A_CHUNKS / kThreads, REM = A_CHUNKS % kThreads;
   constexpr int NA = FULL + (REM ? 1 : 0);
   constexpr int STAGE = BM * 128;
   constexpr int NB = 2 * G;
-  constexpr int EPI_LD = BN + 8;  // bf16 pitch of the epilogue tile
-  constexpr int SMEM = NB * STAGE > BM * EPI_LD * 2 ? NB * STAGE : BM * EPI_LD * 2;
   constexpr int U = lcm3(P, D, NB);  // k steps per unrolled loop iteration
-  constexpr int CPR = CH / 8;        // 8-channel chunks per row in the SwiGLU pass
-  static_assert(SMEM <= 160 * 1024, "LDS budget");
   static_assert(A_CHUNKS >= kThreads, "at least one full activation round");
-  static_assert(CH == 2 * CW, "waves 0-1 take the gate rows, waves 2-3 the up rows");
-  static_assert(CH % 64 == 0 && (BM * CPR) % 64 == 0, "64-channel row maxima over whole waves");
-  __shared__ __align__(1024) uint8_t smem[SMEM];
-
-  const int nblk = tiles_m * tiles_n;
-  const int b = blockIdx.x;
-  int logical = b;
-  if (nblk % kXcds == 0) logical = (b % kXcds) * (nblk / kXcds) + b / kXcds;  // one XCD walks a tile range
-  const int tm = logical % tiles_m, tn = logical / tiles_m;                    // M fastest: L2 shares weights
-  const int m0 = tm * BM;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int r16 = lane & 15, g = lane >> 4;
-  const int KT = K / 128;
+  const int kend = kt0 + nk;
 
   // Activations: chunk c = tid + 256 i is row c / 8, 16-byte chunk c % 8; a
   // partial last round is moved back over the last 256 chunks (the overlap is
@@ -158,18 +146,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
     });
   };
 
-  // Weights: fragment j of this wave is the 16-row group of weight row
-  // (gate half for waves 0-1, up half for waves 2-3) + channel.
-  const __amdgpu_buffer_rsrc_t rB = make_rsrc(qwp, (uint32_t)(2 * half) * (uint32_t)K);
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(qwp, wbytes);
   const uint32_t voffB = 32u * (uint32_t)lane;
-  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-  uint32_t sB[TJ];
-#pragma unroll
-  for (int j = 0; j < TJ; ++j) {
-    const int cl = wave_s * CW + 16 * j;  // tile column
-    const int row = cl < CH ? tn * CH + cl : half + tn * CH + (cl - CH);
-    sB[j] = (uint32_t)(row / 16) * (uint32_t)KT * 2048u;
-  }
   i32x8 bq[P][TJ];
   auto loadB = [&](int kt, auto SLOT) {
     constexpr int slot = decltype(SLOT)::value;
@@ -181,7 +159,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
     }
   };
 
-  f32x4 acc[RA][TJ];
 #pragma unroll
   for (int i = 0; i < RA; ++i)
 #pragma unroll
@@ -198,25 +175,26 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
   ACC_PIN();
   ACC_NOPS();
 
-  // Prologue: LDS stages 0..G-1 = steps 0..G-1, staging slots = steps G..G+D-1,
-  // weight stages = steps 0..P-1, issued in the loop's order (A, then B).
+  // Prologue: LDS stages 0..G-1 = steps kt0..kt0+G-1, staging slots = the next D
+  // steps, weight stages = steps kt0..kt0+P-1, issued in the loop's order (A,
+  // then B) so that the loop entry needs no full drain.
   using I0 = std::integral_constant<int, 0>;
   static_for<0, G>([&](auto S_) {
     constexpr int s = decltype(S_)::value;
-    loadA(min(s, KT - 1), I0{});
+    loadA(min(kt0 + s, kend - 1), I0{});
     writeA(I0{}, std::integral_constant<int, s>{});
   });
   static_for<0, (D > P ? D : P)>([&](auto S_) {
     constexpr int s = decltype(S_)::value;
-    if constexpr (s < D) loadA(min(G + s, KT - 1), std::integral_constant<int, (G + s) % D>{});
+    if constexpr (s < D) loadA(min(kt0 + G + s, kend - 1), std::integral_constant<int, (G + s) % D>{});
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (s < P) loadB(min(s, KT - 1), std::integral_constant<int, s>{});
+    if constexpr (s < P) loadB(min(kt0 + s, kend - 1), std::integral_constant<int, s>{});
     __builtin_amdgcn_sched_barrier(0);
   });
 
   const int frag = 128 * (r16 & 7) + 1024 * (r16 >> 3);
   const int c0 = 16 * ((2 * g) ^ (r16 >> 1)), c1 = 16 * ((2 * g + 1) ^ (r16 >> 1));
-  for (int kb = 0; kb < KT; kb += U) {
+  for (int kb = kt0; kb < kend; kb += U) {
     static_for<0, U>([&](auto U_) {
       constexpr int u = decltype(U_)::value;
       const int kt = kb + u;
@@ -225,7 +203,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
       // with steps kt + G.., are no longer read.
       if constexpr (u % G == 0) __syncthreads();
       writeA(std::integral_constant<int, (u + G) % D>{}, std::integral_constant<int, (u + G) % NB>{});
-      loadA(min(kt + G + D, KT - 1), std::integral_constant<int, (u + G) % D>{});
+      loadA(min(kt + G + D, kend - 1), std::integral_constant<int, (u + G) % D>{});
       const uint8_t* st = smem + (u % NB) * STAGE + frag;
       i32x8 af[RA];
 #pragma unroll
@@ -234,7 +212,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
         const i32x4v hi = *reinterpret_cast<const i32x4v*>(st + 2 * i * 1024 + c1);
         af[i] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
       }
-      const uint32_t ktn = (uint32_t)min(kt + P, KT - 1);
+      const uint32_t ktn = (uint32_t)min(kt + P, kend - 1);
       static_for<0, TJ>([&](auto J_) {
         constexpr int j = decltype(J_)::value;
 #pragma unroll
@@ -249,6 +227,53 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
   ACC_PIN();
 #undef ACC_PIN
 #undef ACC_NOPS
+}
+
+// LDS a kernel below needs: the main loop's stages or the bf16 epilogue tile.
+template <int BM, int CW, int G>
+constexpr int pk_smem() {
+  return 2 * G * BM * 128 > BM * (4 * CW + 8) * 2 ? 2 * G * BM * 128 : BM * (4 * CW + 8) * 2;
+}
+
+// Gate/up: BM tokens x (BN/2 gate + BN/2 up channels), BN = 4 CW; waves 0-1
+// take the gate rows, waves 2-3 the matching up rows.
+template <int BM, int CW, int P, int D, int G>
+__global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
+    const uint8_t* __restrict__ qa, const float* __restrict__ sa, const uint8_t* __restrict__ qwp,
+    const float* __restrict__ sw, bf16_t* __restrict__ h, int64_t ldh, float* __restrict__ pmax, int M, int half,
+    int K, int tiles_m, int tiles_n) {
+  constexpr int BN = 4 * CW, CH = BN / 2;
+  constexpr int RA = BM / 16, TJ = CW / 16;
+  constexpr int EPI_LD = BN + 8;  // bf16 pitch of the epilogue tile
+  constexpr int SMEM = pk_smem<BM, CW, G>();
+  constexpr int CPR = CH / 8;  // 8-channel chunks per row in the SwiGLU pass
+  static_assert(SMEM <= 160 * 1024, "LDS budget");
+  static_assert(CH == 2 * CW, "waves 0-1 take the gate rows, waves 2-3 the up rows");
+  static_assert(CH % 64 == 0 && (BM * CPR) % 64 == 0, "64-channel row maxima over whole waves");
+  __shared__ __align__(1024) uint8_t smem[SMEM];
+
+  const int nblk = tiles_m * tiles_n;
+  const int b = blockIdx.x;
+  int logical = b;
+  if (nblk % kXcds == 0) logical = (b % kXcds) * (nblk / kXcds) + b / kXcds;  // one XCD walks a tile range
+  const int tm = logical % tiles_m, tn = logical / tiles_m;                    // M fastest: L2 shares weights
+  const int m0 = tm * BM;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int KT = K / 128;
+
+  // Weights: fragment j of this wave is the 16-row group of weight row
+  // (gate half for waves 0-1, up half for waves 2-3) + channel.
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  uint32_t sB[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int cl = wave_s * CW + 16 * j;  // tile column
+    const int row = cl < CH ? tn * CH + cl : half + tn * CH + (cl - CH);
+    sB[j] = (uint32_t)(row / 16) * (uint32_t)KT * 2048u;
+  }
+  f32x4 acc[RA][TJ];
+  pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)(2 * half) * (uint32_t)K, sB, 0, KT);
   __syncthreads();  // every wave is done with the stages; the tile reuses the LDS
 
   // y = bf16((acc * sa) * sw) as a row-major tile: gate channels in columns
@@ -295,11 +320,157 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
   }
 }
 
+// y = bf16((acc * sa) * sw) for one BM x 4 CW tile held in the accumulator
+// layout of the kernels above, staged through LDS so that the stores are
+// 16-byte row chunks. sa per row if sa_rows else one value; sw likewise.
+template <int BM, int CW>
+__device__ __forceinline__ void pk_store_tile(const f32x4 (&acc)[BM / 16][CW / 16], uint8_t* smem,
+                                              const float* __restrict__ sa, int sa_rows,
+                                              const float* __restrict__ sw, int sw_cols, bf16_t* __restrict__ y,
+                                              int64_t ldy, int M, int m0, int n0) {
+  constexpr int BN = 4 * CW, RA = BM / 16, TJ = CW / 16, EPI_LD = BN + 8;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  bf16_t* tile = reinterpret_cast<bf16_t*>(smem);
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int cl = wave * CW + 16 * j + r16;
+    const float swv = sw[sw_cols ? n0 + cl : 0];
+#pragma unroll
+    for (int i = 0; i < RA; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int rl = 16 * i + 4 * g + r;
+        const float sav = sa[sa_rows ? min(m0 + rl, M - 1) : 0];
+        tile[rl * EPI_LD + cl] = (bf16_t)f32_to_bf16((acc[i][j][r] * sav) * swv);
+      }
+  }
+  __syncthreads();
+  constexpr int CHUNKS = BM * BN / 8;
+  for (int c = tid; c < CHUNKS; c += kThreads) {
+    const int rl = c / (BN / 8), cl = (c % (BN / 8)) * 8;
+    const int m = m0 + rl;
+    if (m < M)
+      *reinterpret_cast<u32x4*>(y + (int64_t)m * ldy + n0 + cl) = *reinterpret_cast<const u32x4*>(tile + rl * EPI_LD + cl);
+  }
+}
+
+// Plain y = bf16((A . W^T * sa) * sw) with k split S ways: workgroup (tile,
+// split) runs k steps [split KT/S, (split + 1) KT/S). With S == 1 it stores y;
+// with S > 1 it stores its fp32 partial tile in accumulator order (f32x4 (i, j)
+// of thread t at ((tile S + split) RA TJ + i TJ + j) 256 + t) and
+// split_reduce_kernel, the next launch, adds the partials.
+template <int BM, int CW, int P, int D, int G, int S>
+__global__ __launch_bounds__(kThreads, 1) void gemm_fp8_split_packed_kernel(
+    const uint8_t* __restrict__ qa, const float* __restrict__ sa, int sa_rows, const uint8_t* __restrict__ qwp,
+    const float* __restrict__ sw, int sw_cols, bf16_t* __restrict__ y, int64_t ldy, int M, int N, int K,
+    int tiles_m, int tiles_n, f32x4* __restrict__ part) {
+  constexpr int BN = 4 * CW;
+  constexpr int RA = BM / 16, TJ = CW / 16;
+  constexpr int SMEM = pk_smem<BM, CW, G>();
+  static_assert(SMEM <= 160 * 1024, "LDS budget");
+  __shared__ __align__(1024) uint8_t smem[SMEM];
+
+  const int nblk = tiles_m * tiles_n * S;
+  const int b = blockIdx.x;
+  int logical = b;
+  if (nblk % kXcds == 0) logical = (b % kXcds) * (nblk / kXcds) + b / kXcds;
+  const int tm = logical % tiles_m, rest = logical / tiles_m;  // M fastest: L2 shares weights
+  const int split = rest % S, tn = rest / S;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int KT = K / 128, nk = KT / S;
+
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  uint32_t sB[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) sB[j] = (uint32_t)((n0 + wave_s * CW + 16 * j) / 16) * (uint32_t)KT * 2048u;
+  f32x4 acc[RA][TJ];
+  pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, split * nk, nk);
+  if constexpr (S > 1) {
+    f32x4* mine = part + ((int64_t)(tn * tiles_m + tm) * S + split) * (RA * TJ * kThreads) + tid;
+#pragma unroll
+    for (int i = 0; i < RA; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) mine[(i * TJ + j) * kThreads] = acc[i][j];
+  } else {
+    __syncthreads();  // every wave is done with the stages; the tile reuses the LDS
+    pk_store_tile<BM, CW>(acc, smem, sa, sa_rows, sw, sw_cols, y, ldy, M, m0, n0);
+  }
+}
+
+// y for the tiles of a split launch, one workgroup per (tile, 16-row group i):
+// the S partials of each accumulator added in split order 0, 1, .., S-1
+// (independent of which split finished first), then the epilogue of the
+// unsplit kernel for those 16 rows.
+template <int BM, int CW, int S>
+__global__ __launch_bounds__(kThreads) void split_reduce_kernel(
+    const f32x4* __restrict__ part, const float* __restrict__ sa, int sa_rows, const float* __restrict__ sw,
+    int sw_cols, bf16_t* __restrict__ y, int64_t ldy, int M, int tiles_m) {
+  constexpr int RA = BM / 16, TJ = CW / 16, BN = 4 * CW, EPI_LD = BN + 8;
+  __shared__ __align__(16) bf16_t rows[16 * EPI_LD];
+  const int tile = blockIdx.x / RA, i = blockIdx.x % RA;
+  const int tm = tile % tiles_m, tn = tile / tiles_m;
+  const int m0 = tm * BM + 16 * i, n0 = tn * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const f32x4* tp = part + (int64_t)tile * S * (RA * TJ * kThreads) + tid;
+  f32x4 v[TJ][S];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j)
+#pragma unroll
+    for (int s2 = 0; s2 < S; ++s2) v[j][s2] = tp[((int64_t)s2 * RA * TJ + i * TJ + j) * kThreads];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    f32x4 t = v[j][0];
+#pragma unroll
+    for (int s2 = 1; s2 < S; ++s2) t = t + v[j][s2];
+    const int cl = wave * CW + 16 * j + r16;
+    const float swv = sw[sw_cols ? n0 + cl : 0];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int rl = 4 * g + r;
+      const float sav = sa[sa_rows ? min(m0 + rl, M - 1) : 0];
+      rows[rl * EPI_LD + cl] = (bf16_t)f32_to_bf16((t[r] * sav) * swv);
+    }
+  }
+  __syncthreads();
+  for (int c = tid; c < 16 * BN / 8; c += kThreads) {
+    const int rl = c / (BN / 8), cl = (c % (BN / 8)) * 8;
+    const int m = m0 + rl;
+    if (m < M)
+      *reinterpret_cast<u32x4*>(y + (int64_t)m * ldy + n0 + cl) = *reinterpret_cast<const u32x4*>(rows + rl * EPI_LD + cl);
+  }
+}
+
 // The configuration measured for the 8B gate/up shape (576 x 4096 x 2 x 12288):
 // 144 x 384 tiles, one workgroup per CU (4 x 64 = 256 workgroups).
 constexpr int kPkBM = 144, kPkCW = 96, kPkP = 2, kPkD = 2, kPkG = 2;
 constexpr int kPkCH = 2 * kPkCW;
 constexpr int kPkKAlign = 128 * lcm3(kPkP, kPkD, 2 * kPkG);  // k multiple of the unrolled k steps
+
+// Plain GEMM: 144 x 256 tiles, k split so that about 256 workgroups run (the
+// 8B o and down projections: 4 x 16 tiles, 4 splits).
+constexpr int kSpBM = 144, kSpCW = 64, kSpP = 2, kSpD = 2, kSpG = 2;
+constexpr int kSpBN = 4 * kSpCW;
+constexpr int kSpU = lcm3(kSpP, kSpD, 2 * kSpG);
+
+// Splits for an m x n x k plain GEMM on the packed path, 0 if it does not take
+// it: one launch when the tiles fill the GPU, else 4 splits when k is long
+// enough that the extra reduction launch pays off (the 8B down projection,
+// 576 x 4096 x 12288); shorter k stays on the row-major kernels.
+int split_plan(int64_t m, int64_t n, int64_t k) {
+  if (m <= 4 || n % kSpBN || k % 128 || m * k >= (int64_t(1) << 31) || n * k >= (int64_t(1) << 31)) return 0;
+  const int64_t tiles = (m + kSpBM - 1) / kSpBM * (n / kSpBN), kt = k / 128;
+  if (tiles >= 192) return kt % kSpU == 0 ? 1 : 0;
+  return kt >= 64 && kt % (4 * kSpU) == 0 ? 4 : 0;
+}
+
+int64_t split_workspace(int64_t m, int64_t n, int64_t k) {
+  const int s = split_plan(m, n, k);
+  if (s <= 1) return 0;
+  return (m + kSpBM - 1) / kSpBM * (n / kSpBN) * s * kSpBM * kSpBN * 4;
+}
 
 }  // namespace
 
@@ -331,5 +502,43 @@ extern "C" int ff_gemm_fp8_swiglu_pk(const void* qa, const float* sa, const void
                      (const uint8_t*)qa, sa, (const uint8_t*)qw_packed, sw, (bf16_t*)h, ldh, pmax, (int)m, (int)i,
                      (int)k, (int)tiles_m, (int)tiles_n);
   FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu_pk");
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_fp8_pk_workspace(int64_t m, int64_t n, int64_t k, int64_t* bytes) {
+  FF_REQUIRE(bytes && m >= 0 && n >= 0 && k >= 0, "ff_gemm_fp8_pk_workspace: bad arguments");
+  *bytes = split_workspace(m, n, k);
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, const void* qw, const void* qw_packed,
+                              const float* sw, int sw_cols, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
+                              void* workspace, int64_t workspace_bytes, ff_stream_t stream) {
+  FF_REQUIRE(qa && sa && qw && sw && y, "ff_gemm_fp8_pk: null pointer");
+  const int s = qw_packed && ldy % 8 == 0 && ldy >= n && ff_aligned(qa, 16) && ff_aligned(qw_packed, 16) &&
+                        ff_aligned(y, 16)
+                    ? split_plan(m, n, k)
+                    : 0;
+  if (s == 0) return ff_gemm_fp8(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, stream);
+  const int64_t need = split_workspace(m, n, k);
+  FF_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && ff_aligned(workspace, 16)),
+             "ff_gemm_fp8_pk: workspace of %lld bytes (16-byte aligned) required", (long long)need);
+  const int64_t tiles_m = (m + kSpBM - 1) / kSpBM, tiles_n = n / kSpBN, tiles = tiles_m * tiles_n;
+  f32x4* part = (f32x4*)workspace;
+  hipStream_t st = (hipStream_t)stream;
+  if (s == 1) {
+    hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<kSpBM, kSpCW, kSpP, kSpD, kSpG, 1>), dim3((unsigned)tiles),
+                       dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows, (const uint8_t*)qw_packed, sw, sw_cols,
+                       (bf16_t*)y, ldy, (int)m, (int)n, (int)k, (int)tiles_m, (int)tiles_n, part);
+  } else {
+    hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<kSpBM, kSpCW, kSpP, kSpD, kSpG, 4>),
+                       dim3((unsigned)(tiles * 4)), dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows,
+                       (const uint8_t*)qw_packed, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)n, (int)k,
+                       (int)tiles_m, (int)tiles_n, part);
+    hipLaunchKernelGGL((split_reduce_kernel<kSpBM, kSpCW, 4>), dim3((unsigned)(tiles * (kSpBM / 16))),
+                       dim3(kThreads), 0, st,
+                       (const f32x4*)part, sa, sa_rows, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)tiles_m);
+  }
+  FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
   return FF_OK;
 }

@@ -28,6 +28,13 @@ E4M3 = torch.float8_e4m3fn
 BF16 = torch.bfloat16
 
 
+def gemm_pk_workspace(m, n, k):
+    """Bytes of workspace ff_gemm_fp8_pk needs for an m x n x k GEMM (0: none)."""
+    need = ctypes.c_int64(0)
+    call("ff_gemm_fp8_pk_workspace", m, n, k, ctypes.byref(need))
+    return need.value
+
+
 def _rows(x):
     return x.reshape(-1, x.shape[-1])
 
@@ -55,7 +62,7 @@ class FP8Linear:
 
     def pack(self):
         """Add the MFMA-fragment copy of the weight (ff_pack_weight_fp8) that the
-        gate/up tile kernel reads; ``weight`` stays row-major for every other path."""
+        packed tile kernels read; ``weight`` stays row-major for the other paths."""
         n, k = self.weight.shape
         if self.packed is None and n % 16 == 0 and k % 128 == 0:
             self.packed = torch.empty_like(self.weight)
@@ -73,13 +80,26 @@ class FP8Linear:
         call("ff_quant_rows_fp8", ptr(flat), flat.stride(0), ptr(q), ptr(s), m, k, stream())
         return q, s
 
-    def gemm(self, q, s, out=None):
-        """y = bf16(q_a . W^T * s_a * s_w) from pre-quantized activations."""
+    def gemm(self, q, s, out=None, workspace=None):
+        """y = bf16(q_a . W^T * s_a * s_w) from pre-quantized activations. With the
+        packed copy (``pack()``) this is ff_gemm_fp8_pk, whose k split needs a
+        workspace: ``workspace`` if given (a caller's, reused across calls that
+        are ordered on one stream), else one this op keeps."""
         m, k = q.shape
         n = self.weight.shape[0]
         y = torch.empty((m, n), device=q.device, dtype=BF16) if out is None else out
-        call("ff_gemm_fp8", ptr(q), ptr(s), 1, ptr(self.weight), ptr(self.scale), 1, ptr(y), y.stride(0),
-             m, n, k, stream())
+        if self.packed is None:
+            call("ff_gemm_fp8", ptr(q), ptr(s), 1, ptr(self.weight), ptr(self.scale), 1, ptr(y), y.stride(0),
+                 m, n, k, stream())
+            return y
+        if workspace is None:
+            need = gemm_pk_workspace(m, n, k)
+            ws = getattr(self, "_ws", None)
+            if need and (ws is None or ws.numel() < need):
+                self._ws = ws = torch.empty(need, device=q.device, dtype=torch.uint8)
+            workspace = ws if need else None
+        call("ff_gemm_fp8_pk", ptr(q), ptr(s), 1, ptr(self.weight), ptr(self.packed), ptr(self.scale), 1, ptr(y),
+             y.stride(0), m, n, k, ptr(workspace), 0 if workspace is None else workspace.numel(), stream())
         return y
 
     def __call__(self, x):

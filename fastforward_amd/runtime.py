@@ -24,7 +24,7 @@ import torch
 
 from . import ops
 from ._lib import call, ptr, stream
-from .linear import FP8Linear, Linear
+from .linear import FP8Linear, Linear, gemm_pk_workspace
 
 BF16 = torch.bfloat16
 E4M3 = torch.float8_e4m3fn
@@ -123,8 +123,10 @@ class Runtime:
         if self.path == "fused" and not fp8:
             raise ValueError("the fused path needs FP8Linear (per-token / per-channel) weights")
         if self.path == "fused":
-            for L in weights.layers:
-                L.gateup.pack()  # MFMA-fragment copy for the gate/up tile kernel (once per weight)
+            for L in weights.layers:  # MFMA-fragment copies for the packed tile kernels (once per weight)
+                L.o.pack()
+                L.gateup.pack()
+                L.down.pack()
         T, H, D = tokens, cfg.hidden, cfg.head_dim
         HQ, HK, I = cfg.heads, cfg.kv_heads, cfg.inter
         e = lambda *s, dt=BF16: torch.empty(s, device=dev, dtype=dt)  # noqa: E731
@@ -155,6 +157,9 @@ class Runtime:
             self.mq, self.ms = e(T, I, dt=E4M3), e(T, dt=torch.float32)
             self.dn = e(T, H)
             self.hp = e(1, H)
+            # k-split partials of ff_gemm_fp8_pk (o and down share it: their calls are ordered)
+            need = max(gemm_pk_workspace(T, H, HQ * D), gemm_pk_workspace(T, H, I), 256)
+            self.gws = torch.empty(need, device=dev, dtype=torch.uint8)
         self.graph = None
         self.graph_out = None
 
@@ -208,8 +213,7 @@ class Runtime:
             lw = L[j]
             h = self.h[cur]
             self._attention_fused(lw, s)
-            call("ff_gemm_fp8", ptr(self.aq), ptr(self.as_), 1, ptr(lw.o.weight), ptr(lw.o.scale), 1, ptr(self.o), H,
-                 T, H, HQ * D, s)
+            self._gemm(self.aq, self.as_, lw.o, self.o, T, s)
             call("ff_add_rms_quant", ptr(h), ptr(self.o), None, ptr(lw.post_norm.weight), ptr(self.res), None,
                  ptr(self.pq), ptr(self.ps), T, H, float(lw.post_norm.variance_epsilon), 0, 0, s)
             self._mlp_fused(lw, self.pq, self.ps, T, self.dn, s)
@@ -226,8 +230,7 @@ class Runtime:
         lw = L[-1]
         h = self.h[cur]
         self._attention_fused(lw, s, tail=True)
-        call("ff_gemm_fp8", ptr(self.aq), ptr(self.as_), 1, ptr(lw.o.weight), ptr(lw.o.scale), 1, ptr(self.o), H,
-             1, H, HQ * D, s)
+        self._gemm(self.aq, self.as_, lw.o, self.o, 1, s)
         call("ff_gather_rows", ptr(h), H, ptr(self.pick), ptr(self.hp), H, 1, H, T, s)
         call("ff_add_rms_quant", ptr(self.hp), ptr(self.o), None, ptr(lw.post_norm.weight), ptr(self.res), None,
              ptr(self.pq), ptr(self.ps), 1, H, float(lw.post_norm.variance_epsilon), 0, 0, s)
@@ -254,14 +257,21 @@ class Runtime:
                  HQ, HK, D, float(cfg.scaling), s)
             call("ff_quant_rows_fp8", ptr(self.attn), HQ * D, ptr(self.aq), ptr(self.as_), T, HQ * D, s)
 
+    def _gemm(self, q, sc, op, out, m, s):
+        """out[:m] = bf16(q . W^T * sc * s_w) for an FP8Linear op: ff_gemm_fp8_pk (packed
+        weights, k split over the Runtime's workspace where it pays; otherwise the
+        row-major kernels, GEMV for m <= 4)."""
+        n, k = op.weight.shape
+        call("ff_gemm_fp8_pk", ptr(q), ptr(sc), 1, ptr(op.weight), ptr(op.packed), ptr(op.scale), 1, ptr(out), n,
+             m, n, k, ptr(self.gws), self.gws.numel(), s)
+
     def _mlp_fused(self, lw, q, sc, m, out, s):
         I, H = self.cfg.inter, self.cfg.hidden
         # gate/up GEMM with SwiGLU in its epilogue, then per-token quant from its row maxima
         call("ff_gemm_fp8_swiglu_pk", ptr(q), ptr(sc), ptr(lw.gateup.weight), ptr(lw.gateup.packed),
              ptr(lw.gateup.scale), ptr(self.hm), I, ptr(self.pmax), m, I, H, s)
         call("ff_quant_rows_pmax", ptr(self.hm), I, ptr(self.pmax), I // 64, ptr(self.mq), ptr(self.ms), m, I, s)
-        call("ff_gemm_fp8", ptr(self.mq), ptr(self.ms), 1, ptr(lw.down.weight), ptr(lw.down.scale), 1, ptr(out), H,
-             m, H, I, s)
+        self._gemm(self.mq, self.ms, lw.down, out, m, s)
 
     def _step_generic(self, trace=None):
         """The reference's op sequence (scaled_qwen_runtime.py:143-176,

@@ -172,6 +172,22 @@ int ff_gemm_fp8_swiglu_pk(const void* qa, const float* sa, const void* qw, const
                           const float* sw, void* h, int64_t ldh, float* pmax, int64_t m, int64_t i, int64_t k,
                           ff_stream_t stream);
 
+/* ff_gemm_fp8 with an optional packed copy of the weight (ff_pack_weight_fp8 of
+ * qw) and a workspace (no reference counterpart: the down projection of the
+ * step, Linear.apply of scaled_qwen_runtime.py:35-39). When qw_packed is given
+ * and the shape suits it (n % 256 == 0, m > 4, and either 192 or more 144 x 256
+ * tiles or k >= 8192 with k % 2048 == 0) the weights are read from the packed
+ * copy; with fewer tiles k is split 4 ways, each split writes its fp32 partial
+ * tile to the workspace and a second launch adds the partials in split order
+ * (same math as ff_gemm_fp8 up to the fp32 order of adding the 4 partials;
+ * repeatable bit for bit). Otherwise this is ff_gemm_fp8 on qw. workspace:
+ * ff_gemm_fp8_pk_workspace bytes (0 when no split is used), 16-byte aligned;
+ * calls that overlap must not share it. */
+int ff_gemm_fp8_pk_workspace(int64_t m, int64_t n, int64_t k, int64_t* bytes);
+int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, const void* qw, const void* qw_packed,
+                   const float* sw, int sw_cols, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
+                   void* workspace, int64_t workspace_bytes, ff_stream_t stream);
+
 /* Fused QKV GEMM + q/k norm + rotary + V transpose (no reference counterpart as
  * one op; the same arithmetic as ff_gemm_fp8 on the packed QKV weight followed
  * by ff_qkv_post): qw ((hq + 2 hk) * 128, k) e4m3 with per-row scales sw, qa (m, k)

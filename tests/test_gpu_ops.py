@@ -353,6 +353,62 @@ def test_gemm_fp8_swiglu_packed_equals_rowmajor(gpu, m, i, k):
     assert torch.equal(h0, h1) and torch.equal(p0, p1)
 
 
+# (m, n, k, splits the packed path takes); 0 = not taken (row-major kernels)
+PK_SHAPES = [(576, 4096, 12288, 4), (300, 2048, 8192, 4), (1000, 6144, 8192, 4), (576, 12288, 4096, 1),
+             (576, 4096, 4096, 0), (3, 4096, 4096, 0), (576, 4160, 12288, 0)]
+
+
+@pytest.mark.parametrize("m,n,k,splits", PK_SHAPES)
+def test_gemm_fp8_pk_matches_rowmajor(gpu, m, n, k, splits):
+    """ff_gemm_fp8_pk on the packed weight: the same bits as ff_gemm_fp8 unsplit
+    or where it falls back; with a k split, at most 1 bf16 ulp from it (only the
+    fp32 order of adding the partials differs), identical bits on repeated calls
+    and within the exact-product bound."""
+    from fastforward_amd._lib import call, ptr, stream
+    from fastforward_amd.linear import FP8Linear, gemm_pk_workspace
+    x = (torch.randn(m, k, generator=_g(60)) * 2).to(BF16).to(DEV)
+    op = FP8Linear((torch.randn(n, k, generator=_g(61)) * 0.03).to(BF16).to(DEV)).pack()
+    qa, sa = op.quantize(x)
+    need = gemm_pk_workspace(m, n, k)
+    assert (need > 0) == (splits > 1)
+    ws = torch.full((max(need, 256),), 0xFF, device=DEV, dtype=torch.uint8)  # no zeroing needed
+    ref = torch.empty(m, n, device=DEV, dtype=BF16)
+    call("ff_gemm_fp8", ptr(qa), ptr(sa), 1, ptr(op.weight), ptr(op.scale), 1, ptr(ref), n, m, n, k, stream())
+    outs = []
+    for _ in range(3):
+        y = torch.full((m, n), float("nan"), device=DEV, dtype=BF16)
+        call("ff_gemm_fp8_pk", ptr(qa), ptr(sa), 1, ptr(op.weight), ptr(op.packed), ptr(op.scale), 1, ptr(y), n,
+             m, n, k, ptr(ws), ws.numel(), stream())
+        outs.append(y)
+    assert all(torch.equal(outs[0], o) for o in outs[1:])
+    if splits <= 1:
+        assert torch.equal(outs[0], ref)
+    else:
+        d = bf16_ulps(outs[0], ref)
+        assert int(d.max()) <= 1 and float((d > 0).float().mean()) < 0.01
+    if (m, n, k) == (300, 2048, 8192):
+        qa_c, sa_c, qw_c, sw_c = qa.cpu(), sa.cpu(), op.weight.cpu(), op.scale.cpu().reshape(-1)
+        _assert_fp8_gemm(outs[0].cpu(), qa_c, sa_c, qw_c, sw_c, O.fp8_gemm(qa_c, sa_c, qw_c, sw_c),
+                         "gemm_fp8_pk split 4")
+
+
+def test_gemm_fp8_pk_scalar_scales(gpu):
+    """Per-tensor scales (sa_rows = sw_cols = 0) on the split path agree with ff_gemm_fp8."""
+    from fastforward_amd._lib import call, ptr, stream
+    from fastforward_amd.linear import FP8Linear, gemm_pk_workspace
+    m, n, k = 576, 4096, 8192
+    x = (torch.randn(m, k, generator=_g(62))).to(BF16).to(DEV)
+    op = FP8Linear((torch.randn(n, k, generator=_g(63)) * 0.03).to(BF16).to(DEV)).pack()
+    qa, _ = op.quantize(x)
+    sa, sw = torch.tensor([0.01], device=DEV), torch.tensor([0.002], device=DEV)
+    ws = torch.zeros(gemm_pk_workspace(m, n, k), device=DEV, dtype=torch.uint8)
+    ref, y = (torch.empty(m, n, device=DEV, dtype=BF16) for _ in range(2))
+    call("ff_gemm_fp8", ptr(qa), ptr(sa), 0, ptr(op.weight), ptr(sw), 0, ptr(ref), n, m, n, k, stream())
+    call("ff_gemm_fp8_pk", ptr(qa), ptr(sa), 0, ptr(op.weight), ptr(op.packed), ptr(sw), 0, ptr(y), n, m, n, k,
+         ptr(ws), ws.numel(), stream())
+    assert int(bf16_ulps(y, ref).max()) <= 1
+
+
 def test_gemm_fp8_static_scalars(gpu):
     from fastforward_amd.linear import StaticFP8Linear
     m, k, n = 576, 4096, 4096
