@@ -28,6 +28,9 @@ METRIC = "ms per prefill+choice-score step (8B-shape FP8, 576 tok); FP8 GEMM % M
 PEAK_FP8_TFLOPS = 5000.0      # MI355X dense fp8 MFMA
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+GEMM_KERNELS = ("FP8 GEMM launches of the step: gemm_fp8_swiglu_packed_kernel (gate/up), "
+                "gemm_fp8_split_packed_kernel + split_reduce_kernel (down), gemm_fp8_kernel (qkv with its "
+                "epilogue, o), gemv_fp8 kernels (the tail's single row)")
 MICRO_SHAPES = [(320, 2048, 6144), (320, 6144, 2048), (576, 4096, 12288), (576, 12288, 4096),
                 (1024, 5120, 25600)]
 
@@ -78,8 +81,9 @@ def gemm_buffers(cfg, role, n, m, T):
 def launch_gemm(cfg, role, lw, q, s, m, b):
     """One FP8 GEMM launch as the step issues it: the QKV projection with its
     q/k norm + rotary + V^T epilogue (ff_gemm_fp8_qkv), the gate/up projection
-    with its SwiGLU epilogue (ff_gemm_fp8_swiglu_pk: packed weights), o and down plain ff_gemm_fp8
-    (which takes the GEMV kernels for the tail's single row)."""
+    with its SwiGLU epilogue (ff_gemm_fp8_swiglu_pk: packed weights), o and down through
+    ``FP8Linear.gemm`` (ff_gemm_fp8_pk: the k-split packed kernel and its reduction for
+    down, the row-major kernel for o, the GEMV kernels for the tail's single row)."""
     from fastforward_amd._lib import call, ptr, stream
     op = getattr(lw, role)
     n, k = op.weight.shape
@@ -135,10 +139,14 @@ def gemm_roofline(cfg, w, T):
         launches += count
     avg_ms = total_ms / launches
     achieved = total_flop / launches / (avg_ms * 1e-3) / 1e12
+    gu = per_shape[f"gateup {T}x{cfg.hidden}x{2 * cfg.inter}"]
     return dict(bound="mfma", achieved=round(achieved, 1), peak=PEAK_FP8_TFLOPS, unit="TFLOP/s",
                 frac=round(achieved / PEAK_FP8_TFLOPS, 4), traffic=_traffic(),
-                kernel="gemm_fp8_kernel", avg_launch_us=round(avg_ms * 1e3, 2), launches_per_step=launches,
-                gemm_ms_per_step=round(total_ms, 3), by_shape=per_shape)
+                kernel=GEMM_KERNELS, avg_launch_us=round(avg_ms * 1e3, 2), launches_per_step=launches,
+                gemm_ms_per_step=round(total_ms, 3),
+                dominant=dict(kernel="gemm_fp8_swiglu_packed_kernel (gate/up + SwiGLU)", us=gu["us"],
+                              tflops=gu["tflops"], frac=round(gu["tflops"] / PEAK_FP8_TFLOPS, 4)),
+                by_shape=per_shape)
 
 
 def _traffic():

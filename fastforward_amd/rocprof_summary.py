@@ -77,7 +77,7 @@ def _by_grid(path, counters=None):
 
 def step_table(db, fetch_csv, write_csv, mfma_csv, fetch_factor, write_factor, xcds=8, simds=1024,
                skip=("at::native", "__amd_rocclr", "weight_quant_kernel", "row_amax_kernel", "channel_scale_kernel",
-                     "int4_quant_kernel")):
+                     "int4_quant_kernel", "pack_fp8_kernel")):
     con = sqlite3.connect(db)
     dur = collections.defaultdict(list)
     for name, gx, gy, gz, wx, start, end in con.execute(
@@ -129,6 +129,20 @@ def _dispatches(path):
     return [(i, k, c) for i, (k, c) in sorted(rows.items())]
 
 
+def _launches(dispatches):
+    """GEMM launches from dispatches in order: a gemm_fp8*/gemv_fp8* dispatch plus
+    the split_reduce_kernel dispatch that follows it for a k-split launch, counters
+    summed, kernel names joined with '+'."""
+    out = []
+    for i, k, c in dispatches:
+        if k.startswith(("gemm_fp8", "gemv_fp8")):
+            out.append((i, k, dict(c)))
+        elif k.startswith("split_reduce_kernel") and out:
+            j, k0, c0 = out[-1]
+            out[-1] = (j, f"{k0} + {k}", {n: c0.get(n, 0.0) + v for n, v in c.items()})
+    return out
+
+
 def traffic(fetch_csv, write_csv, manifest):
     """GEMM launches of ``bench.py --kernels`` in manifest order (``reps`` each),
     then the calibration copy (the last ``copy_reps`` dispatches)."""
@@ -138,8 +152,7 @@ def traffic(fetch_csv, write_csv, manifest):
     w_copy = sum(c["WRITE_SIZE"] for _, _, c in wr[-reps:]) / reps
     ff = manifest["copy_bytes"] / (f_copy * 1024)
     wf = manifest["copy_bytes"] / (w_copy * 1024)
-    gf = [d for d in fe[:-reps] if d[1].startswith(("gemm_fp8", "gemv_fp8"))]
-    gw = [d for d in wr[:-reps] if d[1].startswith(("gemm_fp8", "gemv_fp8"))]
+    gf, gw = _launches(fe[:-reps]), _launches(wr[:-reps])
     out, pos, tot_b, tot_n = [], 0, 0.0, 0
     for e in manifest["gemm_launches"]:
         n = e["reps"]
@@ -153,7 +166,8 @@ def traffic(fetch_csv, write_csv, manifest):
                         algorithmic_bytes=e["algorithmic_bytes"], ratio=round(hbm / e["algorithmic_bytes"], 2)))
         tot_b += hbm * e["launches_per_step"]
         tot_n += e["launches_per_step"]
-    return dict(kernel="gemm_fp8_kernel", bytes_per_launch=int(tot_b / tot_n), launches_per_step=tot_n,
+    return dict(kernel="FP8 GEMM launches of the step (per shape below)", bytes_per_launch=int(tot_b / tot_n),
+                launches_per_step=tot_n,
                 calibration=dict(copy_bytes=manifest["copy_bytes"], fetch_kib=round(f_copy, 1),
                                  write_kib=round(w_copy, 1), fetch_factor=round(ff, 4), write_factor=round(wf, 4)),
                 by_shape=out)
