@@ -13,8 +13,15 @@
 // * A workgroup of 4 waves owns BM tokens x BN = 4 CW weight rows; wave w owns
 //   all BM tokens x CW rows, so each A fragment read from LDS feeds CW/16 MFMAs
 //   (0.33 KB of LDS reads per MFMA at 144 x 96, a third of a 64 x 64 wave tile).
-//   For the SwiGLU pairing waves 0-1 take BN/2 gate rows and waves 2-3 the
-//   matching up rows.
+//   For the SwiGLU pairing each wave takes CW/2 gate channels and the matching
+//   CW/2 up channels, alternating 16-channel fragments (gate, up, gate, ..).
+// * The weight fragment is the MFMA's first operand and the activation fragment
+//   its second, so the accumulator holds the transposed tile: lane 16 g + r of
+//   fragment (i, j) holds tokens 16 i + r, channels 16 j + 4 g .. + 3. Each lane
+//   thus owns 4 consecutive channels of one token, and the epilogues (SwiGLU,
+//   scaling, bf16 rounding) run in registers and store 8-byte row pieces
+//   without an LDS round trip. The products and their order are those of the
+//   untransposed form, so the bits are the same.
 // * Activations go global -> registers -> LDS (D steps of register staging,
 //   2G LDS stages, one barrier per G steps). Every load is an ordinary
 //   compiler-visible buffer load, so the compiler's wait counts are exact
@@ -72,7 +79,8 @@ __device__ __forceinline__ i32x4v bload16(__amdgpu_buffer_rsrc_t r, uint32_t vof
   return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
 }
 
-// acc += A . B^T for one 16 x 16 x 128 e4m3 tile, accumulator tied in place.
+// acc += A . B^T for one 16 x 16 x 128 e4m3 tile (A rows index the result's
+// rows, held as 4 consecutive rows per lane), accumulator tied in place.
 __device__ __forceinline__ void mfma_acc(f32x4& acc, const i32x8& a, const i32x8& b) {
   asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
@@ -94,7 +102,8 @@ __global__ __launch_bounds__(kThreads) void pack_fp8_kernel(const uint8_t* __res
 }
 
 // Main loop shared by the kernels below: acc (BM x 4 CW tile of this
-// workgroup, wave w owning all BM rows x CW weight rows) = sum over k steps
+// workgroup, wave w owning all BM rows x CW weight rows, transposed: acc[i][j]
+// of lane 16 g + r is tokens 16 i + r, weight rows 16 j + 4 g .. + 3) = sum over k steps
 // [kt0, kt0 + nk) of A . B^T. sB[j] is the byte offset of this wave's weight
 // fragment row j at k step 0. P = weight register stages, D = activation
 // register stages, G = k steps per barrier; nk % lcm(P, D, 2G) == 0.
@@ -216,7 +225,7 @@ __device__ __forceinline__ void pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], uint
       static_for<0, TJ>([&](auto J_) {
         constexpr int j = decltype(J_)::value;
 #pragma unroll
-        for (int i = 0; i < RA; ++i) mfma_acc(acc[i][j], af[i], bq[u % P][j]);
+        for (int i = 0; i < RA; ++i) mfma_acc(acc[i][j], bq[u % P][j], af[i]);
         const i32x4v lo = bload16(rB, voffB, sB[j] + ktn * 2048u);
         const i32x4v hi = bload16(rB, voffB + 16u, sB[j] + ktn * 2048u);
         bq[u % P][j] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
@@ -229,28 +238,34 @@ __device__ __forceinline__ void pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], uint
 #undef ACC_NOPS
 }
 
-// LDS a kernel below needs: the main loop's stages or the bf16 epilogue tile.
-template <int BM, int CW, int G>
+// LDS of the main loop's activation stages.
+template <int BM, int G>
 constexpr int pk_smem() {
-  return 2 * G * BM * 128 > BM * (4 * CW + 8) * 2 ? 2 * G * BM * 128 : BM * (4 * CW + 8) * 2;
+  return 2 * G * BM * 128;
 }
 
-// Gate/up: BM tokens x (BN/2 gate + BN/2 up channels), BN = 4 CW; waves 0-1
-// take the gate rows, waves 2-3 the matching up rows.
+// 4 bf16 (8 bytes) from 4 fp32 values, low to high.
+__device__ __forceinline__ u32x2 pack4_bf16(float a, float b, float c, float d) {
+  return u32x2{pack_bf16x2(a, b), pack_bf16x2(c, d)};
+}
+
+// Gate/up: BM tokens x (BN/2 gate + BN/2 up channels), BN = 4 CW; wave w takes
+// gate channels [w CW/2, (w + 1) CW/2) of the tile and the matching up
+// channels, as fragments j = 2 t (gate, channels 16 t ..) and j = 2 t + 1 (up,
+// the same channels).
 template <int BM, int CW, int P, int D, int G>
 __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
     const uint8_t* __restrict__ qa, const float* __restrict__ sa, const uint8_t* __restrict__ qwp,
     const float* __restrict__ sw, bf16_t* __restrict__ h, int64_t ldh, float* __restrict__ pmax, int M, int half,
     int K, int tiles_m, int tiles_n) {
-  constexpr int BN = 4 * CW, CH = BN / 2;
-  constexpr int RA = BM / 16, TJ = CW / 16;
-  constexpr int EPI_LD = BN + 8;  // bf16 pitch of the epilogue tile
-  constexpr int SMEM = pk_smem<BM, CW, G>();
-  constexpr int CPR = CH / 8;  // 8-channel chunks per row in the SwiGLU pass
+  constexpr int BN = 4 * CW, CH = BN / 2, WCH = CW / 2;
+  constexpr int RA = BM / 16, TJ = CW / 16, TT = TJ / 2;
+  constexpr int SMEM = pk_smem<BM, G>();
+  constexpr int Q16 = CH / 16;  // 16-channel blocks per tile row
   static_assert(SMEM <= 160 * 1024, "LDS budget");
-  static_assert(CH == 2 * CW, "waves 0-1 take the gate rows, waves 2-3 the up rows");
-  static_assert(CH % 64 == 0 && (BM * CPR) % 64 == 0, "64-channel row maxima over whole waves");
+  static_assert(TJ % 2 == 0 && CH % 64 == 0, "gate/up fragment pairs; whole 64-channel row-max blocks");
   __shared__ __align__(1024) uint8_t smem[SMEM];
+  __shared__ float pm16[BM][Q16];  // max |h| per token and 16-channel block of the tile
 
   const int nblk = tiles_m * tiles_n;
   const int b = blockIdx.x;
@@ -262,96 +277,90 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
   const int r16 = lane & 15, g = lane >> 4;
   const int KT = K / 128;
 
-  // Weights: fragment j of this wave is the 16-row group of weight row
-  // (gate half for waves 0-1, up half for waves 2-3) + channel.
+  // Weights: fragment j of this wave is the 16-row group of gate (j even) or
+  // up (j odd) rows of channels tn CH + wave WCH + 16 (j / 2) ..
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   uint32_t sB[TJ];
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
-    const int cl = wave_s * CW + 16 * j;  // tile column
-    const int row = cl < CH ? tn * CH + cl : half + tn * CH + (cl - CH);
+    const int row = (j & 1 ? half : 0) + tn * CH + wave_s * WCH + 16 * (j >> 1);
     sB[j] = (uint32_t)(row / 16) * (uint32_t)KT * 2048u;
   }
   f32x4 acc[RA][TJ];
   pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)(2 * half) * (uint32_t)K, sB, 0, KT);
-  __syncthreads();  // every wave is done with the stages; the tile reuses the LDS
 
-  // y = bf16((acc * sa) * sw) as a row-major tile: gate channels in columns
-  // [0, CH), the matching up channels in [CH, BN).
-  bf16_t* tile = reinterpret_cast<bf16_t*>(smem);
+  // g, u = bf16((acc * sa) * sw); h = bf16(bf16(silu(g)) * u), in registers:
+  // lane 16 g + r holds token 16 i + r, channels c + 4 g .. + 3 of block t.
+  const int c_base = tn * CH + wave * WCH + 4 * g;
+  float swg[TT][4], swu[TT][4];
 #pragma unroll
-  for (int j = 0; j < TJ; ++j) {
-    const int cl = wave * CW + 16 * j + r16;
-    const int row = cl < CH ? tn * CH + cl : half + tn * CH + (cl - CH);
-    const float swv = sw[row];
+  for (int t = 0; t < TT; ++t)
 #pragma unroll
-    for (int i = 0; i < RA; ++i)
+    for (int r = 0; r < 4; ++r) {
+      swg[t][r] = sw[c_base + 16 * t + r];
+      swu[t][r] = sw[half + c_base + 16 * t + r];
+    }
+#pragma unroll
+  for (int i = 0; i < RA; ++i) {
+    const int tl = 16 * i + r16, m = m0 + tl;
+    const float sav = sa[min(m, M - 1)];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      float hv[4], mx = 0.f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int rl = 16 * i + 4 * g + r;
-        const float sav = sa[min(m0 + rl, M - 1)];
-        tile[rl * EPI_LD + cl] = (bf16_t)f32_to_bf16((acc[i][j][r] * sav) * swv);
+        const float gv = round_bf16((acc[i][2 * t][r] * sav) * swg[t][r]);
+        const float uv = round_bf16((acc[i][2 * t + 1][r] * sav) * swu[t][r]);
+        hv[r] = round_bf16(round_bf16(silu(gv)) * uv);
+        mx = fmaxf(mx, fabsf(hv[r]));
       }
+      if (m < M)
+        *reinterpret_cast<u32x2*>(h + (int64_t)m * ldh + c_base + 16 * t) = pack4_bf16(hv[0], hv[1], hv[2], hv[3]);
+      mx = max_rows(mx);  // over the 4 lanes of this token: 16 channels
+      if (g == 0) pm16[tl][wave * TT + t] = mx;
+    }
   }
   __syncthreads();
-  // SwiGLU, 8 channels per thread; the 8 lanes of one row's 64-channel block are
-  // 8 consecutive lanes, which reduce its max |h| for ff_quant_rows_pmax.
-  const int c_base = tn * CH;
+  // Row maxima per 64 channels (4 consecutive 16-channel blocks) for ff_quant_rows_pmax.
   const int64_t npart = half / 64;
-  for (int c = tid; c < BM * CPR; c += kThreads) {
-    const int rl = c / CPR, cc = (c % CPR) * 8;
-    float gv[8], uv[8], hv[8];
-    unpack8(*reinterpret_cast<const u32x4*>(tile + rl * EPI_LD + cc), gv);
-    unpack8(*reinterpret_cast<const u32x4*>(tile + rl * EPI_LD + CH + cc), uv);
-    float mx = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      hv[e] = round_bf16(round_bf16(silu(gv[e])) * uv[e]);
-      mx = fmaxf(mx, fabsf(hv[e]));
-    }
-    mx = fmaxf(mx, dpp<kDppXor1>(mx));
-    mx = fmaxf(mx, dpp<kDppXor2>(mx));
-    mx = fmaxf(mx, dpp<kDppHalfMirror>(mx));
-    const int m = m0 + rl;
-    if (m < M) {
-      *reinterpret_cast<u32x4*>(h + (int64_t)m * ldh + c_base + cc) = pack8(hv);
-      if (cc % 64 == 0) pmax[(int64_t)m * npart + (c_base + cc) / 64] = mx;
-    }
+  for (int c = tid; c < BM * (CH / 64); c += kThreads) {
+    const int tl = c / (CH / 64), q = c % (CH / 64);
+    const int m = m0 + tl;
+    if (m < M)
+      pmax[(int64_t)m * npart + tn * (CH / 64) + q] =
+          fmaxf(fmaxf(pm16[tl][4 * q], pm16[tl][4 * q + 1]), fmaxf(pm16[tl][4 * q + 2], pm16[tl][4 * q + 3]));
   }
 }
 
-// y = bf16((acc * sa) * sw) for one BM x 4 CW tile held in the accumulator
-// layout of the kernels above, staged through LDS so that the stores are
-// 16-byte row chunks. sa per row if sa_rows else one value; sw likewise.
+// y = bf16((acc * sa) * sw) for one BM x 4 CW tile held in the (transposed)
+// accumulator layout of the main loop, stored as 8-byte row pieces: lane
+// 16 g + r of fragment (i, j) writes token m0 + 16 i + r, columns
+// n0 + wave CW + 16 j + 4 g .. + 3. sa per row if sa_rows else one value; sw
+// per column if sw_cols else one value.
 template <int BM, int CW>
-__device__ __forceinline__ void pk_store_tile(const f32x4 (&acc)[BM / 16][CW / 16], uint8_t* smem,
-                                              const float* __restrict__ sa, int sa_rows,
-                                              const float* __restrict__ sw, int sw_cols, bf16_t* __restrict__ y,
-                                              int64_t ldy, int M, int m0, int n0) {
-  constexpr int BN = 4 * CW, RA = BM / 16, TJ = CW / 16, EPI_LD = BN + 8;
+__device__ __forceinline__ void pk_store_tile(const f32x4 (&acc)[BM / 16][CW / 16], const float* __restrict__ sa,
+                                              int sa_rows, const float* __restrict__ sw, int sw_cols,
+                                              bf16_t* __restrict__ y, int64_t ldy, int M, int m0, int n0) {
+  constexpr int RA = BM / 16, TJ = CW / 16;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g = lane >> 4;
-  bf16_t* tile = reinterpret_cast<bf16_t*>(smem);
+  float sav[RA];
+#pragma unroll
+  for (int i = 0; i < RA; ++i) sav[i] = sa[sa_rows ? min(m0 + 16 * i + r16, M - 1) : 0];
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
-    const int cl = wave * CW + 16 * j + r16;
-    const float swv = sw[sw_cols ? n0 + cl : 0];
+    const int col = n0 + wave * CW + 16 * j + 4 * g;
+    float swv[4];
 #pragma unroll
-    for (int i = 0; i < RA; ++i)
+    for (int r = 0; r < 4; ++r) swv[r] = sw[sw_cols ? col + r : 0];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int rl = 16 * i + 4 * g + r;
-        const float sav = sa[sa_rows ? min(m0 + rl, M - 1) : 0];
-        tile[rl * EPI_LD + cl] = (bf16_t)f32_to_bf16((acc[i][j][r] * sav) * swv);
-      }
-  }
-  __syncthreads();
-  constexpr int CHUNKS = BM * BN / 8;
-  for (int c = tid; c < CHUNKS; c += kThreads) {
-    const int rl = c / (BN / 8), cl = (c % (BN / 8)) * 8;
-    const int m = m0 + rl;
-    if (m < M)
-      *reinterpret_cast<u32x4*>(y + (int64_t)m * ldy + n0 + cl) = *reinterpret_cast<const u32x4*>(tile + rl * EPI_LD + cl);
+    for (int i = 0; i < RA; ++i) {
+      const int m = m0 + 16 * i + r16;
+      if (m < M)
+        *reinterpret_cast<u32x2*>(y + (int64_t)m * ldy + col) =
+            pack4_bf16((acc[i][j][0] * sav[i]) * swv[0], (acc[i][j][1] * sav[i]) * swv[1],
+                       (acc[i][j][2] * sav[i]) * swv[2], (acc[i][j][3] * sav[i]) * swv[3]);
+    }
   }
 }
 
@@ -367,7 +376,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_split_packed_kernel(
     int tiles_m, int tiles_n, f32x4* __restrict__ part) {
   constexpr int BN = 4 * CW;
   constexpr int RA = BM / 16, TJ = CW / 16;
-  constexpr int SMEM = pk_smem<BM, CW, G>();
+  constexpr int SMEM = pk_smem<BM, G>();
   static_assert(SMEM <= 160 * 1024, "LDS budget");
   __shared__ __align__(1024) uint8_t smem[SMEM];
 
@@ -394,21 +403,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_split_packed_kernel(
 #pragma unroll
       for (int j = 0; j < TJ; ++j) mine[(i * TJ + j) * kThreads] = acc[i][j];
   } else {
-    __syncthreads();  // every wave is done with the stages; the tile reuses the LDS
-    pk_store_tile<BM, CW>(acc, smem, sa, sa_rows, sw, sw_cols, y, ldy, M, m0, n0);
+    pk_store_tile<BM, CW>(acc, sa, sa_rows, sw, sw_cols, y, ldy, M, m0, n0);
   }
 }
 
 // y for the tiles of a split launch, one workgroup per (tile, 16-row group i):
 // the S partials of each accumulator added in split order 0, 1, .., S-1
 // (independent of which split finished first), then the epilogue of the
-// unsplit kernel for those 16 rows.
+// unsplit kernel for those 16 rows (transposed accumulator layout: lane
+// 16 g + r holds row r, columns 16 j + 4 g .. + 3 of wave w's CW columns).
 template <int BM, int CW, int S>
 __global__ __launch_bounds__(kThreads) void split_reduce_kernel(
     const f32x4* __restrict__ part, const float* __restrict__ sa, int sa_rows, const float* __restrict__ sw,
     int sw_cols, bf16_t* __restrict__ y, int64_t ldy, int M, int tiles_m) {
-  constexpr int RA = BM / 16, TJ = CW / 16, BN = 4 * CW, EPI_LD = BN + 8;
-  __shared__ __align__(16) bf16_t rows[16 * EPI_LD];
+  constexpr int RA = BM / 16, TJ = CW / 16, BN = 4 * CW;
   const int tile = blockIdx.x / RA, i = blockIdx.x % RA;
   const int tm = tile % tiles_m, tn = tile / tiles_m;
   const int m0 = tm * BM + 16 * i, n0 = tn * BN;
@@ -420,26 +428,20 @@ __global__ __launch_bounds__(kThreads) void split_reduce_kernel(
   for (int j = 0; j < TJ; ++j)
 #pragma unroll
     for (int s2 = 0; s2 < S; ++s2) v[j][s2] = tp[((int64_t)s2 * RA * TJ + i * TJ + j) * kThreads];
+  const int m = m0 + r16;
+  const float sav = sa[sa_rows ? min(m, M - 1) : 0];
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
     f32x4 t = v[j][0];
 #pragma unroll
     for (int s2 = 1; s2 < S; ++s2) t = t + v[j][s2];
-    const int cl = wave * CW + 16 * j + r16;
-    const float swv = sw[sw_cols ? n0 + cl : 0];
+    const int col = n0 + wave * CW + 16 * j + 4 * g;
+    float swv[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int rl = 4 * g + r;
-      const float sav = sa[sa_rows ? min(m0 + rl, M - 1) : 0];
-      rows[rl * EPI_LD + cl] = (bf16_t)f32_to_bf16((t[r] * sav) * swv);
-    }
-  }
-  __syncthreads();
-  for (int c = tid; c < 16 * BN / 8; c += kThreads) {
-    const int rl = c / (BN / 8), cl = (c % (BN / 8)) * 8;
-    const int m = m0 + rl;
+    for (int r = 0; r < 4; ++r) swv[r] = sw[sw_cols ? col + r : 0];
     if (m < M)
-      *reinterpret_cast<u32x4*>(y + (int64_t)m * ldy + n0 + cl) = *reinterpret_cast<const u32x4*>(rows + rl * EPI_LD + cl);
+      *reinterpret_cast<u32x2*>(y + (int64_t)m * ldy + col) =
+          pack4_bf16((t[0] * sav) * swv[0], (t[1] * sav) * swv[1], (t[2] * sav) * swv[2], (t[3] * sav) * swv[3]);
   }
 }
 
