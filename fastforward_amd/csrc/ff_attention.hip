@@ -148,9 +148,14 @@ __device__ __forceinline__ void rescale(f32x4 (&o)[8], float alpha) {
   }
 }
 
+// Output row of one (query, head): o / den as bf16, the first DOUT of the 128
+// head dims (DOUT % 4 == 0; the columns past it are the zero padding of a
+// narrower head).
+template <int DOUT = D>
 __device__ __forceinline__ void store_rows(bf16_t* __restrict__ yp, const f32x4 (&o)[8], float den, int g) {
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) {
+    if (16 * dt + 4 * g >= DOUT) continue;
     u32x2 w2;
     w2.x = pack_bf16x2(o[dt][0] / den, o[dt][1] / den);
     w2.y = pack_bf16x2(o[dt][2] / den, o[dt][3] / den);
@@ -352,7 +357,13 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void attention_decode_kernel(
 // Grid: one dimension, heaviest query blocks first across all groups; the
 // group is blockIdx % (hq/HPW), so with 8 XCDs taking workgroups round-robin
 // the groups of one kv head stay on one XCD (and its L2).
-template <int QT, int HPW, int NS>
+//
+// CAUSAL = false: every query sees all t keys (bidirectional attention of the
+// vision tower); only the keys past t in the last block are masked. DOUT: the
+// head dim stored per (query, head) of y, which is (s, hq, DOUT); heads
+// narrower than 128 are zero-padded to 128 in q, k and V^T, which leaves every
+// score and every stored output column exact.
+template <int QT, int HPW, int NS, bool CAUSAL = true, int DOUT = D>
 __global__ __launch_bounds__(kThreads, NS == 2 ? 2 : 1) void attention_prefill_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ vt,
     bf16_t* __restrict__ y, int s_len, int t, int t_pad, int hq, int hk, float c2, int nqb) {
@@ -369,7 +380,7 @@ __global__ __launch_bounds__(kThreads, NS == 2 ? 2 : 1) void attention_prefill_k
   const int kvh = head / (hq / hk);
   const int q0 = qb * QB;
   const int wq0 = q0 + (wave / HPW) * 16 * QT;  // first query of this wave
-  const int kend = min(t, min(s_len, q0 + QB));  // keys [0, kend) are visible to some query
+  const int kend = CAUSAL ? min(t, min(s_len, q0 + QB)) : t;  // keys [0, kend) are visible to some query
   const int nblocks = (kend + 63) / 64;
 
   // Load sources of this lane: blocks wave + 4i, i = 0..7 (0..15 K, 16..31 V^T).
@@ -446,7 +457,7 @@ __global__ __launch_bounds__(kThreads, NS == 2 ? 2 : 1) void attention_prefill_k
     barrier_lds();  // block ib landed for every wave; block ib-1 fully consumed
     if (ib + NS - 1 < nblocks) issue((ib + NS - 1) * 64, (ib + NS - 1) % NS);
     const int kb = ib * 64;
-    if (kb >= s_len || kb > wq0 + 16 * QT - 1) continue;  // wave-uniform: no query of the wave sees it
+    if (CAUSAL && (kb >= s_len || kb > wq0 + 16 * QT - 1)) continue;  // wave-uniform: no query of the wave sees it
     const uint8_t* st_base = smem + (ib % NS) * STAGE;
 
     f32x4 sc[QT][4];
@@ -466,8 +477,8 @@ __global__ __launch_bounds__(kThreads, NS == 2 ? 2 : 1) void attention_prefill_k
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       const int tq0 = wq0 + 16 * qt;  // first query of the tile
-      const bool masked = kb + 63 > tq0 || kb + 63 >= t;
-      const int lim = min(tq0 + r16, t - 1) - kb - 8 * g;
+      const bool masked = CAUSAL ? (kb + 63 > tq0 || kb + 63 >= t) : kb + 63 >= t;
+      const int lim = (CAUSAL ? min(tq0 + r16, t - 1) : t - 1) - kb - 8 * g;
       const float alpha = softmax_block(sc[qt], masked, lim, c2, m[qt], den[qt], pf[qt]);
       rescale(o[qt], alpha);
     }
@@ -484,7 +495,7 @@ __global__ __launch_bounds__(kThreads, NS == 2 ? 2 : 1) void attention_prefill_k
   for (int qt = 0; qt < QT; ++qt) {
     const float dsum = sum_rows(den[qt]);
     const int qi = wq0 + 16 * qt + r16;
-    if (qi < s_len) store_rows(y + ((int64_t)qi * hq + head) * D, o[qt], dsum, g);
+    if (qi < s_len) store_rows<DOUT>(y + ((int64_t)qi * hq + head) * DOUT, o[qt], dsum, g);
   }
 }
 
@@ -610,5 +621,32 @@ extern "C" int ff_attention_vt(const void* q, const void* k, const void* vt, con
                      (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)vt, positions, gather_q, (bf16_t*)y,
                      (int)s, (int)t, (int)t_pad, (int)hq, (int)hk, c2);
   FF_LAUNCH_CHECK("ff_attention_vt");
+  return FF_OK;
+}
+
+extern "C" int ff_attention_full(const void* q, const void* k, const void* vt, void* y, int64_t t, int64_t t_pad,
+                                 int64_t heads, int64_t d_out, float scale, ff_stream_t stream) {
+  FF_REQUIRE(q && k && vt && y, "ff_attention_full: null pointer");
+  FF_REQUIRE(t > 0 && t_pad >= t && t_pad % 64 == 0 && heads > 0, "ff_attention_full: bad sizes t=%lld t_pad=%lld",
+             (long long)t, (long long)t_pad);
+  FF_REQUIRE(d_out == 64 || d_out == 72 || d_out == 128,
+             "ff_attention_full: output head dim %lld unsupported (64, 72, 128)",
+             (long long)d_out);
+  FF_REQUIRE(ff_aligned(q, 16) && ff_aligned(k, 16) && ff_aligned(vt, 16) && ff_aligned(y, 8),
+             "ff_attention_full: alignment");
+  const float c2 = (float)((double)scale * 1.4426950408889634);  // scale * log2(e)
+  const int qt = t <= 1024 ? 1 : 2;
+  const int qb = 16 * qt * 4;  // one head per workgroup: 4 waves x QT tiles of 16 queries
+  const int nqb = (int)((t + qb - 1) / qb);
+  const dim3 grid((unsigned)(nqb * heads)), block(kThreads);
+  hipStream_t st = (hipStream_t)stream;
+#define FF_FULL(QT, DO)                                                                                    \
+  if (qt == QT && d_out == DO)                                                                             \
+    hipLaunchKernelGGL((attention_prefill_kernel<QT, 1, 2, false, DO>), grid, block, 0, st, (const bf16_t*)q, \
+                       (const bf16_t*)k, (const bf16_t*)vt, (bf16_t*)y, (int)t, (int)t, (int)t_pad, (int)heads, \
+                       (int)heads, c2, nqb);
+  FF_FULL(1, 64) FF_FULL(2, 64) FF_FULL(1, 72) FF_FULL(2, 72) FF_FULL(1, 128) FF_FULL(2, 128)
+#undef FF_FULL
+  FF_LAUNCH_CHECK("ff_attention_full");
   return FF_OK;
 }

@@ -1,0 +1,493 @@
+// Vision-tower kernels for gfx950: pixel packing, LayerNorm, the bf16 linear
+// layers (bias, GELU and residual epilogues), the 2-D vision rotary and the
+// zero-padded head layouts the attention kernel reads.
+//
+// The tower is the reference's NativeNormVision.core (scaled_qwen_runtime.py:42-55):
+// patch embedding + interpolated position embedding, then per block
+// h += proj(attn(rope(qkv(LN1(h))))), h += fc2(gelu(fc1(LN2(h)))), DeepStack
+// mergers after the listed blocks and the final patch merger. Every module is
+// a bf16 torch module there, so each kernel rounds to bf16 where that module
+// returns.
+#include <math.h>
+
+#include "ff_common.h"
+
+using namespace ff;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kXcds = 8;
+constexpr int kPatchElems = 1536;  // 3 channels x 2 frames x 16 x 16
+
+// ---------------------------------------------------------------- pixel packing
+//
+// rgb (height, width, 3) uint8 -> patches (n, 1536) bf16 in the order the
+// image processor emits them: patch p of the 2 x 2 merge-block walk (blocks
+// row-major over the (height/32, width/32) grid, the four 16 x 16 patches of a
+// block row-major), element d = (c, frame, y, x) with both frames the same
+// image; value (u8 - 127.5) / 127.5 (pack_rectangle, _family/depth_runtime.py:18-25).
+// One thread per 8 consecutive elements (8 pixels of one row of one channel).
+__global__ __launch_bounds__(kThreads) void pack_pixels_kernel(const uint8_t* __restrict__ rgb,
+                                                               bf16_t* __restrict__ out, int width, int64_t chunks) {
+  const int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x;
+  if (i >= chunks) return;
+  const int64_t p = i / (kPatchElems / 8);
+  const int d = (int)(i % (kPatchElems / 8)) * 8;
+  const int c = d / 512, y0 = (d % 256) / 16, x0 = d % 16;
+  const int gw = width / 16;
+  const int64_t gy = p / (gw / 2 * 4);
+  const int gx = (int)((p / 4) % (gw / 2)), my = (int)(p % 4) / 2, mx = (int)(p % 2);
+  const int64_t y = gy * 32 + my * 16 + y0;
+  const int x = gx * 32 + mx * 16 + x0;
+  const uint8_t* src = rgb + (y * width + x) * 3 + c;
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = ((float)src[3 * e] - 127.5f) / 127.5f;
+  *reinterpret_cast<u32x4*>(out + p * kPatchElems + d) = pack8(v);
+}
+
+// ---------------------------------------------------------------- LayerNorm
+//
+// y = bf16((x - mean) * rstd * w + b) per row, mean and variance in fp32 over
+// the bf16 inputs (two passes over registers), rstd = 1/sqrt(var + eps).
+// One workgroup per row, h % 8 == 0, h <= 8 * 256 * kLnChunks.
+constexpr int kLnChunks = 3;
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = sum_rows(v);
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppRowMirror>(v);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) t += red[w];
+  return t;
+}
+
+__global__ __launch_bounds__(kThreads) void layer_norm_kernel(const bf16_t* __restrict__ x, int64_t x_rs,
+                                                              const bf16_t* __restrict__ w,
+                                                              const bf16_t* __restrict__ b, bf16_t* __restrict__ y,
+                                                              int64_t y_rs, int h, float eps) {
+  __shared__ float red[kThreads / 64];
+  const int64_t row = blockIdx.x;
+  const bf16_t* xr = x + row * x_rs;
+  float v[kLnChunks][8];
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < kLnChunks; ++c) {
+    const int col = 8 * (threadIdx.x + kThreads * c);
+    if (col < h) {
+      unpack8(*reinterpret_cast<const u32x4*>(xr + col), v[c]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += v[c][e];
+    }
+  }
+  const float mean = block_sum(s, red) / (float)h;
+  float q = 0.f;
+#pragma unroll
+  for (int c = 0; c < kLnChunks; ++c) {
+    const int col = 8 * (threadIdx.x + kThreads * c);
+    if (col < h) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float dlt = v[c][e] - mean;
+        q += dlt * dlt;
+      }
+    }
+  }
+  const float var = block_sum(q, red) / (float)h;
+  const float rstd = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int c = 0; c < kLnChunks; ++c) {
+    const int col = 8 * (threadIdx.x + kThreads * c);
+    if (col < h) {
+      float wv[8], bv[8], o[8];
+      unpack8(*reinterpret_cast<const u32x4*>(w + col), wv);
+      unpack8(*reinterpret_cast<const u32x4*>(b + col), bv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (v[c][e] - mean) * rstd * wv[e] + bv[e];
+      *reinterpret_cast<u32x4*>(y + row * y_rs + col) = pack8(o);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- bf16 GEMM
+//
+// y[m, n] = epilogue(sum_k a[m, k] w[n, k]) with a (M, K) and w (N, K) bf16,
+// both K-contiguous (torch Linear weights). A workgroup of 4 waves (2 x 2)
+// owns a BM x BN tile; each wave (BM/2) x (BN/2) as 16 x 16 tiles of
+// v_mfma_f32_16x16x32_bf16. K advances 64 elements (128 bytes) per stage:
+// both operands go global -> LDS with global_load_lds_dwordx4 (8 rows x 128 B
+// per instruction, XOR-swizzled 16-byte chunks), S stages with S - 1 in
+// flight, one barrier per stage. Lane l (row l % 16, g = l / 16) reads chunks
+// 2g and 2g + 1 of its row for the two MFMAs of a stage: k [16 g, 16 g + 8)
+// and [16 g + 8, 16 g + 16) of the 64, the same k for A and B.
+//
+// Epilogue (the bf16 module boundaries of the reference): v = bf16(acc + bias);
+// kGeluTanh: v = bf16(gelu_tanh(v)); kGeluErf: v = bf16(gelu(v)); with a
+// residual r: y = bf16(r + v) (r may be y itself: each element is read and
+// written by one thread).
+constexpr int kActNone = 0, kGeluTanh = 1, kGeluErf = 2;
+
+__device__ __forceinline__ f32x4 mfma_bf16(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                 c, 0, 0, 0);
+}
+
+// GELU with the tanh approximation, as torch computes it in fp32 for bf16
+// tensors: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float k_beta = 0.7978845608028654f;  // sqrt(2 / pi)
+  const float inner = k_beta * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+// Exact GELU: x / 2 (1 + erf(x / sqrt 2)).
+__device__ __forceinline__ float gelu_erf(float x) { return x * 0.5f * (1.0f + erff(x * 0.7071067811865476f)); }
+
+template <int BM, int BN, int S>
+struct GemmCfg {
+  static constexpr int RA = BM / 16, RB = BN / 16;
+  static constexpr int BLOCKS = 2 * (RA + RB);  // 1 KB blocks per stage
+  static constexpr int STAGE = BLOCKS * 1024;
+  static constexpr int WI = RA / 2, WJ = RB / 2;
+  static constexpr int SMEM = S * STAGE;
+  static_assert(SMEM <= 160 * 1024, "LDS budget");
+  static_assert(RA % 2 == 0 && RB % 2 == 0 && BLOCKS % 4 == 0, "2 x 2 waves");
+};
+
+template <int BM, int BN, int S, int OCC, int ACT, bool RESID>
+__global__ __launch_bounds__(kThreads, OCC) void gemm_bf16_kernel(
+    const bf16_t* __restrict__ a, int64_t lda, const bf16_t* __restrict__ w, const bf16_t* __restrict__ bias,
+    bf16_t* y, int64_t ldy, const bf16_t* resid, int64_t ldr, int M, int N, int K, int tiles_m, int tiles_n) {
+  using C = GemmCfg<BM, BN, S>;
+  __shared__ __align__(1024) uint8_t smem[C::SMEM];
+  const int nblk = tiles_m * tiles_n;
+  const int blk_id = blockIdx.x;
+  int logical = blk_id;
+  if (nblk % kXcds == 0) logical = (blk_id % kXcds) * (nblk / kXcds) + blk_id / kXcds;
+  const int tm = logical % tiles_m, tn = logical / tiles_m;  // M fastest: an XCD's tiles share weight slabs
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int r16 = lane & 15, g = lane >> 4;
+
+  // Sources of this lane for each 1 KB block it loads (k offset 0); rows past
+  // M / N are clamped (in bounds; masked at the store).
+  constexpr int PER_WAVE = C::BLOCKS / 4;
+  const uint8_t* src[PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < PER_WAVE; ++i) {
+    const int blk = wave + 4 * i, h = blk & 1;
+    const int rr = 8 * h + (lane >> 3);
+    const int ch = (lane & 7) ^ (rr >> 1);
+    if (blk < 2 * C::RA) {
+      const int row = min(m0 + (blk >> 1) * 16 + rr, M - 1);
+      src[i] = reinterpret_cast<const uint8_t*>(a + (int64_t)row * lda) + 16 * ch;
+    } else {
+      const int row = min(n0 + ((blk - 2 * C::RA) >> 1) * 16 + rr, N - 1);
+      src[i] = reinterpret_cast<const uint8_t*>(w + (int64_t)row * K) + 16 * ch;
+    }
+  }
+  const uint32_t lds0 = lds_addr(smem) + (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 1024;
+  auto issue = [&](int kt, int buf) {
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) lds_dma16(src[i] + (int64_t)kt * 128, lds0 + buf * C::STAGE + 4 * i * 1024);
+  };
+
+  f32x4 acc[C::WI][C::WJ];
+#pragma unroll
+  for (int i = 0; i < C::WI; ++i)
+#pragma unroll
+    for (int j = 0; j < C::WJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = K / 64;
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st)
+    if (st < KT) issue(st, st);
+  const int frag = 128 * (r16 & 7) + 1024 * (r16 >> 3);
+  const int c0 = 16 * ((2 * g) ^ (r16 >> 1)), c1 = 16 * ((2 * g + 1) ^ (r16 >> 1));
+  for (int kt = 0; kt < KT; ++kt) {
+    if (kt + S - 2 < KT) wait_vmcnt<(S - 2) * PER_WAVE>();
+    else wait_vmcnt<0>();
+    barrier_lds();  // every wave's loads for stage kt landed; stage kt - 1 fully consumed
+    if (kt + S - 1 < KT) issue(kt + S - 1, (kt + S - 1) % S);
+    const uint8_t* st = smem + (kt % S) * C::STAGE + frag;
+    u32x4 a0[C::WI], a1[C::WI];
+#pragma unroll
+    for (int i = 0; i < C::WI; ++i) {
+      const uint8_t* p = st + 2 * (wm * C::WI + i) * 1024;
+      a0[i] = *reinterpret_cast<const u32x4*>(p + c0);
+      a1[i] = *reinterpret_cast<const u32x4*>(p + c1);
+    }
+#pragma unroll
+    for (int j = 0; j < C::WJ; ++j) {
+      const uint8_t* p = st + (2 * C::RA + 2 * (wn * C::WJ + j)) * 1024;
+      const u32x4 b0 = *reinterpret_cast<const u32x4*>(p + c0);
+      const u32x4 b1 = *reinterpret_cast<const u32x4*>(p + c1);
+#pragma unroll
+      for (int i = 0; i < C::WI; ++i) acc[i][j] = mfma_bf16(b1, a1[i], mfma_bf16(b0, a0[i], acc[i][j]));
+    }
+  }
+
+  // The weight fragment is the MFMA's first operand, so lane (r16, g) of tile
+  // (i, j) holds row m0 + wm BM/2 + 16 i + r16, columns n0 + wn BN/2 + 16 j + 4 g .. + 3.
+#pragma unroll
+  for (int i = 0; i < C::WI; ++i) {
+    const int m = m0 + wm * (BM / 2) + 16 * i + r16;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < C::WJ; ++j) {
+      const int n = n0 + wn * (BN / 2) + 16 * j + 4 * g;
+      if (n >= N) continue;  // N % 4 == 0: a 4-column group is all in or all out
+      const u32x2 bb = *reinterpret_cast<const u32x2*>(bias + n);
+      float v[4] = {bf16_to_f32(bb.x & 0xFFFFu), bf16_to_f32(bb.x >> 16), bf16_to_f32(bb.y & 0xFFFFu),
+                    bf16_to_f32(bb.y >> 16)};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float t = round_bf16(acc[i][j][r] + v[r]);
+        if constexpr (ACT == kGeluTanh) t = round_bf16(gelu_tanh(t));
+        if constexpr (ACT == kGeluErf) t = round_bf16(gelu_erf(t));
+        v[r] = t;
+      }
+      if constexpr (RESID) {
+        const u32x2 rr = *reinterpret_cast<const u32x2*>(resid + (int64_t)m * ldr + n);
+        v[0] += bf16_to_f32(rr.x & 0xFFFFu);
+        v[1] += bf16_to_f32(rr.x >> 16);
+        v[2] += bf16_to_f32(rr.y & 0xFFFFu);
+        v[3] += bf16_to_f32(rr.y >> 16);
+      }
+      *reinterpret_cast<u32x2*>(y + (int64_t)m * ldy + n) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    }
+  }
+}
+
+// ---------------------------------------------------------------- vision rotary
+//
+// y = bf16(x * cos + rotate_half(x) * sin) in fp32 for q and k of every
+// (token, head), cos / sin (n, hd) fp32 (vision_rope, _legacy/search_kernels.py:111-134;
+// apply_rotary_pos_emb_vision in transformers). Inputs have token stride
+// x_ts and head stride x_hs; outputs y_ts / y_hs, with columns [hd, dpad) of
+// each output head written as zeros. One thread per 4 columns of one
+// (token, head) of q or of k; hd % 8 == 0 so the rotation partner (hd / 2 away)
+// is a whole 4-column group.
+__global__ __launch_bounds__(kThreads) void vision_rope_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, int64_t x_ts, int64_t x_hs,
+    const float* __restrict__ cos, const float* __restrict__ sin, bf16_t* __restrict__ yq, bf16_t* __restrict__ yk,
+    int64_t y_ts, int64_t y_hs, int n, int heads, int hd, int dpad) {
+  const int gpr = dpad / 4;  // 4-column groups per output head row
+  const int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x;
+  const int64_t per = (int64_t)n * heads * gpr;
+  if (i >= 2 * per) return;
+  const bool isk = i >= per;
+  const int64_t r = isk ? i - per : i;
+  const int c = (int)(r % gpr) * 4;
+  const int64_t th = r / gpr;
+  const int head = (int)(th % heads);
+  const int64_t tok = th / heads;
+  bf16_t* dst = (isk ? yk : yq) + tok * y_ts + head * y_hs + c;
+  if (c >= hd) {
+    *reinterpret_cast<u32x2*>(dst) = u32x2{0u, 0u};
+    return;
+  }
+  const bf16_t* xr = (isk ? k : q) + tok * x_ts + head * x_hs;
+  const int half = hd / 2;
+  const int pc = c < half ? c + half : c - half;
+  const u32x2 xv = *reinterpret_cast<const u32x2*>(xr + c);
+  const u32x2 pv = *reinterpret_cast<const u32x2*>(xr + pc);
+  const float4 cv = *reinterpret_cast<const float4*>(cos + tok * hd + c);
+  const float4 sv = *reinterpret_cast<const float4*>(sin + tok * hd + c);
+  const float x4[4] = {bf16_to_f32(xv.x & 0xFFFFu), bf16_to_f32(xv.x >> 16), bf16_to_f32(xv.y & 0xFFFFu),
+                       bf16_to_f32(xv.y >> 16)};
+  float p4[4] = {bf16_to_f32(pv.x & 0xFFFFu), bf16_to_f32(pv.x >> 16), bf16_to_f32(pv.y & 0xFFFFu),
+                 bf16_to_f32(pv.y >> 16)};
+  if (c < half) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) p4[e] = -p4[e];
+  }
+  const float c4[4] = {cv.x, cv.y, cv.z, cv.w}, s4[4] = {sv.x, sv.y, sv.z, sv.w};
+  float o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = x4[e] * c4[e] + p4[e] * s4[e];
+  *reinterpret_cast<u32x2*>(dst) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+}
+
+// V^T with zero padding: v (token stride v_ts, head stride v_hs, hd columns)
+// -> vt (heads, 128, t_pad), rows [hd, 128) and tokens [n, t_pad) zero. One
+// workgroup per (head, 64 tokens): the 64 x hd block is staged in LDS, then
+// each thread writes 8 consecutive tokens of one d row.
+__global__ __launch_bounds__(kThreads) void vision_vt_kernel(const bf16_t* __restrict__ v, int64_t v_ts,
+                                                             int64_t v_hs, bf16_t* __restrict__ vt, int n, int t_pad,
+                                                             int heads, int hd) {
+  __shared__ float tile[64][129];
+  const int head = blockIdx.x % heads, t0 = (blockIdx.x / heads) * 64;
+  for (int c = threadIdx.x; c < 64 * 32; c += kThreads) {
+    const int tt = c / 32, d = (c % 32) * 4;
+    const int tok = t0 + tt;
+    float f[4] = {0.f, 0.f, 0.f, 0.f};
+    if (tok < n && d < hd) {
+      const u32x2 x = *reinterpret_cast<const u32x2*>(v + (int64_t)tok * v_ts + (int64_t)head * v_hs + d);
+      f[0] = bf16_to_f32(x.x & 0xFFFFu);
+      f[1] = bf16_to_f32(x.x >> 16);
+      f[2] = bf16_to_f32(x.y & 0xFFFFu);
+      f[3] = bf16_to_f32(x.y >> 16);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tile[tt][d + e] = f[e];
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < 128 * 8; c += kThreads) {
+    const int d = c % 128, tb = (c / 128) * 8;
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = tile[tb + e][d];
+    *reinterpret_cast<u32x4*>(vt + ((int64_t)head * 128 + d) * t_pad + t0 + tb) = pack8(f);
+  }
+}
+
+// Interpolated position embedding: out[p, :] = bf16(sum_t table[idx[p, t], :] *
+// wt[p, t]) with the products and the sum in fp32, taps in order
+// (fast_pos_embed_interpolate, transformers modeling_qwen3_vl.py:664-679).
+// Indices are clamped to the table's rows. One thread per 8 channels of one
+// patch.
+__global__ __launch_bounds__(kThreads) void pos_interp_kernel(const bf16_t* __restrict__ table,
+                                                              const int64_t* __restrict__ idx,
+                                                              const float* __restrict__ wt, bf16_t* __restrict__ out,
+                                                              int n, int taps, int hidden, int64_t rows) {
+  const int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x;
+  const int cpr = hidden / 8;
+  if (i >= (int64_t)n * cpr) return;
+  const int64_t p = i / cpr;
+  const int c = (int)(i % cpr) * 8;
+  float acc[8];
+  for (int t = 0; t < taps; ++t) {
+    float e[8];
+    const int64_t r = min(max(idx[p * taps + t], (int64_t)0), rows - 1);
+    unpack8(*reinterpret_cast<const u32x4*>(table + r * hidden + c), e);
+    const float wv = wt[p * taps + t];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[q] = t == 0 ? e[q] * wv : acc[q] + e[q] * wv;
+  }
+  *reinterpret_cast<u32x4*>(out + p * hidden + c) = pack8(acc);
+}
+
+template <int BM, int BN, int S, int OCC>
+int launch_gemm(const void* a, int64_t lda, const void* w, const void* bias, void* y, int64_t ldy, const void* resid,
+                int64_t ldr, int64_t m, int64_t n, int64_t k, int act, hipStream_t st) {
+  const int tiles_m = (int)((m + BM - 1) / BM), tiles_n = (int)((n + BN - 1) / BN);
+  const dim3 grid((unsigned)(tiles_m * tiles_n)), block(kThreads);
+#define FF_G(ACT, RES)                                                                                          \
+  if (act == ACT && (resid != nullptr) == RES)                                                                  \
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, S, OCC, ACT, RES>), grid, block, 0, st, (const bf16_t*)a, lda, \
+                       (const bf16_t*)w, (const bf16_t*)bias, (bf16_t*)y, ldy, (const bf16_t*)resid, ldr, (int)m, \
+                       (int)n, (int)k, tiles_m, tiles_n);
+  FF_G(kActNone, false) FF_G(kActNone, true) FF_G(kGeluTanh, false) FF_G(kGeluErf, false)
+#undef FF_G
+  return FF_OK;
+}
+
+}  // namespace
+
+extern "C" int ff_pack_pixels(const void* rgb, void* out, int64_t height, int64_t width, ff_stream_t stream) {
+  FF_REQUIRE(rgb && out, "ff_pack_pixels: null pointer");
+  FF_REQUIRE(height > 0 && width > 0 && height % 32 == 0 && width % 32 == 0,
+             "ff_pack_pixels: height and width must be multiples of 32 (got %lld x %lld)", (long long)height,
+             (long long)width);
+  FF_REQUIRE(ff_aligned(out, 16), "ff_pack_pixels: alignment");
+  const int64_t chunks = (height / 16) * (width / 16) * (kPatchElems / 8);
+  hipLaunchKernelGGL(pack_pixels_kernel, dim3((unsigned)((chunks + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const uint8_t*)rgb, (bf16_t*)out, (int)width, chunks);
+  FF_LAUNCH_CHECK("ff_pack_pixels");
+  return FF_OK;
+}
+
+extern "C" int ff_layer_norm(const void* x, int64_t x_rs, const void* w, const void* b, void* y, int64_t y_rs,
+                             int64_t rows, int64_t h, float eps, ff_stream_t stream) {
+  FF_REQUIRE(x && w && b && y, "ff_layer_norm: null pointer");
+  FF_REQUIRE(rows >= 0 && h > 0 && h % 8 == 0 && h <= 8 * kThreads * kLnChunks && x_rs >= h && y_rs >= h &&
+                 x_rs % 8 == 0 && y_rs % 8 == 0,
+             "ff_layer_norm: bad sizes rows=%lld h=%lld", (long long)rows, (long long)h);
+  FF_REQUIRE(ff_aligned(x, 16) && ff_aligned(w, 16) && ff_aligned(b, 16) && ff_aligned(y, 16),
+             "ff_layer_norm: alignment");
+  if (rows == 0) return FF_OK;
+  hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)rows), dim3(kThreads), 0, (hipStream_t)stream,
+                     (const bf16_t*)x, x_rs, (const bf16_t*)w, (const bf16_t*)b, (bf16_t*)y, y_rs, (int)h, eps);
+  FF_LAUNCH_CHECK("ff_layer_norm");
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_bf16(const void* a, int64_t lda, const void* w, const void* bias, void* y, int64_t ldy,
+                            const void* resid, int64_t ldr, int64_t m, int64_t n, int64_t k, int act,
+                            ff_stream_t stream) {
+  FF_REQUIRE(a && w && bias && y, "ff_gemm_bf16: null pointer");
+  FF_REQUIRE(m > 0 && n > 0 && n % 4 == 0 && k > 0 && k % 64 == 0 && lda >= k && ldy >= n && lda % 8 == 0 &&
+                 ldy % 4 == 0 && (!resid || (ldr >= n && ldr % 4 == 0)) && m * lda < (int64_t(1) << 40),
+             "ff_gemm_bf16: bad sizes m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
+  FF_REQUIRE(act == kActNone || act == kGeluTanh || act == kGeluErf, "ff_gemm_bf16: act %d unknown", act);
+  FF_REQUIRE(!resid || act == kActNone, "ff_gemm_bf16: a residual add takes no activation");
+  FF_REQUIRE(ff_aligned(a, 16) && ff_aligned(w, 16) && ff_aligned(bias, 8) && ff_aligned(y, 8) &&
+                 (!resid || ff_aligned(resid, 8)),
+             "ff_gemm_bf16: alignment");
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t big = ((m + 127) / 128) * ((n + 127) / 128);
+  // 128 x 128 tiles at two workgroups per CU when they fill the GPU twice,
+  // else 64 x 128 tiles (more workgroups for the narrow projections).
+  if (big >= 512)
+    launch_gemm<128, 128, 2, 2>(a, lda, w, bias, y, ldy, resid, ldr, m, n, k, act, st);
+  else
+    launch_gemm<64, 128, 3, 2>(a, lda, w, bias, y, ldy, resid, ldr, m, n, k, act, st);
+  FF_LAUNCH_CHECK("ff_gemm_bf16");
+  return FF_OK;
+}
+
+extern "C" int ff_vision_rope(const void* q, const void* k, int64_t x_ts, int64_t x_hs, const float* cos,
+                              const float* sin, void* yq, void* yk, int64_t y_ts, int64_t y_hs, int64_t n,
+                              int64_t heads, int64_t hd, int64_t dpad, ff_stream_t stream) {
+  FF_REQUIRE(q && k && cos && sin && yq && yk, "ff_vision_rope: null pointer");
+  FF_REQUIRE(n > 0 && heads > 0 && hd > 0 && hd % 8 == 0 && dpad >= hd && dpad % 4 == 0 && x_ts % 4 == 0 &&
+                 x_hs % 4 == 0 && y_ts % 4 == 0 && y_hs % 4 == 0,
+             "ff_vision_rope: bad sizes n=%lld heads=%lld hd=%lld dpad=%lld", (long long)n, (long long)heads,
+             (long long)hd, (long long)dpad);
+  FF_REQUIRE(ff_aligned(q, 8) && ff_aligned(k, 8) && ff_aligned(cos, 16) && ff_aligned(sin, 16) &&
+                 ff_aligned(yq, 8) && ff_aligned(yk, 8),
+             "ff_vision_rope: alignment");
+  const int64_t threads = 2 * n * heads * (dpad / 4);
+  hipLaunchKernelGGL(vision_rope_kernel, dim3((unsigned)((threads + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const bf16_t*)q, (const bf16_t*)k, x_ts, x_hs, cos, sin, (bf16_t*)yq,
+                     (bf16_t*)yk, y_ts, y_hs, (int)n, (int)heads, (int)hd, (int)dpad);
+  FF_LAUNCH_CHECK("ff_vision_rope");
+  return FF_OK;
+}
+
+extern "C" int ff_vision_vt(const void* v, int64_t v_ts, int64_t v_hs, void* vt, int64_t n, int64_t t_pad,
+                            int64_t heads, int64_t hd, ff_stream_t stream) {
+  FF_REQUIRE(v && vt, "ff_vision_vt: null pointer");
+  FF_REQUIRE(n > 0 && t_pad >= n && t_pad % 64 == 0 && heads > 0 && hd > 0 && hd <= 128 && hd % 4 == 0 &&
+                 v_ts % 4 == 0 && v_hs % 4 == 0,
+             "ff_vision_vt: bad sizes");
+  FF_REQUIRE(ff_aligned(v, 8) && ff_aligned(vt, 16), "ff_vision_vt: alignment");
+  hipLaunchKernelGGL(vision_vt_kernel, dim3((unsigned)(heads * (t_pad / 64))), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const bf16_t*)v, v_ts, v_hs, (bf16_t*)vt, (int)n, (int)t_pad, (int)heads,
+                     (int)hd);
+  FF_LAUNCH_CHECK("ff_vision_vt");
+  return FF_OK;
+}
+
+extern "C" int ff_pos_interp(const void* table, const int64_t* idx, const float* wt, void* out, int64_t n,
+                             int64_t taps, int64_t hidden, int64_t rows, ff_stream_t stream) {
+  FF_REQUIRE(table && idx && wt && out, "ff_pos_interp: null pointer");
+  FF_REQUIRE(n > 0 && taps > 0 && hidden > 0 && hidden % 8 == 0 && rows > 0, "ff_pos_interp: bad sizes");
+  FF_REQUIRE(ff_aligned(table, 16) && ff_aligned(out, 16), "ff_pos_interp: alignment");
+  const int64_t threads = n * (hidden / 8);
+  hipLaunchKernelGGL(pos_interp_kernel, dim3((unsigned)((threads + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const bf16_t*)table, idx, wt, (bf16_t*)out, (int)n, (int)taps,
+                     (int)hidden, rows);
+  FF_LAUNCH_CHECK("ff_pos_interp");
+  return FF_OK;
+}

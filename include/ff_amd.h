@@ -258,6 +258,68 @@ int ff_mrope_cos_sin(const int64_t* pos, const float* inv_freq, void* cos, void*
                      int64_t d, int sec_h, int sec_w, ff_stream_t stream);
 
 #ifdef __cplusplus
+/* ---------------------------------------------------------------- vision tower
+ * The reference runs the vision tower as bf16 torch modules inside
+ * NativeNormVision.core (scaled_qwen_runtime.py:42-55) with only the rotary
+ * fused (vision_rope); the entry points below replace those modules. */
+
+/* pack_rectangle / pack_rgb (_family/depth_runtime.py:18-25,
+ * _legacy/sub10_runtime.py:22-29): rgb (height, width, 3) uint8 -> patches
+ * (height/16 * width/16, 1536) bf16 in the processor's 2 x 2 merge-block order,
+ * both temporal frames the same image, value bf16((u8 - 127.5) / 127.5).
+ * height % 32 == 0, width % 32 == 0. */
+int ff_pack_pixels(const void* rgb, void* out, int64_t height, int64_t width, ff_stream_t stream);
+
+/* The vision tower's interpolated position embedding
+ * (fast_pos_embed_interpolate, transformers modeling_qwen3_vl.py:664-679, which
+ * the reference computes once per image geometry in VisionGraph.geo,
+ * _legacy/vision_graph_runtime.py:11-15): out[p] = bf16(sum_t table[idx[p, t]] *
+ * wt[p, t]) in fp32, taps in order; table (rows, hidden) bf16, idx (n, taps)
+ * int64 (clamped to [0, rows)), wt (n, taps) fp32. hidden % 8 == 0. */
+int ff_pos_interp(const void* table, const int64_t* idx, const float* wt, void* out, int64_t n,
+                  int64_t taps, int64_t hidden, int64_t rows, ff_stream_t stream);
+
+/* torch.nn.LayerNorm (the vision blocks' norm1/norm2 and the patch mergers'
+ * norm, transformers modeling_qwen3_vl.py:122-137,279-306): y = bf16((x - mean)
+ * * rstd * w + b) per row of h elements, statistics in fp32. Row strides x_rs,
+ * y_rs. h % 8 == 0, h <= 6144. */
+int ff_layer_norm(const void* x, int64_t x_rs, const void* w, const void* b, void* y, int64_t y_rs,
+                  int64_t rows, int64_t h, float eps, ff_stream_t stream);
+
+/* A bf16 torch.nn.Linear with its neighbours fused (the vision tower's qkv,
+ * proj, linear_fc1/fc2 and patch-embedding projection, modeling_qwen3_vl.py:77-107,
+ * 196-306): v = bf16(a . w^T + bias) for a (m, k) row stride lda and w (n, k);
+ * act 1: v = bf16(gelu_tanh(v)), act 2: v = bf16(gelu(v)) (erf); with resid
+ * (row stride ldr, may be y): y = bf16(resid + v). y row stride ldy.
+ * k % 64 == 0 (pad k with zero columns of a and w), n % 4 == 0. */
+int ff_gemm_bf16(const void* a, int64_t lda, const void* w, const void* bias, void* y, int64_t ldy,
+                 const void* resid, int64_t ldr, int64_t m, int64_t n, int64_t k, int act, ff_stream_t stream);
+
+/* vision_rope (_legacy/search_kernels.py:111-134): yq/yk = bf16(x * cos +
+ * rotate_half(x) * sin) in fp32, cos/sin (n, hd) fp32. q, k with token stride
+ * x_ts and head stride x_hs (views of the packed qkv output); outputs with
+ * y_ts / y_hs and columns [hd, dpad) of each head set to 0 (dpad = hd for the
+ * reference's (n, heads, hd) layout, 128 for the zero-padded head-major layout
+ * ff_attention_full reads). hd % 8 == 0. */
+int ff_vision_rope(const void* q, const void* k, int64_t x_ts, int64_t x_hs, const float* cos,
+                   const float* sin, void* yq, void* yk, int64_t y_ts, int64_t y_hs, int64_t n,
+                   int64_t heads, int64_t hd, int64_t dpad, ff_stream_t stream);
+
+/* The transposed, zero-padded V of the vision attention (no reference
+ * counterpart: the layout ff_attention_full reads): v (token stride v_ts, head
+ * stride v_hs, hd columns) -> vt (heads, 128, t_pad), zeros for d >= hd and
+ * tokens >= n. hd <= 128, t_pad % 64 == 0. */
+int ff_vision_vt(const void* v, int64_t v_ts, int64_t v_hs, void* vt, int64_t n, int64_t t_pad,
+                 int64_t heads, int64_t hd, ff_stream_t stream);
+
+/* Bidirectional multi-head attention of the vision blocks (the sdpa call with
+ * is_causal=False of scaled_qwen_runtime.py:51): q, k (heads, t, 128) with head
+ * dims past the model's zero, vt (heads, 128, t_pad) from ff_vision_vt; fp32
+ * scores and softmax statistics, P rounded to bf16 before P.V, fp32
+ * accumulation. y (t, heads, d_out) bf16. d_out in {64, 72, 128}. */
+int ff_attention_full(const void* q, const void* k, const void* vt, void* y, int64_t t, int64_t t_pad,
+                      int64_t heads, int64_t d_out, float scale, ff_stream_t stream);
+
 }
 #endif
 #endif /* FF_AMD_H */

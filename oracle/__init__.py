@@ -13,7 +13,7 @@ Every function cites the reference file:line it restates (paths relative to
 (independent numpy / brute-force / closed-form / third-party checks) is listed
 in ``oracle.PINNING``; ``tests/test_oracle_pins.py`` runs those checks.
 """
-from . import ops, model  # noqa: F401
+from . import ops, model, vision  # noqa: F401
 
 # function -> the independent checks in tests/test_oracle_pins.py that pin it.
 PINNING = {
@@ -35,4 +35,13 @@ PINNING = {
     "mrope_cos_sin": "transformers Qwen3VLTextRotaryEmbedding (test_mrope_cos_sin_match_hf)",
     "choice": "reference contract tests: ties -> lowest index, probabilities sum to 1",
     "model.step": "unquantized layer stack vs transformers Qwen3VLTextModel (test_model_matches_hf_text_model)",
+    "vision.pack_pixels": "transformers Qwen2-VL PIL image processor, bit-exact; division-rounding stability "
+                          "(tests/test_oracle_vision_pins.py)",
+    "vision.rot_pos_freqs / pos_interp / pos_embeds": "transformers rot_pos_emb, "
+                          "get_vision_interpolation_indices_and_weights, fast_pos_embed_interpolate, bit-exact",
+    "vision.vision_rope": "transformers apply_rotary_pos_emb_vision, bit-exact",
+    "vision.layer_norm": "torch layer_norm (bf16) and fp64 closed form, <= 1 ulp",
+    "vision.gelu_tanh / gelu_erf": "fp64 closed forms within 1 ulp + fp32 cancellation",
+    "vision.attention": "pure-Python softmax loops (fp64)",
+    "vision.tower": "transformers Qwen3VLVisionModel (bf16, CPU) end to end, rel L2 <= 1%",
 }

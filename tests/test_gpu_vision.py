@@ -1,0 +1,312 @@
+"""Vision tower on the gfx950 kernels against the CPU oracle (oracle/vision.py).
+
+Tolerances (stated per op):
+* bit-exact: pixel packing (the same fp32 quotient rounded once), the vision
+  rotary (the same two fp32 products and sum, rounded once), the zero-padded
+  V^T layout, the interpolated position embedding (fp32 products summed in tap
+  order), graph replays against the eager step.
+* LayerNorm: <= 1 bf16 ulp, exact for all but 2% (fp32 statistics summed in a
+  different order than the oracle's).
+* bf16 linear (+ GELU / residual): within 1 bf16 ulp + 2^-16 * sum_k |a_k w_k|
+  of the fp64 product before the epilogue's rounding, and equal to the oracle's
+  bf16 output for >= 95% of the elements; after GELU / residual within 2 ulps
+  + that bound (an absolute bound: outputs near zero after cancellation carry
+  it), equal for >= 90%.
+* attention: |gpu - oracle| <= 1/64 absolute and relative RMS <= 0.5% (P rounded
+  to bf16 inside the online softmax; the oracle is exact fp64).
+* whole tower (teacher-forced per block and end to end over 3 blocks):
+  relative L2 <= 1% per block output, <= 2% for the merged and DeepStack
+  features.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import vision as OV
+from tests.helpers import assert_bf16_close, bf16_ulps
+
+pytestmark = pytest.mark.gpu
+
+BF16 = torch.bfloat16
+F32 = torch.float32
+DEV = "cuda"
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _rel_l2(a, b):
+    a, b = a.float().cpu(), b.float().cpu()
+    return float((a - b).norm() / b.norm())
+
+
+def test_pack_pixels_bit_exact(gpu):
+    from fastforward_amd.vision import pack_rgb
+    rng = np.random.default_rng(3)
+    for h, w in ((64, 96), (32, 32), (128, 64)):
+        rgb = rng.integers(0, 256, size=(h, w, 3), dtype=np.uint8)
+        got = pack_rgb(torch.from_numpy(rgb).to(DEV)).cpu()
+        assert torch.equal(got, OV.pack_pixels(rgb)), (h, w)
+
+
+@pytest.mark.parametrize("rows,h", [(37, 1152), (5, 4608), (64, 1024), (3, 64)])
+def test_layer_norm(gpu, rows, h):
+    from fastforward_amd.vision import Norm, layer_norm
+    x = (torch.randn(rows, h, generator=_g(h)) * 3 + 0.5).to(BF16)
+    w = (1 + 0.2 * torch.randn(h, generator=_g(h + 1))).to(BF16)
+    b = (0.3 * torch.randn(h, generator=_g(h + 2))).to(BF16)
+    got = layer_norm(x.to(DEV), Norm(w.to(DEV), b.to(DEV)), 1e-6).cpu()
+    assert_bf16_close(got, OV.layer_norm(x, w, b, 1e-6), max_ulps=1, max_frac=0.02, what="layer_norm")
+
+
+def _ulp(x):
+    return torch.from_numpy(2.0 ** (np.floor(np.log2(np.maximum(np.abs(x.numpy()), 2.0 ** -126))) - 7))
+
+
+def _linear_bound(x, w, b):
+    """(exact, |y - exact| allowed before the epilogue rounding): 1 bf16 ulp +
+    2^-16 sum_k |a_k w_k| (fp32 accumulation of exact bf16 products)."""
+    xd, wd = x.to(torch.float64), w.to(torch.float64)
+    exact = xd @ wd.T + b.to(torch.float64)
+    mag = xd.abs() @ wd.abs().T
+    return exact, _ulp(exact) + mag * 2.0 ** -16
+
+
+def _assert_within(got, want, slack, what):
+    """|got - want| <= 2 bf16 ulps of want + slack (an absolute bound carried from
+    the GEMM), and equal to the oracle's bf16 value for >= 90% of the elements."""
+    g, w_ = got.to(torch.float64), want.to(torch.float64)
+    d = (g - w_).abs()
+    ok = d <= 2 * _ulp(w_) + slack
+    assert bool(ok.all()), f"{what}: {int((~ok).sum())} elements outside the bound"
+    eq = float((got.to(BF16) == want.to(BF16)).float().mean())
+    assert eq >= 0.9, f"{what}: only {eq:.3f} of the elements equal the oracle's"
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 256, 1152), (64, 3456, 1152), (513, 1152, 4352), (2048, 512, 1536)])
+def test_gemm_bf16_plain(gpu, m, n, k):
+    from fastforward_amd.vision import Lin, linear
+    x = torch.randn(m, k, generator=_g(m + k)).to(BF16)
+    w = (torch.randn(n, k, generator=_g(n)) * 0.03).to(BF16)
+    b = (torch.randn(n, generator=_g(n + 1)) * 0.1).to(BF16)
+    got = linear(x.to(DEV), Lin(w.to(DEV), b.to(DEV))).cpu().to(torch.float64)
+    exact, bound = _linear_bound(x, w, b)
+    assert bool(((got - exact).abs() <= bound).all()), "bf16 GEMM outside the fp32-accumulation bound"
+    eq = float((got.to(BF16) == OV.linear(x, w, b)).float().mean())
+    assert eq >= 0.95, f"only {eq:.3f} of the outputs equal the oracle's"
+
+
+@pytest.mark.parametrize("act", [1, 2])
+def test_gemm_bf16_gelu(gpu, act):
+    from fastforward_amd.vision import Lin, linear
+    m, n, k = 200, 4352, 1152
+    x = torch.randn(m, k, generator=_g(5)).to(BF16)
+    w = (torch.randn(n, k, generator=_g(6)) * 0.05).to(BF16)
+    b = (torch.randn(n, generator=_g(7)) * 0.1).to(BF16)
+    got = linear(x.to(DEV), Lin(w.to(DEV), b.to(DEV)), act=act).cpu()
+    f = OV.gelu_tanh if act == 1 else OV.gelu_erf
+    _, bound = _linear_bound(x, w, b)
+    # |gelu'| <= 1.13: the pre-activation bound carries over
+    _assert_within(got, f(OV.linear(x, w, b)), 1.13 * bound, f"gemm_bf16 act {act}")
+
+
+def test_gemm_bf16_residual_in_place(gpu):
+    from fastforward_amd.vision import Lin, linear
+    m, n, k = 260, 1152, 1152
+    x = torch.randn(m, k, generator=_g(8)).to(BF16)
+    w = (torch.randn(n, k, generator=_g(9)) * 0.03).to(BF16)
+    b = (torch.randn(n, generator=_g(10)) * 0.1).to(BF16)
+    h = torch.randn(m, n, generator=_g(11)).to(BF16)
+    hd = h.to(DEV)
+    linear(x.to(DEV), Lin(w.to(DEV), b.to(DEV)), resid=hd, out=hd)
+    want = (h.float() + OV.linear(x, w, b).float()).to(BF16)
+    _, bound = _linear_bound(x, w, b)
+    _assert_within(hd.cpu(), want, bound, "gemm_bf16 residual")
+
+
+def test_vision_rope_bit_exact_and_padded_layout(gpu):
+    from fastforward_amd._lib import call, ptr, stream
+    from fastforward_amd.vision import VISION_PRESETS, rope_tables, vision_rope
+    cfg = VISION_PRESETS["qwen3vl-8b"]
+    gh, gw = 8, 12
+    n, nh, hd = gh * gw, cfg.heads, cfg.head_dim
+    cos, sin = rope_tables(cfg, gh, gw)
+    qkv = torch.randn(n, 3, nh, hd, generator=_g(12)).to(BF16)
+    q, k = qkv[:, 0], qkv[:, 1]
+    want_q, want_k = OV.vision_rope(q, k, cos, sin)
+    qd = qkv.to(DEV)
+    yq, yk = vision_rope(qd[:, 0], qd[:, 1], cos.to(DEV), sin.to(DEV))
+    assert torch.equal(yq.cpu(), want_q) and torch.equal(yk.cpu(), want_k)
+    # head-major, zero-padded to 128 (the attention layout); every device input
+    # is held in a variable until the kernel has run
+    pq = torch.full((nh, n, 128), float("nan"), device=DEV).to(BF16)
+    pk = torch.full((nh, n, 128), float("nan"), device=DEV).to(BF16)
+    cd, sd = cos.to(DEV), sin.to(DEV)
+    call("ff_vision_rope", ptr(qd[:, 0]), ptr(qd[:, 1]), 3 * nh * hd, hd, ptr(cd), ptr(sd),
+         ptr(pq), ptr(pk), 128, n * 128, n, nh, hd, 128, stream())
+    torch.cuda.synchronize()
+    assert torch.equal(pq[:, :, :hd].cpu(), want_q.transpose(0, 1))
+    assert torch.equal(pk[:, :, :hd].cpu(), want_k.transpose(0, 1))
+    assert not bool(pq[:, :, hd:].float().abs().sum()) and not bool(pk[:, :, hd:].float().abs().sum())
+
+
+def test_vision_vt_layout(gpu):
+    from fastforward_amd._lib import call, ptr, stream
+    n, nh, hd, n_pad = 100, 4, 72, 128
+    v = torch.randn(n, nh, hd, generator=_g(13)).to(BF16)
+    vt = torch.full((nh, 128, n_pad), float("nan"), device=DEV).to(BF16)
+    vd = v.to(DEV)
+    call("ff_vision_vt", ptr(vd), nh * hd, hd, ptr(vt), n, n_pad, nh, hd, stream())
+    torch.cuda.synchronize()
+    want = torch.zeros(nh, 128, n_pad, dtype=BF16)
+    want[:, :hd, :n] = v.permute(1, 2, 0)
+    assert torch.equal(vt.cpu(), want)
+
+
+@pytest.mark.parametrize("n,nh,hd", [(300, 4, 72), (2048, 2, 72), (130, 3, 64)])
+def test_attention_full(gpu, n, nh, hd):
+    from fastforward_amd._lib import call, ptr, stream
+    q, k, v = (torch.randn(n, nh, hd, generator=_g(20 + i)).to(BF16) for i in range(3))
+    n_pad = (n + 63) // 64 * 64
+    def pad(x):
+        out = torch.zeros(nh, n, 128, dtype=BF16)
+        out[:, :, :hd] = x.transpose(0, 1)
+        return out.to(DEV)
+    vt = torch.zeros(nh, 128, n_pad, dtype=BF16)
+    vt[:, :hd, :n] = v.permute(1, 2, 0)
+    y = torch.empty(n, nh * hd, device=DEV, dtype=BF16)
+    qd, kd, vtd = pad(q), pad(k), vt.to(DEV)
+    call("ff_attention_full", ptr(qd), ptr(kd), ptr(vtd), ptr(y), n, n_pad, nh, hd, float(hd ** -0.5), stream())
+    torch.cuda.synchronize()
+    want = OV.attention(q, k, v, hd ** -0.5).float()
+    got = y.cpu().float()
+    assert float((got - want).abs().max()) <= 1 / 64
+    assert float(((got - want).norm() / want.norm())) <= 5e-3
+
+
+def test_pos_interp_bit_exact(gpu):
+    from fastforward_amd.vision import VisionConfig, interp_taps
+    from fastforward_amd._lib import call, ptr, stream
+    cfg = VisionConfig("t", 1, 64, 2, 96, 32, (), pos_side=6)
+    table = (torch.randn(36, 64, generator=_g(30)) * 0.1).to(BF16)
+    shape = OV.VisionShape(depth=1, hidden=64, heads=2, inter=96, out_hidden=32, deepstack=(), pos_side=6)
+    for gh, gw in ((4, 8), (6, 6), (2, 10)):
+        idx, wt = interp_taps(cfg, gh, gw)
+        out = torch.empty(gh * gw, 64, device=DEV, dtype=BF16)
+        td, idd, wd = table.to(DEV), idx.to(DEV), wt.to(DEV)
+        call("ff_pos_interp", ptr(td), ptr(idd), ptr(wd), ptr(out), gh * gw, 4, 64, 36, stream())
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), OV.pos_embeds(shape, table, gh, gw)), (gh, gw)
+
+
+def _small_tower(seed=0):
+    """A 3-block tower with the 8B head width (8 heads of 72), padded MLP
+    (200 -> 256) and DeepStack after blocks 0 and 2."""
+    from fastforward_amd.vision import VisionConfig, make_vision
+    cfg = VisionConfig("small", 3, 576, 8, 200, 96, (0, 2), pos_side=6)
+    return cfg, make_vision(cfg, seed=seed, std=0.05)
+
+
+def _to_oracle(cfg, w):
+    shape = OV.VisionShape(depth=cfg.depth, hidden=cfg.hidden, heads=cfg.heads, inter=cfg.inter,
+                           out_hidden=cfg.out_hidden, deepstack=tuple(cfg.deepstack), pos_side=cfg.pos_side)
+    c = lambda t: t.cpu()  # noqa: E731
+    blocks = [OV.VisionBlock(c(b.norm1.w), c(b.norm1.b), c(b.qkv.w), c(b.qkv.b), c(b.proj.w), c(b.proj.b),
+                             c(b.norm2.w), c(b.norm2.b), c(b.fc1.w[:cfg.inter]), c(b.fc1.b[:cfg.inter]),
+                             c(b.fc2.w[:, :cfg.inter]), c(b.fc2.b)) for b in w.blocks]
+    mg = lambda m: OV.Merger(c(m.norm.w), c(m.norm.b), c(m.fc1.w), c(m.fc1.b), c(m.fc2.w), c(m.fc2.b),  # noqa: E731
+                             m.postshuffle)
+    return shape, OV.VisionWeights(c(w.patch.w), c(w.patch.b), c(w.pos_embed), blocks, mg(w.merger),
+                                   [mg(m) for m in w.deep])
+
+
+def test_vision_tower_matches_oracle(gpu):
+    from fastforward_amd.vision import VisionRuntime
+    cfg, w = _small_tower()
+    gh, gw = 8, 12
+    rt = VisionRuntime(cfg, w, gh, gw)
+    rng = np.random.default_rng(4)
+    rgb = rng.integers(0, 256, size=(16 * gh, 16 * gw, 3), dtype=np.uint8)
+    rt.set_image(torch.from_numpy(rgb))
+    trace = []
+    merged, deep = rt.step(trace)
+    torch.cuda.synchronize()
+    shape, ow = _to_oracle(cfg, w)
+    otrace = []
+    omerged, odeep = OV.tower(shape, ow, OV.pack_pixels(rgb), gh, gw, otrace)
+    for j, (a, b) in enumerate(zip(trace, otrace)):
+        assert _rel_l2(a, b) <= 1e-2, f"block {j}: {_rel_l2(a, b):.3e}"
+    assert _rel_l2(merged, omerged) <= 2e-2
+    for a, b in zip(deep, odeep):
+        assert _rel_l2(a, b) <= 2e-2
+    # teacher-forced: blocks 1.. from the oracle's input to them
+    cos, sin = OV.rope_cos_sin(shape, gh, gw)
+    for j in range(1, cfg.depth):
+        rt.h.copy_(otrace[j - 1].to(DEV))
+        _run_block(rt, j)
+        want = OV.block(shape, ow.blocks[j], otrace[j - 1], cos, sin)
+        assert _rel_l2(rt.h, want) <= 5e-3, f"teacher-forced block {j}: {_rel_l2(rt.h, want):.3e}"
+
+
+def _run_block(rt, j):
+    """Block j of the runtime's weights on rt.h in place (the step's calls)."""
+    from fastforward_amd._lib import call, ptr, stream
+    from fastforward_amd.vision import ACT_GELU_TANH, layer_norm, linear
+    cfg, blk, s = rt.cfg, rt.w.blocks[j], stream()
+    n, H, HD, NH = rt.n, cfg.hidden, cfg.head_dim, cfg.heads
+    layer_norm(rt.h, blk.norm1, cfg.eps, out=rt.x)
+    linear(rt.x, blk.qkv, out=rt.qkv)
+    call("ff_vision_rope", ptr(rt.qkv), ptr(rt.qkv[:, H:]), 3 * H, HD, ptr(rt.cos), ptr(rt.sin), ptr(rt.q),
+         ptr(rt.k), 128, n * 128, n, NH, HD, 128, s)
+    call("ff_vision_vt", ptr(rt.qkv[:, 2 * H:]), 3 * H, HD, ptr(rt.vt), n, rt.n_pad, NH, HD, s)
+    call("ff_attention_full", ptr(rt.q), ptr(rt.k), ptr(rt.vt), ptr(rt.z), n, rt.n_pad, NH, HD, float(HD ** -0.5), s)
+    linear(rt.z, blk.proj, resid=rt.h, out=rt.h)
+    layer_norm(rt.h, blk.norm2, cfg.eps, out=rt.x)
+    linear(rt.x, blk.fc1, ACT_GELU_TANH, out=rt.u)
+    linear(rt.u, blk.fc2, resid=rt.h, out=rt.h)
+    torch.cuda.synchronize()
+
+
+def test_vision_graph_replays_equal_eager(gpu):
+    from fastforward_amd.vision import VisionRuntime
+    cfg, w = _small_tower(seed=1)
+    rt = VisionRuntime(cfg, w, 8, 12)
+    rng = np.random.default_rng(5)
+    images = [rng.integers(0, 256, size=(128, 192, 3), dtype=np.uint8) for _ in range(2)]
+    eager = []
+    for img in images:
+        rt.set_image(torch.from_numpy(img))
+        m, d = rt.step()
+        eager.append((m.clone(), [x.clone() for x in d]))
+    rt.capture()
+    for _ in range(2):
+        for img, (em, ed) in zip(images, eager):
+            rt.set_image(torch.from_numpy(img))
+            torch.cuda.synchronize()
+            m, d = rt.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(m, em) and all(torch.equal(a, b) for a, b in zip(d, ed))
+
+
+def test_vision_8b_shape_two_blocks(gpu):
+    """The 8B tower's real widths (1152 hidden, 16 heads of 72, MLP 4304 padded to
+    4352, 4608-wide mergers) on a 16 x 32 patch grid, two blocks, against the oracle."""
+    from fastforward_amd.vision import VISION_PRESETS, VisionConfig, VisionRuntime, make_vision
+    base = VISION_PRESETS["qwen3vl-8b"]
+    cfg = VisionConfig("8b-2", 2, base.hidden, base.heads, base.inter, base.out_hidden, (0,))
+    w = make_vision(cfg, seed=2)
+    gh, gw = 16, 32
+    rt = VisionRuntime(cfg, w, gh, gw)
+    rng = np.random.default_rng(6)
+    rgb = rng.integers(0, 256, size=(16 * gh, 16 * gw, 3), dtype=np.uint8)
+    rt.set_image(torch.from_numpy(rgb))
+    trace = []
+    merged, deep = rt.step(trace)
+    torch.cuda.synchronize()
+    shape, ow = _to_oracle(cfg, w)
+    otrace = []
+    omerged, odeep = OV.tower(shape, ow, OV.pack_pixels(rgb), gh, gw, otrace)
+    for j, (a, b) in enumerate(zip(trace, otrace)):
+        assert _rel_l2(a, b) <= 1e-2, f"block {j}: {_rel_l2(a, b):.3e}"
+    assert _rel_l2(merged, omerged) <= 2e-2 and _rel_l2(deep[0], odeep[0]) <= 2e-2
