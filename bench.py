@@ -223,6 +223,49 @@ def micro_gemms():
     return out
 
 
+def vision_flop(vc, n):
+    """Algorithmic FLOPs of one vision step over n patches (unpadded widths)."""
+    H, I, W4 = vc.hidden, vc.inter, vc.hidden * vc.merge ** 2
+    nm = n // vc.merge ** 2
+    block = 2 * n * H * (3 * H + H + 2 * I) + 4 * n * n * H
+    merger = 2 * nm * W4 * (W4 + vc.out_hidden)
+    return 2 * n * 1536 * H + vc.depth * block + (len(vc.deepstack) + 1) * merger
+
+
+def vision_extras(cfg, w, T, grid, args):
+    """The vision tower of the same model size on the step's image (merged grid
+    16 x 32 = 2048 patches of 16 x 16 pixels), one hipGraph replay per step,
+    and the image + prompt step (vision tower, then the LM step with the image
+    tokens scattered in and DeepStack in the first layers) as one graph."""
+    from fastforward_amd.pipeline import ImageStep
+    from fastforward_amd.synthetic import make_request
+    from fastforward_amd.vision import VISION_PRESETS, VisionRuntime, make_vision
+    vc = VISION_PRESETS[cfg.name]
+    gh, gw = 2 * grid[0], 2 * grid[1]
+    vw = make_vision(vc, seed=0)
+    rgb = torch.randint(0, 256, (16 * gh, 16 * gw, 3), generator=torch.Generator().manual_seed(0),
+                        dtype=torch.uint8)
+    vr = VisionRuntime(vc, vw, gh, gw)
+    vr.set_image(rgb)
+    vr.capture()
+    ms = time_graph(vr, args.steps, args.warmup)
+    flop = vision_flop(vc, gh * gw)
+    tag = f"vision_{cfg.name.split('-')[-1]}_{gh * gw}patch"
+    out = {f"{tag}_step_ms": round(ms, 4), f"{tag}_tflops": round(flop / ms / 1e9, 1)}
+    log(f"vision step {ms:.3f} ms ({out[tag + '_tflops']} TFLOP/s algorithmic)")
+    del vr
+    ids, pos, pick = make_request(cfg, T, *grid, seed=0)
+    st = ImageStep(cfg, w, vc, vw, gh, gw, T, image_start=4)
+    st.set_inputs(rgb, ids, pos, pick)
+    st.capture()
+    key = f"image_step_{cfg.name.split('-')[-1]}_{T}_ms"
+    out[key] = round(time_graph(st, args.steps, args.warmup), 4)
+    log(f"image + prompt step {out[key]} ms")
+    del st, vw
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(cfg, w, ids, pos, pick, T, layers_sample):
     """The CPU oracle on ``layers_sample`` decoder layers + the pick-only tail of the
     same step, on this host's cores; scaled to the full depth."""
@@ -279,6 +322,8 @@ def main():
     ap.add_argument("--profile", action="store_true", help="only replay the graph (for rocprofv3 runs)")
     ap.add_argument("--linear", default="fp8", choices=("fp8", "fp8_static", "w4a16"),
                     help="linear format of the --profile step (the benchmark line is always FP8)")
+    ap.add_argument("--vision", action="store_true",
+                    help="with --profile: replay the vision tower's graph instead of the LM step")
     ap.add_argument("--kernels", action="store_true",
                     help="only run the step's GEMM shapes and a calibration copy (rocprofv3 --pmc runs)")
     args = ap.parse_args()
@@ -294,6 +339,19 @@ def main():
     cfg = PRESETS[args.preset]
     T = args.tokens
     grid = (16, 32) if T >= 576 else (16, 16)
+    if args.profile and args.vision:
+        from fastforward_amd.vision import VISION_PRESETS, VisionRuntime, make_vision
+        vc = VISION_PRESETS[cfg.name]
+        gh, gw = 2 * grid[0], 2 * grid[1]
+        vr = VisionRuntime(vc, make_vision(vc, seed=0), gh, gw)
+        vr.set_image(torch.randint(0, 256, (16 * gh, 16 * gw, 3), generator=torch.Generator().manual_seed(0),
+                                   dtype=torch.uint8))
+        vr.capture()
+        ms = time_graph(vr, args.steps, args.warmup)
+        log(f"vision step {ms:.3f} ms")
+        print(json.dumps(dict(metric=f"ms per vision step ({vc.name} tower, {gh * gw} patches)", value=round(ms, 4),
+                              unit="ms", profile_run=True)))
+        return
     log(f"building {cfg.name} fp8 (random init, seed 0)")
     w = make_model(cfg, mode=args.linear if args.profile else "fp8", seed=0, n_options=8)
     for L in w.layers:  # as Runtime does: the packed tile kernels read these copies
@@ -326,6 +384,7 @@ def main():
         cpu = cpu_baseline(cfg, w, ids, pos, pick, T, args.cpu_layers)
     del rt
     if not args.no_extras:
+        extras.update(vision_extras(cfg, w, T, grid, args))
         del w
         torch.cuda.empty_cache()
         # the other LM configurations, each one hipGraph replay per step

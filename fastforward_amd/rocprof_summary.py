@@ -87,8 +87,11 @@ def step_table(db, fetch_csv, write_csv, mfma_csv, fetch_factor, write_factor, x
             continue
         dur[(k, gx * gy * gz)].append((end - start) / 1e3)
     fe, wr, mf = (_by_grid(p) if p else {} for p in (fetch_csv, write_csv, mfma_csv))
-    steps = max(len(v) for k, v in dur.items() if k[0].startswith("readout_kernel")) if any(
-        k[0].startswith("readout_kernel") for k in dur) else 1
+    steps = 1  # a step is one readout launch (LM step) or one pixel packing launch (vision step)
+    for first in ("readout_kernel", "pack_pixels_kernel"):
+        if any(k[0].startswith(first) for k in dur):
+            steps = max(len(v) for k, v in dur.items() if k[0].startswith(first))
+            break
     rows = []
     for (k, g), d in dur.items():
         us = sum(d) / len(d)
