@@ -59,6 +59,7 @@ SIGNATURES = {
     "ff_vision_vt": [P, I64, I64, P, I64, I64, I64, I64, P],
     "ff_attention_full": [P, P, P, P, I64, I64, I64, I64, F32, P],
     "ff_pos_interp": [P, P, P, P, I64, I64, I64, I64, P],
+    "ff_vision_qkv": [P, P, P, P, P, P, I64, I64, I64, I64, P],
 }
 
 _lib = None

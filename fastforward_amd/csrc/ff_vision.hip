@@ -277,12 +277,12 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_bf16_kernel(
 // each output head written as zeros. One thread per 4 columns of one
 // (token, head) of q or of k; hd % 8 == 0 so the rotation partner (hd / 2 away)
 // is a whole 4-column group.
-__global__ __launch_bounds__(kThreads) void vision_rope_kernel(
-    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, int64_t x_ts, int64_t x_hs,
+__device__ __forceinline__ void vision_rope_block(
+    int64_t blk, const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, int64_t x_ts, int64_t x_hs,
     const float* __restrict__ cos, const float* __restrict__ sin, bf16_t* __restrict__ yq, bf16_t* __restrict__ yk,
     int64_t y_ts, int64_t y_hs, int n, int heads, int hd, int dpad) {
   const int gpr = dpad / 4;  // 4-column groups per output head row
-  const int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x;
+  const int64_t i = blk * kThreads + threadIdx.x;
   const int64_t per = (int64_t)n * heads * gpr;
   if (i >= 2 * per) return;
   const bool isk = i >= per;
@@ -318,15 +318,21 @@ __global__ __launch_bounds__(kThreads) void vision_rope_kernel(
   *reinterpret_cast<u32x2*>(dst) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
 }
 
+__global__ __launch_bounds__(kThreads) void vision_rope_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, int64_t x_ts, int64_t x_hs,
+    const float* __restrict__ cos, const float* __restrict__ sin, bf16_t* __restrict__ yq, bf16_t* __restrict__ yk,
+    int64_t y_ts, int64_t y_hs, int n, int heads, int hd, int dpad) {
+  vision_rope_block(blockIdx.x, q, k, x_ts, x_hs, cos, sin, yq, yk, y_ts, y_hs, n, heads, hd, dpad);
+}
+
 // V^T with zero padding: v (token stride v_ts, head stride v_hs, hd columns)
 // -> vt (heads, 128, t_pad), rows [hd, 128) and tokens [n, t_pad) zero. One
 // workgroup per (head, 64 tokens): the 64 x hd block is staged in LDS, then
 // each thread writes 8 consecutive tokens of one d row.
-__global__ __launch_bounds__(kThreads) void vision_vt_kernel(const bf16_t* __restrict__ v, int64_t v_ts,
-                                                             int64_t v_hs, bf16_t* __restrict__ vt, int n, int t_pad,
-                                                             int heads, int hd) {
-  __shared__ float tile[64][129];
-  const int head = blockIdx.x % heads, t0 = (blockIdx.x / heads) * 64;
+__device__ __forceinline__ void vision_vt_block(int blk, float (&tile)[64][129], const bf16_t* __restrict__ v,
+                                                int64_t v_ts, int64_t v_hs, bf16_t* __restrict__ vt, int n, int t_pad,
+                                                int heads, int hd) {
+  const int head = blk % heads, t0 = (blk / heads) * 64;
   for (int c = threadIdx.x; c < 64 * 32; c += kThreads) {
     const int tt = c / 32, d = (c % 32) * 4;
     const int tok = t0 + tt;
@@ -348,6 +354,31 @@ __global__ __launch_bounds__(kThreads) void vision_vt_kernel(const bf16_t* __res
 #pragma unroll
     for (int e = 0; e < 8; ++e) f[e] = tile[tb + e][d];
     *reinterpret_cast<u32x4*>(vt + ((int64_t)head * 128 + d) * t_pad + t0 + tb) = pack8(f);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void vision_vt_kernel(const bf16_t* __restrict__ v, int64_t v_ts,
+                                                             int64_t v_hs, bf16_t* __restrict__ vt, int n, int t_pad,
+                                                             int heads, int hd) {
+  __shared__ float tile[64][129];
+  vision_vt_block(blockIdx.x, tile, v, v_ts, v_hs, vt, n, t_pad, heads, hd);
+}
+
+// Both of the above for the packed qkv output (n, 3, heads, hd) in one launch:
+// workgroups [0, nrope) rotate q and k into the zero-padded head-major layout
+// (heads, n, 128), the rest write the padded V^T (heads, 128, t_pad).
+__global__ __launch_bounds__(kThreads) void vision_qkv_kernel(const bf16_t* __restrict__ qkv,
+                                                              const float* __restrict__ cos,
+                                                              const float* __restrict__ sin, bf16_t* __restrict__ yq,
+                                                              bf16_t* __restrict__ yk, bf16_t* __restrict__ vt, int n,
+                                                              int t_pad, int heads, int hd, int nrope) {
+  __shared__ float tile[64][129];
+  const int64_t ts = 3 * (int64_t)heads * hd;
+  if ((int)blockIdx.x < nrope) {
+    vision_rope_block(blockIdx.x, qkv, qkv + (int64_t)heads * hd, ts, hd, cos, sin, yq, yk, 128, (int64_t)n * 128, n,
+                      heads, hd, 128);
+  } else {
+    vision_vt_block((int)blockIdx.x - nrope, tile, qkv + 2 * (int64_t)heads * hd, ts, hd, vt, n, t_pad, heads, hd);
   }
 }
 
@@ -436,9 +467,10 @@ extern "C" int ff_gemm_bf16(const void* a, int64_t lda, const void* w, const voi
              "ff_gemm_bf16: alignment");
   hipStream_t st = (hipStream_t)stream;
   const int64_t big = ((m + 127) / 128) * ((n + 127) / 128);
-  // 128 x 128 tiles at two workgroups per CU when they fill the GPU twice,
-  // else 64 x 128 tiles (more workgroups for the narrow projections).
-  if (big >= 512)
+  // 128 x 128 tiles at two workgroups per CU when they fill at least three
+  // quarters of the 512 slots, else 64 x 128 tiles (more workgroups for the
+  // narrow projections).
+  if (big >= 384)
     launch_gemm<128, 128, 2, 2>(a, lda, w, bias, y, ldy, resid, ldr, m, n, k, act, st);
   else
     launch_gemm<64, 128, 3, 2>(a, lda, w, bias, y, ldy, resid, ldr, m, n, k, act, st);
@@ -489,5 +521,24 @@ extern "C" int ff_pos_interp(const void* table, const int64_t* idx, const float*
                      (hipStream_t)stream, (const bf16_t*)table, idx, wt, (bf16_t*)out, (int)n, (int)taps,
                      (int)hidden, rows);
   FF_LAUNCH_CHECK("ff_pos_interp");
+  return FF_OK;
+}
+
+extern "C" int ff_vision_qkv(const void* qkv, const float* cos, const float* sin, void* yq, void* yk, void* vt,
+                             int64_t n, int64_t t_pad, int64_t heads, int64_t hd, ff_stream_t stream) {
+  FF_REQUIRE(qkv && cos && sin && yq && yk && vt, "ff_vision_qkv: null pointer");
+  FF_REQUIRE(n > 0 && heads > 0 && hd > 0 && hd <= 128 && hd % 8 == 0 && t_pad >= n && t_pad % 64 == 0,
+             "ff_vision_qkv: bad sizes n=%lld heads=%lld hd=%lld t_pad=%lld", (long long)n, (long long)heads,
+             (long long)hd, (long long)t_pad);
+  FF_REQUIRE(ff_aligned(qkv, 8) && ff_aligned(cos, 16) && ff_aligned(sin, 16) && ff_aligned(yq, 8) &&
+                 ff_aligned(yk, 8) && ff_aligned(vt, 16),
+             "ff_vision_qkv: alignment");
+  const int64_t rope_threads = 2 * n * heads * (128 / 4);
+  const int nrope = (int)((rope_threads + kThreads - 1) / kThreads);
+  const int nvt = (int)(heads * (t_pad / 64));
+  hipLaunchKernelGGL(vision_qkv_kernel, dim3((unsigned)(nrope + nvt)), dim3(kThreads), 0, (hipStream_t)stream,
+                     (const bf16_t*)qkv, cos, sin, (bf16_t*)yq, (bf16_t*)yk, (bf16_t*)vt, (int)n, (int)t_pad,
+                     (int)heads, (int)hd, nrope);
+  FF_LAUNCH_CHECK("ff_vision_qkv");
   return FF_OK;
 }

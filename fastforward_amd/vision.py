@@ -10,8 +10,8 @@ blocks and the final patch merger, with the per-geometry constants cached as
 captured in one graph as ``VisionGraph.build`` does (:28-36).
 
 Every op runs on the library's HIP kernels (``ff_pack_pixels``,
-``ff_layer_norm``, ``ff_gemm_bf16``, ``ff_vision_rope``, ``ff_vision_vt``,
-``ff_attention_full``, ``ff_pos_interp``). Layout choices of this build: the
+``ff_layer_norm``, ``ff_gemm_bf16``, ``ff_vision_qkv`` (rotary + padded
+layouts in one launch), ``ff_attention_full``, ``ff_pos_interp``). Layout choices of this build: the
 attention reads q and k head-major with each head zero-padded to 128 dims and
 V transposed (heads, 128, n_pad); the MLP intermediate is zero-padded to a
 multiple of 64 (fc1 rows and fc2 columns), which leaves every sum exact.
@@ -333,10 +333,8 @@ class VisionRuntime:
         for j, blk in enumerate(w.blocks):
             layer_norm(self.h, blk.norm1, cfg.eps, out=self.x)
             linear(self.x, blk.qkv, out=self.qkv)
-            q, k, v = self.qkv, self.qkv[:, H:], self.qkv[:, 2 * H:]
-            call("ff_vision_rope", ptr(q), ptr(k), 3 * H, HD, ptr(self.cos), ptr(self.sin), ptr(self.q),
-                 ptr(self.k), 128, n * 128, n, NH, HD, 128, s)
-            call("ff_vision_vt", ptr(v), 3 * H, HD, ptr(self.vt), n, self.n_pad, NH, HD, s)
+            call("ff_vision_qkv", ptr(self.qkv), ptr(self.cos), ptr(self.sin), ptr(self.q), ptr(self.k),
+                 ptr(self.vt), n, self.n_pad, NH, HD, s)
             call("ff_attention_full", ptr(self.q), ptr(self.k), ptr(self.vt), ptr(self.z), n, self.n_pad, NH, HD,
                  float(HD ** -0.5), s)
             linear(self.z, blk.proj, resid=self.h, out=self.h)

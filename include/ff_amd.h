@@ -312,6 +312,13 @@ int ff_vision_rope(const void* q, const void* k, int64_t x_ts, int64_t x_hs, con
 int ff_vision_vt(const void* v, int64_t v_ts, int64_t v_hs, void* vt, int64_t n, int64_t t_pad,
                  int64_t heads, int64_t hd, ff_stream_t stream);
 
+/* ff_vision_rope + ff_vision_vt on the packed qkv output of a vision block in
+ * one launch (no reference counterpart as one op): qkv (n, 3, heads, hd)
+ * contiguous -> yq, yk (heads, n, 128) rotated and zero-padded, vt (heads,
+ * 128, t_pad) zero-padded. hd % 8 == 0, hd <= 128, t_pad % 64 == 0. */
+int ff_vision_qkv(const void* qkv, const float* cos, const float* sin, void* yq, void* yk, void* vt,
+                  int64_t n, int64_t t_pad, int64_t heads, int64_t hd, ff_stream_t stream);
+
 /* Bidirectional multi-head attention of the vision blocks (the sdpa call with
  * is_causal=False of scaled_qwen_runtime.py:51): q, k (heads, t, 128) with head
  * dims past the model's zero, vt (heads, 128, t_pad) from ff_vision_vt; fp32

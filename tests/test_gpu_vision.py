@@ -151,6 +151,31 @@ def test_vision_rope_bit_exact_and_padded_layout(gpu):
     assert not bool(pq[:, :, hd:].float().abs().sum()) and not bool(pk[:, :, hd:].float().abs().sum())
 
 
+def test_vision_qkv_equals_rope_and_vt(gpu):
+    """The one-launch form equals ff_vision_rope (padded, head-major) + ff_vision_vt."""
+    from fastforward_amd._lib import call, ptr, stream
+    from fastforward_amd.vision import VISION_PRESETS, rope_tables
+    cfg = VISION_PRESETS["qwen3vl-8b"]
+    gh, gw = 10, 12
+    n, nh, hd, n_pad = gh * gw, cfg.heads, cfg.head_dim, 128
+    cd, sd = (t.to(DEV) for t in rope_tables(cfg, gh, gw))
+    qkv = torch.randn(n, 3 * nh * hd, generator=_g(14)).to(BF16).to(DEV)
+    outs = []
+    for fused in (False, True):
+        yq, yk = (torch.full((nh, n, 128), float("nan"), device=DEV).to(BF16) for _ in range(2))
+        vt = torch.full((nh, 128, n_pad), float("nan"), device=DEV).to(BF16)
+        if fused:
+            call("ff_vision_qkv", ptr(qkv), ptr(cd), ptr(sd), ptr(yq), ptr(yk), ptr(vt), n, n_pad, nh, hd, stream())
+        else:
+            call("ff_vision_rope", ptr(qkv), ptr(qkv[:, nh * hd:]), 3 * nh * hd, hd, ptr(cd), ptr(sd), ptr(yq),
+                 ptr(yk), 128, n * 128, n, nh, hd, 128, stream())
+            call("ff_vision_vt", ptr(qkv[:, 2 * nh * hd:]), 3 * nh * hd, hd, ptr(vt), n, n_pad, nh, hd, stream())
+        torch.cuda.synchronize()
+        outs.append((yq, yk, vt))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
 def test_vision_vt_layout(gpu):
     from fastforward_amd._lib import call, ptr, stream
     n, nh, hd, n_pad = 100, 4, 72, 128
@@ -257,9 +282,8 @@ def _run_block(rt, j):
     n, H, HD, NH = rt.n, cfg.hidden, cfg.head_dim, cfg.heads
     layer_norm(rt.h, blk.norm1, cfg.eps, out=rt.x)
     linear(rt.x, blk.qkv, out=rt.qkv)
-    call("ff_vision_rope", ptr(rt.qkv), ptr(rt.qkv[:, H:]), 3 * H, HD, ptr(rt.cos), ptr(rt.sin), ptr(rt.q),
-         ptr(rt.k), 128, n * 128, n, NH, HD, 128, s)
-    call("ff_vision_vt", ptr(rt.qkv[:, 2 * H:]), 3 * H, HD, ptr(rt.vt), n, rt.n_pad, NH, HD, s)
+    call("ff_vision_qkv", ptr(rt.qkv), ptr(rt.cos), ptr(rt.sin), ptr(rt.q), ptr(rt.k), ptr(rt.vt), n, rt.n_pad,
+         NH, HD, s)
     call("ff_attention_full", ptr(rt.q), ptr(rt.k), ptr(rt.vt), ptr(rt.z), n, rt.n_pad, NH, HD, float(HD ** -0.5), s)
     linear(rt.z, blk.proj, resid=rt.h, out=rt.h)
     layer_norm(rt.h, blk.norm2, cfg.eps, out=rt.x)
