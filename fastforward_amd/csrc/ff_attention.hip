@@ -139,12 +139,13 @@ __device__ __forceinline__ float softmax_block(f32x4 (&s)[4], bool masked, int l
   return alpha;
 }
 
-// acc *= alpha, skipped when no query of the wave changed its max (alpha == 1
-// exactly leaves acc unchanged).
+// acc *= alpha (its first DTN 16-column tiles), skipped when no query of the
+// wave changed its max (alpha == 1 exactly leaves acc unchanged).
+template <int DTN = 8>
 __device__ __forceinline__ void rescale(f32x4 (&o)[8], float alpha) {
   if (__ballot(alpha != 1.f)) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[dt] = o[dt] * alpha;
+    for (int dt = 0; dt < DTN; ++dt) o[dt] = o[dt] * alpha;
   }
 }
 
@@ -437,19 +438,22 @@ __global__ __launch_bounds__(kThreads, NS == 2 ? 2 : 1) void attention_prefill_k
   // loop would also wait for the prefetches issued there.
   issue(0, 0);
   if (NS == 3 && nblocks > 1) issue(64, 1);
+  // Head dims past DOUT are zero in q, k and V^T: only the first KST 32-dim
+  // steps of q.k and the first DTN 16-dim tiles of P.V are computed.
+  constexpr int KST = (DOUT + 31) / 32, DTN = (DOUT + 15) / 16;
   u32x4 qf[QT][4];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int qrow = min(wq0 + 16 * qt + r16, s_len - 1);
     const bf16_t* qp = q + ((int64_t)head * s_len + qrow) * D;
 #pragma unroll
-    for (int st = 0; st < 4; ++st) qf[qt][st] = *reinterpret_cast<const u32x4*>(qp + 32 * st + 8 * g);
+    for (int st = 0; st < KST; ++st) qf[qt][st] = *reinterpret_cast<const u32x4*>(qp + 32 * st + 8 * g);
   }
   // consuming the registers here makes the compiler wait for the loads now
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-    for (int st = 0; st < 4; ++st)
+    for (int st = 0; st < KST; ++st)
       asm volatile("" : : "v"(qf[qt][st].x), "v"(qf[qt][st].y), "v"(qf[qt][st].z), "v"(qf[qt][st].w));
   for (int ib = 0; ib < nblocks; ++ib) {
     if (NS == 3 && ib + 1 < nblocks) wait_vmcnt<8>();
@@ -466,7 +470,7 @@ __global__ __launch_bounds__(kThreads, NS == 2 ? 2 : 1) void attention_prefill_k
 #pragma unroll
       for (int i = 0; i < 4; ++i) sc[qt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int st = 0; st < 4; ++st)
+    for (int st = 0; st < KST; ++st)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const u32x4 kf = *reinterpret_cast<const u32x4*>(st_base + koff(i >> 1, i & 1, st));
@@ -480,12 +484,12 @@ __global__ __launch_bounds__(kThreads, NS == 2 ? 2 : 1) void attention_prefill_k
       const bool masked = CAUSAL ? (kb + 63 > tq0 || kb + 63 >= t) : kb + 63 >= t;
       const int lim = (CAUSAL ? min(tq0 + r16, t - 1) : t - 1) - kb - 8 * g;
       const float alpha = softmax_block(sc[qt], masked, lim, c2, m[qt], den[qt], pf[qt]);
-      rescale(o[qt], alpha);
+      rescale<DTN>(o[qt], alpha);
     }
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
+      for (int dt = 0; dt < DTN; ++dt) {
         const u32x4 vf = *reinterpret_cast<const u32x4*>(st_base + voff(dt, c));
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) o[qt][dt] = mfma_bf16(vf, pf[qt][c], o[qt][dt]);
