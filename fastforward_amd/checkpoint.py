@@ -99,6 +99,8 @@ def _linear(w, mode, static_bound):
         return RuntimeScaleLinear(w, 448.0 / static_bound)
     if mode == "w4a16":
         return Int4(w)
+    if mode == "int4":      # the reference's asymmetric group-32 quantizer
+        return Int4(w, group=32, symmetric=False)
     raise ValueError(f"unknown linear mode {mode!r}")
 
 

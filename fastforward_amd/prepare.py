@@ -71,10 +71,76 @@ def letterbox(resized, shape, top, left, fill=128):
     return out
 
 
-def prepare_image(rgb, variant, resize):
+def decode_image(path):
+    """(h, w, 3) uint8 RGB of an image file. The reference decodes JPEG with
+    imagecodecs, PNG with pyspng and anything else with PIL
+    (_family/depth_runtime.py:55-65); PIL (libjpeg-turbo / zlib) decodes all
+    three here."""
+    from PIL import Image
+    with Image.open(path) as im:
+        rgb = np.array(im.convert("RGB"))
+    if rgb.dtype != np.uint8 or rgb.ndim != 3 or rgb.shape[2] != 3 or 0 in rgb.shape:
+        raise ValueError(f"could not decode {path} as an RGB image")
+    return rgb
+
+
+def _area_weights(n_in, n_out):
+    """(n_out, n_in) coverage matrix of area resampling for n_out <= n_in: output
+    pixel d covers source [d s, (d+1) s), s = n_in/n_out; each row sums to 1."""
+    s = n_in / n_out
+    w = np.zeros((n_out, n_in))
+    for d in range(n_out):
+        lo, hi = d * s, (d + 1) * s
+        for i in range(int(np.floor(lo)), min(n_in, int(np.ceil(hi)))):
+            w[d, i] = min(hi, i + 1) - max(lo, i)
+    return w / s
+
+
+def _area_linear_weights(n_in, n_out):
+    """(n_out, n_in) interpolation matrix of area mode when the image grows on
+    some axis: output d reads source s = floor(d n_in/n_out) and s + 1 with
+    weight f = frac((d+1) - (s+1) n_out/n_in), f = 0 where that is <= 0 (pixel
+    replication with a linear blend across source pixel edges)."""
+    scale = n_in / n_out
+    w = np.zeros((n_out, n_in))
+    for d in range(n_out):
+        s = int(np.floor(d * scale))
+        f = (d + 1) - (s + 1) / scale
+        f = 0.0 if f <= 0 else f - np.floor(f)
+        if s >= n_in - 1:
+            s, f = n_in - 1, 0.0
+        w[d, s] += 1 - f
+        if f:
+            w[d, s + 1] += f
+    return w
+
+
+def area_resize(img, size):
+    """``img`` (h, w, 3) uint8 resampled to ``size`` = (height, width) the way
+    OpenCV's INTER_AREA is specified: when neither side grows, every output
+    pixel is the coverage-weighted mean of the source pixels under it; when a
+    side grows, area-mode linear weights (``_area_linear_weights``) on both
+    axes. Separable, float64, rounded half to even. The reference calls
+    cv2.resize(..., INTER_AREA) (_family/depth_runtime.py:70-71); cv2 is not
+    part of this build and its fixed-point paths can differ by one level."""
+    img = np.asarray(img)
+    h, w = img.shape[:2]
+    nh, nw = int(size[0]), int(size[1])
+    if nh <= 0 or nw <= 0:
+        raise ValueError("resize target must be positive")
+    if (nh, nw) == (h, w):
+        return img.astype(np.uint8, copy=True)
+    weights = _area_weights if nh <= h and nw <= w else _area_linear_weights
+    wy, wx = weights(h, nh), weights(w, nw)
+    out = np.einsum("yh,hwc,xw->yxc", wy, img.astype(np.float64), wx, optimize=True)
+    return np.clip(np.rint(out), 0, 255).astype(np.uint8)
+
+
+def prepare_image(rgb, variant, resize=area_resize):
     """The canvas image of ``rgb`` for ``variant``: square variants resize to
     the canvas, aspect variants resize to the fitted size and letterbox.
-    ``resize(image, (height, width)) -> uint8 image`` is the caller's resampler."""
+    ``resize(image, (height, width)) -> uint8 image`` is the resampler
+    (default ``area_resize``)."""
     rgb = np.asarray(rgb)
     height, width = rgb.shape[:2]
     shape = canvas(height, width, variant)

@@ -57,7 +57,8 @@ def make_model(cfg, mode="fp8", seed=0, device="cuda", n_options=8, norm_jitter=
     """Build ModelWeights for ``cfg``.
 
     mode: "fp8" (FP8Linear: per-token / per-channel), "fp8_static"
-    (RuntimeScaleLinear with activation bound ``static_bound``), "w4a16" (Int4).
+    (RuntimeScaleLinear with activation bound ``static_bound``), "w4a16" (Int4,
+    ``int4_group`` / ``int4_symmetric``), "int4" (Int4, asymmetric group 32).
     ``keep_bf16`` (a dict) receives the bf16 weights by (layer, role) on the CPU.
     """
     H, D = cfg.hidden, cfg.head_dim
@@ -76,6 +77,8 @@ def make_model(cfg, mode="fp8", seed=0, device="cuda", n_options=8, norm_jitter=
                 ops[role] = RuntimeScaleLinear(w, 448.0 / static_bound)
             elif mode == "w4a16":
                 ops[role] = Int4(w, group=int4_group, symmetric=int4_symmetric)
+            elif mode == "int4":    # the reference's asymmetric group-32 quantizer
+                ops[role] = Int4(w, group=32, symmetric=False)
             else:
                 raise ValueError(mode)
             del w

@@ -1,0 +1,215 @@
+"""Image requests over a local checkpoint (fastforward_amd.family, the
+qwen3_vl_family bundle of fastforward_amd.api, the CLI).
+
+CPU: bundle checks, the identity repair-adapter check, the prompt prefix with
+its image placeholder expanded per canvas, request preparation (canvas,
+tokens, readout row, no truncation), CLI argument handling.
+
+GPU: ``Accelerator.predict(image, question, candidates)`` on a tiny
+random-init transformers Qwen3-VL checkpoint with an offline word-level
+tokenizer agrees with transformers' own bf16 forward of the same model on the
+same canvas pixels and token ids, its LM linears given the same per-token /
+per-channel e4m3 rounding: relative L2 of the 8 option logits <= 0.08 (0.04
+measured) and under a quarter of the two test images' own difference; a
+second request on the captured graph reproduces a fresh eager step of the
+same inputs bit for bit.
+"""
+import hashlib
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from tests.test_checkpoint import IMAGE_ID, _tiny_hf
+
+SPECIALS = {"<|image_pad|>": IMAGE_ID, "<|vision_start|>": 998, "<|vision_end|>": 996, "<|im_start|>": 995,
+            "<|im_end|>": 994}
+
+
+def _tiny_tokenizer(path):
+    """Word-level tokenizer.json with the Qwen chat / vision special tokens at
+    the tiny config's ids; unknown words map to [UNK] (id 0)."""
+    from tokenizers import AddedToken, Tokenizer, models, pre_tokenizers
+    words = (["[UNK]"] + [chr(c) for c in range(65, 91)] + [chr(c) for c in range(97, 123)] + list(".,:?!") +
+             "user assistant system Answer Options Reply with one letter of the What color is shown".split())
+    vocab = {w: i for i, w in enumerate(dict.fromkeys(words))}
+    vocab.update(SPECIALS)
+    tok = Tokenizer(models.WordLevel(vocab, unk_token="[UNK]"))
+    tok.pre_tokenizer = pre_tokenizers.Whitespace()
+    tok.add_special_tokens([AddedToken(s, special=True, normalized=False) for s in SPECIALS])
+    tok.save(str(path / "tokenizer.json"))
+    return tok
+
+
+def _repair(tmp_path, nonzero=False):
+    p = tmp_path / "repair.pt"
+    up = torch.zeros(4, 8)
+    if nonzero:
+        up[1, 2] = 1.0
+    torch.save({"state_dict": {"up": up, "bias": torch.zeros(8), "down": torch.randn(8, 4)}}, p)
+    return p, hashlib.sha256(p.read_bytes()).hexdigest()
+
+
+def _bundle(tmp_path, model, **kw):
+    c = dict(schema_version=1, task="visual_choice", architecture="qwen3_vl_family", model=str(model),
+             buckets=[64, 96, 128, 192], variant="aspect256", prompt_style="short")
+    c.update(kw)
+    p = tmp_path / "bundle.json"
+    p.write_text(json.dumps(c))
+    return p
+
+
+def test_family_bundle_checks(tmp_path):
+    from fastforward_amd.api import check_identity_repair, read_bundle
+    with pytest.raises(FileNotFoundError):
+        read_bundle(_bundle(tmp_path, tmp_path / "absent"))
+    for bad in ([], [0, 64], "64", None):
+        with pytest.raises(ValueError):
+            read_bundle(_bundle(tmp_path, tmp_path, buckets=bad))
+    with pytest.raises(ValueError):
+        read_bundle(_bundle(tmp_path, tmp_path, linear="fp16"))
+    ck, digest = _repair(tmp_path)
+    assert read_bundle(_bundle(tmp_path, tmp_path, checkpoint=str(ck), checkpoint_sha256=digest))["model"]
+    with pytest.raises(ValueError):
+        read_bundle(_bundle(tmp_path, tmp_path, checkpoint=str(ck), checkpoint_sha256="0" * 64))
+    check_identity_repair(ck)
+    bad, _ = _repair(tmp_path, nonzero=True)
+    with pytest.raises(ValueError):
+        check_identity_repair(bad)
+
+
+def _cpu_runtime(tmp_path, variant="aspect256", buckets=(64, 96, 128, 192)):
+    """A FamilyRuntime with its tokenizer and request state but no weights
+    (the request-preparation half needs no GPU)."""
+    from fastforward_amd.family import FamilyRuntime
+    rt = FamilyRuntime.__new__(FamilyRuntime)
+    rt.tokenizer = _tiny_tokenizer(tmp_path)
+    rt.image_token = IMAGE_ID
+    rt.buckets = sorted(buckets)
+    rt.max_tokens = rt.buckets[-1]
+    rt.style = "short"
+    rt.variant = variant
+    rt.geometry, rt.cache, rt.profiles = {}, {}, {}
+    return rt
+
+
+def test_prefix_expansion_and_prepare(tmp_path):
+    rt = _cpu_runtime(tmp_path)
+    g = rt.setup_side((192, 320))
+    # <|im_start|> user <|vision_start|> then 6 x 10 image tokens, then <|vision_end|>
+    assert g["image_start"] == 3 and g["grid"] == (6, 10)
+    pre = g["prefix"].tolist()
+    assert pre[:3] == [995, rt.tokenizer.token_to_id("user"), 998]
+    assert pre[3:63] == [IMAGE_ID] * 60 and pre[63:] == [996]
+    rgb = np.random.default_rng(0).integers(0, 256, size=(200, 300, 3), dtype=np.uint8)
+    row = dict(rgb=rgb, instruction="What color is shown?", candidates=["red", "green", "blue"])
+    p = rt.prepare(row)
+    assert p["side"] == (192, 320) and p["rgb"].shape == (192, 320, 3)
+    assert p["k"] == 3 and p["pick"] == len(p["ids"]) - 1
+    assert p["ids"][:64].tolist() == pre
+    tail = [rt.tokenizer.id_to_token(int(i)) for i in p["ids"][-4:]]
+    assert tail == ["<|im_start|>", "assistant", "Answer", ":"]
+    assert rt.bucket_for(len(p["ids"])) == 96
+    # square variants: the whole 256 x 256 canvas, 64 image tokens
+    sq = _cpu_runtime(tmp_path, variant="square256")
+    q = sq.prepare(row)
+    assert q["side"] == (256, 256) and int((q["ids"] == IMAGE_ID).sum()) == 64
+    # text is never truncated
+    small = _cpu_runtime(tmp_path, buckets=(64,))
+    with pytest.raises(ValueError):
+        small.prepare(row)
+
+
+def test_cli_arguments(tmp_path):
+    from fastforward_amd.cli import main
+    with pytest.raises(SystemExit):
+        main(["--bundle", "b.json"])
+    with pytest.raises(FileNotFoundError):
+        main(["--bundle", str(tmp_path / "absent.json"), "--image", "x.png", "--question", "q", "--choices", "a",
+              "b"])
+
+
+def _fp8_reference(m):
+    """Give transformers' LM linears the step's FP8 rounding: weights replaced
+    by their per-output-channel e4m3 round trip (s = amax/448), inputs by
+    their per-token e4m3 round trip (forward pre-hooks). What remains between
+    the two paths is bf16 rounding of the dequantised operands and
+    accumulation order."""
+    def rt(x, dim):
+        x = x.float()
+        s = x.abs().amax(dim=dim, keepdim=True).clamp_min(1e-12) / 448.0
+        return ((x / s).clamp(-448, 448).to(torch.float8_e4m3fn).float() * s).to(torch.bfloat16)
+
+    def hook(mod, args):
+        return (rt(args[0], -1),) + tuple(args[1:])
+
+    for layer in m.model.language_model.layers:
+        for lin in (layer.self_attn.q_proj, layer.self_attn.k_proj, layer.self_attn.v_proj, layer.self_attn.o_proj,
+                    layer.mlp.gate_proj, layer.mlp.up_proj, layer.mlp.down_proj):
+            with torch.no_grad():
+                lin.weight.copy_(rt(lin.weight, 1))
+            lin.register_forward_pre_hook(hook)
+    return m
+
+
+def _hf_option_logits(m, g, option_ids):
+    from oracle import vision as OV
+    ids = torch.from_numpy(np.asarray(g["ids"], dtype=np.int64))[None]
+    h, w = g["side"]
+    pix = OV.pack_pixels(g["rgb"])
+    with torch.no_grad():
+        out = m(input_ids=ids, pixel_values=pix.float(), image_grid_thw=torch.tensor([[1, h // 16, w // 16]]),
+                mm_token_type_ids=(ids == IMAGE_ID).int())
+    return out.logits[0, -1, option_ids[:g["k"]]].float()
+
+
+@pytest.mark.gpu
+def test_predict_matches_transformers(gpu, tmp_path):
+    from PIL import Image
+
+    from fastforward_amd.api import Accelerator
+    from fastforward_amd.pipeline import ImageStep
+    m, path = _tiny_hf(tmp_path, seed=5)
+    from pathlib import Path
+    _tiny_tokenizer(Path(path))
+    ck, digest = _repair(tmp_path)
+    bundle = _bundle(tmp_path, path, checkpoint=str(ck), checkpoint_sha256=digest, expected_dimensions=[2, 512, 2])
+    rng = np.random.default_rng(6)
+    imgs = []
+    for j, shape in enumerate([(200, 300, 3), (210, 290, 3)]):
+        f = tmp_path / f"img{j}.png"
+        Image.fromarray(rng.integers(0, 256, size=shape, dtype=np.uint8)).save(f)
+        imgs.append(f)
+    acc = Accelerator(bundle)      # loads (and quantises) the saved bf16 weights first
+    rt = acc.runtime
+    _fp8_reference(m)
+    cands = ["red", "green", "blue", "black", "white", "gray", "pink", "brown"]
+    q = "What color is shown?"
+    print("family predict: tiny checkpoint, aspect256, 2 images, 8 options", flush=True)
+    r0 = acc.predict(imgs[0], q, cands, item_id="a")
+    assert r0["id"] == "a" and len(r0["probabilities"]) == 8
+    # second request, same canvas and bucket: the refilled graph equals a fresh eager step
+    r1 = acc.predict(imgs[1], q, cands, item_id="b")
+    assert len(rt.cache) == 1
+    g = [rt.prepare(dict(image_path=str(f), instruction=q, candidates=cands)) for f in imgs]
+    geo = rt.setup_side(g[1]["side"])
+    bucket = rt.bucket_for(len(g[1]["ids"]))
+    st = ImageStep(rt.lm_cfg, rt.lm_w, rt.vis_cfg, rt.vis_w, g[1]["side"][0] // 16, g[1]["side"][1] // 16, bucket,
+                   geo["image_start"])
+    st.set_inputs(torch.from_numpy(g[1]["rgb"]), torch.from_numpy(g[1]["ids"]), rt.positions(g[1]["side"], bucket),
+                  g[1]["pick"])
+    eager = st.step()[:8].float().cpu()
+    torch.cuda.synchronize()
+    assert torch.equal(eager, torch.tensor(r1["logits"])), (eager.tolist(), r1["logits"])
+    # both requests against transformers; the two images' own difference is the scale a wiring
+    # mistake (image rows, positions, pixels) would show
+    want = [_hf_option_logits(m, gi, rt.meta["option_ids"]) for gi in g]
+    got = [torch.tensor(r["logits"]) for r in (r0, r1)]
+    rel = [float((a - b).norm() / b.norm()) for a, b in zip(got, want)]
+    between = float((want[0] - want[1]).norm() / want[0].norm())
+    for j in range(2):
+        print(f"request {j}: ours {got[j].tolist()}\n           hf   {want[j].tolist()}", flush=True)
+    print(f"vs transformers (FP8-rounded linears): rel L2 {rel[0]:.4f}, {rel[1]:.4f}; "
+          f"between the two images {between:.4f}", flush=True)
+    assert max(rel) <= 0.08 and max(rel) < between / 4

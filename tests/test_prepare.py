@@ -105,3 +105,55 @@ def test_option_strings():
     assert P.option_strings(3) == [" A", " B", " C"]
     with pytest.raises(ValueError):
         P.option_strings(27)
+
+
+def _fine_area(img, nh, nw):
+    """Area resampling by exact supersampling: every source pixel replicated
+    onto a grid of lcm resolution, then each output's block averaged."""
+    h, w = img.shape[:2]
+    ly, lx = math.lcm(h, nh), math.lcm(w, nw)
+    fine = np.repeat(np.repeat(img.astype(np.float64), ly // h, 0), lx // w, 1)
+    return fine.reshape(nh, ly // nh, nw, lx // nw, 3).mean(axis=(1, 3))
+
+
+def test_area_resize_identity_and_constant():
+    rng = np.random.default_rng(1)
+    img = rng.integers(0, 256, size=(13, 17, 3), dtype=np.uint8)
+    assert np.array_equal(P.area_resize(img, (13, 17)), img)
+    flat = np.full((40, 30, 3), 77, dtype=np.uint8)
+    for size in [(7, 11), (40, 60), (90, 13)]:
+        assert np.array_equal(P.area_resize(flat, size), np.full(size + (3,), 77, dtype=np.uint8))
+
+
+@pytest.mark.parametrize("src,dst", [((64, 48), (16, 12)), ((21, 14), (7, 7)), ((37, 53), (10, 16)),
+                                     ((60, 90), (25, 36))])
+def test_area_resize_downscale_is_the_area_integral(src, dst):
+    rng = np.random.default_rng(2)
+    img = rng.integers(0, 256, size=src + (3,), dtype=np.uint8)
+    got = P.area_resize(img, dst).astype(np.float64)
+    want = _fine_area(img, *dst)
+    assert np.abs(got - want).max() <= 0.5 + 1e-9        # the integral, rounded
+    if src[0] % dst[0] == 0 and src[1] % dst[1] == 0:  # integer factors: block means
+        fy, fx = src[0] // dst[0], src[1] // dst[1]
+        block = img.astype(np.float64).reshape(dst[0], fy, dst[1], fx, 3).mean(axis=(1, 3))
+        clear = np.abs(block - np.floor(block) - 0.5) > 1e-6    # ties may round either way
+        assert np.array_equal(got[clear], np.rint(block)[clear])
+
+
+def test_area_resize_integer_upscale_replicates():
+    rng = np.random.default_rng(3)
+    img = rng.integers(0, 256, size=(5, 7, 3), dtype=np.uint8)
+    assert np.array_equal(P.area_resize(img, (15, 14)), np.repeat(np.repeat(img, 3, 0), 2, 1))
+    up = P.area_resize(img, (12, 17)).astype(int)          # non-integer growth stays within source range
+    assert up.min() >= img.min() and up.max() <= img.max()
+
+
+def test_decode_image_roundtrip(tmp_path):
+    from PIL import Image
+    rng = np.random.default_rng(4)
+    img = rng.integers(0, 256, size=(9, 23, 3), dtype=np.uint8)
+    Image.fromarray(img).save(tmp_path / "x.png")
+    assert np.array_equal(P.decode_image(tmp_path / "x.png"), img)
+    Image.fromarray(img[..., 0]).convert("L").save(tmp_path / "g.png")   # gray -> RGB
+    g = P.decode_image(tmp_path / "g.png")
+    assert g.shape == (9, 23, 3) and np.array_equal(g[..., 1], img[..., 0])
