@@ -459,16 +459,16 @@ int launch(const void* qa, const float* sa, int sa_rows, const void* qw, const f
 // Tile choice, measured at M = 576 with the weights streamed from HBM as in the
 // step (each launch on a different weight matrix): 128 x 128 tiles with two
 // stages and two workgroups per CU when there are at least two such tiles per
-// CU; 128 x 128 tiles with four stages (three in flight), one workgroup per CU,
-// when the tiles about fill the CUs once; otherwise 64 x 128 tiles (three
-// stages, two per CU), which double the workgroups at the price of more
-// operand traffic.
+// CU; otherwise 64 x 128 tiles (three stages, two per CU), which double the
+// workgroups at the price of more operand traffic. At 576 x 4096 x 6144 (240
+// tiles of 128 x 128, the 8B QKV) 64 x 128 takes 22.9 us plain and 25-27 us
+// with the QKV epilogue against 26-27 / 29-30 us for 128 x 128 with four
+// stages at one workgroup per CU (k128x128Deep, kept for FF_GEMM_FP8_TILE).
 enum Tile { k64x128, k128x128, k128x128Deep, k128x256 };
 
 Tile pick_tile(int64_t m, int64_t n) {
   const int64_t tiles_128 = ((m + 127) / 128) * ((n + 127) / 128);
   if (tiles_128 >= 2 * 256) return k128x128;
-  if (tiles_128 >= 192 && tiles_128 <= 256) return k128x128Deep;
   return k64x128;
 }
 
@@ -548,7 +548,8 @@ extern "C" int ff_gemm_fp8_qkv(const void* qa, const float* sa, const void* qw, 
   QkvEpilogue qe{(const bf16_t*)q_norm, (const bf16_t*)k_norm, eps_q, eps_k, (const bf16_t*)cos,
                  (const bf16_t*)sin, (bf16_t*)yq, (bf16_t*)yk, (bf16_t*)vt, (int)hq, (int)hk, (int)t_pad};
   hipStream_t s = (hipStream_t)stream;
-  const int tile = pick_tile(m, n);
+  static const int forced = forced_tile();
+  const int tile = forced >= 0 && forced != k128x256 ? forced : pick_tile(m, n);
   if (tile == k128x128)
     launch<128, 128, 1, 2, 2, kQkv>(qa, sa, 1, qw, sw, 1, nullptr, 0, m, n, k, s, nullptr, qe);
   else if (tile == k128x128Deep)
