@@ -10,6 +10,9 @@
 // returns.
 #include <math.h>
 
+#include <stdlib.h>
+#include <string.h>
+
 #include "ff_common.h"
 
 using namespace ff;
@@ -467,11 +470,26 @@ extern "C" int ff_gemm_bf16(const void* a, int64_t lda, const void* w, const voi
              "ff_gemm_bf16: alignment");
   hipStream_t st = (hipStream_t)stream;
   const int64_t big = ((m + 127) / 128) * ((n + 127) / 128);
+  // FF_GEMM_BF16_TILE=64x128 | 128x128 | 64x128o3 forces a tile (tuning sweeps).
+  static const int forced = [] {
+    const char* e = getenv("FF_GEMM_BF16_TILE");
+    if (!e) return -1;
+    if (!strcmp(e, "64x128")) return 0;
+    if (!strcmp(e, "128x128")) return 1;
+    if (!strcmp(e, "64x128o3")) return 2;
+    return -1;
+  }();
   // 128 x 128 tiles at two workgroups per CU when they fill at least three
   // quarters of the 512 slots, else 64 x 128 tiles (more workgroups for the
-  // narrow projections).
-  if (big >= 384)
+  // narrow projections). The GELU-tanh MLP input projection (the tower's fc1,
+  // 2048 x 1152 -> 4352 at 2048 patches) runs 64 x 128 tiles at three per CU
+  // instead: 42.7 us against 51.5 (128 x 128) and 50.3 (64 x 128, two per CU),
+  // its VALU-heavy epilogue overlapping the other workgroups' main loops.
+  const int tile = forced >= 0 ? forced : (big >= 384 ? (act == kGeluTanh ? 2 : 1) : 0);
+  if (tile == 1)
     launch_gemm<128, 128, 2, 2>(a, lda, w, bias, y, ldy, resid, ldr, m, n, k, act, st);
+  else if (tile == 2)
+    launch_gemm<64, 128, 2, 3>(a, lda, w, bias, y, ldy, resid, ldr, m, n, k, act, st);
   else
     launch_gemm<64, 128, 3, 2>(a, lda, w, bias, y, ldy, resid, ldr, m, n, k, act, st);
   FF_LAUNCH_CHECK("ff_gemm_bf16");
