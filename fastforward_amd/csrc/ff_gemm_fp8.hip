@@ -459,16 +459,18 @@ int launch(const void* qa, const float* sa, int sa_rows, const void* qw, const f
 // Tile choice, measured at M = 576 with the weights streamed from HBM as in the
 // step (each launch on a different weight matrix): 128 x 128 tiles with two
 // stages and two workgroups per CU when there are at least two such tiles per
-// CU; otherwise 64 x 128 tiles (three stages, two per CU), which double the
-// workgroups at the price of more operand traffic. At 576 x 4096 x 6144 (240
-// tiles of 128 x 128, the 8B QKV) 64 x 128 takes 22.9 us plain and 25-27 us
-// with the QKV epilogue against 26-27 / 29-30 us for 128 x 128 with four
-// stages at one workgroup per CU (k128x128Deep, kept for FF_GEMM_FP8_TILE).
+// CU; 128 x 128 tiles with four stages (three in flight), one workgroup per CU,
+// when the tiles about fill the CUs once (the 8B QKV: 30.4 us in the step
+// against 30.9 us for 64 x 128 tiles; with the weights resident in the last-level
+// cache, as in a loop over a few weight copies, 64 x 128 looks 3 us faster);
+// otherwise 64 x 128 tiles (three stages, two per CU), which double the
+// workgroups at the price of more operand traffic.
 enum Tile { k64x128, k128x128, k128x128Deep, k128x256 };
 
 Tile pick_tile(int64_t m, int64_t n) {
   const int64_t tiles_128 = ((m + 127) / 128) * ((n + 127) / 128);
   if (tiles_128 >= 2 * 256) return k128x128;
+  if (tiles_128 >= 192 && tiles_128 <= 256) return k128x128Deep;
   return k64x128;
 }
 
