@@ -213,3 +213,83 @@ def test_predict_matches_transformers(gpu, tmp_path):
     print(f"vs transformers (FP8-rounded linears): rel L2 {rel[0]:.4f}, {rel[1]:.4f}; "
           f"between the two images {between:.4f}", flush=True)
     assert max(rel) <= 0.08 and max(rel) < between / 4
+
+
+def _fp8_static_reference(m, bounds):
+    """transformers' LM linears with the static-FP8 rounding of a calibration
+    profile: weights round-tripped through e4m3 with one scale per packed
+    weight (amax/448 over q/k/v together, over gate/up together, o, down),
+    inputs through e4m3(clamp(x * 448/bound, +-448)) * bound/448 with the
+    layer's bound for that role. Returns the hook handles."""
+    def wq(ws):
+        s = max(float(w.detach().float().abs().max()) for w in ws) / 448.0
+        with torch.no_grad():
+            for w in ws:
+                w.copy_(((w.float() / s).to(torch.float8_e4m3fn).float() * s).to(torch.bfloat16))
+
+    def act(bound):
+        inv = 448.0 / bound
+
+        def hook(mod, args):
+            x = args[0].float()
+            q = (x * inv).clamp(-448, 448).to(torch.float8_e4m3fn).float() * (bound / 448.0)
+            return (q.to(torch.bfloat16),) + tuple(args[1:])
+        return hook
+
+    handles = []
+    for j, layer in enumerate(m.model.language_model.layers):
+        a, mlp = layer.self_attn, layer.mlp
+        groups = {"qkv": [a.q_proj, a.k_proj, a.v_proj], "output": [a.o_proj], "gateup": [mlp.gate_proj, mlp.up_proj],
+                  "down": [mlp.down_proj]}
+        for role, lins in groups.items():
+            wq([lin.weight for lin in lins])
+            for lin in lins:
+                handles.append(lin.register_forward_pre_hook(act(bounds[f"{j}:{role}"])))
+    return handles
+
+
+@pytest.mark.gpu
+def test_predict_with_calibration_profile_and_select(gpu, tmp_path):
+    """A bundle with a calibration profile: static FP8 linears (one weight scale
+    per packed weight, the profile's activation bounds), the variant's canvas;
+    ``select`` switches bounds and canvas and re-captures. Each variant's answer
+    logits agree with transformers given the same static e4m3 rounding: relative
+    L2 <= 0.10 (0.046 and 0.072 measured; the static bounds quantise more
+    coarsely than per-token scales, so rounding flips weigh more)."""
+    from pathlib import Path
+
+    from PIL import Image
+
+    from fastforward_amd.api import Accelerator
+    m0, path = _tiny_hf(tmp_path, seed=7)
+    _tiny_tokenizer(Path(path))
+    roles = ("qkv", "output", "gateup", "down")
+    profiles = {"aspect256": {f"{j}:{r}": b for j in range(2) for r, b in zip(roles, (6.0, 4.0, 8.0, 2.0))},
+                "square256": {f"{j}:{r}": b for j in range(2) for r, b in zip(roles, (5.0, 3.0, 6.0, 1.5))}}
+    prof = tmp_path / "profiles.json"
+    prof.write_text(json.dumps({"profiles": profiles}))
+    digest = hashlib.sha256(prof.read_bytes()).hexdigest()
+    bundle = _bundle(tmp_path, path, profile_path=str(prof), profile_sha256=digest, variant="aspect256")
+    f = tmp_path / "img.png"
+    Image.fromarray(np.random.default_rng(8).integers(0, 256, size=(200, 300, 3), dtype=np.uint8)).save(f)
+    acc = Accelerator(bundle)
+    rt = acc.runtime
+    assert rt.linear == "fp8_static"
+    cands = ["red", "green", "blue", "black", "white", "gray", "pink", "brown"]
+    q = "What color is shown?"
+    for variant, side in (("aspect256", (192, 320)), ("square256", (256, 256))):
+        if variant != acc.variant:
+            acc.select(variant)
+        print(f"calibrated predict: variant {variant}", flush=True)
+        r = acc.predict(f, q, cands)
+        g = rt.prepare(dict(image_path=str(f), instruction=q, candidates=cands))
+        assert g["side"] == side
+        m, _ = _tiny_hf(tmp_path, seed=7, save=False)      # a fresh bf16 copy of the same model
+        handles = _fp8_static_reference(m, profiles[variant])
+        want = _hf_option_logits(m, g, rt.meta["option_ids"])
+        for h in handles:
+            h.remove()
+        got = torch.tensor(r["logits"])
+        rel = float((got - want).norm() / want.norm())
+        print(f"{variant}: ours {got.tolist()}\n           hf   {want.tolist()}\n  rel L2 {rel:.4f}", flush=True)
+        assert rel <= 0.10
