@@ -293,3 +293,55 @@ def test_predict_with_calibration_profile_and_select(gpu, tmp_path):
         rel = float((got - want).norm() / want.norm())
         print(f"{variant}: ours {got.tolist()}\n           hf   {want.tolist()}\n  rel L2 {rel:.4f}", flush=True)
         assert rel <= 0.10
+
+
+def _int4_reference(m):
+    """transformers' LM linear weights replaced by the reference's asymmetric
+    group-32 int4 round trip (_family/night_runtime.py:18-23): per group
+    s = max((max - min)/15, 1e-6), q = clamp(round((w - min)/s), 0, 15),
+    z = min + 8 s, stored as bf16 (s, z); w = (q - 8) s + z."""
+    for layer in m.model.language_model.layers:
+        a, mlp = layer.self_attn, layer.mlp
+        for lin in (a.q_proj, a.k_proj, a.v_proj, a.o_proj, mlp.gate_proj, mlp.up_proj, mlp.down_proj):
+            w = lin.weight.detach().float()
+            n, k = w.shape
+            x = w.reshape(n, k // 32, 32)
+            low, high = x.amin(-1, keepdim=True), x.amax(-1, keepdim=True)
+            s = ((high - low) / 15).clamp_min(1e-6)
+            q = ((x - low) / s).round().clamp(0, 15)
+            z = low + s * 8
+            sb, zb = s.to(torch.bfloat16).float(), z.to(torch.bfloat16).float()
+            with torch.no_grad():
+                lin.weight.copy_(((q - 8) * sb + zb).reshape(n, k).to(torch.bfloat16))
+    return m
+
+
+@pytest.mark.gpu
+def test_predict_int4_execution_mode(gpu, tmp_path):
+    """execution_mode 'int4' loads the reference's asymmetric group-32 W4A16
+    linears; the answer logits agree with transformers whose weights took the
+    same int4 round trip (bf16 activations on both sides): relative L2 <= 0.05,
+    0.014 measured."""
+    from pathlib import Path
+
+    from PIL import Image
+
+    from fastforward_amd.api import Accelerator
+    m, path = _tiny_hf(tmp_path, seed=9)
+    _tiny_tokenizer(Path(path))
+    bundle = _bundle(tmp_path, path, execution_mode="int4")
+    f = tmp_path / "img.png"
+    Image.fromarray(np.random.default_rng(10).integers(0, 256, size=(200, 300, 3), dtype=np.uint8)).save(f)
+    acc = Accelerator(bundle)
+    rt = acc.runtime
+    assert rt.linear == "int4"
+    cands = ["red", "green", "blue", "black", "white", "gray", "pink", "brown"]
+    q = "What color is shown?"
+    print("int4 predict", flush=True)
+    r = acc.predict(f, q, cands)
+    g = rt.prepare(dict(image_path=str(f), instruction=q, candidates=cands))
+    want = _hf_option_logits(_int4_reference(m), g, rt.meta["option_ids"])
+    got = torch.tensor(r["logits"])
+    rel = float((got - want).norm() / want.norm())
+    print(f"int4: ours {got.tolist()}\n      hf   {want.tolist()}\n  rel L2 {rel:.4f}", flush=True)
+    assert rel <= 0.05
