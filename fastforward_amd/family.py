@@ -28,7 +28,7 @@ import torch
 from .checkpoint import load_pretrained
 from .pipeline import ImageStep
 from .prepare import canvas, decode_image, prepare_image, text_parts
-from .runtime import mrope_positions
+from .runtime import Arena, mrope_positions
 
 # The reference's execution modes (_family/night_runtime.py:56-65) -> the
 # linear format loaded here. Accumulation is fp32 in every FP8 mode.
@@ -68,6 +68,8 @@ class FamilyRuntime:
         self.variant = c.get("variant", "square256")
         self.profiles = profiles or {}
         self.warmup = warmup
+        # the LM activations of every (canvas, bucket) step alias one region (requests run one at a time)
+        self.arena = Arena(Arena.size_for(self.lm_cfg, self.lm_w, self.max_tokens), self.lm_w.embed.device)
         self.geometry = {}   # canvas (h, w) -> prefix ids, image start, merged grid
         self.cache = {}      # (canvas, bucket) -> (ImageStep, pinned rgb, pinned ids, pinned pick, event)
         if self.profiles:
@@ -133,7 +135,8 @@ class FamilyRuntime:
         if captured:
             geo = self.setup_side(g["side"])
             gh, gw = g["side"][0] // 16, g["side"][1] // 16
-            st = ImageStep(self.lm_cfg, self.lm_w, self.vis_cfg, self.vis_w, gh, gw, bucket, geo["image_start"])
+            st = ImageStep(self.lm_cfg, self.lm_w, self.vis_cfg, self.vis_w, gh, gw, bucket, geo["image_start"],
+                           arena=self.arena)
             st.set_inputs(torch.from_numpy(g["rgb"]), torch.from_numpy(g["ids"]), self.positions(g["side"], bucket),
                           g["pick"])
             st.capture(warmup=self.warmup)

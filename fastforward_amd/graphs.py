@@ -8,6 +8,8 @@ per-bucket position templates of ``setup_side`` (_family/depth_runtime.py:
   zero-padded to the bucket.
 * Each bucket is one ``Runtime`` whose step is captured once (after warm-up
   runs) on its first request; later requests only refill the static inputs.
+  The buckets' activation buffers alias one ``Arena`` sized for the largest
+  bucket (requests run one at a time).
 * The M-RoPE positions of a bucket are a template computed once for the
   bundle's layout (prefix text, one image grid, text after it) and stay
   resident; only token ids and the scored row change per request.
@@ -19,7 +21,7 @@ per-bucket position templates of ``setup_side`` (_family/depth_runtime.py:
 import numpy as np
 import torch
 
-from .runtime import Runtime, mrope_positions
+from .runtime import Arena, Runtime, mrope_positions
 
 
 class StepGraphs:
@@ -34,6 +36,7 @@ class StepGraphs:
         if not self.buckets or self.buckets[0] < self.min_tokens:
             raise ValueError(f"every bucket must hold the {self.min_tokens}-token prompt prefix and image")
         self.warmup = warmup
+        self.arena = None   # one activation region for every bucket's runtime (made at the first capture)
         self.cache = {}     # bucket -> captured Runtime
         self.staging = {}   # bucket -> (pinned ids (bucket,), pinned pick (1,), event)
 
@@ -78,7 +81,9 @@ class StepGraphs:
         b = self.bucket_for(n)
         captured = b not in self.cache
         if captured:
-            rt = Runtime(self.cfg, self.w, b)
+            if self.arena is None:     # sized for the largest bucket, so later buckets fit
+                self.arena = Arena(Arena.size_for(self.cfg, self.w, self.buckets[-1]), self.w.embed.device)
+            rt = Runtime(self.cfg, self.w, b, arena=self.arena)
             rt.set_inputs(ids, self.positions(b), int(pick))
             rt.capture(warmup=self.warmup)
             self.cache[b] = rt

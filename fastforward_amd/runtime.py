@@ -8,7 +8,7 @@ and the pick-only tail of the fp8/precise execution modes
 Two step bodies produce identical numbers:
 
 * ``fused`` (FP8Linear weights): every activation buffer is allocated once per
-  token bucket; the per-token e4m3 quantization of each GEMM input is fused into
+  token bucket (or laid out in an ``Arena`` that the buckets share); the per-token e4m3 quantization of each GEMM input is fused into
   the kernel that produces it (add_rms, fast_norm, swiglu), and V is written
   transposed by the q/k-norm + rotary kernel. 10 launches per layer.
 * ``generic`` (any linear op): the reference's own op sequence through the
@@ -109,10 +109,60 @@ class ModelWeights:
     extra: dict = field(default_factory=dict)
 
 
-class Runtime:
-    """One bucket (T tokens) of the LM step with static device buffers."""
+class Arena:
+    """Device bytes that the activation buffers of several step runtimes share.
 
-    def __init__(self, cfg, weights, tokens, path=None, visual_rows=0, image_start=0, deep_layers=0):
+    Requests run one at a time, and a step writes each activation buffer before
+    it reads it, so nothing lives in them between steps: the runtimes of all
+    token buckets (and image canvases) of one model can alias a single region
+    sized for the largest of them instead of holding one set each (about
+    100 MB per 576-token bucket at the 8B shape). Static inputs (ids,
+    positions, pick), the image-token buffers and the logits stay per runtime.
+    Steps of runtimes that share an arena must not overlap in time.
+    """
+
+    ALIGN = 256
+
+    def __init__(self, nbytes, device):
+        self.nbytes = int(nbytes)
+        self.buf = torch.empty(max(self.nbytes, self.ALIGN), dtype=torch.uint8, device=device)
+
+    @staticmethod
+    def size_for(cfg, weights, tokens, path=None):
+        """Bytes of arena a Runtime of ``tokens`` tokens takes (counted by laying
+        its buffers out without allocating them)."""
+        counter = _Carver(None)
+        Runtime(cfg, weights, tokens, path=path, _carver=counter)
+        return counter.cursor
+
+
+class _Carver:
+    """Lays one runtime's activation buffers out from offset 0 of an arena
+    (``arena`` None: only counts the bytes)."""
+
+    def __init__(self, arena):
+        self.arena, self.cursor = arena, 0
+
+    def __call__(self, shape, dtype, device):
+        n = int(np.prod(shape)) * torch.empty((), dtype=dtype).element_size()
+        off = (self.cursor + Arena.ALIGN - 1) // Arena.ALIGN * Arena.ALIGN
+        self.cursor = off + n
+        if self.arena is None:
+            return torch.empty(shape, dtype=dtype, device="meta")
+        if self.cursor > self.arena.nbytes:
+            raise ValueError(f"arena of {self.arena.nbytes} bytes is too small for this runtime")
+        return self.arena.buf[off:off + n].view(dtype).view(shape)
+
+
+class Runtime:
+    """One bucket (T tokens) of the LM step with static device buffers.
+
+    ``arena``: an ``Arena`` whose bytes the activation buffers alias (shared
+    with the other runtimes of the same model; see ``Arena``); None allocates
+    them for this runtime alone."""
+
+    def __init__(self, cfg, weights, tokens, path=None, visual_rows=0, image_start=0, deep_layers=0, arena=None,
+                 _carver=None):
         self.cfg, self.w = cfg, weights
         self.T = tokens
         self.Tp = (tokens + 63) // 64 * 64
@@ -130,6 +180,9 @@ class Runtime:
         T, H, D = tokens, cfg.hidden, cfg.head_dim
         HQ, HK, I = cfg.heads, cfg.kv_heads, cfg.inter
         e = lambda *s, dt=BF16: torch.empty(s, device=dev, dtype=dt)  # noqa: E731
+        carve = _carver or (_Carver(arena) if arena is not None else None)
+        # activations: aliased into the shared arena when one is given
+        a = (lambda *s, dt=BF16: carve(s, dt, dev)) if carve is not None else e  # noqa: E731
         # static inputs
         self.ids = torch.zeros(T, device=dev, dtype=torch.int64)
         self.pos = torch.zeros(3, T, device=dev, dtype=torch.int64)
@@ -141,25 +194,25 @@ class Runtime:
         self.deep = [e(visual_rows, H) for _ in range(deep_layers)] if visual_rows else []
         self.inv_freq = rope_inv_freq(cfg.theta, D).to(dev)
         # activations
-        self.cos, self.sin = e(T, D), e(T, D)
-        self.h = [e(T, H), e(T, H)]
-        self.res = e(T, H)
+        self.cos, self.sin = a(T, D), a(T, D)
+        self.h = [a(T, H), a(T, H)]
+        self.res = a(T, H)
         self.logits = torch.zeros(weights.head.shape[0], device=dev, dtype=torch.float32)
         if self.path == "fused":
-            self.xq, self.xs = e(T, H, dt=E4M3), e(T, dt=torch.float32)
-            self.yq, self.yk, self.vt = e(HQ, T, D), e(HK, T, D), e(HK, D, self.Tp)
-            self.attn = e(T, HQ * D)
-            self.aq, self.as_ = e(T, HQ * D, dt=E4M3), e(T, dt=torch.float32)
-            self.o = e(T, H)
-            self.pq, self.ps = e(T, H, dt=E4M3), e(T, dt=torch.float32)
-            self.hm = e(T, I)                                    # swiglu output (bf16)
-            self.pmax = e(T, I // 64, dt=torch.float32)          # its row maxima per 64 channels
-            self.mq, self.ms = e(T, I, dt=E4M3), e(T, dt=torch.float32)
-            self.dn = e(T, H)
-            self.hp = e(1, H)
+            self.xq, self.xs = a(T, H, dt=E4M3), a(T, dt=torch.float32)
+            self.yq, self.yk, self.vt = a(HQ, T, D), a(HK, T, D), a(HK, D, self.Tp)
+            self.attn = a(T, HQ * D)
+            self.aq, self.as_ = a(T, HQ * D, dt=E4M3), a(T, dt=torch.float32)
+            self.o = a(T, H)
+            self.pq, self.ps = a(T, H, dt=E4M3), a(T, dt=torch.float32)
+            self.hm = a(T, I)                                    # swiglu output (bf16)
+            self.pmax = a(T, I // 64, dt=torch.float32)          # its row maxima per 64 channels
+            self.mq, self.ms = a(T, I, dt=E4M3), a(T, dt=torch.float32)
+            self.dn = a(T, H)
+            self.hp = a(1, H)
             # k-split partials of ff_gemm_fp8_pk (o and down share it: their calls are ordered)
             need = max(gemm_pk_workspace(T, H, HQ * D), gemm_pk_workspace(T, H, I), 256)
-            self.gws = torch.empty(need, device=dev, dtype=torch.uint8)
+            self.gws = a(need, dt=torch.uint8)
         self.graph = None
         self.graph_out = None
 

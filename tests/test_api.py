@@ -110,7 +110,8 @@ def test_step_graphs_buckets_and_position_templates():
 def test_bucketed_graphs_match_eager_and_isolate_padding(gpu, tmp_path):
     """Requests of 270, 300 and 280 tokens over buckets (288, 320): each bucket
     captures on its first request only, every replay equals an eager step of
-    its bucket bit for bit, and the gate (position template, graph == eager,
+    its bucket bit for bit (the buckets' activations alias one arena; the eager
+    steps have their own), and the gate (position template, graph == eager,
     padding ids set to 42 leave the answer's bits unchanged) passes."""
     import torch
     from fastforward_amd.runtime import Runtime
@@ -133,6 +134,13 @@ def test_bucketed_graphs_match_eager_and_isolate_padding(gpu, tmp_path):
         assert r["logits"] == z.cpu().tolist()
     src, pin, _ = acc.graphs.staging[288]
     assert src.is_pinned() and pin.is_pinned()
+    # the two buckets' activations alias one arena (each bucket's replays above
+    # ran after the other bucket had overwritten it, and still equalled eager steps)
+    r288, r320 = acc.graphs.cache[288], acc.graphs.cache[320]
+    base, size = acc.graphs.arena.buf.data_ptr(), acc.graphs.arena.nbytes
+    assert r288.cos.data_ptr() == r320.cos.data_ptr() == base   # both laid out from offset 0
+    for rt in (r288, r320):
+        assert base <= rt.gws.data_ptr() and rt.gws.data_ptr() + rt.gws.numel() <= base + size
 
 
 def _profile(tmp_path, variants, layers=28):
