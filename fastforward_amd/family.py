@@ -27,8 +27,9 @@ import torch
 
 from .checkpoint import load_pretrained
 from .pipeline import ImageStep
-from .prepare import canvas, decode_image, prepare_image, text_parts
+from .prepare import canvas, canvases, decode_image, prepare_image, text_parts
 from .runtime import Arena, mrope_positions
+from .vision import VisionRuntime
 
 # The reference's execution modes (_family/night_runtime.py:56-65) -> the
 # linear format loaded here. Accumulation is fp32 in every FP8 mode.
@@ -68,8 +69,10 @@ class FamilyRuntime:
         self.variant = c.get("variant", "square256")
         self.profiles = profiles or {}
         self.warmup = warmup
-        # the LM activations of every (canvas, bucket) step alias one region (requests run one at a time)
+        # the LM activations of every (canvas, bucket) step alias one region, the vision tower's
+        # another (requests run one at a time); the tower's is sized per variant
         self.arena = Arena(Arena.size_for(self.lm_cfg, self.lm_w, self.max_tokens), self.lm_w.embed.device)
+        self.vision_arena = None
         self.geometry = {}   # canvas (h, w) -> prefix ids, image start, merged grid
         self.cache = {}      # (canvas, bucket) -> (ImageStep, pinned rgb, pinned ids, pinned pick, event)
         if self.profiles:
@@ -135,8 +138,12 @@ class FamilyRuntime:
         if captured:
             geo = self.setup_side(g["side"])
             gh, gw = g["side"][0] // 16, g["side"][1] // 16
+            if self.vision_arena is None:    # sized for the variant's largest canvas, so every canvas fits
+                big = max(canvases(self.variant), key=lambda c: c[0] * c[1])
+                self.vision_arena = Arena(VisionRuntime.arena_bytes(self.vis_cfg, self.vis_w, big[0] // 16,
+                                                                    big[1] // 16), self.lm_w.embed.device)
             st = ImageStep(self.lm_cfg, self.lm_w, self.vis_cfg, self.vis_w, gh, gw, bucket, geo["image_start"],
-                           arena=self.arena)
+                           arena=self.arena, vision_arena=self.vision_arena)
             st.set_inputs(torch.from_numpy(g["rgb"]), torch.from_numpy(g["ids"]), self.positions(g["side"], bucket),
                           g["pick"])
             st.capture(warmup=self.warmup)
@@ -187,6 +194,7 @@ class FamilyRuntime:
         if variant in VARIANTS:
             self.variant = variant
         self.cache.clear()
+        self.vision_arena = None      # re-sized for the new variant's canvases at the next capture
 
     def canvas_of(self, height, width):
         """The canvas (height, width) a height x width image gets under the

@@ -20,17 +20,20 @@ class ImageStep:
 
     The image occupies rows [image_start, image_start + gh*gw/4) of the
     prompt; DeepStack features go to the first len(deepstack) LM layers.
-    ``arena``: a ``runtime.Arena`` shared with the model's other steps for the
-    LM activations (steps that share one must not overlap in time).
+    ``arena`` / ``vision_arena``: ``runtime.Arena`` regions shared with the
+    model's other steps for the LM / vision tower activations (steps that
+    share them must not overlap in time).
     """
 
-    def __init__(self, lm_cfg, lm_weights, vis_cfg, vis_weights, gh, gw, tokens, image_start, path=None, arena=None):
+    def __init__(self, lm_cfg, lm_weights, vis_cfg, vis_weights, gh, gw, tokens, image_start, path=None, arena=None,
+                 vision_arena=None):
         nm = gh * gw // vis_cfg.merge ** 2
         if vis_cfg.out_hidden != lm_cfg.hidden:
             raise ValueError("the vision tower's output width must be the LM's hidden size")
         self.lm = Runtime(lm_cfg, lm_weights, tokens, path=path, visual_rows=nm, image_start=image_start,
                           deep_layers=len(vis_cfg.deepstack), arena=arena)
-        self.vision = VisionRuntime(vis_cfg, vis_weights, gh, gw, merged=self.lm.visual, deep=self.lm.deep)
+        self.vision = VisionRuntime(vis_cfg, vis_weights, gh, gw, merged=self.lm.visual, deep=self.lm.deep,
+                                    arena=vision_arena)
         self.graph = None
         self.graph_out = None
 

@@ -5,11 +5,12 @@ work):
 
 * ``canvas`` / ``fit`` -- the canvas each image variant uses and the
   aspect-preserving fit inside it (_family/depth_geometry.py:7-22);
+  ``canvases`` lists every canvas a variant can produce;
+* ``decode_image`` / ``area_resize`` -- decode to RGB and the INTER_AREA
+  resampling the reference does with cv2 (_family/depth_runtime.py:54-71);
 * ``letterbox`` -- the image placed in a gray (128) canvas at the fitted
   offset, as ``prepare`` does for the aspect variants
-  (_family/depth_runtime.py:66-70); the resize itself (cv2.resize with
-  INTER_AREA in the reference) is the caller's, since OpenCV is not part of
-  this build;
+  (_family/depth_runtime.py:66-70);
 * ``text_parts`` -- the prompt prefix (up to and including the image
   placeholder) and the per-question suffix ending at the readout position
   (_legacy/sub10_runtime.py:43-49 and, for the 'standard' style,
@@ -45,6 +46,16 @@ def canvas(height, width, variant):
     target = height / width
     h, w = min(pairs, key=lambda p: (abs(math.log((p[0] / p[1]) / target)), -p[0] * p[1], p))
     return h * 32, w * 32
+
+
+def canvases(variant):
+    """Every (canvas height, canvas width) ``canvas`` can return for ``variant``."""
+    if variant not in VARIANTS:
+        raise ValueError(f"unknown variant {variant!r}")
+    side = 256 if variant.endswith("256") else 320
+    if variant.startswith("square"):
+        return [(side, side)]
+    return sorted({(32 * h, 32 * w) for a, b in _PAIRS[side] for h, w in ((a, b), (b, a))})
 
 
 def fit(height, width, target):

@@ -25,6 +25,7 @@ from dataclasses import dataclass
 import torch
 
 from ._lib import call, ptr, stream
+from .runtime import _Carver
 
 BF16 = torch.bfloat16
 F32 = torch.float32
@@ -261,10 +262,19 @@ class VisionRuntime:
 
     ``merged`` / ``deep`` may be given (the LM runtime's ``visual`` and ``deep``
     buffers) so the step writes the image tokens straight where the LM step
-    reads them.
+    reads them. ``arena``: a ``runtime.Arena`` that the activations alias,
+    shared with the towers of the model's other image geometries (their steps
+    must not overlap in time); the per-geometry tables stay private.
     """
 
-    def __init__(self, cfg, weights, gh, gw, merged=None, deep=None):
+    @staticmethod
+    def arena_bytes(cfg, weights, gh, gw):
+        """Arena bytes a tower of a (gh, gw) patch grid lays its activations out in."""
+        counter = _Carver(None)
+        VisionRuntime(cfg, weights, gh, gw, _carver=counter)
+        return counter.cursor
+
+    def __init__(self, cfg, weights, gh, gw, merged=None, deep=None, arena=None, _carver=None):
         if gh % cfg.merge or gw % cfg.merge:
             raise ValueError("the patch grid must be a whole number of merge blocks")
         self.cfg, self.w = cfg, weights
@@ -276,8 +286,11 @@ class VisionRuntime:
         H, HD, NH = cfg.hidden, cfg.head_dim, cfg.heads
         W4 = H * cfg.merge ** 2
         e = lambda *s, dt=BF16: torch.empty(s, device=dev, dtype=dt)  # noqa: E731
+        carve = _carver or (_Carver(arena) if arena is not None else None)
+        # activations (written in full by every step): aliased into a shared arena when one is given
+        a = (lambda *s, dt=BF16: carve(s, dt, dev)) if carve is not None else e  # noqa: E731
         self.rgb = torch.zeros((16 * gh, 16 * gw, 3), device=dev, dtype=torch.uint8)
-        self.pixels = e(n, 1536)
+        self.pixels = a(n, 1536)
         # per-geometry constants (VisionGraph.geo)
         cos, sin = rope_tables(cfg, gh, gw)
         self.cos, self.sin = cos.to(dev), sin.to(dev)
@@ -290,15 +303,15 @@ class VisionRuntime:
         call("ff_pos_interp", ptr(weights.pos_embed), ptr(self._taps[0]), ptr(self._taps[1]), ptr(self.pos), n, 4,
              H, weights.pos_embed.shape[0], stream())
         # activations
-        self.h = e(n, H)
-        self.x = e(n, H)
-        self.qkv = e(n, 3 * H)
-        self.q, self.k = e(NH, n, 128), e(NH, n, 128)
-        self.vt = e(NH, 128, self.n_pad)
-        self.z = e(n, H)
-        self.u = e(n, cfg.inter_pad)
-        self.x4 = e(self.nm, W4)
-        self.u4 = e(self.nm, W4)
+        self.h = a(n, H)
+        self.x = a(n, H)
+        self.qkv = a(n, 3 * H)
+        self.q, self.k = a(NH, n, 128), a(NH, n, 128)
+        self.vt = a(NH, 128, self.n_pad)
+        self.z = a(n, H)
+        self.u = a(n, cfg.inter_pad)
+        self.x4 = a(self.nm, W4)
+        self.u4 = a(self.nm, W4)
         self.merged = e(self.nm, cfg.out_hidden) if merged is None else merged
         self.deep = [e(self.nm, cfg.out_hidden) for _ in cfg.deepstack] if deep is None else deep
         if len(self.deep) != len(cfg.deepstack):

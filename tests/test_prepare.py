@@ -157,3 +157,16 @@ def test_decode_image_roundtrip(tmp_path):
     Image.fromarray(img[..., 0]).convert("L").save(tmp_path / "g.png")   # gray -> RGB
     g = P.decode_image(tmp_path / "g.png")
     assert g.shape == (9, 23, 3) and np.array_equal(g[..., 1], img[..., 0])
+
+
+@pytest.mark.parametrize("variant", P.VARIANTS)
+def test_canvases_cover_every_canvas(variant):
+    cs = set(P.canvases(variant))
+    rng = np.random.default_rng(5)
+    seen = set()
+    for _ in range(3000):
+        h, w = (int(x) for x in rng.integers(1, 5000, size=2))
+        c = P.canvas(h, w, variant)
+        assert c in cs
+        seen.add(c)
+    assert seen == cs      # and each listed canvas is reachable
