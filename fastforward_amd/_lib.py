@@ -22,6 +22,7 @@ SIGNATURES = {
     "ff_version": [],
     "ff_last_error": [],
     "ff_device_check": [],
+    "ff_set_tuning": [I32, I32],
     "ff_fast_norm": [P, P, P, I64, I64, F32, P],
     "ff_add_rms": [P, P, P, P, P, P, I64, I64, F32, I64, I64, P],
     "ff_add_rms_quant": [P, P, P, P, P, P, P, P, I64, I64, F32, I64, I64, P],

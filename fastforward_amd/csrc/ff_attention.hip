@@ -246,18 +246,52 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(
 
 // Selected rows, split over keys: for at most 16 queries (the pick-only tail
 // scores one), one workgroup per head runs 8 waves over interleaved 64-key
-// blocks (wave w takes blocks w, w + 8, ...), each with its own online softmax
-// (the routine above), and the waves' partial results are merged in LDS:
-// M = max_w m_w, den = sum_w den_w 2^((m_w - M) log2e scale), acc likewise,
-// out = acc / den. P is rounded to bf16 relative to each wave's running max
-// rather than the global one, so the result can differ from the one-pass
-// kernels in the last bits of P (well inside the attention tolerance).
+// blocks (wave w takes blocks w, w + 8, ...) and keeps the reference's
+// sequential schedule bit for bit in P:
+//   pass 1: every wave computes its blocks' scores and each block's max per
+//           query into LDS; the running max after block b of the sequential
+//           walk is the prefix max pm[b] = max(bmax[0..b]), one scan per query;
+//   pass 2: every wave recomputes its blocks' scores (same instructions, same
+//           bits) and forms p = exp(s - pm[b]) with the running max the
+//           sequential walk would hold at block b, so bf16(p) -- the rounding
+//           the output depends on -- is identical. Its partial den and
+//           acc = sum bf16(p).V are kept in the frame of its latest pm and
+//           rescaled as pm grows, like the one-pass kernels' alpha.
+// The waves' partials are merged in LDS in the frame of the final max
+// M = pm[last]: den = sum_w den_w 2^((pm_w - M) log2e scale), acc likewise,
+// out = acc / den. Only the fp32 order of the rescales differs from the
+// one-pass kernels (a factor 2^((pm_b - M) c2) per wave instead of a product of
+// per-block alphas).
 constexpr int kDecodeWaves = 8;
+constexpr int kDecodeMaxBlocks = 256;  // 64-key blocks the LDS block maxima hold (t <= 16384)
+
+// Scores of one 64-key block (kb) for the lane's query, masked past lim
+// (the routine of softmax_block's mask), and the block max over the tile's rows
+// of this lane's query (reduced over the 4 key groups).
+__device__ __forceinline__ float decode_block_scores(const bf16_t* __restrict__ kp, const u32x4 (&qf)[4], int kb,
+                                                    int kend, int t, int r16, int g, int lim, f32x4 (&sc)[4]) {
+  score_chunk(kp, qf, kb, t, r16, g, sc[0], sc[1]);
+  if (kb + 32 < kend) {
+    score_chunk(kp, qf, kb + 32, t, r16, g, sc[2], sc[3]);
+  } else {
+    sc[2] = sc[3] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (32 * (i >> 1) + 4 * (i & 1) + r > lim) sc[i][r] = -INFINITY;
+  float bmax = fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3]));
+#pragma unroll
+  for (int i = 1; i < 4; ++i) bmax = fmaxf(bmax, fmaxf(fmaxf(sc[i][0], sc[i][1]), fmaxf(sc[i][2], sc[i][3])));
+  return max_rows(bmax);
+}
 
 __global__ __launch_bounds__(kDecodeWaves * 64) void attention_decode_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ vt,
     const int64_t* __restrict__ positions, int gather_q, bf16_t* __restrict__ y, int s_len, int t, int t_pad,
     int hq, int hk, float c2) {
+  __shared__ float pm[kDecodeMaxBlocks][16];
   __shared__ float sm[kDecodeWaves][16];
   __shared__ float sden[kDecodeWaves][16];
   __shared__ float so[kDecodeWaves][16][D + 1];
@@ -272,6 +306,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void attention_decode_kernel(
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) kend = max(kend, __shfl_xor(kend, o, 64));
   kend = min(kend, t);
+  const int nb = (kend + 63) / 64;  // <= kDecodeMaxBlocks (checked at launch)
   const int64_t qsrc = gather_q ? min(max(pos, 0), t - 1) : qrow;
   const bf16_t* qp = q + ((int64_t)head * (gather_q ? t : s_len) + qsrc) * D;
   u32x4 qf[4];
@@ -279,22 +314,55 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void attention_decode_kernel(
   for (int st = 0; st < 4; ++st) qf[st] = *reinterpret_cast<const u32x4*>(qp + 32 * st + 8 * g);
   const bf16_t* kp = k + (int64_t)kvh * t * D;
   const bf16_t* vp = vt + (int64_t)kvh * D * t_pad;
+  const int plim = min(pos, t - 1);
+
+  // pass 1: block maxima, then the running max of the sequential walk
+  for (int kb = wave * 64; kb < kend; kb += kDecodeWaves * 64) {
+    f32x4 sc[4];
+    const float bmax = decode_block_scores(kp, qf, kb, kend, t, r16, g, plim - kb - 8 * g, sc);
+    if (g == 0) pm[kb / 64][r16] = bmax;
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    float run = -INFINITY;
+    for (int b = 0; b < nb; ++b) {
+      run = fmaxf(run, pm[b][threadIdx.x]);
+      pm[b][threadIdx.x] = run;
+    }
+  }
+  __syncthreads();
+
+  // pass 2: P against the sequential running max of each block
   f32x4 o[8];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, den = 0.f;
-  const int plim = min(pos, t - 1);
+  float m = -INFINITY, den = 0.f;  // the frame (a prefix max) of this wave's partials
   for (int kb = wave * 64; kb < kend; kb += kDecodeWaves * 64) {
     const bool two = kb + 32 < kend;
     f32x4 sc[4];
-    score_chunk(kp, qf, kb, t, r16, g, sc[0], sc[1]);
-    if (two) {
-      score_chunk(kp, qf, kb + 32, t, r16, g, sc[2], sc[3]);
-    } else {
-      sc[2] = sc[3] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    }
+    decode_block_scores(kp, qf, kb, kend, t, r16, g, plim - kb - 8 * g, sc);
+    const float mnew = pm[kb / 64][r16];
+    const float mref = mnew == -INFINITY ? 0.f : mnew;  // a fully masked query keeps p = 0
+    const float alpha = __builtin_amdgcn_exp2f((m - mref) * c2);
+    float p[16], psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float e = __builtin_amdgcn_exp2f((sc[i][r] - mref) * c2);
+        p[4 * i + r] = e;
+        psum += e;
+      }
+    den = den * alpha + psum;
+    m = mnew;
     u32x4 pf[2];
-    const float alpha = softmax_block(sc, true, plim - kb - 8 * g, c2, m, den, pf);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      pf[c].x = pack_bf16x2(p[8 * c + 0], p[8 * c + 1]);
+      pf[c].y = pack_bf16x2(p[8 * c + 2], p[8 * c + 3]);
+      pf[c].z = pack_bf16x2(p[8 * c + 4], p[8 * c + 5]);
+      pf[c].w = pack_bf16x2(p[8 * c + 6], p[8 * c + 7]);
+    }
     rescale(o, alpha);
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
@@ -313,17 +381,17 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void attention_decode_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) so[wave][r16][16 * dt + 4 * g + r] = o[dt][r];
   __syncthreads();
-  // merge: thread -> (query, 4 consecutive d)
+  // merge: thread -> (query, 4 consecutive d), in the frame of the final running max
   for (int e = threadIdx.x; e < 16 * (D / 4); e += kDecodeWaves * 64) {
     const int qi = e / (D / 4), d0 = (e % (D / 4)) * 4;
     if (qi >= s_len) continue;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) mx = fmaxf(mx, sm[w][qi]);
+    const float mx = nb > 0 ? pm[nb - 1][qi] : -INFINITY;
+    const float mref = mx == -INFINITY ? 0.f : mx;
     float dsum = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < kDecodeWaves; ++w) {
-      const float wt = sm[w][qi] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((sm[w][qi] - mx) * c2);
+      if (w * 64 >= kend) continue;  // a wave without blocks holds nothing
+      const float wt = __builtin_amdgcn_exp2f((sm[w][qi] - mref) * c2);
       dsum += sden[w][qi] * wt;
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[r] += so[w][qi][d0 + r] * wt;
@@ -582,17 +650,11 @@ extern "C" int ff_attention_vt(const void* q, const void* k, const void* vt, con
   const int hpw = group % 4 == 0 ? 4 : (group == 2 ? 2 : (group == 1 ? 1 : 0));
   hipStream_t st = (hipStream_t)stream;
   if (!positions && s == t && hpw) {
-    // FF_ATTN_QT=<1|2|4> overrides the query tiles per wave (tuning).
-    static const int qt_env = [] {
-      const char* e = getenv("FF_ATTN_QT");
-      return e ? atoi(e) : 0;
-    }();
+    // ff_set_tuning(FF_TUNE_ATTN_QT, 1 | 2 | 4) overrides the query tiles per wave.
+    const int qt_env = ff_tuning(FF_TUNE_ATTN_QT);
     const int qt = (qt_env == 1 || qt_env == 2 || qt_env == 4) ? qt_env : (s <= 1024 ? 1 : (s <= 2048 ? 2 : 4));
-    // FF_ATTN_NS=<2|3> overrides the number of K/V LDS stages (tuning).
-    static const int ns_env = [] {
-      const char* e = getenv("FF_ATTN_NS");
-      return e ? atoi(e) : 0;
-    }();
+    // ff_set_tuning(FF_TUNE_ATTN_NS, 2 | 3) overrides the number of K/V LDS stages.
+    const int ns_env = ff_tuning(FF_TUNE_ATTN_NS);
     // Two stages run at two workgroups per CU, which fits the registers of
     // QT <= 2 only (QT = 4 would spill); at QT = 1 the 8B prefill (576 tokens,
     // 32/8 heads) takes 12.9 us with two stages and 15.2 us with three.
@@ -614,7 +676,7 @@ extern "C" int ff_attention_vt(const void* q, const void* k, const void* vt, con
     FF_LAUNCH_CHECK("ff_attention_vt");
     return FF_OK;
   }
-  if (positions && s <= 16) {
+  if (positions && s <= 16 && (t + 63) / 64 <= kDecodeMaxBlocks) {
     hipLaunchKernelGGL(attention_decode_kernel, dim3((unsigned)hq), dim3(kDecodeWaves * 64), 0, st,
                        (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)vt, positions, gather_q, (bf16_t*)y,
                        (int)s, (int)t, (int)t_pad, (int)hq, (int)hk, c2);

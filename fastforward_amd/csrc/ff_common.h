@@ -263,6 +263,8 @@ __device__ __forceinline__ float rsqrt_rn(float v) { return 1.0f / __builtin_sqr
 // ------------------------------------------------------------------ host side
 
 void ff_set_error(const char* fmt, ...);
+// Value of an ff_set_tuning override (FF_TUNE_*); 0 = the library's own choice.
+int ff_tuning(int knob);
 
 #define FF_REQUIRE(cond, ...)          \
   do {                                 \

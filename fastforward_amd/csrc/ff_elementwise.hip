@@ -22,6 +22,22 @@ void ff_set_error(const char* fmt, ...) {
 
 extern "C" int ff_version(void) { return 100; }  // 0.1.0
 
+namespace {
+constexpr int kTuneKnobs = 7;
+// Upper bound of each knob's values (index = FF_TUNE_*).
+constexpr int kTuneMax[kTuneKnobs] = {0, 4, 3, 2, 8, 4, 3};
+int g_tuning[kTuneKnobs] = {};
+}  // namespace
+
+int ff_tuning(int knob) { return knob > 0 && knob < kTuneKnobs ? __atomic_load_n(&g_tuning[knob], __ATOMIC_RELAXED) : 0; }
+
+extern "C" int ff_set_tuning(int knob, int value) {
+  FF_REQUIRE(knob > 0 && knob < kTuneKnobs, "ff_set_tuning: unknown knob %d", knob);
+  FF_REQUIRE(value >= 0 && value <= kTuneMax[knob], "ff_set_tuning: value %d out of range for knob %d", value, knob);
+  __atomic_store_n(&g_tuning[knob], value, __ATOMIC_RELAXED);
+  return FF_OK;
+}
+
 extern "C" const char* ff_last_error(void) { return g_err; }
 
 extern "C" int ff_device_check(void) {

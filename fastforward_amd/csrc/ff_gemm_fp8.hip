@@ -474,16 +474,16 @@ Tile pick_tile(int64_t m, int64_t n) {
   return k64x128;
 }
 
-// FF_GEMM_FP8_TILE=64x128 | 128x128 | 128x128s4 | 128x256 forces a tile (tuning
-// sweeps); unset or unknown = the choice above.
+// ff_set_tuning(FF_TUNE_GEMM_FP8_TILE, 1..4) forces a tile (measurement
+// sweeps); 0 = the choice above.
 int forced_tile() {
-  const char* e = getenv("FF_GEMM_FP8_TILE");
-  if (!e) return -1;
-  if (!strcmp(e, "64x128")) return k64x128;
-  if (!strcmp(e, "128x128")) return k128x128;
-  if (!strcmp(e, "128x128s4")) return k128x128Deep;
-  if (!strcmp(e, "128x256")) return k128x256;
-  return -1;
+  switch (ff_tuning(FF_TUNE_GEMM_FP8_TILE)) {
+    case 1: return k64x128;
+    case 2: return k128x128;
+    case 3: return k128x128Deep;
+    case 4: return k128x256;
+    default: return -1;
+  }
 }
 
 }  // namespace
@@ -505,7 +505,7 @@ extern "C" int ff_gemm_fp8(const void* qa, const float* sa, int sa_rows, const v
     FF_LAUNCH_CHECK("ff_gemm_fp8");
     return FF_OK;
   }
-  static const int forced = forced_tile();
+  const int forced = forced_tile();
   const int tile = forced >= 0 ? forced : pick_tile(m, n);
   if (tile == k128x256) launch<128, 256, 1, 3, 1>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
   else if (tile == k128x128) launch<128, 128, 1, 2, 2>(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, s);
@@ -550,7 +550,7 @@ extern "C" int ff_gemm_fp8_qkv(const void* qa, const float* sa, const void* qw, 
   QkvEpilogue qe{(const bf16_t*)q_norm, (const bf16_t*)k_norm, eps_q, eps_k, (const bf16_t*)cos,
                  (const bf16_t*)sin, (bf16_t*)yq, (bf16_t*)yk, (bf16_t*)vt, (int)hq, (int)hk, (int)t_pad};
   hipStream_t s = (hipStream_t)stream;
-  static const int forced = forced_tile();
+  const int forced = forced_tile();
   const int tile = forced >= 0 && forced != k128x256 ? forced : pick_tile(m, n);
   if (tile == k128x128)
     launch<128, 128, 1, 2, 2, kQkv>(qa, sa, 1, qw, sw, 1, nullptr, 0, m, n, k, s, nullptr, qe);

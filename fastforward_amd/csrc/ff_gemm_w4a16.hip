@@ -373,13 +373,10 @@ void launch_w4(const void* x, int64_t ldx, const void* packed, const void* scale
 
 // 192 x 192 tiles dequantise each weight for 192 rows (a third of the VALU work
 // per MFMA of 64-row tiles) but need enough tiles to cover the 256 CUs; below
-// that, 64 x 256 tiles at two workgroups per CU. FF_W4A16_TILE=64x256|192x192
-// overrides the choice.
+// that, 64 x 256 tiles at two workgroups per CU. ff_set_tuning(FF_TUNE_W4A16_TILE,
+// 1 | 2) forces 64x256 | 192x192.
 W4Tile pick_w4_tile(int64_t m, int64_t n) {
-  if (const char* e = getenv("FF_W4A16_TILE")) {
-    if (!strcmp(e, "64x256")) return kW64x256;
-    if (!strcmp(e, "192x192")) return kW192x192;
-  }
+  if (const int f = ff_tuning(FF_TUNE_W4A16_TILE)) return f == 1 ? kW64x256 : kW192x192;
   const int64_t tiles192 = ((m + 191) / 192) * ((n + 191) / 192);
   return (m > 64 && tiles192 >= 256) ? kW192x192 : kW64x256;
 }
@@ -388,14 +385,14 @@ W4Tile pick_w4_tile(int64_t m, int64_t n) {
 // idle, so the k range is split until about two workgroups per CU (at most 8
 // ways, at least one pair of stages each); the fp32 partials cost 8 bytes per
 // output per split (written once, read once by the reduction).
-// FF_W4A16_SPLITS overrides the choice.
+// ff_set_tuning(FF_TUNE_W4A16_SPLITS, s) overrides the choice.
 int pick_w4_splits(W4Tile t, int64_t m, int64_t n, int64_t k) {
   static_assert(W4Cfg<64, 64, 4>::kSplitK, "the 64 x 256 tile stages its fp32 partials in LDS");
   if (t != kW64x256) return 1;
   const int64_t pairs = k / (2 * KSTAGE);
   int64_t s;
-  if (const char* e = getenv("FF_W4A16_SPLITS")) {
-    s = atoi(e);
+  if (const int f = ff_tuning(FF_TUNE_W4A16_SPLITS)) {
+    s = f;
   } else {
     const int64_t tiles = ((m + 63) / 64) * ((n + 255) / 256);
     s = tiles >= 256 ? 1 : 512 / tiles;
@@ -453,3 +450,4 @@ extern "C" int ff_gemm_w4a16_ws(const void* x, int64_t ldx, const void* packed, 
                                 int64_t workspace_bytes, ff_stream_t stream) {
   return gemm_w4a16(x, ldx, packed, scales, group, y, ldy, m, n, k, workspace, workspace_bytes, stream);
 }
+

@@ -470,15 +470,8 @@ extern "C" int ff_gemm_bf16(const void* a, int64_t lda, const void* w, const voi
              "ff_gemm_bf16: alignment");
   hipStream_t st = (hipStream_t)stream;
   const int64_t big = ((m + 127) / 128) * ((n + 127) / 128);
-  // FF_GEMM_BF16_TILE=64x128 | 128x128 | 64x128o3 forces a tile (tuning sweeps).
-  static const int forced = [] {
-    const char* e = getenv("FF_GEMM_BF16_TILE");
-    if (!e) return -1;
-    if (!strcmp(e, "64x128")) return 0;
-    if (!strcmp(e, "128x128")) return 1;
-    if (!strcmp(e, "64x128o3")) return 2;
-    return -1;
-  }();
+  // ff_set_tuning(FF_TUNE_GEMM_BF16_TILE, 1..3) forces 64x128 | 128x128 | 64x128 at three per CU.
+  const int forced = ff_tuning(FF_TUNE_GEMM_BF16_TILE) - 1;
   // 128 x 128 tiles at two workgroups per CU when they fill at least three
   // quarters of the 512 slots, else 64 x 128 tiles (more workgroups for the
   // narrow projections). The GELU-tanh MLP input projection (the tower's fc1,

@@ -21,6 +21,7 @@ The image branch runs the vision tower and the LM step in one hipGraph
 (``pipeline.ImageStep``); weights come from ``checkpoint.load_pretrained``.
 """
 import os
+import threading
 
 import numpy as np
 import torch
@@ -28,7 +29,7 @@ import torch
 from .checkpoint import load_pretrained
 from .pipeline import ImageStep
 from .prepare import canvas, canvases, decode_image, prepare_image, text_parts
-from .runtime import Arena, mrope_positions
+from .runtime import Arena, Runtime, mrope_positions
 from .vision import VisionRuntime
 
 # The reference's execution modes (_family/night_runtime.py:56-65) -> the
@@ -71,10 +72,13 @@ class FamilyRuntime:
         self.warmup = warmup
         # the LM activations of every (canvas, bucket) step alias one region, the vision tower's
         # another (requests run one at a time); the tower's is sized per variant
-        self.arena = Arena(Arena.size_for(self.lm_cfg, self.lm_w, self.max_tokens), self.lm_w.embed.device)
+        self.arena = Arena(Arena.size_for_buckets(self.lm_cfg, self.buckets, Runtime.path_for(self.lm_w)),
+                           self.lm_w.embed.device)
         self.vision_arena = None
         self.geometry = {}   # canvas (h, w) -> prefix ids, image start, merged grid
         self.cache = {}      # (canvas, bucket) -> (ImageStep, pinned rgb, pinned ids, pinned pick, event)
+        # every step shares the two arenas, so requests (refill, replay, read-back) are serialised
+        self.lock = threading.RLock()
         if self.profiles:
             self.select(self.variant)
 
@@ -129,8 +133,14 @@ class FamilyRuntime:
         return b
 
     def graph(self, g):
-        """Option logits (first k, fp32 device tensor) of prepared inputs and
-        whether this call captured the (canvas, bucket) step."""
+        """Option logits (first k, fp32 device tensor, a view of the step's
+        static output: valid until the next request, so a caller on another
+        thread reads it under ``lock``) of prepared inputs and whether this call
+        captured the (canvas, bucket) step."""
+        with self.lock:
+            return self._graph(g)
+
+    def _graph(self, g):
         n = len(g["ids"])
         bucket = self.bucket_for(n)
         key = (g["side"], bucket)
@@ -138,10 +148,10 @@ class FamilyRuntime:
         if captured:
             geo = self.setup_side(g["side"])
             gh, gw = g["side"][0] // 16, g["side"][1] // 16
-            if self.vision_arena is None:    # sized for the variant's largest canvas, so every canvas fits
-                big = max(canvases(self.variant), key=lambda c: c[0] * c[1])
-                self.vision_arena = Arena(VisionRuntime.arena_bytes(self.vis_cfg, self.vis_w, big[0] // 16,
-                                                                    big[1] // 16), self.lm_w.embed.device)
+            if self.vision_arena is None:    # sized so that every canvas of the variant fits
+                need = max(VisionRuntime.arena_bytes(self.vis_cfg, c[0] // 16, c[1] // 16)
+                           for c in canvases(self.variant))
+                self.vision_arena = Arena(need, self.lm_w.embed.device)
             st = ImageStep(self.lm_cfg, self.lm_w, self.vis_cfg, self.vis_w, gh, gw, bucket, geo["image_start"],
                            arena=self.arena, vision_arena=self.vision_arena)
             st.set_inputs(torch.from_numpy(g["rgb"]), torch.from_numpy(g["ids"]), self.positions(g["side"], bucket),
@@ -173,8 +183,9 @@ class FamilyRuntime:
     def predict(self, row):
         """Option logits (python floats) of one request row."""
         g = self.prepare(row)
-        z, _ = self.graph(g)
-        return z.float().cpu().tolist()
+        with self.lock:
+            z, _ = self._graph(g)
+            return z.float().cpu().tolist()
 
     # ------------------------------------------------------------ calibration
 
@@ -182,19 +193,20 @@ class FamilyRuntime:
         """Canvas variant and, for static FP8 linears, its calibration bounds;
         captured steps are dropped (the activation multiplier is recorded at
         capture)."""
-        from .prepare import VARIANTS
-        if variant not in VARIANTS and variant not in self.profiles:
-            raise ValueError(f"Unknown variant {variant!r}")
-        torch.cuda.synchronize()
-        if self.profiles:
-            if variant not in self.profiles:
-                raise ValueError(f"Unknown calibration variant {variant!r}")
-            from .profiles import apply_profile
-            apply_profile(self.lm_w, self.profiles[variant])
-        if variant in VARIANTS:
-            self.variant = variant
-        self.cache.clear()
-        self.vision_arena = None      # re-sized for the new variant's canvases at the next capture
+        with self.lock:
+            from .prepare import VARIANTS
+            if variant not in VARIANTS and variant not in self.profiles:
+                raise ValueError(f"Unknown variant {variant!r}")
+            torch.cuda.synchronize()
+            if self.profiles:
+                if variant not in self.profiles:
+                    raise ValueError(f"Unknown calibration variant {variant!r}")
+                from .profiles import apply_profile
+                apply_profile(self.lm_w, self.profiles[variant])
+            if variant in VARIANTS:
+                self.variant = variant
+            self.cache.clear()
+            self.vision_arena = None      # re-sized for the new variant's canvases at the next capture
 
     def canvas_of(self, height, width):
         """The canvas (height, width) a height x width image gets under the

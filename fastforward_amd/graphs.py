@@ -8,8 +8,8 @@ per-bucket position templates of ``setup_side`` (_family/depth_runtime.py:
   zero-padded to the bucket.
 * Each bucket is one ``Runtime`` whose step is captured once (after warm-up
   runs) on its first request; later requests only refill the static inputs.
-  The buckets' activation buffers alias one ``Arena`` sized for the largest
-  bucket (requests run one at a time).
+  The buckets' activation buffers alias one ``Arena`` that holds the largest
+  of their layouts (requests run one at a time).
 * The M-RoPE positions of a bucket are a template computed once for the
   bundle's layout (prefix text, one image grid, text after it) and stay
   resident; only token ids and the scored row change per request.
@@ -18,6 +18,8 @@ per-bucket position templates of ``setup_side`` (_family/depth_runtime.py:
   pinned buffers by the next request (only the preceding copy must finish
   before the host writes them again).
 """
+import threading
+
 import numpy as np
 import torch
 
@@ -39,6 +41,9 @@ class StepGraphs:
         self.arena = None   # one activation region for every bucket's runtime (made at the first capture)
         self.cache = {}     # bucket -> captured Runtime
         self.staging = {}   # bucket -> (pinned ids (bucket,), pinned pick (1,), event)
+        # the buckets share one arena and one set of static inputs per bucket, so
+        # requests are serialised; callers reading the returned logits view hold it
+        self.lock = threading.RLock()
 
     def select(self, bounds):
         """Apply a calibration profile ({"j:role": bound}) to the static FP8
@@ -46,10 +51,11 @@ class StepGraphs:
         kernel argument recorded at capture, so each bucket re-captures on its
         next request (the reference selects before it captures)."""
         from .profiles import apply_profile
-        torch.cuda.synchronize()
-        apply_profile(self.w, bounds)
-        self.cache.clear()
-        self.staging.clear()
+        with self.lock:
+            torch.cuda.synchronize()
+            apply_profile(self.w, bounds)
+            self.cache.clear()
+            self.staging.clear()
 
     def bucket_for(self, n):
         b = next((b for b in self.buckets if b >= n), None)
@@ -75,14 +81,21 @@ class StepGraphs:
         return ids, n
 
     def run(self, ids, pick, k):
-        """Logits of the first ``k`` options (fp32 device tensor) and whether
-        this call captured the bucket's graph."""
+        """Logits of the first ``k`` options (fp32 device tensor, a view of the
+        bucket's static output: valid until the next request, so a caller on
+        another thread reads it under ``lock``) and whether this call captured
+        the bucket's graph."""
+        with self.lock:
+            return self._run(ids, pick, k)
+
+    def _run(self, ids, pick, k):
         ids, n = self._check(ids, pick, k)
         b = self.bucket_for(n)
         captured = b not in self.cache
         if captured:
-            if self.arena is None:     # sized for the largest bucket, so later buckets fit
-                self.arena = Arena(Arena.size_for(self.cfg, self.w, self.buckets[-1]), self.w.embed.device)
+            if self.arena is None:     # sized so that every bucket's layout fits
+                self.arena = Arena(Arena.size_for_buckets(self.cfg, self.buckets, Runtime.path_for(self.w)),
+                                   self.w.embed.device)
             rt = Runtime(self.cfg, self.w, b, arena=self.arena)
             rt.set_inputs(ids, self.positions(b), int(pick))
             rt.capture(warmup=self.warmup)

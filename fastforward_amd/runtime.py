@@ -17,6 +17,7 @@ Two step bodies produce identical numbers:
 Inputs are a bucket-sized token id buffer (zero padded), M-RoPE positions
 (3, T) and the picked row; the step writes the choice logits (n_options,) fp32.
 """
+import types
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -115,10 +116,15 @@ class Arena:
     Requests run one at a time, and a step writes each activation buffer before
     it reads it, so nothing lives in them between steps: the runtimes of all
     token buckets (and image canvases) of one model can alias a single region
-    sized for the largest of them instead of holding one set each (about
-    100 MB per 576-token bucket at the 8B shape). Static inputs (ids,
-    positions, pick), the image-token buffers and the logits stay per runtime.
-    Steps of runtimes that share an arena must not overlap in time.
+    instead of holding one set each (about 100 MB per 576-token bucket at the
+    8B shape). Static inputs (ids, positions, pick), the image-token buffers and
+    the logits stay per runtime. Steps of runtimes that share an arena must not
+    overlap in time.
+
+    The region must hold the largest layout over every bucket, which is not
+    always the largest bucket's: the k-split workspace of the packed GEMMs
+    depends on whether a shape's tiles fill the GPU unsplit, so a smaller
+    bucket can need more bytes (``size_for_buckets``).
     """
 
     ALIGN = 256
@@ -128,12 +134,17 @@ class Arena:
         self.buf = torch.empty(max(self.nbytes, self.ALIGN), dtype=torch.uint8, device=device)
 
     @staticmethod
-    def size_for(cfg, weights, tokens, path=None):
-        """Bytes of arena a Runtime of ``tokens`` tokens takes (counted by laying
-        its buffers out without allocating them)."""
+    def size_for(cfg, tokens, path="fused"):
+        """Bytes of arena a Runtime of ``tokens`` tokens on ``path`` takes
+        (counted by laying its activation buffers out without allocating them)."""
         counter = _Carver(None)
-        Runtime(cfg, weights, tokens, path=path, _carver=counter)
+        _lay_out_activations(types.SimpleNamespace(), cfg, tokens, path, lambda *s, dt=BF16: counter(s, dt, None))
         return counter.cursor
+
+    @staticmethod
+    def size_for_buckets(cfg, buckets, path="fused"):
+        """Bytes of arena that every bucket of ``buckets`` fits in."""
+        return max(Arena.size_for(cfg, int(b), path) for b in buckets)
 
 
 class _Carver:
@@ -144,7 +155,7 @@ class _Carver:
         self.arena, self.cursor = arena, 0
 
     def __call__(self, shape, dtype, device):
-        n = int(np.prod(shape)) * torch.empty((), dtype=dtype).element_size()
+        n = int(np.prod(shape)) * torch.empty((), dtype=dtype, device="meta").element_size()
         off = (self.cursor + Arena.ALIGN - 1) // Arena.ALIGN * Arena.ALIGN
         self.cursor = off + n
         if self.arena is None:
@@ -154,6 +165,32 @@ class _Carver:
         return self.arena.buf[off:off + n].view(dtype).view(shape)
 
 
+def _lay_out_activations(rt, cfg, tokens, path, a):
+    """Give ``rt`` the step's activation buffers, each from ``a(*shape, dt=dtype)``
+    (an arena carve, a plain allocation, or a byte counter), in a fixed order."""
+    T, Tp, H, D = tokens, (tokens + 63) // 64 * 64, cfg.hidden, cfg.head_dim
+    HQ, HK, I = cfg.heads, cfg.kv_heads, cfg.inter
+    rt.cos, rt.sin = a(T, D), a(T, D)
+    rt.h = [a(T, H), a(T, H)]
+    rt.res = a(T, H)
+    if path != "fused":
+        return
+    rt.xq, rt.xs = a(T, H, dt=E4M3), a(T, dt=torch.float32)
+    rt.yq, rt.yk, rt.vt = a(HQ, T, D), a(HK, T, D), a(HK, D, Tp)
+    rt.attn = a(T, HQ * D)
+    rt.aq, rt.as_ = a(T, HQ * D, dt=E4M3), a(T, dt=torch.float32)
+    rt.o = a(T, H)
+    rt.pq, rt.ps = a(T, H, dt=E4M3), a(T, dt=torch.float32)
+    rt.hm = a(T, I)                                    # swiglu output (bf16)
+    rt.pmax = a(T, I // 64, dt=torch.float32)          # its row maxima per 64 channels
+    rt.mq, rt.ms = a(T, I, dt=E4M3), a(T, dt=torch.float32)
+    rt.dn = a(T, H)
+    rt.hp = a(1, H)
+    # k-split partials of ff_gemm_fp8_pk (o and down share it: their calls are ordered)
+    need = max(gemm_pk_workspace(T, H, HQ * D), gemm_pk_workspace(T, H, I), 256)
+    rt.gws = a(need, dt=torch.uint8)
+
+
 class Runtime:
     """One bucket (T tokens) of the LM step with static device buffers.
 
@@ -161,16 +198,15 @@ class Runtime:
     with the other runtimes of the same model; see ``Arena``); None allocates
     them for this runtime alone."""
 
-    def __init__(self, cfg, weights, tokens, path=None, visual_rows=0, image_start=0, deep_layers=0, arena=None,
-                 _carver=None):
+    def __init__(self, cfg, weights, tokens, path=None, visual_rows=0, image_start=0, deep_layers=0, arena=None):
         self.cfg, self.w = cfg, weights
         self.T = tokens
         self.Tp = (tokens + 63) // 64 * 64
         dev = weights.embed.device
         self.dev = dev
-        fp8 = all(isinstance(op, FP8Linear) for L in weights.layers for op in (L.qkv, L.o, L.gateup, L.down))
-        self.path = path or ("fused" if fp8 else "generic")
-        if self.path == "fused" and not fp8:
+        fused_ok = self.path_for(weights) == "fused"
+        self.path = path or self.path_for(weights)
+        if self.path == "fused" and not fused_ok:
             raise ValueError("the fused path needs FP8Linear (per-token / per-channel) weights")
         if self.path == "fused":
             for L in weights.layers:  # MFMA-fragment copies for the packed tile kernels (once per weight)
@@ -178,11 +214,13 @@ class Runtime:
                 L.gateup.pack()
                 L.down.pack()
         T, H, D = tokens, cfg.hidden, cfg.head_dim
-        HQ, HK, I = cfg.heads, cfg.kv_heads, cfg.inter
         e = lambda *s, dt=BF16: torch.empty(s, device=dev, dtype=dt)  # noqa: E731
-        carve = _carver or (_Carver(arena) if arena is not None else None)
         # activations: aliased into the shared arena when one is given
-        a = (lambda *s, dt=BF16: carve(s, dt, dev)) if carve is not None else e  # noqa: E731
+        if arena is not None:
+            carve = _Carver(arena)
+            a = lambda *s, dt=BF16: carve(s, dt, dev)  # noqa: E731
+        else:
+            a = e
         # static inputs
         self.ids = torch.zeros(T, device=dev, dtype=torch.int64)
         self.pos = torch.zeros(3, T, device=dev, dtype=torch.int64)
@@ -193,28 +231,17 @@ class Runtime:
         self.visual = e(visual_rows, H) if visual_rows else None
         self.deep = [e(visual_rows, H) for _ in range(deep_layers)] if visual_rows else []
         self.inv_freq = rope_inv_freq(cfg.theta, D).to(dev)
-        # activations
-        self.cos, self.sin = a(T, D), a(T, D)
-        self.h = [a(T, H), a(T, H)]
-        self.res = a(T, H)
         self.logits = torch.zeros(weights.head.shape[0], device=dev, dtype=torch.float32)
-        if self.path == "fused":
-            self.xq, self.xs = a(T, H, dt=E4M3), a(T, dt=torch.float32)
-            self.yq, self.yk, self.vt = a(HQ, T, D), a(HK, T, D), a(HK, D, self.Tp)
-            self.attn = a(T, HQ * D)
-            self.aq, self.as_ = a(T, HQ * D, dt=E4M3), a(T, dt=torch.float32)
-            self.o = a(T, H)
-            self.pq, self.ps = a(T, H, dt=E4M3), a(T, dt=torch.float32)
-            self.hm = a(T, I)                                    # swiglu output (bf16)
-            self.pmax = a(T, I // 64, dt=torch.float32)          # its row maxima per 64 channels
-            self.mq, self.ms = a(T, I, dt=E4M3), a(T, dt=torch.float32)
-            self.dn = a(T, H)
-            self.hp = a(1, H)
-            # k-split partials of ff_gemm_fp8_pk (o and down share it: their calls are ordered)
-            need = max(gemm_pk_workspace(T, H, HQ * D), gemm_pk_workspace(T, H, I), 256)
-            self.gws = a(need, dt=torch.uint8)
+        _lay_out_activations(self, cfg, tokens, self.path, a)
         self.graph = None
         self.graph_out = None
+
+    @staticmethod
+    def path_for(weights):
+        """"fused" when every linear is an FP8Linear (per-token / per-channel),
+        else "generic" (the reference's op sequence through the drop-in ops)."""
+        fp8 = all(isinstance(op, FP8Linear) for L in weights.layers for op in (L.qkv, L.o, L.gateup, L.down))
+        return "fused" if fp8 else "generic"
 
     # ------------------------------------------------------------ inputs
 

@@ -20,6 +20,7 @@ The outputs feed the LM step: ``merged`` (n/4, out_hidden) are the image-token
 embeddings that ``Runtime`` scatters into the hidden states, and ``deep`` the
 DeepStack features its first layers add (``add_rms`` with ``deep``).
 """
+import types
 from dataclasses import dataclass
 
 import torch
@@ -256,6 +257,25 @@ def layer_norm(x, norm, eps, out=None):
 
 # ---------------------------------------------------------------- runtime
 
+def _lay_out_vision(rt, cfg, n, n_pad, nm, a):
+    """Give ``rt`` the tower's activation buffers, each from ``a(*shape, dt=dtype)``
+    (an arena carve, a plain allocation, or a byte counter), in a fixed order.
+    Every size grows with the patch count, so the largest canvas of a variant
+    has the largest layout."""
+    H, NH = cfg.hidden, cfg.heads
+    W4 = H * cfg.merge ** 2
+    rt.pixels = a(n, 1536)
+    rt.h = a(n, H)
+    rt.x = a(n, H)
+    rt.qkv = a(n, 3 * H)
+    rt.q, rt.k = a(NH, n, 128), a(NH, n, 128)
+    rt.vt = a(NH, 128, n_pad)
+    rt.z = a(n, H)
+    rt.u = a(n, cfg.inter_pad)
+    rt.x4 = a(nm, W4)
+    rt.u4 = a(nm, W4)
+
+
 class VisionRuntime:
     """The vision step for one image geometry (a (gh, gw) patch grid, i.e. an
     image of 16 gh x 16 gw pixels) with static device buffers.
@@ -268,13 +288,15 @@ class VisionRuntime:
     """
 
     @staticmethod
-    def arena_bytes(cfg, weights, gh, gw):
+    def arena_bytes(cfg, gh, gw):
         """Arena bytes a tower of a (gh, gw) patch grid lays its activations out in."""
         counter = _Carver(None)
-        VisionRuntime(cfg, weights, gh, gw, _carver=counter)
+        n = gh * gw
+        _lay_out_vision(types.SimpleNamespace(), cfg, n, (n + 63) // 64 * 64, n // cfg.merge ** 2,
+                        lambda *s, dt=BF16: counter(s, dt, None))
         return counter.cursor
 
-    def __init__(self, cfg, weights, gh, gw, merged=None, deep=None, arena=None, _carver=None):
+    def __init__(self, cfg, weights, gh, gw, merged=None, deep=None, arena=None):
         if gh % cfg.merge or gw % cfg.merge:
             raise ValueError("the patch grid must be a whole number of merge blocks")
         self.cfg, self.w = cfg, weights
@@ -283,18 +305,22 @@ class VisionRuntime:
         self.n, self.nm = n, n // cfg.merge ** 2
         self.n_pad = (n + 63) // 64 * 64
         dev = weights.pos_embed.device
-        H, HD, NH = cfg.hidden, cfg.head_dim, cfg.heads
-        W4 = H * cfg.merge ** 2
+        H = cfg.hidden
         e = lambda *s, dt=BF16: torch.empty(s, device=dev, dtype=dt)  # noqa: E731
-        carve = _carver or (_Carver(arena) if arena is not None else None)
         # activations (written in full by every step): aliased into a shared arena when one is given
-        a = (lambda *s, dt=BF16: carve(s, dt, dev)) if carve is not None else e  # noqa: E731
+        if arena is not None:
+            carve = _Carver(arena)
+            a = lambda *s, dt=BF16: carve(s, dt, dev)  # noqa: E731
+        else:
+            a = e
         self.rgb = torch.zeros((16 * gh, 16 * gw, 3), device=dev, dtype=torch.uint8)
-        self.pixels = a(n, 1536)
         # per-geometry constants (VisionGraph.geo)
         cos, sin = rope_tables(cfg, gh, gw)
         self.cos, self.sin = cos.to(dev), sin.to(dev)
         idx, wt = interp_taps(cfg, gh, gw)
+        rows = weights.pos_embed.shape[0]
+        if idx.numel() and (int(idx.min()) < 0 or int(idx.max()) >= rows):
+            raise ValueError(f"position-embedding taps outside the {rows}-row table")
         # the tap tables stay referenced until the kernel has read them: a
         # temporary freed inside the argument list could hand its memory to
         # the next one before the launch
@@ -302,16 +328,7 @@ class VisionRuntime:
         self.pos = e(n, H)
         call("ff_pos_interp", ptr(weights.pos_embed), ptr(self._taps[0]), ptr(self._taps[1]), ptr(self.pos), n, 4,
              H, weights.pos_embed.shape[0], stream())
-        # activations
-        self.h = a(n, H)
-        self.x = a(n, H)
-        self.qkv = a(n, 3 * H)
-        self.q, self.k = a(NH, n, 128), a(NH, n, 128)
-        self.vt = a(NH, 128, self.n_pad)
-        self.z = a(n, H)
-        self.u = a(n, cfg.inter_pad)
-        self.x4 = a(self.nm, W4)
-        self.u4 = a(self.nm, W4)
+        _lay_out_vision(self, cfg, n, self.n_pad, self.nm, a)
         self.merged = e(self.nm, cfg.out_hidden) if merged is None else merged
         self.deep = [e(self.nm, cfg.out_hidden) for _ in cfg.deepstack] if deep is None else deep
         if len(self.deep) != len(cfg.deepstack):

@@ -33,6 +33,19 @@ const char* ff_last_error(void);
 /* FF_OK if the current HIP device is a gfx950 (MI355X). */
 int ff_device_check(void);
 
+/* Tile-choice overrides for measurement sweeps and tests (no reference
+ * counterpart). `value` 0 restores the library's own choice for `knob`. The
+ * library never reads them from the environment: a process that does not call
+ * ff_set_tuning runs the built-in choices. Set them only while no launch of an
+ * affected entry point is being issued from another thread. */
+#define FF_TUNE_GEMM_FP8_TILE 1   /* ff_gemm_fp8 / _qkv: 1 64x128, 2 128x128, 3 128x128 4-stage, 4 128x256 */
+#define FF_TUNE_GEMM_BF16_TILE 2  /* ff_gemm_bf16: 1 64x128, 2 128x128, 3 64x128 at three per CU */
+#define FF_TUNE_W4A16_TILE 3      /* ff_gemm_w4a16*: 1 64x256, 2 192x192 */
+#define FF_TUNE_W4A16_SPLITS 4    /* ff_gemm_w4a16_ws: k splits of the 64x256 tile, 1..8 */
+#define FF_TUNE_ATTN_QT 5         /* ff_attention_vt prefill: query tiles per wave, 1, 2 or 4 */
+#define FF_TUNE_ATTN_NS 6         /* ff_attention_vt prefill: K/V LDS stages, 2 or 3 */
+int ff_set_tuning(int knob, int value);
+
 /* fast_norm(x, module): out = bf16(bf16(x*rsqrt(sum(x^2)/h + eps)) * w), one row
  * per token. Replaces _legacy/sub10_runtime.py:37 (fast_norm / rms_one :31-36).
  * x, out: (rows, h) contiguous, h % 8 == 0, h <= 16384. */

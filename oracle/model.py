@@ -59,7 +59,8 @@ def linear(x, spec):
 
     fp8_dynamic: {q (N,K) e4m3, scale (N,)}           -> ops.fp8_linear_dynamic
     fp8_static:  {q, scale (1,), inverse_scale, input_scale} -> ops.fp8_linear_static
-    w4a16:       {packed (N,K/2) u8, scales [K/g,N,2], group} -> ops.w4a16_linear
+    w4a16:       {packed (N,K/2) u8, scales [K/g,N,2], group, weight_bf16 (optional)}
+                                                       -> ops.w4a16_linear
     bf16:        {w (N,K) bf16}                        -> bf16(x @ w^T) in fp32
     """
     kind = spec['kind']
@@ -68,7 +69,7 @@ def linear(x, spec):
     if kind == 'fp8_static':
         return ops.fp8_linear_static(x, spec['q'], spec['scale'], spec['inverse_scale'], spec['input_scale'])
     if kind == 'w4a16':
-        return ops.w4a16_linear(x, spec['packed'], spec['scales'], spec['group'])
+        return ops.w4a16_linear(x, spec['packed'], spec['scales'], spec['group'], spec.get('weight_bf16', False))
     if kind == 'bf16':
         flat = x.reshape(-1, x.shape[-1]).to(F32)
         return (flat @ spec['w'].to(F32).T).to(BF16).reshape(*x.shape[:-1], spec['w'].shape[0])

@@ -344,10 +344,18 @@ def int4_dequant(packed, scales, group):
     return ((q.reshape(n, -1, group) - 8) * s[..., None] + z[..., None]).reshape(n, k)
 
 
-def w4a16_linear(x, packed, scales, group):
-    """``Int4.__call__`` (_family/night_runtime.py:31-42): y = x @ Wdq^T, bf16 out,
-    against the fp32 dequantized weight as the reference's own operator check does."""
+def w4a16_linear(x, packed, scales, group, weight_bf16=False):
+    """``Int4.__call__`` (_family/night_runtime.py:31-42): y = x @ Wdq^T, bf16 out.
+
+    ``weight_bf16=False``: against the fp32 dequantized weight, as the reference's
+    own operator check does (:28-30, :36-40).
+    ``weight_bf16=True``: the dequantized weight rounded to bf16 first, the form
+    the reference's runtime GEMM ``_weight_int4pack_mm`` (:33) multiplies on bf16
+    tensor cores: a bf16 matrix unit takes bf16 operands, so each dequantized
+    weight bf16((q-8)*s + z) enters the products rounded once."""
     flat = x.reshape(-1, x.shape[-1]).to(F32)
     w = int4_dequant(packed, scales, group)
+    if weight_bf16:
+        w = bf16(w)
     y = (flat @ w.T).to(BF16)
     return y.reshape(*x.shape[:-1], w.shape[0])

@@ -224,3 +224,24 @@ def test_select_switches_static_fp8_variants(gpu, tmp_path):
     assert torch.equal(acc.graphs.run(ids, 299, 4)[0].cpu(), za)
     with pytest.raises(ValueError):
         acc.select("c")
+
+
+def test_arena_holds_every_bucket_layout():
+    """The shared activation arena is sized by the largest layout over all
+    buckets, not the largest bucket's: the k-split workspace of the packed FP8
+    GEMMs is needed only where a shape's tiles do not fill the GPU unsplit, so
+    mid-sized buckets can need more bytes than the largest one. Walks the 8B
+    shape over the reference's 8B bucket list (64..2048 in steps of 16,
+    configs/8B.json:10-141) on the host: every bucket's layout fits, and at
+    least one bucket needs more than the largest bucket (the case the sizing
+    must cover)."""
+    from fastforward_amd.runtime import PRESETS, Arena
+    cfg = PRESETS["qwen3vl-8b"]
+    buckets = list(range(64, 2049, 16))
+    sizes = {b: Arena.size_for(cfg, b) for b in buckets}
+    need = Arena.size_for_buckets(cfg, buckets)
+    assert need == max(sizes.values())
+    assert all(s <= need for s in sizes.values())
+    assert any(s > sizes[2048] for s in sizes.values()), "no bucket exceeds the largest one's layout"
+    # the generic path (non-FP8Linear weights) lays out only the shared buffers
+    assert Arena.size_for(cfg, 2048, "generic") < Arena.size_for(cfg, 2048)

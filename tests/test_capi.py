@@ -54,3 +54,19 @@ def test_binding_matches_header(lib_path):
     lib = _lib.load()
     assert lib.ff_version() >= 100
     assert lib.ff_last_error() == b""
+
+
+def test_tuning_knobs_validate_without_a_gpu(lib_path):
+    """ff_set_tuning checks knob and value ranges on the host and never reads the
+    environment; 0 restores the built-in choice."""
+    from fastforward_amd import _lib
+    _lib.load()
+    _lib.call("ff_set_tuning", 3, 2)
+    _lib.call("ff_set_tuning", 3, 0)
+    with pytest.raises(RuntimeError, match="unknown knob"):
+        _lib.call("ff_set_tuning", 99, 1)
+    with pytest.raises(RuntimeError, match="out of range"):
+        _lib.call("ff_set_tuning", 4, 9)
+    text = "".join(open(os.path.join(ROOT, "fastforward_amd", "csrc", f)).read()
+                   for f in os.listdir(os.path.join(ROOT, "fastforward_amd", "csrc")))
+    assert "getenv" not in text

@@ -345,3 +345,52 @@ def test_predict_int4_execution_mode(gpu, tmp_path):
     rel = float((got - want).norm() / want.norm())
     print(f"int4: ours {got.tolist()}\n      hf   {want.tolist()}\n  rel L2 {rel:.4f}", flush=True)
     assert rel <= 0.05
+
+
+@pytest.mark.gpu
+def test_two_canvases_alternate_over_shared_arenas(gpu, tmp_path):
+    """Requests that alternate between two canvases (a landscape and a portrait
+    image under aspect256) run two captured image steps whose LM activations
+    alias one arena and whose vision activations alias another: both steps'
+    buffers start at the arenas' bases, and every replay, over two rounds,
+    equals an eager ImageStep of the same inputs on private buffers bit for bit."""
+    from pathlib import Path
+
+    from PIL import Image
+
+    from fastforward_amd.api import Accelerator
+    from fastforward_amd.pipeline import ImageStep
+    m, path = _tiny_hf(tmp_path, seed=11)
+    _tiny_tokenizer(Path(path))
+    acc = Accelerator(_bundle(tmp_path, path))
+    rt = acc.runtime
+    rng = np.random.default_rng(12)
+    files = []
+    for j, shape in enumerate([(200, 300, 3), (300, 200, 3)]):
+        f = tmp_path / f"alt{j}.png"
+        Image.fromarray(rng.integers(0, 256, size=shape, dtype=np.uint8)).save(f)
+        files.append(f)
+    cands = ["red", "green", "blue", "black"]
+    q = "What color is shown?"
+    g = [rt.prepare(dict(image_path=str(f), instruction=q, candidates=cands)) for f in files]
+    assert g[0]["side"] != g[1]["side"], "the two images must land on different canvases"
+    eager = []
+    for gi in g:
+        geo = rt.setup_side(gi["side"])
+        bucket = rt.bucket_for(len(gi["ids"]))
+        st = ImageStep(rt.lm_cfg, rt.lm_w, rt.vis_cfg, rt.vis_w, gi["side"][0] // 16, gi["side"][1] // 16, bucket,
+                       geo["image_start"])
+        st.set_inputs(torch.from_numpy(gi["rgb"]), torch.from_numpy(gi["ids"]), rt.positions(gi["side"], bucket),
+                      gi["pick"])
+        eager.append(st.step()[:len(cands)].float().cpu())
+        del st
+    print("two canvases alternating over the shared arenas", flush=True)
+    for rnd in range(2):
+        for j, f in enumerate(files):
+            r = acc.predict(f, q, cands)
+            assert torch.equal(torch.tensor(r["logits"]), eager[j]), (rnd, j, r["logits"], eager[j].tolist())
+    assert len(rt.cache) == 2
+    for st, *_ in rt.cache.values():
+        assert st.lm.cos.data_ptr() == rt.arena.buf.data_ptr()
+        assert st.vision.pixels.data_ptr() == rt.vision_arena.buf.data_ptr()
+    assert not torch.equal(eager[0], eager[1])

@@ -5,24 +5,37 @@ What is asserted, and why:
 * Bit-exact internal consistency: the fused FP8 path equals the reference op
   sequence (generic path), every hipGraph replay equals the eager step, and
   padding tokens after the picked row cannot change the logits.
-* Choice logits of the final layer + readout given the same final-layer input
-  (teacher-forced tail), at the full 2B / 8B shapes, within a stated relative
-  bound (max_c |dz_c| <= tol * max_c |z_c|) with the identical argmax:
-  tol = 2e-2 for W4A16 (bf16-rounded dequantized weights) and 3e-2 for FP8, whose GEMMs run on the f8f6f4 matrix
-  instructions (each 32-product block is summed with ~13 significant bits, then
-  blocks are summed in fp32 -- the same structure as the reference's Hopper FP8
-  MMA), so ~1% of GEMM outputs round to a neighbouring bf16 of the oracle's fp32
-  result and the final layer's per-token requantizations carry that to the logits.
-* Every decoder layer, given the same input, within a stated relative L2 bound
-  of the oracle's layer (FP8: 6%, W4A16: 2%).
-
-Why not end to end at 1e-2: the per-token dynamic e4m3 quantization in front of
-every GEMM turns one-ulp differences of its input into a shifted row scale and
-flipped codes, so the step's output is sensitive to the GEMM summation order
-itself -- the oracle moves by several percent when only its fp32 accumulation is
-replaced by exact accumulation, and FP8 matrix units (v_mfma_*_f8f6f4 here,
-Hopper's FP8 MMA in the reference) sum each 32-product block with ~13-14 bits.
-The end-to-end gap is printed next to that oracle self-sensitivity.
+* Teacher-forced tail (final layer + readout given the same final-layer input)
+  at the full 2B / 8B shapes, for every seed: choice logits within 1e-2
+  (max_c |dz_c| <= 1e-2 * max_c |z_c|) with the identical argmax. The tiny
+  model is held to 3e-2 in its FP8 modes: its rows have 512 e4m3 codes, 8x
+  fewer than the 8B shape's 4096, so each code that a requantization flips moves
+  a dot product by sqrt(8) ~ 2.8x more relative to its size, and its logits
+  (magnitude 0.1-0.5) sit where one bf16 ulp of the readout is 0.4-0.8 % of
+  max |z|; in its W4A16 mode (no requantization) it keeps 1e-2.
+* Every sampled decoder layer, given the same input, within a stated relative
+  L2 bound of the oracle's layer (FP8: 6 %, W4A16: 2 %).
+* End to end, over four seeds per configuration, the step is compared with the
+  oracle and with the oracle's own sensitivity to its summation order:
+  - FP8 (per-token dynamic activation scales): the per-token e4m3 quantization
+    in front of every GEMM turns a one-ulp difference of its input into a
+    shifted row scale and flipped codes, so the step is chaotic in the GEMM
+    summation order itself: the oracle moves by 10-40 % when only its fp32
+    accumulation is replaced by exact accumulation, which flips the bf16
+    rounding of ~0.005 % of GEMM outputs. The GPU's matrix unit sums each
+    32-product block with ~13 bits (~1.2 % of outputs round to a neighbouring
+    bf16, the same structure as the reference's Hopper FP8 MMA).
+  - W4A16 (against the oracle's bf16-operand form: each dequantized weight
+    rounded once to bf16, as any bf16 matrix unit, and the reference's
+    ``_weight_int4pack_mm``, consumes it): no requantization, but every bf16
+    rounding point re-draws its rounding when its input moves by a fraction of
+    an ulp -- exact instead of fp32 accumulation moves one 8B layer of the
+    oracle by 0.35 % (relative L2) and the 36-layer logits by a few percent,
+    the size of the GPU-vs-oracle gap.
+  The bar in both: the GPU-vs-oracle gap averaged over the seeds is at most
+  1.5x the oracle's own exact-vs-fp32 gap averaged over the same seeds (for
+  two saturated perturbations of the same map the two gaps are equally
+  distributed); argmax agreement is printed beside the oracle's own.
 """
 import os
 import sys
@@ -54,7 +67,10 @@ def _run(cfg, w, tokens, ids, pos, pick, path=None, **kw):
     return rt, z.cpu()
 
 
-TAIL_TOL = {"fp8": 3e-2, "fp8_static": 3e-2, "w4a16": 2e-2}
+TAIL_TOL = 1e-2                                   # the full-size shapes
+TINY_TAIL_TOL = {"fp8": 3e-2, "fp8_static": 3e-2, "w4a16": 1e-2}
+E2E_MULTIPLE = 1.5
+SEEDS = (7, 8, 9, 10)
 
 
 def _check_vs_oracle(z, want, what, tol):
@@ -89,16 +105,29 @@ def _exact_gemm(qa, sa, qw, sw):
     return (acc * sa.double().reshape(-1, 1) * sw.double().reshape(1, -1)).to(torch.bfloat16)
 
 
-def _check_teacher_forced(cfg, w, mode, ids, pos, pick, layers, what, copy_all=True):
+def _exact_w4a16(x, packed, scales, group, weight_bf16=False):
+    """The W4A16 GEMM with fp64 accumulation (bf16 x bf16 products are exact in
+    fp64 and their sums keep 53 bits): the oracle's form up to the fp32
+    summation order."""
+    flat = x.reshape(-1, x.shape[-1]).double()
+    w = O.int4_dequant(packed, scales, group)
+    if weight_bf16:
+        w = O.bf16(w)
+    return (flat @ w.double().T).to(torch.bfloat16).reshape(*x.shape[:-1], w.shape[0])
+
+
+def _check_teacher_forced(cfg, w, mode, ids, pos, pick, layers, what, copy_all=True, tail_tol=TAIL_TOL):
     """Run the GPU step with a residual trace, then check the chosen layers and the
-    tail against the oracle fed with the GPU's own layer inputs."""
+    tail against the oracle fed with the GPU's own layer inputs. W4A16 linears
+    use the oracle's bf16-operand form."""
     from fastforward_amd.runtime import Runtime
     rt = Runtime(cfg, w, pos.shape[1])
     rt.set_inputs(ids, pos, pick)
     trace = []
     z = rt.step(trace=trace).clone().cpu()
     trace = [t.cpu() for t in trace]
-    shape, ow = to_oracle(cfg, w, only=None if copy_all else set(layers) | {cfg.layers - 1})
+    shape, ow = to_oracle(cfg, w, only=None if copy_all else set(layers) | {cfg.layers - 1},
+                          int4_bf16=mode == "w4a16")
     del rt
     cos, sin = O.mrope_cos_sin(pos, shape.theta, shape.head_dim, shape.sections)
     full = torch.zeros(pos.shape[1], dtype=torch.int64)
@@ -109,7 +138,7 @@ def _check_teacher_forced(cfg, w, mode, ids, pos, pick, layers, what, copy_all=T
         print(f"{what} layer {j}: teacher-forced rel L2 {got:.4f}", flush=True)
         assert got <= LAYER_BOUND[mode], (what, j, got)
     zt = omodel.tail(shape, ow.layers[-1], ow, hin[-1], cos, sin, pick)
-    _check_vs_oracle(z, zt, f"{what} teacher-forced tail", TAIL_TOL[mode])
+    _check_vs_oracle(z, zt, f"{what} teacher-forced tail", tail_tol)
     return z, shape, ow
 
 
@@ -119,7 +148,8 @@ def test_tiny_model_teacher_forced(gpu, mode):
     cfg = _tiny()
     w = make_model(cfg, mode=mode, seed=1, norm_jitter=0.2, n_options=4)
     ids, pos, pick = make_request(cfg, 96, 4, 6, seed=1)
-    _check_teacher_forced(cfg, w, mode, ids, pos, pick, range(cfg.layers - 1), f"tiny {mode}")
+    _check_teacher_forced(cfg, w, mode, ids, pos, pick, range(cfg.layers - 1), f"tiny {mode}",
+                          tail_tol=TINY_TAIL_TOL[mode])
 
 
 def test_fused_path_equals_reference_op_sequence(gpu):
@@ -201,45 +231,60 @@ def test_visual_rows_and_deepstack_vs_oracle(gpu):
     assert torch.equal(rt2.step().cpu(), z)
 
 
+@pytest.mark.timeout(900)
 @pytest.mark.parametrize("preset,tokens,grid,choices,mode", [
     ("qwen3vl-2b", 320, (16, 16), 4, "fp8"),
     ("qwen3vl-8b", 576, (16, 32), 8, "fp8"),
     ("qwen3vl-8b", 576, (16, 32), 8, "w4a16"),
 ])
 def test_full_model_vs_oracle(gpu, preset, tokens, grid, choices, mode):
-    """The full-depth shapes (random-init N(0, 0.02) weights, bf16 embeddings):
-    the hipGraph replay equals the eager step; sampled layers and the tail are
-    teacher-forced against the oracle; the end-to-end gap is reported beside the
-    oracle's own sensitivity to exact accumulation."""
+    """The full-depth shapes (random-init N(0, 0.02) weights, bf16 embeddings),
+    one model and request per seed: the hipGraph replay equals the eager step;
+    sampled layers and the tail are teacher-forced against the oracle; the
+    end-to-end logits are held to the bars stated in the module docstring."""
     from fastforward_amd.runtime import PRESETS, Runtime
     from fastforward_amd.synthetic import make_model, make_request
     cfg = PRESETS[preset]
-    print(f"building {preset} {mode}", flush=True)
-    w = make_model(cfg, mode=mode, seed=7, n_options=choices)
-    ids, pos, pick = make_request(cfg, tokens, *grid, seed=7)
-    rt = Runtime(cfg, w, tokens)
-    rt.set_inputs(ids, pos, pick)
-    z_eager = rt.step().clone()
-    rt.capture()
-    z_graph = rt.replay().clone()
-    torch.cuda.synchronize()
-    assert torch.equal(z_graph, z_eager)
-    del rt
     layers = (0, 1, cfg.layers // 2, cfg.layers - 2)
-    z, shape, ow = _check_teacher_forced(cfg, w, mode, ids, pos, pick, layers, f"{preset} {mode}")
-    assert torch.equal(z, z_eager.cpu())
-    del w
-    torch.cuda.empty_cache()
-    ze = omodel.step(shape, ow, ids, pos, pick)
-    orig = O.fp8_gemm
-    O.fp8_gemm = _exact_gemm
-    try:
-        zx = omodel.step(shape, ow, ids, pos, pick)
-    finally:
-        O.fp8_gemm = orig
-    print(f"{preset} {mode} end to end: gpu={z.tolist()} oracle={ze.tolist()} "
-          f"gpu-vs-oracle {rel_err(z, ze):.4f}, oracle(exact acc)-vs-oracle {rel_err(zx, ze):.4f}", flush=True)
-    assert rel_err(z, ze) <= 1.0, "gross end-to-end disagreement"
+    gaps, self_gaps, agree, self_agree = [], [], 0, 0
+    for n, seed in enumerate(SEEDS):
+        what = f"{preset} {mode} seed {seed}"
+        print(f"building {what}", flush=True)
+        w = make_model(cfg, mode=mode, seed=seed, n_options=choices)
+        ids, pos, pick = make_request(cfg, tokens, *grid, seed=seed)
+        rt = Runtime(cfg, w, tokens)
+        rt.set_inputs(ids, pos, pick)
+        z_eager = rt.step().clone()
+        if n == 0:
+            rt.capture()
+            z_graph = rt.replay().clone()
+            torch.cuda.synchronize()
+            assert torch.equal(z_graph, z_eager)
+        del rt
+        z, shape, ow = _check_teacher_forced(cfg, w, mode, ids, pos, pick, layers, what)
+        assert torch.equal(z, z_eager.cpu())
+        del w
+        torch.cuda.empty_cache()
+        ze = omodel.step(shape, ow, ids, pos, pick)
+        name, exact = ("w4a16_linear", _exact_w4a16) if mode == "w4a16" else ("fp8_gemm", _exact_gemm)
+        orig = getattr(O, name)
+        setattr(O, name, exact)
+        try:
+            zx = omodel.step(shape, ow, ids, pos, pick)
+        finally:
+            setattr(O, name, orig)
+        gaps.append(rel_err(z, ze))
+        self_gaps.append(rel_err(zx, ze))
+        agree += O.choose(z.tolist()) == O.choose(ze.tolist())
+        self_agree += O.choose(zx.tolist()) == O.choose(ze.tolist())
+        print(f"{what} end to end: gpu={z.tolist()} oracle={ze.tolist()} oracle(exact acc)={zx.tolist()} "
+              f"gpu-vs-oracle {gaps[-1]:.4f}, oracle(exact acc)-vs-oracle {self_gaps[-1]:.4f}", flush=True)
+        del ow
+    mg, ms = sum(gaps) / len(gaps), sum(self_gaps) / len(self_gaps)
+    print(f"{preset} {mode} over seeds {SEEDS}: mean gpu-vs-oracle {mg:.4f}, mean oracle self-gap {ms:.4f} "
+          f"(ratio {mg / ms:.2f}); argmax agreement gpu {agree}/{len(SEEDS)}, "
+          f"oracle(exact acc) {self_agree}/{len(SEEDS)}", flush=True)
+    assert mg <= E2E_MULTIPLE * ms, (mg, ms)
     sys.stdout.flush()
 
 

@@ -237,8 +237,11 @@ def test_int4_quant_bit_exact(gpu, sym, group):
 
 # ------------------------------------------------------------------ GEMMs
 
+# the microbench shapes, the 8B step's row-major tiles (qkv: 128 x 128 four-stage; o: 64 x 128;
+# gate/up width: 128 x 128 two-stage), a tail row and ragged edges
 FP8_SHAPES = [(320, 2048, 6144), (320, 6144, 2048), (576, 4096, 12288), (576, 12288, 4096),
-              (1024, 5120, 25600), (1, 4096, 24576), (17, 256, 384), (130, 1024, 200), (33, 25600, 1024)]
+              (1024, 5120, 25600), (576, 4096, 6144), (576, 4096, 4096), (576, 4096, 24576), (1, 4096, 24576),
+              (17, 256, 384), (130, 1024, 200), (33, 25600, 1024)]
 
 
 def _assert_fp8_gemm(y, qa, sa, qw, sw, oracle, what):
@@ -436,17 +439,37 @@ def test_gemm_w4a16(gpu, m, k, n, sym, group):
     assert float((want - exact).pow(2).mean().sqrt() / exact.pow(2).mean().sqrt()) <= 5e-3
 
 
-@pytest.mark.parametrize("tile,splits", [("64x256", None), ("64x256", "1"), ("64x256", "3"), ("192x192", None)])
+W4_TILES = {"64x256": 1, "192x192": 2}
+
+
+@pytest.fixture
+def tuning(gpu):
+    """ff_set_tuning(knob, value) for one test; every knob is reset afterwards."""
+    from fastforward_amd._lib import call
+    used = []
+
+    def set_(knob, value):
+        used.append(knob)
+        call("ff_set_tuning", knob, value)
+    yield set_
+    for knob in used:
+        call("ff_set_tuning", knob, 0)
+
+
+FF_TUNE_W4A16_TILE, FF_TUNE_W4A16_SPLITS = 3, 4
+
+
+@pytest.mark.parametrize("tile,splits", [("64x256", None), ("64x256", 1), ("64x256", 3), ("192x192", None)])
 @pytest.mark.parametrize("m,k,n", [(576, 4096, 6144), (200, 1024, 392), (1, 12288, 4096)])
-def test_gemm_w4a16_both_tiles(gpu, monkeypatch, m, k, n, tile, splits):
+def test_gemm_w4a16_both_tiles(gpu, tuning, m, k, n, tile, splits):
     """Each tile shape of the W4A16 GEMM (chosen by size in production) and the
     split-K form of the 64 x 256 tile (automatic, off, forced to 3) against the
     fp64 product with the exactly dequantised weight, asymmetric group 32 and
     ragged M / N edges included."""
     from fastforward_amd.linear import Int4
-    monkeypatch.setenv("FF_W4A16_TILE", tile)
+    tuning(FF_TUNE_W4A16_TILE, W4_TILES[tile])
     if splits is not None:
-        monkeypatch.setenv("FF_W4A16_SPLITS", splits)
+        tuning(FF_TUNE_W4A16_SPLITS, splits)
     x = torch.randn(m, k, generator=_g(36)).to(BF16)
     w = (torch.randn(n, k, generator=_g(37)) * 0.02).to(BF16)
     for sym, group in ((True, 128), (False, 32)):
@@ -461,13 +484,13 @@ def test_gemm_w4a16_both_tiles(gpu, monkeypatch, m, k, n, tile, splits):
 
 
 @pytest.mark.parametrize("tile", ["64x256", "192x192"])
-def test_w4a16_dequant_bit_exact_via_one_hot(gpu, monkeypatch, tile):
+def test_w4a16_dequant_bit_exact_via_one_hot(gpu, tuning, tile):
     """x = rows of the identity: y[r, n] = bf16((q-8)*s + z) for k = r exactly.
     Columns 0-39 hold a constant 64.0 in their first 32 k: the asymmetric
     quantizer then stores s = bf16(1e-6), z = 64, for which z - 8s is not exact
     in fp32, so those stages take the kernel's exact (q-8, then fma) form."""
     from fastforward_amd.linear import Int4
-    monkeypatch.setenv("FF_W4A16_TILE", tile)
+    tuning(FF_TUNE_W4A16_TILE, W4_TILES[tile])
     k, n = 256, 128
     w = (torch.randn(n, k, generator=_g(31)) * 0.02).to(BF16)
     w[:40, :32] = 64.0
@@ -529,6 +552,31 @@ def test_attention_selected_positions_and_strided_v(gpu):
     want = O.attention_direct(q, k, packed[..., (hq + hk) * d:].view(1, t, hk, d).transpose(1, 2), d ** -0.5,
                               positions=pick).float()
     assert float((got - want).abs().max()) <= 1 / 64
+
+
+@pytest.mark.parametrize("t,hq,hk", [(576, 32, 8), (2000, 16, 8)])
+def test_attention_decode_follows_sequential_schedule(gpu, t, hq, hk):
+    """Selected rows (<= 16 queries, the pick-only tail) run split over keys, but
+    P is rounded against the running max the reference's sequential 64-key walk
+    holds at each block (_legacy/limit_kernels.py:8-45): against the oracle the
+    output is within relative RMS 2e-4 (a split walk whose waves keep their own
+    maxima measured 2.7e-3, the size of P's bf16 rounding itself), and it equals
+    the sequential per-head kernel (17 rows take that one) to 1 bf16 ulp for
+    all but 0.1 % of values (only the fp32 order of the rescales differs)."""
+    from fastforward_amd import ops
+    d = 128
+    q = torch.randn(1, hq, 17, d, generator=_g(40)).to(BF16)
+    k = torch.randn(1, hk, t, d, generator=_g(41)).to(BF16)
+    v = torch.randn(1, hk, t, d, generator=_g(42)).to(BF16)
+    pos = torch.cat([torch.tensor([t - 1, 0, 63, 64]), torch.randint(0, t, (13,), generator=_g(43))])
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    seq = ops.attention_direct(qd, kd, vd, d ** -0.5, positions=pos.to(DEV)).cpu()            # per-head kernel
+    dec = ops.attention_direct(qd[:, :, :16].contiguous(), kd, vd, d ** -0.5, positions=pos[:16].to(DEV)).cpu()
+    want = O.attention_direct(q[:, :, :16], k, v, d ** -0.5, positions=pos[:16])
+    rel = float((dec.float() - want.float()).norm() / want.float().norm())
+    print(f"decode t={t}: rel RMS vs oracle {rel:.2e}", flush=True)
+    assert rel <= 2e-4, rel
+    assert_bf16_close(dec, seq[:, :16], 1, 1e-3, "decode vs sequential per-head kernel")
 
 
 # ------------------------------------------------------------------ readout, gathers, rope

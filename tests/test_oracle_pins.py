@@ -408,6 +408,30 @@ def test_w4a16_linear_matches_fp64():
         # the reference's own operator bar: relative RMS <= 1% against the fp32 dequant
         ref = x.double().numpy() @ w.double().numpy().T
         assert np.sqrt(((y - ref) ** 2).mean()) / np.sqrt((ref ** 2).mean()) < 0.2
+        # the bf16-operand form: each dequantized weight rounded once to bf16 (numpy bit RNE)
+        yb = ops.w4a16_linear(x, packed, scales, grp, weight_bf16=True).float().numpy()
+        wb = bf16_round_np(wd.astype(np.float32)).astype(np.float64)
+        _close_bf16(yb, bf16_round_np((x.double().numpy() @ wb.T).astype(np.float32)), frac=0.05)
+        assert not np.array_equal(wb, wd), "the test weights must have dequantized values that bf16 rounds"
+
+
+def test_w4a16_linear_matches_torch_int4pack_cpu():
+    """The fp32-dequant form equals torch's own CPU int4 GEMM
+    (aten._weight_int4pack_mm_for_cpu, the CPU sibling of the reference's
+    _weight_int4pack_mm, _family/night_runtime.py:33) given the same nibble codes
+    and [K/g, N, 2] (scale, zero) table, bit for bit on the symmetric group-128
+    form and for >= 99% of outputs on the asymmetric group-32 form (the library
+    folds the zero point in a different order)."""
+    g = _gen(20)
+    m, k, n = 8, 1024, 256
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    w = torch.randn(n, k, generator=g) * 0.02
+    for quant, grp, need in ((ops.int4_quantize_sym, 128, 1.0), (ops.int4_quantize_asym, 32, 0.99)):
+        q, packed, scales = quant(w, grp)
+        wp = torch.ops.aten._convert_weight_to_int4pack_for_cpu(q.to(torch.int32), 1)
+        lib = torch.ops.aten._weight_int4pack_mm_for_cpu(x, wp, grp, scales)
+        ours = ops.w4a16_linear(x, packed, scales, grp)
+        assert float((lib == ours).float().mean()) >= need, (grp, float((lib == ours).float().mean()))
 
 
 # ------------------------------------------------------------------ composition vs HF
