@@ -49,6 +49,7 @@ SIGNATURES = {
     "ff_gemm_w4a16": [P, I64, P, P, I64, P, I64, I64, I64, I64, P],
     "ff_gemm_w4a16_workspace": [I64, I64, I64, PI64],
     "ff_gemm_w4a16_ws": [P, I64, P, P, I64, P, I64, I64, I64, I64, P, I64, P],
+    "ff_gemm_w4a16_noalloc": [P, I64, P, P, I64, P, I64, I64, I64, I64, P],
     "ff_embed": [P, P, P, I64, I64, I64, P],
     "ff_gather_rows": [P, I64, P, P, I64, I64, I64, I64, P],
     "ff_scatter_rows": [P, P, I64, I64, I64, P],

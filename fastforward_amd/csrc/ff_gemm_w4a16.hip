@@ -43,6 +43,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "ff_common.h"
@@ -451,3 +452,68 @@ extern "C" int ff_gemm_w4a16_ws(const void* x, int64_t ldx, const void* packed, 
   return gemm_w4a16(x, ldx, packed, scales, group, y, ldy, m, n, k, workspace, workspace_bytes, stream);
 }
 
+// ------------------------------------------------------------------ allocation-free variant
+//
+// ff_gemm_w4a16_noalloc keeps the split-K partials in `scratch`, a file-scope
+// device array of kScratchBytes: each GPU the library runs on holds its own copy
+// until the process ends. The array's host-side name is not a device address;
+// its address on a device comes from hipGetSymbolAddress, taken once per device
+// on the first call made with that device current, and only that address is
+// handed to kernels. Every split writes all of its partials before the reduction
+// reads them, so nothing has to start at zero. All calls on one GPU share its
+// array: calls that overlap in time on one GPU (two streams, two threads) race.
+
+namespace {
+
+constexpr int64_t kScratchBytes = int64_t(32) << 20;
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+// Device address of this device's `scratch` (taken once per device), or nullptr
+// with the error set.
+void* scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    ff_set_error("ff_gemm_w4a16_noalloc: no current HIP device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      ff_set_error("ff_gemm_w4a16_noalloc: hipGetSymbolAddress failed on device %d: %s", dev,
+                   hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch[dev] = p;
+  }
+  return g_scratch[dev];
+}
+
+}  // namespace
+
+extern "C" int ff_gemm_w4a16_noalloc(const void* x, int64_t ldx, const void* packed, const void* scales,
+                                     int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
+                                     ff_stream_t stream) {
+  FF_REQUIRE(m >= 0 && n > 0 && k > 0, "ff_gemm_w4a16_noalloc: bad sizes");
+  int64_t need = 0;
+  if (k % (2 * KSTAGE) == 0) {
+    const int splits = pick_w4_splits(pick_w4_tile(m, n), m, n, k);
+    need = splits > 1 ? (int64_t)splits * m * n * 4 : 0;
+  }
+  FF_REQUIRE(need <= kScratchBytes,
+             "ff_gemm_w4a16_noalloc: this %lld x %lld x %lld product needs %lld bytes of split-K scratch; the "
+             "static scratch holds %lld (use ff_gemm_w4a16_ws with a workspace)",
+             (long long)m, (long long)n, (long long)k, (long long)need, (long long)kScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    ws = scratch_on_current_device();
+    if (!ws) return FF_EDEVICE;
+  }
+  return gemm_w4a16(x, ldx, packed, scales, group, y, ldy, m, n, k, ws, need, stream);
+}

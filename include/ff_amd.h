@@ -249,6 +249,19 @@ int ff_gemm_w4a16_ws(const void* x, int64_t ldx, const void* packed, const void*
                      int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
                      void* workspace, int64_t workspace_bytes, ff_stream_t stream);
 
+/* ff_gemm_w4a16_ws without a workspace argument and without any allocation. No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under hipGraph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). The split-K partials go to a static device scratch of
+ * 32 MiB per GPU, held until the process ends. The split the library picks by
+ * itself always fits (it keeps splits * m * n <= 2^23); a split forced with
+ * ff_set_tuning that wants more is rejected with FF_EINVAL. Results equal
+ * ff_gemm_w4a16_ws given ff_gemm_w4a16_workspace bytes, bit for bit. All calls
+ * on one GPU share its scratch: calls that overlap in time on one GPU race. */
+int ff_gemm_w4a16_noalloc(const void* x, int64_t ldx, const void* packed, const void* scales,
+                          int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
+                          ff_stream_t stream);
+
 /* Embedding gather h[t] = table[ids[t]] (scaled_qwen_runtime.py:145
  * embed_tokens). Ids outside [0, vocab) read row 0 (the host validates ids). */
 int ff_embed(const int64_t* ids, const void* table, void* out, int64_t t, int64_t h,
