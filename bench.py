@@ -88,7 +88,7 @@ def launch_gemm(cfg, role, lw, q, s, m, b):
     op = getattr(lw, role)
     n, k = op.weight.shape
     if role == "qkv":
-        call("ff_gemm_fp8_qkv", ptr(q), ptr(s), ptr(op.weight), ptr(op.scale), m, k, cfg.heads, cfg.kv_heads,
+        call("ff_gemm_fp8_qkv", ptr(q), ptr(s), 1, ptr(op.weight), ptr(op.scale), 1, m, k, cfg.heads, cfg.kv_heads,
              ptr(lw.q_norm.weight), ptr(lw.k_norm.weight), float(lw.q_norm.variance_epsilon),
              float(lw.k_norm.variance_epsilon), ptr(b["cos"]), ptr(b["sin"]), ptr(b["yq"]), ptr(b["yk"]),
              ptr(b["vt"]), b["Tp"], stream())
@@ -389,6 +389,7 @@ def main():
         torch.cuda.empty_cache()
         # the other LM configurations, each one hipGraph replay per step
         for key, preset, mode, tokens, gx, n_opt in (
+                ("fp8_static_8b_576_step_ms", args.preset, "fp8_static", T, grid, 8),
                 ("w4a16_g128_8b_576_step_ms", args.preset, "w4a16", T, grid, 8),
                 ("fp8_2b_320_step_ms", "qwen3vl-2b", "fp8", 320, (16, 16), 4),
                 ("fp8_32b_1024_step_ms", "qwen3vl-32b", "fp8", 1024, (30, 32), 2)):

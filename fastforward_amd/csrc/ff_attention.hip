@@ -164,6 +164,19 @@ __device__ __forceinline__ void store_rows(bf16_t* __restrict__ yp, const f32x4 
   }
 }
 
+// The same output row quantised with a static calibrated multiplier instead of
+// stored: e4m3(clamp(bf16(o / den) * inv, +-448)), i.e. the bf16 attention
+// output the reference writes, then its runtime-scale cast, 4 bytes per dt.
+__device__ __forceinline__ void store_rows_q(uint8_t* __restrict__ yp, const f32x4 (&o)[8], float den, int g,
+                                             float inv) {
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    *reinterpret_cast<uint32_t*>(yp + 16 * dt + 4 * g) =
+        quant4_static(round_bf16(o[dt][0] / den), round_bf16(o[dt][1] / den), round_bf16(o[dt][2] / den),
+                      round_bf16(o[dt][3] / den), inv);
+  }
+}
+
 // S^T tiles of one 32-key chunk starting at kc read straight from global
 // memory: A-row i of tile tt is key kc + 8*(i/4) + 4*tt + (i%4), so lane group
 // g of the result holds keys kc + 8g + 4tt + r.
@@ -432,10 +445,10 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void attention_decode_kernel(
 // head dim stored per (query, head) of y, which is (s, hq, DOUT); heads
 // narrower than 128 are zero-padded to 128 in q, k and V^T, which leaves every
 // score and every stored output column exact.
-template <int QT, int HPW, int NS, bool CAUSAL = true, int DOUT = D>
+template <int QT, int HPW, int NS, bool CAUSAL = true, int DOUT = D, bool QOUT = false>
 __global__ __launch_bounds__(kThreads, NS == 2 ? 2 : 1) void attention_prefill_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ vt,
-    bf16_t* __restrict__ y, int s_len, int t, int t_pad, int hq, int hk, float c2, int nqb) {
+    bf16_t* __restrict__ y, int s_len, int t, int t_pad, int hq, int hk, float c2, int nqb, float qinv) {
   constexpr int QB = 16 * QT * (4 / HPW);
   constexpr int STAGE = 32 * 1024;
   static_assert(NS == 2 || NS == 3, "two or three K/V stages");
@@ -567,7 +580,11 @@ __global__ __launch_bounds__(kThreads, NS == 2 ? 2 : 1) void attention_prefill_k
   for (int qt = 0; qt < QT; ++qt) {
     const float dsum = sum_rows(den[qt]);
     const int qi = wq0 + 16 * qt + r16;
-    if (qi < s_len) store_rows<DOUT>(y + ((int64_t)qi * hq + head) * DOUT, o[qt], dsum, g);
+    if (qi >= s_len) continue;
+    if constexpr (QOUT)
+      store_rows_q(reinterpret_cast<uint8_t*>(y) + ((int64_t)qi * hq + head) * D, o[qt], dsum, g, qinv);
+    else
+      store_rows<DOUT>(y + ((int64_t)qi * hq + head) * DOUT, o[qt], dsum, g);
   }
 }
 
@@ -633,17 +650,19 @@ extern "C" int ff_v_transpose(const void* v, int64_t v_ts, int64_t v_hs, void* v
   return FF_OK;
 }
 
-extern "C" int ff_attention_vt(const void* q, const void* k, const void* vt, const int64_t* positions,
-                               int gather_q, void* y, int64_t s, int64_t t, int64_t t_pad, int64_t hq,
-                               int64_t hk, int64_t d, float scale, ff_stream_t stream) {
+// y: bf16 output (s, hq, 128); or, with yq, the e4m3 codes of it under the
+// static multiplier qinv (grouped prefill only).
+static int attention_vt(const void* q, const void* k, const void* vt, const int64_t* positions, int gather_q,
+                        void* y, void* yq, float qinv, int64_t s, int64_t t, int64_t t_pad, int64_t hq, int64_t hk,
+                        int64_t d, float scale, ff_stream_t stream) {
   FF_REQUIRE(d == D, "ff_attention_vt: head_dim %lld unsupported (128 only)", (long long)d);
-  FF_REQUIRE(q && k && vt && y, "ff_attention_vt: null pointer");
+  FF_REQUIRE(q && k && vt && (y || yq), "ff_attention_vt: null pointer");
   FF_REQUIRE(s > 0 && t > 0 && t_pad >= t && t_pad % 64 == 0 && hq > 0 && hk > 0 && hq % hk == 0,
              "ff_attention_vt: bad sizes s=%lld t=%lld t_pad=%lld hq=%lld hk=%lld", (long long)s,
              (long long)t, (long long)t_pad, (long long)hq, (long long)hk);
   FF_REQUIRE(positions || s <= t, "ff_attention_vt: without positions s must be <= t");
   FF_REQUIRE(!gather_q || positions, "ff_attention_vt: gather_q needs positions");
-  FF_REQUIRE(ff_aligned(q, 16) && ff_aligned(k, 16) && ff_aligned(vt, 16) && ff_aligned(y, 8),
+  FF_REQUIRE(ff_aligned(q, 16) && ff_aligned(k, 16) && ff_aligned(vt, 16) && ff_aligned(y ? y : yq, 8),
              "ff_attention_vt: alignment");
   const float c2 = (float)((double)scale * 1.4426950408889634);  // scale * log2(e)
   const int group = (int)(hq / hk);
@@ -663,10 +682,16 @@ extern "C" int ff_attention_vt(const void* q, const void* k, const void* vt, con
     const int nqb = (int)((s + qb - 1) / qb);
     const dim3 grid((unsigned)(nqb * (hq / hpw))), block(kThreads);
 #define FF_PREFILL(QT, HPW, NS)                                                                              \
-  if (qt == QT && hpw == HPW && ns == NS)                                                                    \
-    hipLaunchKernelGGL((attention_prefill_kernel<QT, HPW, NS>), grid, block, 0, st, (const bf16_t*)q,        \
-                       (const bf16_t*)k, (const bf16_t*)vt, (bf16_t*)y, (int)s, (int)t, (int)t_pad, (int)hq, \
-                       (int)hk, c2, nqb);
+  if (qt == QT && hpw == HPW && ns == NS) {                                                                  \
+    if (yq)                                                                                                   \
+      hipLaunchKernelGGL((attention_prefill_kernel<QT, HPW, NS, true, D, true>), grid, block, 0, st,         \
+                         (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)vt, (bf16_t*)yq, (int)s, (int)t,   \
+                         (int)t_pad, (int)hq, (int)hk, c2, nqb, qinv);                                        \
+    else                                                                                                      \
+      hipLaunchKernelGGL((attention_prefill_kernel<QT, HPW, NS>), grid, block, 0, st, (const bf16_t*)q,      \
+                         (const bf16_t*)k, (const bf16_t*)vt, (bf16_t*)y, (int)s, (int)t, (int)t_pad,        \
+                         (int)hq, (int)hk, c2, nqb, 0.f);                                                     \
+  }
 #define FF_PREFILL_NS(QT, HPW) FF_PREFILL(QT, HPW, 2) FF_PREFILL(QT, HPW, 3)
     FF_PREFILL_NS(1, 4) FF_PREFILL_NS(2, 4) FF_PREFILL(4, 4, 3)
     FF_PREFILL_NS(1, 2) FF_PREFILL_NS(2, 2) FF_PREFILL(4, 2, 3)
@@ -676,6 +701,8 @@ extern "C" int ff_attention_vt(const void* q, const void* k, const void* vt, con
     FF_LAUNCH_CHECK("ff_attention_vt");
     return FF_OK;
   }
+  FF_REQUIRE(!yq, "ff_attention_vt_q: quantised output only for causal prefill (s == t, no positions, hq/hk in "
+                  "{1, 2} or a multiple of 4)");
   if (positions && s <= 16 && (t + 63) / 64 <= kDecodeMaxBlocks) {
     hipLaunchKernelGGL(attention_decode_kernel, dim3((unsigned)hq), dim3(kDecodeWaves * 64), 0, st,
                        (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)vt, positions, gather_q, (bf16_t*)y,
@@ -688,6 +715,19 @@ extern "C" int ff_attention_vt(const void* q, const void* k, const void* vt, con
                      (int)s, (int)t, (int)t_pad, (int)hq, (int)hk, c2);
   FF_LAUNCH_CHECK("ff_attention_vt");
   return FF_OK;
+}
+
+extern "C" int ff_attention_vt(const void* q, const void* k, const void* vt, const int64_t* positions,
+                               int gather_q, void* y, int64_t s, int64_t t, int64_t t_pad, int64_t hq,
+                               int64_t hk, int64_t d, float scale, ff_stream_t stream) {
+  return attention_vt(q, k, vt, positions, gather_q, y, nullptr, 0.f, s, t, t_pad, hq, hk, d, scale, stream);
+}
+
+extern "C" int ff_attention_vt_q(const void* q, const void* k, const void* vt, void* yq, float inv, int64_t s,
+                                 int64_t t, int64_t t_pad, int64_t hq, int64_t hk, int64_t d, float scale,
+                                 ff_stream_t stream) {
+  FF_REQUIRE(yq, "ff_attention_vt_q: null output");
+  return attention_vt(q, k, vt, nullptr, 0, nullptr, yq, inv, s, t, t_pad, hq, hk, d, scale, stream);
 }
 
 extern "C" int ff_attention_full(const void* q, const void* k, const void* vt, void* y, int64_t t, int64_t t_pad,
@@ -710,7 +750,7 @@ extern "C" int ff_attention_full(const void* q, const void* k, const void* vt, v
   if (qt == QT && d_out == DO)                                                                             \
     hipLaunchKernelGGL((attention_prefill_kernel<QT, 1, 2, false, DO>), grid, block, 0, st, (const bf16_t*)q, \
                        (const bf16_t*)k, (const bf16_t*)vt, (bf16_t*)y, (int)t, (int)t, (int)t_pad, (int)heads, \
-                       (int)heads, c2, nqb);
+                       (int)heads, c2, nqb, 0.f);
   FF_FULL(1, 64) FF_FULL(2, 64) FF_FULL(1, 72) FF_FULL(2, 72) FF_FULL(1, 128) FF_FULL(2, 128)
 #undef FF_FULL
   FF_LAUNCH_CHECK("ff_attention_full");

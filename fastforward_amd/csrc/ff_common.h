@@ -148,6 +148,19 @@ __device__ __forceinline__ u32x2 quant8(const float* x, float scale, float r) {
   return p;
 }
 
+// Static (per-tensor) quantisation of 4 values with the calibrated multiplier
+// inv: e4m3(clamp(x * inv, +-448)), the reference's runtime-scale cast.
+__device__ __forceinline__ uint32_t quant4_static(float a, float b, float c, float d, float inv) {
+  return e4m3x4(clamp448(a * inv), clamp448(b * inv), clamp448(c * inv), clamp448(d * inv));
+}
+
+__device__ __forceinline__ u32x2 quant8_static(const float* x, float inv) {
+  u32x2 p;
+  p.x = quant4_static(x[0], x[1], x[2], x[3], inv);
+  p.y = quant4_static(x[4], x[5], x[6], x[7], inv);
+  return p;
+}
+
 
 // ------------------------------------------------------------------ reductions
 
@@ -265,6 +278,12 @@ __device__ __forceinline__ float rsqrt_rn(float v) { return 1.0f / __builtin_sqr
 void ff_set_error(const char* fmt, ...);
 // Value of an ff_set_tuning override (FF_TUNE_*); 0 = the library's own choice.
 int ff_tuning(int knob);
+
+namespace ff {
+// Row-major / GEMV form of ff_gemm_fp8_swiglu_static (defined with the row-major kernels).
+int gemm_swiglu_static_rowmajor(const void* qa, const float* sa, const void* qw, const float* sw, void* hq,
+                                int64_t ldh, float inv, int64_t m, int64_t i, int64_t k, hipStream_t s);
+}  // namespace ff
 
 #define FF_REQUIRE(cond, ...)          \
   do {                                 \

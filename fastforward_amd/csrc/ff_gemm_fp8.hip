@@ -75,7 +75,11 @@ struct Cfg {
 // of the packed QKV output: q/k heads get the per-head RMSNorm + rotary of
 // qk_pair and are stored head-major (heads, M, 128); v heads are stored
 // transposed, vt (hk, 128, t_pad), with zeros for tokens in [M, t_pad).
-constexpr int kPlain = 0, kSwiglu = 1, kQkv = 2;
+// kSwigluQ: kSwiglu whose output is the e4m3 code of h under a static
+// multiplier, e4m3(clamp(h * qinv, +-448)) (y is then bytes, ldy in bytes),
+// and no row maxima.
+constexpr int kPlain = 0, kSwiglu = 1, kQkv = 2, kSwigluQ = 3;
+constexpr bool is_swiglu(int epi) { return epi == kSwiglu || epi == kSwigluQ; }
 
 struct QkvEpilogue {
   const bf16_t* qn;  // q_norm weight (128)
@@ -94,7 +98,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
     const uint8_t* __restrict__ qa, const float* __restrict__ sa, int sa_rows,
     const uint8_t* __restrict__ qw, const float* __restrict__ sw, int sw_cols,
     bf16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int tiles_m, int tiles_n, int half,
-    float* __restrict__ pmax, QkvEpilogue qe) {
+    float* __restrict__ pmax, QkvEpilogue qe, float qinv) {
   using C = Cfg<BM, BN, KS, S>;
   __shared__ __align__(16) uint8_t smem[C::SMEM];
 
@@ -124,7 +128,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
       src[i] = qa + (size_t)row * K + ks * 128 + 16 * ch;
     } else {
       const int r = ((rem - 2 * C::RA) >> 1) * 16 + rr;  // B row within the tile
-      const int row = EPI == kSwiglu ? weight_row_swiglu(r, tn, half) : min(n0 + r, N - 1);
+      const int row = is_swiglu(EPI) ? weight_row_swiglu(r, tn, half) : min(n0 + r, N - 1);
       src[i] = qw + (size_t)row * K + ks * 128 + 16 * ch;
     }
   }
@@ -200,7 +204,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
 #pragma unroll
   for (int j = 0; j < C::WJ; ++j) {
     const int cl = wn * (BN / 2) + j * 16 + r16;
-    const int n = EPI == kSwiglu ? weight_row_swiglu(cl, tn, half) : min(n0 + cl, N - 1);
+    const int n = is_swiglu(EPI) ? weight_row_swiglu(cl, tn, half) : min(n0 + cl, N - 1);
     const float swv = sw[sw_cols ? n : 0];
 #pragma unroll
     for (int i = 0; i < C::WI; ++i)
@@ -213,7 +217,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
       }
   }
   __syncthreads();
-  if constexpr (EPI == kSwiglu) {
+  if constexpr (is_swiglu(EPI)) {
     // 8 channels per thread; the 8 threads of one row are 8 consecutive lanes.
     constexpr int CH = BN / 2, CPR = CH / 8;
     static_assert(CPR == 8, "row max reduces over 8 lanes");
@@ -234,7 +238,11 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_fp8_kernel(
       mx = fmaxf(mx, dpp<kDppXor2>(mx));
       mx = fmaxf(mx, dpp<kDppHalfMirror>(mx));
       const int m = m0 + rl;
-      if (m < M) {
+      if constexpr (EPI == kSwigluQ) {
+        if (m < M)
+          *reinterpret_cast<u32x2*>(reinterpret_cast<uint8_t*>(y) + (size_t)m * ldy + g0 + cc) =
+              quant8_static(hv, qinv);
+      } else if (m < M) {
         *reinterpret_cast<u32x4*>(y + (size_t)m * ldy + g0 + cc) = pack8(hv);
         if (cc == 0) pmax[(size_t)m * tiles_n + tn] = mx;
       }
@@ -374,14 +382,17 @@ __global__ __launch_bounds__(256) void gemv_fp8_kernel(const uint8_t* __restrict
 
 // SwiGLU GEMV: workgroup = 16 waves = 64 channels, 4 per wave; gate row c and
 // up row half + c per channel; h = bf16(bf16(silu(g)) * u); pmax[m, block] = the
-// block's max |h| (the 64-channel blocks of ff_gemm_fp8_swiglu).
+// block's max |h| (the 64-channel blocks of ff_gemm_fp8_swiglu). With hq, h is
+// written as e4m3(clamp(h * qinv, +-448)) instead (static quantisation of the
+// next GEMM's input) and no maxima. sa / sw per row / column or one value.
 template <int MM>
 __global__ __launch_bounds__(1024) void gemv_fp8_swiglu_kernel(const uint8_t* __restrict__ qa,
-                                                              const float* __restrict__ sa,
+                                                              const float* __restrict__ sa, int sa_rows,
                                                               const uint8_t* __restrict__ qw,
-                                                              const float* __restrict__ sw, bf16_t* __restrict__ h,
-                                                              int64_t ldh, float* __restrict__ pmax, int half,
-                                                              int K) {
+                                                              const float* __restrict__ sw, int sw_cols,
+                                                              bf16_t* __restrict__ h, int64_t ldh,
+                                                              float* __restrict__ pmax, uint8_t* __restrict__ hq,
+                                                              float qinv, int half, int K) {
   __shared__ float red[16][kGemvMaxM];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c0 = (int)blockIdx.x * 64 + wave * 4;
@@ -397,17 +408,21 @@ __global__ __launch_bounds__(1024) void gemv_fp8_swiglu_kernel(const uint8_t* __
 #pragma unroll
   for (int m = 0; m < MM; ++m) {
     mx[m] = 0.f;
+    const float sav = sa[sa_rows ? m : 0];
+    float hv[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float sav = sa[m];
-      const float g = round_bf16((acc[2 * j][m] * sav) * sw[c0 + j]);
-      const float u = round_bf16((acc[2 * j + 1][m] * sav) * sw[half + c0 + j]);
-      const float hv = round_bf16(round_bf16(silu(g)) * u);
-      mx[m] = fmaxf(mx[m], fabsf(hv));
-      if (lane == 0) h[(size_t)m * ldh + c0 + j] = (bf16_t)f32_to_bf16(hv);
+      const float g = round_bf16((acc[2 * j][m] * sav) * sw[sw_cols ? c0 + j : 0]);
+      const float u = round_bf16((acc[2 * j + 1][m] * sav) * sw[sw_cols ? half + c0 + j : 0]);
+      hv[j] = round_bf16(round_bf16(silu(g)) * u);
+      mx[m] = fmaxf(mx[m], fabsf(hv[j]));
+      if (lane == 0 && !hq) h[(size_t)m * ldh + c0 + j] = (bf16_t)f32_to_bf16(hv[j]);
     }
+    if (lane == 0 && hq)
+      *reinterpret_cast<uint32_t*>(hq + (size_t)m * ldh + c0) = quant4_static(hv[0], hv[1], hv[2], hv[3], qinv);
     if (lane == 0) red[wave][m] = mx[m];
   }
+  if (hq) return;
   __syncthreads();
   if (threadIdx.x < MM) {
     float v = 0.f;
@@ -429,13 +444,14 @@ int launch_gemv(const void* qa, const float* sa, int sa_rows, const void* qw, co
   return FF_OK;
 }
 
-int launch_gemv_swiglu(const void* qa, const float* sa, const void* qw, const float* sw, void* h, int64_t ldh,
-                       float* pmax, int64_t m, int64_t i, int64_t k, hipStream_t s) {
+int launch_gemv_swiglu(const void* qa, const float* sa, int sa_rows, const void* qw, const float* sw, int sw_cols,
+                       void* h, int64_t ldh, float* pmax, uint8_t* hq, float qinv, int64_t m, int64_t i, int64_t k,
+                       hipStream_t s) {
   const dim3 grid((unsigned)(i / 64)), block(1024);
 #define FF_GEMVS(MM)                                                                                      \
   case MM:                                                                                                \
-    hipLaunchKernelGGL(gemv_fp8_swiglu_kernel<MM>, grid, block, 0, s, (const uint8_t*)qa, sa,              \
-                       (const uint8_t*)qw, sw, (bf16_t*)h, ldh, pmax, (int)i, (int)k);                     \
+    hipLaunchKernelGGL(gemv_fp8_swiglu_kernel<MM>, grid, block, 0, s, (const uint8_t*)qa, sa, sa_rows,     \
+                       (const uint8_t*)qw, sw, sw_cols, (bf16_t*)h, ldh, pmax, hq, qinv, (int)i, (int)k);  \
     break;
   switch (m) { FF_GEMVS(1) FF_GEMVS(2) FF_GEMVS(3) FF_GEMVS(4) }
 #undef FF_GEMVS
@@ -445,14 +461,14 @@ int launch_gemv_swiglu(const void* qa, const float* sa, const void* qw, const fl
 template <int BM, int BN, int KS, int S, int OCC, int EPI = kPlain>
 int launch(const void* qa, const float* sa, int sa_rows, const void* qw, const float* sw, int sw_cols,
            void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, hipStream_t s, float* pmax = nullptr,
-           QkvEpilogue qe = QkvEpilogue{}) {
+           QkvEpilogue qe = QkvEpilogue{}, float qinv = 0.f) {
   static_assert(OCC * Cfg<BM, BN, KS, S>::SMEM <= 160 * 1024, "LDS budget for the occupancy");
-  // kSwiglu: n = 2 * half weight rows, BN/2 channels of each half per tile
+  // kSwiglu / kSwigluQ: n = 2 * half weight rows, BN/2 channels of each half per tile
   const int tiles_m = (int)((m + BM - 1) / BM);
-  const int tiles_n = EPI == kSwiglu ? (int)(n / BN) : (int)((n + BN - 1) / BN);
+  const int tiles_n = is_swiglu(EPI) ? (int)(n / BN) : (int)((n + BN - 1) / BN);
   hipLaunchKernelGGL((gemm_fp8_kernel<BM, BN, KS, S, OCC, EPI>), dim3(tiles_m * tiles_n), dim3(kThreads), 0, s,
                      (const uint8_t*)qa, sa, sa_rows, (const uint8_t*)qw, sw, sw_cols, (bf16_t*)y, ldy, (int)m,
-                     (int)n, (int)k, tiles_m, tiles_n, (int)(n / 2), pmax, qe);
+                     (int)n, (int)k, tiles_m, tiles_n, (int)(n / 2), pmax, qe, qinv);
   return FF_OK;
 }
 
@@ -525,17 +541,35 @@ extern "C" int ff_gemm_fp8_swiglu(const void* qa, const float* sa, const void* q
              "ff_gemm_fp8_swiglu: operands must be 16-byte aligned");
   if (m == 0) return FF_OK;
   if (m <= kGemvMaxM)
-    launch_gemv_swiglu(qa, sa, qw, sw, h, ldh, pmax, m, i, k, (hipStream_t)stream);
+    launch_gemv_swiglu(qa, sa, 1, qw, sw, 1, h, ldh, pmax, nullptr, 0.f, m, i, k, (hipStream_t)stream);
   else
     launch<128, 128, 1, 2, 2, kSwiglu>(qa, sa, 1, qw, sw, 1, h, ldh, m, 2 * i, k, (hipStream_t)stream, pmax);
   FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu");
   return FF_OK;
 }
 
-extern "C" int ff_gemm_fp8_qkv(const void* qa, const float* sa, const void* qw, const float* sw, int64_t m,
-                               int64_t k, int64_t hq, int64_t hk, const void* q_norm, const void* k_norm, float eps_q,
-                               float eps_k, const void* cos, const void* sin, void* yq, void* yk, void* vt,
-                               int64_t t_pad, ff_stream_t stream) {
+namespace ff {
+
+// Gate/up GEMM with the SwiGLU epilogue writing e4m3(clamp(h * inv, +-448)),
+// per-tensor scales sa[0], sw[0]: the GEMV kernel for m <= 4 rows, else the
+// row-major tile (the packed file's fallback for shapes its tile does not take).
+int gemm_swiglu_static_rowmajor(const void* qa, const float* sa, const void* qw, const float* sw, void* hq,
+                                int64_t ldh, float inv, int64_t m, int64_t i, int64_t k, hipStream_t s) {
+  if (m == 0) return FF_OK;
+  if (m <= kGemvMaxM)
+    launch_gemv_swiglu(qa, sa, 0, qw, sw, 0, nullptr, ldh, nullptr, (uint8_t*)hq, inv, m, i, k, s);
+  else
+    launch<128, 128, 1, 2, 2, kSwigluQ>(qa, sa, 0, qw, sw, 0, hq, ldh, m, 2 * i, k, s, nullptr, QkvEpilogue{}, inv);
+  FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu_static");
+  return FF_OK;
+}
+
+}  // namespace ff
+
+extern "C" int ff_gemm_fp8_qkv(const void* qa, const float* sa, int sa_rows, const void* qw, const float* sw,
+                               int sw_cols, int64_t m, int64_t k, int64_t hq, int64_t hk, const void* q_norm,
+                               const void* k_norm, float eps_q, float eps_k, const void* cos, const void* sin, void* yq,
+                               void* yk, void* vt, int64_t t_pad, ff_stream_t stream) {
   FF_REQUIRE(qa && sa && qw && sw && q_norm && k_norm && cos && sin && yq && yk && vt,
              "ff_gemm_fp8_qkv: null pointer");
   FF_REQUIRE(m > 0 && k > 0 && k % BK == 0 && hq > 0 && hk > 0 && hq % hk == 0 && t_pad >= m && t_pad % 64 == 0 &&
@@ -553,11 +587,11 @@ extern "C" int ff_gemm_fp8_qkv(const void* qa, const float* sa, const void* qw, 
   const int forced = forced_tile();
   const int tile = forced >= 0 && forced != k128x256 ? forced : pick_tile(m, n);
   if (tile == k128x128)
-    launch<128, 128, 1, 2, 2, kQkv>(qa, sa, 1, qw, sw, 1, nullptr, 0, m, n, k, s, nullptr, qe);
+    launch<128, 128, 1, 2, 2, kQkv>(qa, sa, sa_rows, qw, sw, sw_cols, nullptr, 0, m, n, k, s, nullptr, qe);
   else if (tile == k128x128Deep)
-    launch<128, 128, 1, 4, 1, kQkv>(qa, sa, 1, qw, sw, 1, nullptr, 0, m, n, k, s, nullptr, qe);
+    launch<128, 128, 1, 4, 1, kQkv>(qa, sa, sa_rows, qw, sw, sw_cols, nullptr, 0, m, n, k, s, nullptr, qe);
   else
-    launch<64, 128, 1, 3, 2, kQkv>(qa, sa, 1, qw, sw, 1, nullptr, 0, m, n, k, s, nullptr, qe);
+    launch<64, 128, 1, 3, 2, kQkv>(qa, sa, sa_rows, qw, sw, sw_cols, nullptr, 0, m, n, k, s, nullptr, qe);
   FF_LAUNCH_CHECK("ff_gemm_fp8_qkv");
   return FF_OK;
 }

@@ -253,11 +253,14 @@ __device__ __forceinline__ u32x2 pack4_bf16(float a, float b, float c, float d) 
 // gate channels [w CW/2, (w + 1) CW/2) of the tile and the matching up
 // channels, as fragments j = 2 t (gate, channels 16 t ..) and j = 2 t + 1 (up,
 // the same channels).
-template <int BM, int CW, int P, int D, int G>
+// SQ (static quantisation of the output): sa[0] and sw[0] are per-tensor
+// scales and h is written as e4m3(clamp(h * qinv, +-448)) into hq (ldh bytes
+// per row), without row maxima.
+template <int BM, int CW, int P, int D, int G, bool SQ = false>
 __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
     const uint8_t* __restrict__ qa, const float* __restrict__ sa, const uint8_t* __restrict__ qwp,
     const float* __restrict__ sw, bf16_t* __restrict__ h, int64_t ldh, float* __restrict__ pmax, int M, int half,
-    int K, int tiles_m, int tiles_n) {
+    int K, int tiles_m, int tiles_n, uint8_t* __restrict__ hq, float qinv) {
   constexpr int BN = 4 * CW, CH = BN / 2, WCH = CW / 2;
   constexpr int RA = BM / 16, TJ = CW / 16, TT = TJ / 2;
   constexpr int SMEM = pk_smem<BM, G>();
@@ -297,13 +300,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
   for (int t = 0; t < TT; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      swg[t][r] = sw[c_base + 16 * t + r];
-      swu[t][r] = sw[half + c_base + 16 * t + r];
+      swg[t][r] = sw[SQ ? 0 : c_base + 16 * t + r];
+      swu[t][r] = sw[SQ ? 0 : half + c_base + 16 * t + r];
     }
 #pragma unroll
   for (int i = 0; i < RA; ++i) {
     const int tl = 16 * i + r16, m = m0 + tl;
-    const float sav = sa[min(m, M - 1)];
+    const float sav = sa[SQ ? 0 : min(m, M - 1)];
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
       float hv[4], mx = 0.f;
@@ -314,12 +317,19 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
         hv[r] = round_bf16(round_bf16(silu(gv)) * uv);
         mx = fmaxf(mx, fabsf(hv[r]));
       }
+      if constexpr (SQ) {
+        if (m < M)
+          *reinterpret_cast<uint32_t*>(hq + (int64_t)m * ldh + c_base + 16 * t) =
+              quant4_static(hv[0], hv[1], hv[2], hv[3], qinv);
+        continue;
+      }
       if (m < M)
         *reinterpret_cast<u32x2*>(h + (int64_t)m * ldh + c_base + 16 * t) = pack4_bf16(hv[0], hv[1], hv[2], hv[3]);
       mx = max_rows(mx);  // over the 4 lanes of this token: 16 channels
       if (g == 0) pm16[tl][wave * TT + t] = mx;
     }
   }
+  if constexpr (SQ) return;
   __syncthreads();
   // Row maxima per 64 channels (4 consecutive 16-channel blocks) for ff_quant_rows_pmax.
   const int64_t npart = half / 64;
@@ -502,8 +512,30 @@ extern "C" int ff_gemm_fp8_swiglu_pk(const void* qa, const float* sa, const void
   hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<kPkBM, kPkCW, kPkP, kPkD, kPkG>),
                      dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads), 0, (hipStream_t)stream,
                      (const uint8_t*)qa, sa, (const uint8_t*)qw_packed, sw, (bf16_t*)h, ldh, pmax, (int)m, (int)i,
-                     (int)k, (int)tiles_m, (int)tiles_n);
+                     (int)k, (int)tiles_m, (int)tiles_n, nullptr, 0.f);
   FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu_pk");
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_fp8_swiglu_static(const void* qa, const float* sa, const void* qw, const void* qw_packed,
+                                         const float* sw, void* hq, int64_t ldh, float inv, int64_t m, int64_t i,
+                                         int64_t k, ff_stream_t stream) {
+  FF_REQUIRE(qa && sa && qw && sw && hq, "ff_gemm_fp8_swiglu_static: null pointer");
+  FF_REQUIRE(m >= 0 && i > 0 && i % 64 == 0 && k > 0 && k % 128 == 0 && ldh >= i && ldh % 8 == 0 &&
+                 m < (1 << 30) && i < (1 << 29) && k < (1 << 30),
+             "ff_gemm_fp8_swiglu_static: bad sizes (i %% 64, k %% 128, ldh %% 8)");
+  FF_REQUIRE(ff_aligned(qa, 16) && ff_aligned(qw, 16) && ff_aligned(hq, 16),
+             "ff_gemm_fp8_swiglu_static: operands must be 16-byte aligned");
+  const int64_t tiles_m = (m + kPkBM - 1) / kPkBM, tiles_n = i / kPkCH;
+  const bool packed_fits = qw_packed && m > 4 && i % kPkCH == 0 && k % kPkKAlign == 0 &&
+                           m * k < (int64_t(1) << 31) && 2 * i * k < (int64_t(1) << 31) &&
+                           tiles_m * tiles_n >= 192 && ff_aligned(qw_packed, 16);
+  if (!packed_fits) return gemm_swiglu_static_rowmajor(qa, sa, qw, sw, hq, ldh, inv, m, i, k, (hipStream_t)stream);
+  hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<kPkBM, kPkCW, kPkP, kPkD, kPkG, true>),
+                     dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads), 0, (hipStream_t)stream,
+                     (const uint8_t*)qa, sa, (const uint8_t*)qw_packed, sw, nullptr, ldh, nullptr, (int)m, (int)i,
+                     (int)k, (int)tiles_m, (int)tiles_n, (uint8_t*)hq, inv);
+  FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu_static");
   return FF_OK;
 }
 

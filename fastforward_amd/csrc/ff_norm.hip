@@ -12,13 +12,17 @@ using namespace ff;
 namespace {
 
 
+// e4m3 output of the normalised row: none, per-token dynamic scale (written to
+// scales[row]) or a static calibrated multiplier (e4m3(clamp(x * sinv, +-448))).
+constexpr int kNoQuant = 0, kDynamic = 1, kStatic = 2;
+
 // One workgroup per row, blockDim.x threads (a multiple of 64, <= 1024) with
 // CPT 16-byte chunks each (row_shape picks both from h).
-template <int CPT, bool ADD, bool DEEP, bool WRITE_RES, bool WRITE_OUT, bool QUANT>
+template <int CPT, bool ADD, bool DEEP, bool WRITE_RES, bool WRITE_OUT, int QUANT>
 __global__ __launch_bounds__(1024) void row_norm_kernel(
     const bf16_t* __restrict__ a, const bf16_t* __restrict__ b, const bf16_t* __restrict__ deep,
     const bf16_t* __restrict__ w, bf16_t* __restrict__ residual, bf16_t* __restrict__ out,
-    uint8_t* __restrict__ q, float* __restrict__ scales, int h, float eps, int start, int nv) {
+    uint8_t* __restrict__ q, float* __restrict__ scales, int h, float eps, int start, int nv, float sinv) {
   __shared__ float red[16];
   const int row = blockIdx.x;
   const int nchunk = h >> 3;
@@ -76,7 +80,14 @@ __global__ __launch_bounds__(1024) void row_norm_kernel(
       if (WRITE_OUT) *reinterpret_cast<u32x4*>(out + base + (size_t)idx * 8) = pack8(x[c]);
     }
   }
-  if (QUANT) {
+  if constexpr (QUANT == kStatic) {
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int idx = threadIdx.x + c * nt;
+      if (idx < nchunk) *reinterpret_cast<u32x2*>(q + base + (size_t)idx * 8) = quant8_static(x[c], sinv);
+    }
+  }
+  if constexpr (QUANT == kDynamic) {
     amax = block_max_rt(amax, red);
     const float scale = fmaxf(amax, 1e-12f) / 448.0f;
     const float r = 1.0f / scale;
@@ -89,10 +100,10 @@ __global__ __launch_bounds__(1024) void row_norm_kernel(
   }
 }
 
-template <bool ADD, bool DEEP, bool WRITE_RES, bool WRITE_OUT, bool QUANT>
+template <bool ADD, bool DEEP, bool WRITE_RES, bool WRITE_OUT, int QUANT>
 int launch_row_norm(const void* a, const void* b, const void* deep, const void* w, void* residual,
                     void* out, void* q, float* scales, int64_t rows, int64_t h, float eps,
-                    int64_t start, int64_t nv, hipStream_t s, const char* name) {
+                    int64_t start, int64_t nv, hipStream_t s, const char* name, float sinv = 0.f) {
   int threads, cpt;
   row_shape(h / 8, &threads, &cpt);
   dim3 grid((unsigned)rows), block((unsigned)threads);
@@ -101,7 +112,7 @@ int launch_row_norm(const void* a, const void* b, const void* deep, const void* 
     hipLaunchKernelGGL((row_norm_kernel<N, ADD, DEEP, WRITE_RES, WRITE_OUT, QUANT>), grid, block, \
                        0, s, (const bf16_t*)a, (const bf16_t*)b, (const bf16_t*)deep,             \
                        (const bf16_t*)w, (bf16_t*)residual, (bf16_t*)out, (uint8_t*)q, scales,    \
-                       (int)h, eps, (int)start, (int)nv);                                         \
+                       (int)h, eps, (int)start, (int)nv, sinv);                                   \
     break;
   switch (cpt) {
     FF_ROWNORM_CASE(1)
@@ -190,7 +201,7 @@ extern "C" int ff_fast_norm(const void* x, const void* w, void* out, int64_t row
   if (st) return st;
   FF_REQUIRE(out && w && ff_aligned(out, 16) && ff_aligned(w, 16), "ff_fast_norm: bad out/w");
   if (rows == 0) return FF_OK;
-  return launch_row_norm<false, false, false, true, false>(x, nullptr, nullptr, w, nullptr, out,
+  return launch_row_norm<false, false, false, true, kNoQuant>(x, nullptr, nullptr, w, nullptr, out,
                                                            nullptr, nullptr, rows, h, eps, 0, 0,
                                                            (hipStream_t)stream, "ff_fast_norm");
 }
@@ -204,10 +215,10 @@ extern "C" int ff_fast_norm_quant(const void* x, const void* w, void* out, void*
   if (rows == 0) return FF_OK;
   hipStream_t s = (hipStream_t)stream;
   if (out)
-    return launch_row_norm<false, false, false, true, true>(x, nullptr, nullptr, w, nullptr, out, q,
+    return launch_row_norm<false, false, false, true, kDynamic>(x, nullptr, nullptr, w, nullptr, out, q,
                                                             scales, rows, h, eps, 0, 0, s,
                                                             "ff_fast_norm_quant");
-  return launch_row_norm<false, false, false, false, true>(x, nullptr, nullptr, w, nullptr, nullptr,
+  return launch_row_norm<false, false, false, false, kDynamic>(x, nullptr, nullptr, w, nullptr, nullptr,
                                                            q, scales, rows, h, eps, 0, 0, s,
                                                            "ff_fast_norm_quant");
 }
@@ -224,10 +235,10 @@ extern "C" int ff_add_rms(const void* a, const void* b, const void* deep, const 
   if (rows == 0) return FF_OK;
   hipStream_t s = (hipStream_t)stream;
   if (deep && nv > 0)
-    return launch_row_norm<true, true, true, true, false>(a, b, deep, w, residual, out, nullptr,
+    return launch_row_norm<true, true, true, true, kNoQuant>(a, b, deep, w, residual, out, nullptr,
                                                           nullptr, rows, h, eps, start, nv, s,
                                                           "ff_add_rms");
-  return launch_row_norm<true, false, true, true, false>(a, b, nullptr, w, residual, out, nullptr,
+  return launch_row_norm<true, false, true, true, kNoQuant>(a, b, nullptr, w, residual, out, nullptr,
                                                          nullptr, rows, h, eps, 0, 0, s, "ff_add_rms");
 }
 
@@ -246,18 +257,62 @@ extern "C" int ff_add_rms_quant(const void* a, const void* b, const void* deep, 
   hipStream_t s = (hipStream_t)stream;
   const bool d = deep && nv > 0;
   if (d && out)
-    return launch_row_norm<true, true, true, true, true>(a, b, deep, w, residual, out, q, scales, rows,
+    return launch_row_norm<true, true, true, true, kDynamic>(a, b, deep, w, residual, out, q, scales, rows,
                                                          h, eps, start, nv, s, "ff_add_rms_quant");
   if (d)
-    return launch_row_norm<true, true, true, false, true>(a, b, deep, w, residual, nullptr, q, scales,
+    return launch_row_norm<true, true, true, false, kDynamic>(a, b, deep, w, residual, nullptr, q, scales,
                                                           rows, h, eps, start, nv, s,
                                                           "ff_add_rms_quant");
   if (out)
-    return launch_row_norm<true, false, true, true, true>(a, b, nullptr, w, residual, out, q, scales,
+    return launch_row_norm<true, false, true, true, kDynamic>(a, b, nullptr, w, residual, out, q, scales,
                                                           rows, h, eps, 0, 0, s, "ff_add_rms_quant");
-  return launch_row_norm<true, false, true, false, true>(a, b, nullptr, w, residual, nullptr, q,
+  return launch_row_norm<true, false, true, false, kDynamic>(a, b, nullptr, w, residual, nullptr, q,
                                                          scales, rows, h, eps, 0, 0, s,
                                                          "ff_add_rms_quant");
+}
+
+extern "C" int ff_fast_norm_quant_static(const void* x, const void* w, void* out, void* q, float inv, int64_t rows,
+                                         int64_t h, float eps, ff_stream_t stream) {
+  int st = check_rows("ff_fast_norm_quant_static", x, rows, h);
+  if (st) return st;
+  FF_REQUIRE(q && w && ff_aligned(q, 8) && ff_aligned(w, 16), "ff_fast_norm_quant_static: bad q/w");
+  FF_REQUIRE(!out || ff_aligned(out, 16), "ff_fast_norm_quant_static: out not aligned");
+  if (rows == 0) return FF_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (out)
+    return launch_row_norm<false, false, false, true, kStatic>(x, nullptr, nullptr, w, nullptr, out, q, nullptr,
+                                                               rows, h, eps, 0, 0, s, "ff_fast_norm_quant_static",
+                                                               inv);
+  return launch_row_norm<false, false, false, false, kStatic>(x, nullptr, nullptr, w, nullptr, nullptr, q, nullptr,
+                                                              rows, h, eps, 0, 0, s, "ff_fast_norm_quant_static",
+                                                              inv);
+}
+
+extern "C" int ff_add_rms_quant_static(const void* a, const void* b, const void* deep, const void* w,
+                                       void* residual, void* out, void* q, float inv, int64_t rows, int64_t h,
+                                       float eps, int64_t start, int64_t nv, ff_stream_t stream) {
+  int st = check_rows("ff_add_rms_quant_static", a, rows, h);
+  if (st) return st;
+  FF_REQUIRE(b && w && residual && q && ff_aligned(b, 16) && ff_aligned(w, 16) && ff_aligned(residual, 16) &&
+                 ff_aligned(q, 8),
+             "ff_add_rms_quant_static: bad b/w/residual/q");
+  FF_REQUIRE(!out || ff_aligned(out, 16), "ff_add_rms_quant_static: out not aligned");
+  FF_REQUIRE(!deep || (ff_aligned(deep, 16) && nv >= 0 && start >= 0), "ff_add_rms_quant_static: bad deep");
+  if (rows == 0) return FF_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const bool d = deep && nv > 0;
+  const char* nm = "ff_add_rms_quant_static";
+  if (d && out)
+    return launch_row_norm<true, true, true, true, kStatic>(a, b, deep, w, residual, out, q, nullptr, rows, h, eps,
+                                                            start, nv, s, nm, inv);
+  if (d)
+    return launch_row_norm<true, true, true, false, kStatic>(a, b, deep, w, residual, nullptr, q, nullptr, rows, h,
+                                                             eps, start, nv, s, nm, inv);
+  if (out)
+    return launch_row_norm<true, false, true, true, kStatic>(a, b, nullptr, w, residual, out, q, nullptr, rows, h,
+                                                             eps, 0, 0, s, nm, inv);
+  return launch_row_norm<true, false, true, false, kStatic>(a, b, nullptr, w, residual, nullptr, q, nullptr, rows,
+                                                            h, eps, 0, 0, s, nm, inv);
 }
 
 extern "C" int ff_lm_readout(const void* x, const void* x2, const void* norm_w, const void* head,

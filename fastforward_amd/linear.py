@@ -125,6 +125,9 @@ class StaticFP8Linear:
         self.inverse_scale = inverse_scale
         self.input_scale = torch.tensor([1. / inverse_scale], device=w.device, dtype=torch.float32)
         self.fast_accum = True
+        self.packed = None
+
+    pack = FP8Linear.pack
 
     def set_bound(self, bound):
         """Calibrate to activation bound ``bound`` as the reference's ``select``

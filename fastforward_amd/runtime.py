@@ -25,7 +25,7 @@ import torch
 
 from . import ops
 from ._lib import call, ptr, stream
-from .linear import FP8Linear, Linear, gemm_pk_workspace
+from .linear import FP8Linear, Linear, StaticFP8Linear, gemm_pk_workspace
 
 BF16 = torch.bfloat16
 E4M3 = torch.float8_e4m3fn
@@ -173,6 +173,20 @@ def _lay_out_activations(rt, cfg, tokens, path, a):
     rt.cos, rt.sin = a(T, D), a(T, D)
     rt.h = [a(T, H), a(T, H)]
     rt.res = a(T, H)
+    if path == "fused_static":
+        # static-scale linears: every GEMM input is e4m3 written by its producer
+        rt.xq = a(T, H, dt=E4M3)
+        rt.yq, rt.yk, rt.vt = a(HQ, T, D), a(HK, T, D), a(HK, D, Tp)
+        rt.aq = a(T, HQ * D, dt=E4M3)
+        rt.attn = a(1, HQ * D)                             # the tail's attention row (bf16)
+        rt.o = a(T, H)
+        rt.pq = a(T, H, dt=E4M3)
+        rt.mq = a(T, I, dt=E4M3)
+        rt.dn = a(T, H)
+        rt.hp = a(1, H)
+        need = max(gemm_pk_workspace(T, H, HQ * D), gemm_pk_workspace(T, H, I), 256)
+        rt.gws = a(need, dt=torch.uint8)
+        return
     if path != "fused":
         return
     rt.xq, rt.xs = a(T, H, dt=E4M3), a(T, dt=torch.float32)
@@ -204,11 +218,13 @@ class Runtime:
         self.Tp = (tokens + 63) // 64 * 64
         dev = weights.embed.device
         self.dev = dev
-        fused_ok = self.path_for(weights) == "fused"
-        self.path = path or self.path_for(weights)
-        if self.path == "fused" and not fused_ok:
-            raise ValueError("the fused path needs FP8Linear (per-token / per-channel) weights")
-        if self.path == "fused":
+        natural = self.path_for(weights)
+        self.path = path or natural
+        if self.path in ("fused", "fused_static") and self.path != natural:
+            raise ValueError(f"the {self.path} path needs "
+                             + ("FP8Linear (per-token / per-channel)" if self.path == "fused"
+                                else "StaticFP8Linear / RuntimeScaleLinear (calibrated per-tensor)") + " weights")
+        if self.path in ("fused", "fused_static"):
             for L in weights.layers:  # MFMA-fragment copies for the packed tile kernels (once per weight)
                 L.o.pack()
                 L.gateup.pack()
@@ -239,9 +255,15 @@ class Runtime:
     @staticmethod
     def path_for(weights):
         """"fused" when every linear is an FP8Linear (per-token / per-channel),
-        else "generic" (the reference's op sequence through the drop-in ops)."""
-        fp8 = all(isinstance(op, FP8Linear) for L in weights.layers for op in (L.qkv, L.o, L.gateup, L.down))
-        return "fused" if fp8 else "generic"
+        "fused_static" when every linear is a StaticFP8Linear /
+        RuntimeScaleLinear (calibrated per-tensor scales), else "generic" (the
+        reference's op sequence through the drop-in ops)."""
+        ops_ = [op for L in weights.layers for op in (L.qkv, L.o, L.gateup, L.down)]
+        if all(isinstance(op, FP8Linear) for op in ops_):
+            return "fused"
+        if all(isinstance(op, StaticFP8Linear) for op in ops_):
+            return "fused_static"
+        return "generic"
 
     # ------------------------------------------------------------ inputs
 
@@ -324,7 +346,7 @@ class Runtime:
         T, Tp, H, D = self.T, self.Tp, cfg.hidden, cfg.head_dim
         HQ, HK = cfg.heads, cfg.kv_heads
         # QKV GEMM with q/k norm + rotary and the V transpose in its epilogue
-        call("ff_gemm_fp8_qkv", ptr(self.xq), ptr(self.xs), ptr(lw.qkv.weight), ptr(lw.qkv.scale), T, H, HQ, HK,
+        call("ff_gemm_fp8_qkv", ptr(self.xq), ptr(self.xs), 1, ptr(lw.qkv.weight), ptr(lw.qkv.scale), 1, T, H, HQ, HK,
              ptr(lw.q_norm.weight), ptr(lw.k_norm.weight), float(lw.q_norm.variance_epsilon),
              float(lw.k_norm.variance_epsilon), ptr(self.cos), ptr(self.sin), ptr(self.yq), ptr(self.yk),
              ptr(self.vt), Tp, s)
@@ -352,6 +374,77 @@ class Runtime:
              ptr(lw.gateup.scale), ptr(self.hm), I, ptr(self.pmax), m, I, H, s)
         call("ff_quant_rows_pmax", ptr(self.hm), I, ptr(self.pmax), I // 64, ptr(self.mq), ptr(self.ms), m, I, s)
         self._gemm(self.mq, self.ms, lw.down, out, m, s)
+
+    def _step_static(self, trace=None):
+        """The fused step for static-scale linears (the reference's calibrated
+        mode: RuntimeScaleLinear, _family/depth_fp8.py:8-26, with select()'s
+        bounds): every GEMM input is cast to e4m3 with the consuming linear's
+        inverse_scale inside the kernel that produces it (norms, attention, the
+        gate/up SwiGLU epilogue), and the GEMMs take the per-tensor
+        input_scale / weight_scale. 7 launches per full layer (8 where the
+        down projection splits k)."""
+        cfg, w, s = self.cfg, self.w, stream()
+        T, Tp, H, D = self.T, self.Tp, cfg.hidden, cfg.head_dim
+        HQ, HK, I = cfg.heads, cfg.kv_heads, cfg.inter
+        h = self._prologue()
+        L = w.layers
+        call("ff_fast_norm_quant_static", ptr(h), ptr(L[0].input_norm.weight), None, ptr(self.xq),
+             float(L[0].qkv.inverse_scale), T, H, float(L[0].input_norm.variance_epsilon), s)
+        cur = 0
+        for j in range(cfg.layers - 1):
+            lw = L[j]
+            h = self.h[cur]
+            self._qkv_static(lw, T, s)
+            call("ff_attention_vt_q", ptr(self.yq), ptr(self.yk), ptr(self.vt), ptr(self.aq),
+                 float(lw.o.inverse_scale), T, T, Tp, HQ, HK, D, float(cfg.scaling), s)
+            self._gemm_static(self.aq, lw.o, self.o, T, s)
+            call("ff_add_rms_quant_static", ptr(h), ptr(self.o), None, ptr(lw.post_norm.weight), ptr(self.res), None,
+                 ptr(self.pq), float(lw.gateup.inverse_scale), T, H, float(lw.post_norm.variance_epsilon), 0, 0, s)
+            self._mlp_static(lw, T, s)
+            nxt = self.h[cur ^ 1]
+            deep = self.deep[j] if j < len(self.deep) else None
+            nn = L[j + 1].input_norm
+            call("ff_add_rms_quant_static", ptr(self.res), ptr(self.dn), ptr(deep), ptr(nn.weight), ptr(nxt), None,
+                 ptr(self.xq), float(L[j + 1].qkv.inverse_scale), T, H, float(nn.variance_epsilon), self.image_start,
+                 self.nv if deep is not None else 0, s)
+            cur ^= 1
+            if trace is not None:
+                trace.append(nxt.clone())
+        # pick-only tail (_family/night_runtime.py:92-105)
+        lw = L[-1]
+        h = self.h[cur]
+        self._qkv_static(lw, T, s)
+        call("ff_attention_vt", ptr(self.yq), ptr(self.yk), ptr(self.vt), ptr(self.pick), 1, ptr(self.attn), 1, T,
+             Tp, HQ, HK, D, float(cfg.scaling), s)
+        call("ff_quant_static_fp8", ptr(self.attn), ptr(self.aq), 1, 1, HQ * D, float(lw.o.inverse_scale), s)
+        self._gemm_static(self.aq, lw.o, self.o, 1, s)
+        call("ff_gather_rows", ptr(h), H, ptr(self.pick), ptr(self.hp), H, 1, H, T, s)
+        call("ff_add_rms_quant_static", ptr(self.hp), ptr(self.o), None, ptr(lw.post_norm.weight), ptr(self.res), None,
+             ptr(self.pq), float(lw.gateup.inverse_scale), 1, H, float(lw.post_norm.variance_epsilon), 0, 0, s)
+        self._mlp_static(lw, 1, s)
+        call("ff_lm_readout", ptr(self.res), ptr(self.dn), ptr(w.norm.weight), ptr(w.head), ptr(self.logits), H,
+             w.head.shape[0], float(w.norm.variance_epsilon), s)
+        return self.logits
+
+    def _qkv_static(self, lw, m, s):
+        cfg = self.cfg
+        op = lw.qkv
+        call("ff_gemm_fp8_qkv", ptr(self.xq), ptr(op.input_scale), 0, ptr(op.weight), ptr(op.weight_scale), 0, m,
+             cfg.hidden, cfg.heads, cfg.kv_heads, ptr(lw.q_norm.weight), ptr(lw.k_norm.weight),
+             float(lw.q_norm.variance_epsilon), float(lw.k_norm.variance_epsilon), ptr(self.cos), ptr(self.sin),
+             ptr(self.yq), ptr(self.yk), ptr(self.vt), self.Tp, s)
+
+    def _gemm_static(self, q, op, out, m, s):
+        n, k = op.weight.shape
+        call("ff_gemm_fp8_pk", ptr(q), ptr(op.input_scale), 0, ptr(op.weight), ptr(op.packed), ptr(op.weight_scale),
+             0, ptr(out), n, m, n, k, ptr(self.gws), self.gws.numel(), s)
+
+    def _mlp_static(self, lw, m, s):
+        I, H = self.cfg.inter, self.cfg.hidden
+        op = lw.gateup
+        call("ff_gemm_fp8_swiglu_static", ptr(self.pq), ptr(op.input_scale), ptr(op.weight), ptr(op.packed),
+             ptr(op.weight_scale), ptr(self.mq), I, float(lw.down.inverse_scale), m, I, H, s)
+        self._gemm_static(self.mq, lw.down, self.dn, m, s)
 
     def _step_generic(self, trace=None):
         """The reference's op sequence (scaled_qwen_runtime.py:143-176,
@@ -422,7 +515,11 @@ class Runtime:
         """Run the step eagerly on the current stream; returns the logits buffer.
         ``trace`` (a list) receives a copy of the residual stream after every
         full layer (eager runs only)."""
-        return self._step_fused(trace) if self.path == "fused" else self._step_generic(trace)
+        if self.path == "fused":
+            return self._step_fused(trace)
+        if self.path == "fused_static":
+            return self._step_static(trace)
+        return self._step_generic(trace)
 
     # ------------------------------------------------------------ hipGraph
 

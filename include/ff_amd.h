@@ -203,15 +203,41 @@ int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, const void* qw,
 
 /* Fused QKV GEMM + q/k norm + rotary + V transpose (no reference counterpart as
  * one op; the same arithmetic as ff_gemm_fp8 on the packed QKV weight followed
- * by ff_qkv_post): qw ((hq + 2 hk) * 128, k) e4m3 with per-row scales sw, qa (m, k)
- * with per-token scales sa. Writes yq (hq, m, 128), yk (hk, m, 128) (per-head
- * RMSNorm with q_norm / k_norm, then rotary with cos / sin (m, 128)) and vt
- * (hk, 128, t_pad) with zeros for tokens in [m, t_pad). Head dim 128. Replaces
- * the qkv linear + qk_pair of scaled_qwen_runtime.py:150-155. */
-int ff_gemm_fp8_qkv(const void* qa, const float* sa, const void* qw, const float* sw, int64_t m, int64_t k,
-                    int64_t hq, int64_t hk, const void* q_norm, const void* k_norm, float eps_q, float eps_k,
-                    const void* cos, const void* sin, void* yq, void* yk, void* vt, int64_t t_pad,
-                    ff_stream_t stream);
+ * by ff_qkv_post): qw ((hq + 2 hk) * 128, k) e4m3 with scales sw (per row if
+ * sw_cols, else sw[0]), qa (m, k) with scales sa (per token if sa_rows, else
+ * sa[0]: the static-scale linears). Writes yq (hq, m, 128), yk (hk, m, 128)
+ * (per-head RMSNorm with q_norm / k_norm, then rotary with cos / sin (m, 128))
+ * and vt (hk, 128, t_pad) with zeros for tokens in [m, t_pad). Head dim 128.
+ * Replaces the qkv linear + qk_pair of scaled_qwen_runtime.py:150-155. */
+int ff_gemm_fp8_qkv(const void* qa, const float* sa, int sa_rows, const void* qw, const float* sw, int sw_cols,
+                    int64_t m, int64_t k, int64_t hq, int64_t hk, const void* q_norm, const void* k_norm,
+                    float eps_q, float eps_k, const void* cos, const void* sin, void* yq, void* yk, void* vt,
+                    int64_t t_pad, ff_stream_t stream);
+
+/* Static-scale (calibrated) FP8 producers of the step, no reference counterpart
+ * as separate ops: each is the op it extends followed by the runtime-scale cast
+ * q = e4m3(clamp(x * inv, +-448)) of _family/depth_fp8.py:8-19 (quantize_runtime)
+ * on its bf16 output, with inv the consuming linear's inverse_scale, so the
+ * next GEMM reads e4m3 codes directly.
+ * ff_fast_norm_quant_static / ff_add_rms_quant_static: ff_fast_norm_quant /
+ * ff_add_rms_quant with that cast in place of the per-token scale (out may be
+ * NULL). ff_attention_vt_q: the causal prefill of ff_attention_vt (no
+ * positions, s == t) writing the codes of its (s, hq, 128) output. */
+int ff_fast_norm_quant_static(const void* x, const void* w, void* out, void* q, float inv, int64_t rows, int64_t h,
+                              float eps, ff_stream_t stream);
+int ff_add_rms_quant_static(const void* a, const void* b, const void* deep, const void* w, void* residual, void* out,
+                            void* q, float inv, int64_t rows, int64_t h, float eps, int64_t start, int64_t nv,
+                            ff_stream_t stream);
+int ff_attention_vt_q(const void* q, const void* k, const void* vt, void* yq, float inv, int64_t s, int64_t t,
+                      int64_t t_pad, int64_t hq, int64_t hk, int64_t d, float scale, ff_stream_t stream);
+/* Gate/up GEMM with the SwiGLU epilogue for static-scale linears: per-tensor
+ * scales sa[0], sw[0]; h = bf16(bf16(silu(g)) * u) written as the codes
+ * e4m3(clamp(h * inv, +-448)) (m, i) with row pitch ldh bytes (inv: the down
+ * projection's inverse_scale). The packed tile when qw_packed is given and
+ * the shape suits it (as ff_gemm_fp8_swiglu_pk), else the row-major tile or,
+ * for m <= 4, the GEMV kernel. */
+int ff_gemm_fp8_swiglu_static(const void* qa, const float* sa, const void* qw, const void* qw_packed, const float* sw,
+                              void* hq, int64_t ldh, float inv, int64_t m, int64_t i, int64_t k, ff_stream_t stream);
 
 /* ff_quant_rows_fp8 with the row amax given as npart partial maxima per row
  * (pmax (rows, npart), as ff_gemm_fp8_swiglu writes them): identical codes and

@@ -162,12 +162,27 @@ def test_fused_path_equals_reference_op_sequence(gpu):
     assert torch.equal(z1, z2), (z1, z2)
 
 
-@pytest.mark.parametrize("path", ["fused", "generic"])
-def test_graph_replays_equal_eager(gpu, path):
+def test_fused_static_path_equals_reference_op_sequence(gpu):
+    """Static-scale linears (RuntimeScaleLinear, _family/depth_fp8.py:22-26):
+    the fused step, whose producers cast to e4m3 with the consumer's
+    inverse_scale, equals the reference's op sequence (quantize_runtime +
+    _scaled_mm per linear) bit for bit."""
+    from fastforward_amd.synthetic import make_model, make_request
+    cfg = _tiny(4)
+    w = make_model(cfg, mode="fp8_static", seed=2, norm_jitter=0.2)
+    ids, pos, pick = make_request(cfg, 130, 5, 5, seed=2)
+    rt1, z1 = _run(cfg, w, 130, ids, pos, pick)
+    assert rt1.path == "fused_static"
+    _, z2 = _run(cfg, w, 130, ids, pos, pick, path="generic")
+    assert torch.equal(z1, z2), (z1, z2)
+
+
+@pytest.mark.parametrize("mode,path", [("fp8", "fused"), ("fp8", "generic"), ("fp8_static", "fused_static")])
+def test_graph_replays_equal_eager(gpu, mode, path):
     from fastforward_amd.runtime import Runtime
     from fastforward_amd.synthetic import make_model, make_request
     cfg = _tiny()
-    w = make_model(cfg, mode="fp8", seed=3, norm_jitter=0.2)
+    w = make_model(cfg, mode=mode, seed=3, norm_jitter=0.2)
     rt = Runtime(cfg, w, 128, path=path)
     reqs = [make_request(cfg, 128, 4, 4, seed=s, real_tokens=n) for s, n in ((10, 128), (11, 100), (12, 77))]
     eager = []
@@ -235,6 +250,7 @@ def test_visual_rows_and_deepstack_vs_oracle(gpu):
 @pytest.mark.parametrize("preset,tokens,grid,choices,mode", [
     ("qwen3vl-2b", 320, (16, 16), 4, "fp8"),
     ("qwen3vl-8b", 576, (16, 32), 8, "fp8"),
+    ("qwen3vl-8b", 576, (16, 32), 8, "fp8_static"),
     ("qwen3vl-8b", 576, (16, 32), 8, "w4a16"),
 ])
 def test_full_model_vs_oracle(gpu, preset, tokens, grid, choices, mode):

@@ -663,7 +663,114 @@ def test_gemm_fp8_qkv_equals_unfused(gpu, t, k, hq, hk):
     yq = torch.full_like(rq, float("nan"))
     yk = torch.full_like(rk, float("nan"))
     vt = torch.full_like(rv, float("nan"))
-    call("ff_gemm_fp8_qkv", ptr(qa_d), ptr(sa_d), ptr(qw_d), ptr(sw_d), t, k, hq, hk, ptr(qn.weight), ptr(kn.weight),
+    call("ff_gemm_fp8_qkv", ptr(qa_d), ptr(sa_d), 1, ptr(qw_d), ptr(sw_d), 1, t, k, hq, hk, ptr(qn.weight), ptr(kn.weight),
          1e-6, 1e-6, ptr(cos), ptr(sin), ptr(yq), ptr(yk), ptr(vt), tp, stream())
     assert torch.equal(yq, rq) and torch.equal(yk, rk)
     assert torch.equal(vt, rv)
+
+
+# ------------------------------------------------------------------ static-scale (calibrated) producers
+
+@pytest.mark.parametrize("deep", [False, True])
+def test_norm_quant_static_equals_unfused(gpu, deep):
+    """ff_add_rms_quant_static / ff_fast_norm_quant_static write the same
+    residual and normalised row as ff_add_rms / ff_fast_norm and the codes
+    ff_quant_static_fp8 gives on that row (the reference's quantize_runtime,
+    _family/depth_fp8.py:8-19), bit for bit."""
+    from fastforward_amd import ops
+    from fastforward_amd._lib import call, ptr, stream
+    t, h, inv = 576, 4096, 448.0 / 6.5
+    a = torch.randn(1, t, h, generator=_g(70)).to(BF16).to(DEV)
+    b = torch.randn(1, t, h, generator=_g(71)).to(BF16).to(DEV)
+    mod, _ = _norm_module(h, 72)
+    start, nv = (4, 512) if deep else (0, 0)
+    dp = torch.randn(nv, h, generator=_g(73)).to(BF16).to(DEV) if deep else None
+    res, out = ops.add_rms(a, b, dp, mod, start, nv)
+    want = torch.empty(t, h, device=DEV, dtype=torch.uint8)
+    call("ff_quant_static_fp8", ptr(out), ptr(want), t, t, h, inv, stream())
+    r2 = torch.empty_like(res)
+    q = torch.full((t, h), 0xAA, device=DEV, dtype=torch.uint8)
+    call("ff_add_rms_quant_static", ptr(a), ptr(b), ptr(dp), ptr(mod.weight), ptr(r2), None, ptr(q), inv, t, h,
+         1e-6, start, nv, stream())
+    assert torch.equal(r2, res) and torch.equal(q, want)
+    fn = ops.fast_norm(a, mod)
+    call("ff_quant_static_fp8", ptr(fn), ptr(want), t, t, h, inv, stream())
+    o2 = torch.empty_like(fn)
+    call("ff_fast_norm_quant_static", ptr(a), ptr(mod.weight), ptr(o2), ptr(q), inv, t, h, 1e-6, stream())
+    assert torch.equal(o2, fn) and torch.equal(q, want)
+
+
+@pytest.mark.parametrize("t,hq,hk", [(576, 32, 8), (320, 16, 8), (1024, 64, 8)])
+def test_attention_q_equals_unfused(gpu, t, hq, hk):
+    """ff_attention_vt_q writes the codes of exactly the bf16 output
+    ff_attention_vt gives (causal prefill), under the static multiplier."""
+    from fastforward_amd._lib import call, ptr, stream
+    d, inv = 128, 448.0 / 3.0
+    tp = (t + 63) // 64 * 64
+    q = torch.randn(hq, t, d, generator=_g(74)).to(BF16).to(DEV)
+    k = torch.randn(hk, t, d, generator=_g(75)).to(BF16).to(DEV)
+    vt = torch.zeros(hk, d, tp, dtype=BF16)
+    vt[:, :, :t] = torch.randn(hk, d, t, generator=_g(76)).to(BF16)
+    vt = vt.to(DEV)
+    y = torch.empty(t, hq * d, device=DEV, dtype=BF16)
+    call("ff_attention_vt", ptr(q), ptr(k), ptr(vt), None, 0, ptr(y), t, t, tp, hq, hk, d, d ** -0.5, stream())
+    want = torch.empty(t, hq * d, device=DEV, dtype=torch.uint8)
+    call("ff_quant_static_fp8", ptr(y), ptr(want), t, t, hq * d, inv, stream())
+    got = torch.full((t, hq * d), 0xAA, device=DEV, dtype=torch.uint8)
+    call("ff_attention_vt_q", ptr(q), ptr(k), ptr(vt), ptr(got), inv, t, t, tp, hq, hk, d, d ** -0.5, stream())
+    assert torch.equal(got, want)
+    with pytest.raises(RuntimeError, match="causal prefill"):
+        call("ff_attention_vt_q", ptr(q), ptr(k), ptr(vt), ptr(got), inv, 1, t, tp, hq, hk, d, d ** -0.5, stream())
+
+
+@pytest.mark.parametrize("m,i,k", [(576, 12288, 4096), (320, 6144, 2048), (1, 12288, 4096), (3, 640, 256)])
+def test_gemm_swiglu_static_equals_unfused(gpu, m, i, k):
+    """ff_gemm_fp8_swiglu_static (packed tile, row-major tile and GEMV by shape)
+    equals ff_gemm_fp8 with per-tensor scales, then swiglu, then the static cast,
+    bit for bit."""
+    from fastforward_amd import ops
+    from fastforward_amd._lib import call, ptr, stream
+    from fastforward_amd.linear import StaticFP8Linear
+    op = StaticFP8Linear((torch.randn(2 * i, k, generator=_g(77)) * 0.03).to(BF16).to(DEV), 448.0 / 5.0).pack()
+    x = torch.randn(m, k, generator=_g(78)).to(BF16).to(DEV)
+    qa = torch.empty(m, k, device=DEV, dtype=torch.uint8)
+    call("ff_quant_static_fp8", ptr(x), ptr(qa), m, m, k, float(op.inverse_scale), stream())
+    gu = torch.empty(m, 2 * i, device=DEV, dtype=BF16)
+    call("ff_gemm_fp8", ptr(qa), ptr(op.input_scale), 0, ptr(op.weight), ptr(op.weight_scale), 0, ptr(gu), 2 * i, m,
+         2 * i, k, stream())
+    hh = ops.swiglu(*gu.chunk(2, -1)).contiguous()
+    inv = 448.0 / 0.75
+    want = torch.empty(m, i, device=DEV, dtype=torch.uint8)
+    call("ff_quant_static_fp8", ptr(hh), ptr(want), m, m, i, inv, stream())
+    got = torch.full((m, i), 0xAA, device=DEV, dtype=torch.uint8)
+    call("ff_gemm_fp8_swiglu_static", ptr(qa), ptr(op.input_scale), ptr(op.weight), ptr(op.packed),
+         ptr(op.weight_scale), ptr(got), i, inv, m, i, k, stream())
+    assert torch.equal(got, want)
+
+
+def test_gemm_qkv_static_scales_equal_unfused(gpu):
+    """ff_gemm_fp8_qkv with per-tensor scales (sa_rows = sw_cols = 0) equals
+    ff_gemm_fp8 with the same scalars followed by ff_qkv_post, bit for bit."""
+    from fastforward_amd._lib import call, ptr, stream
+    t, k, hq, hk, d = 576, 4096, 32, 8, 128
+    tp, n = (t + 63) // 64 * 64, (hq + 2 * hk) * d
+    qa = torch.randint(0, 126, (t, k), generator=_g(79), dtype=torch.uint8)
+    qa[torch.rand(t, k, generator=_g(80)) < 0.5] |= 0x80
+    qw = torch.randint(0, 126, (n, k), generator=_g(81), dtype=torch.uint8)
+    qa_d, qw_d = qa.to(DEV), qw.to(DEV)
+    sa, sw = torch.tensor([0.011], device=DEV), torch.tensor([0.0007], device=DEV)
+    qn, _ = _norm_module(d, 82, 0.3)
+    kn, _ = _norm_module(d, 83, 0.3)
+    cos, sin = O.mrope_cos_sin(O.mrope_positions(4, 16, 32, t), 5e6, d)
+    cos, sin = cos[0].to(DEV), sin[0].to(DEV)
+    raw = torch.empty(t, n, device=DEV, dtype=BF16)
+    call("ff_gemm_fp8", ptr(qa_d), ptr(sa), 0, ptr(qw_d), ptr(sw), 0, ptr(raw), n, t, n, k, stream())
+    rq, rk = torch.empty(hq, t, d, device=DEV, dtype=BF16), torch.empty(hk, t, d, device=DEV, dtype=BF16)
+    rv = torch.empty(hk, d, tp, device=DEV, dtype=BF16)
+    base = raw.data_ptr()
+    call("ff_qkv_post", base, base + hq * d * 2, base + (hq + hk) * d * 2, n, ptr(qn.weight), ptr(kn.weight), 1e-6,
+         1e-6, ptr(cos), ptr(sin), ptr(rq), ptr(rk), ptr(rv), t, tp, hq, hk, d, stream())
+    yq, yk, vt = torch.empty_like(rq), torch.empty_like(rk), torch.empty_like(rv)
+    call("ff_gemm_fp8_qkv", ptr(qa_d), ptr(sa), 0, ptr(qw_d), ptr(sw), 0, t, k, hq, hk, ptr(qn.weight),
+         ptr(kn.weight), 1e-6, 1e-6, ptr(cos), ptr(sin), ptr(yq), ptr(yk), ptr(vt), tp, stream())
+    assert torch.equal(yq, rq) and torch.equal(yk, rk) and torch.equal(vt, rv)

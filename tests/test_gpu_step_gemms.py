@@ -176,7 +176,7 @@ def test_step_qkv_epilogue_vs_oracle(gpu, preset):
     yq = torch.full((hq, t, D), float("nan"), device=DEV, dtype=BF16)
     yk = torch.full((hk, t, D), float("nan"), device=DEV, dtype=BF16)
     vt = torch.full((hk, D, tp), float("nan"), device=DEV, dtype=BF16)
-    call("ff_gemm_fp8_qkv", ptr(qa_d), ptr(sa_d), ptr(op.weight), ptr(op.scale), t, h, hq, hk, ptr(qn_d.weight),
+    call("ff_gemm_fp8_qkv", ptr(qa_d), ptr(sa_d), 1, ptr(op.weight), ptr(op.scale), 1, t, h, hq, hk, ptr(qn_d.weight),
          ptr(kn_d.weight), 1e-6, 1e-6, ptr(cos_d), ptr(sin_d), ptr(yq), ptr(yk), ptr(vt), tp, stream())
     raw = torch.empty(t, n, device=DEV, dtype=BF16)
     call("ff_gemm_fp8", ptr(qa_d), ptr(sa_d), 1, ptr(op.weight), ptr(op.scale), 1, ptr(raw), n, t, n, h, stream())
