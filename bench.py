@@ -266,6 +266,36 @@ def vision_extras(cfg, w, T, grid, args):
     return out
 
 
+def production_extras(cfg, mode, args):
+    """The reference's deployed request geometry, as context for its published
+    end-to-end latencies (which add image decode and host work): an aspect320
+    canvas of 320 x 320 pixels (20 x 20 patches -> 100 image tokens), the
+    minimal prompt with a four-option question (the prefix puts the image at
+    token 4; about 70 suffix tokens), in the smallest 16-token bucket that holds
+    it, 176 tokens (configs/8B.json buckets, variant aspect320, prompt_style
+    minimal). One hipGraph replay of the vision tower + the LM step per step."""
+    from fastforward_amd.pipeline import ImageStep
+    from fastforward_amd.runtime import mrope_positions
+    from fastforward_amd.synthetic import make_model
+    from fastforward_amd.vision import VISION_PRESETS, make_vision
+    vc = VISION_PRESETS[cfg.name]
+    gh = gw = 20
+    tokens, start, real = 176, 4, 175
+    w = make_model(cfg, mode=mode, seed=0, n_options=4)
+    vw = make_vision(vc, seed=0)
+    g = torch.Generator().manual_seed(0)
+    rgb = torch.randint(0, 256, (16 * gh, 16 * gw, 3), generator=g, dtype=torch.uint8)
+    ids = torch.randint(0, cfg.vocab, (real,), generator=g, dtype=torch.int64)
+    pos = torch.from_numpy(mrope_positions(start, gh // 2, gw // 2, tokens))
+    st = ImageStep(cfg, w, vc, vw, gh, gw, tokens, image_start=start)
+    st.set_inputs(rgb, ids, pos, real - 1)
+    st.capture()
+    ms = time_graph(st, args.steps, args.warmup)
+    del st, w, vw
+    torch.cuda.empty_cache()
+    return round(ms, 4)
+
+
 def cpu_baseline(cfg, w, ids, pos, pick, T, layers_sample):
     """The CPU oracle on ``layers_sample`` decoder layers + the pick-only tail of the
     same step, on this host's cores; scaled to the full depth."""
@@ -388,6 +418,10 @@ def main():
         del w
         torch.cuda.empty_cache()
         # the other LM configurations, each one hipGraph replay per step
+        for mode in ("fp8_static", "fp8"):
+            key = f"image_step_8b_aspect320_100img_176tok_{mode}_ms"
+            extras[key] = production_extras(cfg, mode, args)
+            log(f"{key} {extras[key]}")
         for key, preset, mode, tokens, gx, n_opt in (
                 ("fp8_static_8b_576_step_ms", args.preset, "fp8_static", T, grid, 8),
                 ("w4a16_g128_8b_576_step_ms", args.preset, "w4a16", T, grid, 8),

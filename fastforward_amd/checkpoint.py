@@ -19,7 +19,7 @@ import os
 
 import torch
 
-from .linear import FP8Linear, Int4, RuntimeScaleLinear
+from .linear import MIXED_MODES, FP8Linear, Int4, RuntimeScaleLinear, bank_of
 from .ops import RMSNorm
 from .runtime import LayerWeights, LMConfig, ModelWeights
 from .vision import Lin, Norm, VBlock, VisionConfig, VisionWeights, VMerger, pad_mlp
@@ -104,23 +104,32 @@ def _linear(w, mode, static_bound):
     raise ValueError(f"unknown linear mode {mode!r}")
 
 
-def load_lm(path, cfg, option_ids, mode="fp8", device="cuda", static_bound=8.0, tensors=None):
-    """ModelWeights of the language model, one decoder layer at a time."""
+def load_lm(path, cfg, option_ids, mode="fp8", device="cuda", static_bound=8.0, tensors=None, fp8_bank="fp8"):
+    """ModelWeights of the language model, one decoder layer at a time.
+    ``mode`` "int4_half" / "int4_ffn" mixes the int4 bank (the reference's
+    asymmetric group-32 Int4) into the interior layers (``bank_of``) and
+    takes the other linears in the ``fp8_bank`` format ("fp8" or
+    "fp8_static")."""
     ts = tensors or Tensors(path)
     p = "model.language_model."
     embed = ts.get(p + "embed_tokens.weight", device)
     layers = []
+
+    def lin(w, j, role):
+        if mode in MIXED_MODES:
+            return _linear(w, "int4" if bank_of(mode, j, cfg.layers, role) == "int4" else fp8_bank, static_bound)
+        return _linear(w, mode, static_bound)
     for j in range(cfg.layers):
         q = f"{p}layers.{j}."
         ops = {}
         w = torch.cat([ts.get(q + f"self_attn.{x}_proj.weight", device) for x in "qkv"])
-        ops["qkv"] = _linear(w, mode, static_bound)
+        ops["qkv"] = lin(w, j, "qkv")
         del w
-        ops["o"] = _linear(ts.get(q + "self_attn.o_proj.weight", device), mode, static_bound)
+        ops["o"] = lin(ts.get(q + "self_attn.o_proj.weight", device), j, "o")
         w = torch.cat([ts.get(q + f"mlp.{x}_proj.weight", device) for x in ("gate", "up")])
-        ops["gateup"] = _linear(w, mode, static_bound)
+        ops["gateup"] = lin(w, j, "gateup")
         del w
-        ops["down"] = _linear(ts.get(q + "mlp.down_proj.weight", device), mode, static_bound)
+        ops["down"] = lin(ts.get(q + "mlp.down_proj.weight", device), j, "down")
         layers.append(LayerWeights(
             input_norm=RMSNorm(ts.get(q + "input_layernorm.weight", device), cfg.eps),
             post_norm=RMSNorm(ts.get(q + "post_attention_layernorm.weight", device), cfg.eps),
@@ -160,7 +169,7 @@ def load_vision(path, vcfg, device="cuda", tensors=None):
                          [merger(f"deepstack_merger_list.{i}.", True) for i in range(len(vcfg.deepstack))])
 
 
-def load_pretrained(path, option_ids=None, mode="fp8", device="cuda", n_options=8):
+def load_pretrained(path, option_ids=None, mode="fp8", device="cuda", n_options=8, fp8_bank="fp8"):
     """(lm_cfg, lm_weights, vis_cfg, vis_weights, meta) of a local Qwen3-VL
     checkpoint directory. ``option_ids`` default to the first tokens of
     ' A' ... from the checkpoint's tokenizer."""
@@ -168,7 +177,7 @@ def load_pretrained(path, option_ids=None, mode="fp8", device="cuda", n_options=
     if option_ids is None:
         option_ids = option_ids_from_tokenizer(path, n_options)
     ts = Tensors(path)
-    lw = load_lm(path, lm, option_ids, mode=mode, device=device, tensors=ts)
+    lw = load_lm(path, lm, option_ids, mode=mode, device=device, tensors=ts, fp8_bank=fp8_bank)
     vw = load_vision(path, vis, device=device, tensors=ts)
     meta["option_ids"] = list(option_ids)
     return lm, lw, vis, vw, meta

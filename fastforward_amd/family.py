@@ -33,8 +33,12 @@ from .runtime import Arena, Runtime, mrope_positions
 from .vision import VisionRuntime
 
 # The reference's execution modes (_family/night_runtime.py:56-65) -> the
-# linear format loaded here. Accumulation is fp32 in every FP8 mode.
-EXECUTION_MODES = {"precise": None, "fp8": None, "anchor": None, "int4": "int4"}
+# linear format loaded here (None: FP8, static with a calibration profile).
+# "int4_half" / "int4_ffn" mix the int4 bank into the interior layers
+# (linear.bank_of). The FP8 modes share one accumulation (the matrix
+# instruction promotes every 32 products to fp32; fast_accum changes nothing).
+EXECUTION_MODES = {"precise": None, "fp8": None, "anchor": None, "int4": "int4", "int4_half": "int4_half",
+                   "int4_ffn": "int4_ffn"}
 
 
 class FamilyRuntime:
@@ -57,7 +61,9 @@ class FamilyRuntime:
             raise ValueError(f"execution mode {mode!r} is not supported by this build")
         linear = c.get("linear") or EXECUTION_MODES[mode] or ("fp8_static" if "profile_path" in c else "fp8")
         self.linear = linear
-        self.lm_cfg, self.lm_w, self.vis_cfg, self.vis_w, self.meta = load_pretrained(path, mode=linear)
+        fp8_bank = "fp8_static" if "profile_path" in c else "fp8"
+        self.lm_cfg, self.lm_w, self.vis_cfg, self.vis_w, self.meta = load_pretrained(path, mode=linear,
+                                                                                      fp8_bank=fp8_bank)
         dims = (self.lm_cfg.layers, self.lm_cfg.hidden, self.vis_cfg.depth)
         if "expected_dimensions" in c and tuple(c["expected_dimensions"]) != dims:
             raise ValueError(f"checkpoint dimensions {dims} differ from the bundle's {tuple(c['expected_dimensions'])}")

@@ -35,6 +35,28 @@ def gemm_pk_workspace(m, n, k):
     return need.value
 
 
+# Execution modes that mix the FP8 and int4 banks per layer and role.
+MIXED_MODES = ("int4_half", "int4_ffn")
+
+
+def bank_of(mode, layer, layers, role):
+    """Bank ("fp8" or "int4") of linear ``role`` ("qkv", "o", "gateup", "down")
+    of layer ``layer`` of ``layers`` under the reference's execution ``mode``
+    (``set_mode``, _family/night_runtime.py:56-65): with final = layers - 1 the
+    interior layers are 3 <= layer < final - 3; "int4_half" takes every role of
+    the even interior layers from the int4 bank, "int4_ffn" the gate/up and
+    down projections of every interior layer; "int4" every linear; any other
+    mode the FP8 bank."""
+    if mode == "int4":
+        return "int4"
+    interior = 3 <= layer < layers - 1 - 3
+    if mode == "int4_half" and interior and layer % 2 == 0:
+        return "int4"
+    if mode == "int4_ffn" and interior and role in ("gateup", "down"):
+        return "int4"
+    return "fp8"
+
+
 def _rows(x):
     return x.reshape(-1, x.shape[-1])
 

@@ -9,7 +9,7 @@ concatenated row-wise as the reference packs them.
 """
 import torch
 
-from .linear import FP8Linear, Int4, RuntimeScaleLinear
+from .linear import MIXED_MODES, FP8Linear, Int4, RuntimeScaleLinear, bank_of
 from .ops import RMSNorm
 from .runtime import LayerWeights, ModelWeights, mrope_positions
 
@@ -53,12 +53,15 @@ def _norm(n, jitter, device, seed):
 
 
 def make_model(cfg, mode="fp8", seed=0, device="cuda", n_options=8, norm_jitter=0.0,
-               static_bound=8.0, int4_group=128, int4_symmetric=True, keep_bf16=None):
+               static_bound=8.0, int4_group=128, int4_symmetric=True, keep_bf16=None, fp8_bank="fp8_static"):
     """Build ModelWeights for ``cfg``.
 
     mode: "fp8" (FP8Linear: per-token / per-channel), "fp8_static"
     (RuntimeScaleLinear with activation bound ``static_bound``), "w4a16" (Int4,
-    ``int4_group`` / ``int4_symmetric``), "int4" (Int4, asymmetric group 32).
+    ``int4_group`` / ``int4_symmetric``), "int4" (Int4, asymmetric group 32),
+    "int4_half" / "int4_ffn" (the reference's mixed execution modes: the
+    asymmetric group-32 int4 bank in the interior layers by ``bank_of``, the
+    ``fp8_bank`` format elsewhere).
     ``keep_bf16`` (a dict) receives the bf16 weights by (layer, role) on the CPU.
     """
     H, D = cfg.hidden, cfg.head_dim
@@ -71,13 +74,16 @@ def make_model(cfg, mode="fp8", seed=0, device="cuda", n_options=8, norm_jitter=
             w = linear_weight(cfg, j, role, seed, device)
             if keep_bf16 is not None:
                 keep_bf16[(j, role)] = w.cpu()
-            if mode == "fp8":
+            m = mode
+            if mode in MIXED_MODES:
+                m = "int4" if bank_of(mode, j, cfg.layers, role) == "int4" else fp8_bank
+            if m == "fp8":
                 ops[role] = FP8Linear(w)
-            elif mode == "fp8_static":
+            elif m == "fp8_static":
                 ops[role] = RuntimeScaleLinear(w, 448.0 / static_bound)
-            elif mode == "w4a16":
+            elif m == "w4a16":
                 ops[role] = Int4(w, group=int4_group, symmetric=int4_symmetric)
-            elif mode == "int4":    # the reference's asymmetric group-32 quantizer
+            elif m == "int4":       # the reference's asymmetric group-32 quantizer
                 ops[role] = Int4(w, group=32, symmetric=False)
             else:
                 raise ValueError(mode)

@@ -245,3 +245,24 @@ def test_arena_holds_every_bucket_layout():
     assert any(s > sizes[2048] for s in sizes.values()), "no bucket exceeds the largest one's layout"
     # the generic path (non-FP8Linear weights) lays out only the shared buffers
     assert Arena.size_for(cfg, 2048, "generic") < Arena.size_for(cfg, 2048)
+
+
+def test_mixed_execution_mode_banks():
+    """int4_half / int4_ffn pick banks as the reference's set_mode does
+    (_family/night_runtime.py:60-64): interior = 3 <= j < final - 3; int4_half
+    takes all four roles of the even interior layers from the int4 bank,
+    int4_ffn the gate/up and down projections of every interior layer."""
+    from fastforward_amd.linear import bank_of
+    layers = 36
+    final = layers - 1
+    roles = ("qkv", "o", "gateup", "down")
+    for j in range(layers):
+        interior = 3 <= j < final - 3
+        for r in roles:
+            assert bank_of("int4_half", j, layers, r) == ("int4" if interior and j % 2 == 0 else "fp8")
+            assert bank_of("int4_ffn", j, layers, r) == ("int4" if interior and r in ("gateup", "down") else "fp8")
+            assert bank_of("int4", j, layers, r) == "int4"
+            assert bank_of("precise", j, layers, r) == "fp8"
+    half = sum(bank_of("int4_half", j, layers, r) == "int4" for j in range(layers) for r in roles)
+    ffn = sum(bank_of("int4_ffn", j, layers, r) == "int4" for j in range(layers) for r in roles)
+    assert (half, ffn) == (14 * 4, 29 * 2)

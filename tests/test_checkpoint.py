@@ -17,12 +17,12 @@ DEV = "cuda"
 IMAGE_ID = 999
 
 
-def _tiny_hf(tmp_path, seed=0, save=True):
+def _tiny_hf(tmp_path, seed=0, save=True, layers=2):
     from transformers.models.qwen3_vl.configuration_qwen3_vl import Qwen3VLConfig
     from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLForConditionalGeneration
     torch.manual_seed(seed)
     cfg = Qwen3VLConfig(
-        text_config=dict(vocab_size=1000, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+        text_config=dict(vocab_size=1000, hidden_size=512, intermediate_size=1024, num_hidden_layers=layers,
                          num_attention_heads=4, num_key_value_heads=2, head_dim=128, rms_norm_eps=1e-6,
                          rope_parameters={"rope_type": "default", "rope_theta": 5e6, "mrope_section": [24, 20, 20],
                                           "mrope_interleaved": True}),
@@ -77,6 +77,38 @@ def test_loaded_weights_equal_hf(gpu, tmp_path):
     assert torch.equal(vw.blocks[0].fc1.w[:200].cpu(), vb.mlp.linear_fc1.weight.detach())
     assert not bool(vw.blocks[0].fc1.w[200:].float().abs().sum())
     assert torch.equal(vw.patch.w.cpu(), m.model.visual.patch_embed.proj.weight.detach().reshape(576, -1))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["int4_half", "int4_ffn"])
+def test_loaded_mixed_banks(gpu, tmp_path, mode):
+    """A 10-layer checkpoint loaded in a mixed execution mode: the interior
+    linears that the mode takes from the int4 bank hold the reference's
+    asymmetric group-32 codes and (scale, zero) table of the HF weight (the
+    oracle's int4_quantize_asym, bit for bit), the others the static-FP8 codes
+    and per-tensor scale."""
+    from oracle import ops as O
+    from fastforward_amd.checkpoint import load_pretrained
+    from fastforward_amd.linear import Int4, StaticFP8Linear, bank_of
+    m, path = _tiny_hf(tmp_path, seed=3, layers=10)
+    lm, lw, _, _, _ = load_pretrained(path, option_ids=list(range(10, 18)), mode=mode, fp8_bank="fp8_static")
+    hl = m.model.language_model.layers
+    for j in (2, 3, 4, 5, 6):
+        a, mlp = hl[j].self_attn, hl[j].mlp
+        full = {"qkv": torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight]), "o": a.o_proj.weight,
+                "gateup": torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight]), "down": mlp.down_proj.weight}
+        for role, wt in full.items():
+            op = getattr(lw.layers[j], role)
+            wt = wt.detach()
+            if bank_of(mode, j, lm.layers, role) == "int4":
+                assert isinstance(op, Int4) and op.group == 32 and not op.symmetric
+                _, packed, scales = O.int4_quantize_asym(wt.float(), 32)
+                assert torch.equal(op.packed.cpu(), packed) and torch.equal(op.scales.cpu(), scales), (j, role)
+            else:
+                assert isinstance(op, StaticFP8Linear)
+                q, sc = O.fp8_weight_quant(wt, per_channel=False)
+                assert torch.equal(op.weight.cpu().view(torch.uint8), q.view(torch.uint8)), (j, role)
+                assert torch.equal(op.weight_scale.cpu(), sc), (j, role)
 
 
 @pytest.mark.gpu

@@ -79,7 +79,7 @@ def _check_vs_oracle(z, want, what, tol):
     assert O.choose(z.tolist()) == O.choose(want.tolist()), what
 
 
-LAYER_BOUND = {"fp8": 0.06, "fp8_static": 0.06, "w4a16": 0.02}
+LAYER_BOUND = {"fp8": 0.06, "fp8_static": 0.06, "w4a16": 0.02, "int4_half": 0.06, "int4_ffn": 0.06}
 
 
 def _rel(a, b):
@@ -127,7 +127,7 @@ def _check_teacher_forced(cfg, w, mode, ids, pos, pick, layers, what, copy_all=T
     z = rt.step(trace=trace).clone().cpu()
     trace = [t.cpu() for t in trace]
     shape, ow = to_oracle(cfg, w, only=None if copy_all else set(layers) | {cfg.layers - 1},
-                          int4_bf16=mode == "w4a16")
+                          int4_bf16=mode in ("w4a16", "int4_half", "int4_ffn"))
     del rt
     cos, sin = O.mrope_cos_sin(pos, shape.theta, shape.head_dim, shape.sections)
     full = torch.zeros(pos.shape[1], dtype=torch.int64)
@@ -150,6 +150,27 @@ def test_tiny_model_teacher_forced(gpu, mode):
     ids, pos, pick = make_request(cfg, 96, 4, 6, seed=1)
     _check_teacher_forced(cfg, w, mode, ids, pos, pick, range(cfg.layers - 1), f"tiny {mode}",
                           tail_tol=TINY_TAIL_TOL[mode])
+
+
+@pytest.mark.parametrize("mode", ["int4_half", "int4_ffn"])
+def test_mixed_bank_model_teacher_forced(gpu, mode):
+    """The reference's mixed execution modes on a 10-layer model (interior
+    layers 3..5): static-FP8 linears with the asymmetric group-32 int4 bank
+    mixed in by layer and role; every layer and the tail teacher-forced
+    against the oracle (int4 in its bf16-operand form) on the generic path."""
+    from fastforward_amd.linear import Int4, StaticFP8Linear, bank_of
+    from fastforward_amd.runtime import Runtime
+    from fastforward_amd.synthetic import make_model, make_request
+    cfg = _tiny(10)
+    w = make_model(cfg, mode=mode, seed=6, norm_jitter=0.2, n_options=4)
+    for j, L in enumerate(w.layers):
+        for role in ("qkv", "o", "gateup", "down"):
+            want = Int4 if bank_of(mode, j, cfg.layers, role) == "int4" else StaticFP8Linear
+            assert isinstance(getattr(L, role), want), (mode, j, role)
+    assert Runtime.path_for(w) == "generic"
+    ids, pos, pick = make_request(cfg, 96, 4, 6, seed=6)
+    _check_teacher_forced(cfg, w, mode, ids, pos, pick, range(cfg.layers - 1), f"tiny {mode}",
+                          tail_tol=TINY_TAIL_TOL["fp8"])
 
 
 def test_fused_path_equals_reference_op_sequence(gpu):
