@@ -6,10 +6,14 @@
 // identical bits. What differs is how the operands reach the matrix cores:
 //
 // * Weights are repacked once at setup (ff_pack_weight_fp8) so that the MFMA
-//   operand of one 16-row x 128-byte fragment is 2 KB contiguous, lane l's 32
-//   bytes at 32 l. Each wave loads its weight fragments with buffer loads
-//   straight into the operand registers: every load instruction moves 1 KB of
-//   whole cache lines, and no LDS traffic or barrier is spent on the weights.
+//   operand of one 16-row x 128-byte fragment is 2 KB contiguous: lane l's 32
+//   bytes are split into two 1 KB planes, the first 16 at 16 l and the last 16
+//   at 1024 + 16 l. Each wave loads its weight fragments with buffer loads
+//   straight into the operand registers: each of the two load instructions of
+//   a fragment moves one contiguous 1 KB plane (whole cache lines, every byte
+//   used; interleaving a lane's 32 bytes would make each instruction touch 2 KB
+//   of lines for 1 KB of data), and no LDS traffic or barrier is spent on the
+//   weights.
 // * A workgroup of 4 waves owns BM tokens x BN = 4 CW weight rows; wave w owns
 //   all BM tokens x CW rows, so each A fragment read from LDS feeds CW/16 MFMAs
 //   (0.33 KB of LDS reads per MFMA at 144 x 96, a third of a 64 x 64 wave tile).
@@ -39,7 +43,8 @@
 //
 // Packed layout (ff_pack_weight_fp8): fragment (f, kt) of rows [16 f, 16 f + 16)
 // and k bytes [128 kt, 128 kt + 128) is the 2048 bytes at (f * K/128 + kt) * 2048;
-// lane l = 16 g + r holds row 16 f + r, k bytes [128 kt + 32 g, +32) at 32 l.
+// lane l = 16 g + r holds row 16 f + r, k bytes [128 kt + 32 g, +16) at 16 l and
+// [128 kt + 32 g + 16, +16) at 1024 + 16 l.
 // That is the operand layout of the MFMA for both A and B (the row-major
 // kernels feed the same k range to the same lane).
 #include <stdio.h>
@@ -95,9 +100,9 @@ __global__ __launch_bounds__(kThreads) void pack_fp8_kernel(const uint8_t* __res
     const int64_t kt = f % kt_n, f16 = f / kt_n;
     const int64_t row = f16 * 16 + (l & 15);
     const u32x4* src = reinterpret_cast<const u32x4*>(w + row * k + kt * 128 + 32 * (l >> 4));
-    u32x4* dst = reinterpret_cast<u32x4*>(p + f * 2048 + 32 * l);
-    dst[0] = src[0];
-    dst[1] = src[1];
+    uint8_t* dst = p + f * 2048 + 16 * l;
+    *reinterpret_cast<u32x4*>(dst) = src[0];
+    *reinterpret_cast<u32x4*>(dst + 1024) = src[1];
   }
 }
 
@@ -156,14 +161,14 @@ __device__ __forceinline__ void pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], uint
   };
 
   const __amdgpu_buffer_rsrc_t rB = make_rsrc(qwp, wbytes);
-  const uint32_t voffB = 32u * (uint32_t)lane;
+  const uint32_t voffB = 16u * (uint32_t)lane;
   i32x8 bq[P][TJ];
   auto loadB = [&](int kt, auto SLOT) {
     constexpr int slot = decltype(SLOT)::value;
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
       const i32x4v lo = bload16(rB, voffB, sB[j] + (uint32_t)kt * 2048u);
-      const i32x4v hi = bload16(rB, voffB + 16u, sB[j] + (uint32_t)kt * 2048u);
+      const i32x4v hi = bload16(rB, voffB + 1024u, sB[j] + (uint32_t)kt * 2048u);
       bq[slot][j] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
     }
   };
@@ -227,7 +232,7 @@ __device__ __forceinline__ void pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], uint
 #pragma unroll
         for (int i = 0; i < RA; ++i) mfma_acc(acc[i][j], bq[u % P][j], af[i]);
         const i32x4v lo = bload16(rB, voffB, sB[j] + ktn * 2048u);
-        const i32x4v hi = bload16(rB, voffB + 16u, sB[j] + ktn * 2048u);
+        const i32x4v hi = bload16(rB, voffB + 1024u, sB[j] + ktn * 2048u);
         bq[u % P][j] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
       });
     });

@@ -171,8 +171,9 @@ int ff_gemm_fp8_swiglu(const void* qa, const float* sa, const void* qw, const fl
  * layout read by ff_gemm_fp8_swiglu_pk (no reference counterpart: a storage
  * layout of this library): fragment (f, kt), rows [16 f, 16 f + 16) x k bytes
  * [128 kt, 128 kt + 128), is the 2048 bytes at (f * k/128 + kt) * 2048; lane
- * l = 16 g + r holds row 16 f + r, k bytes [128 kt + 32 g, +32) at 32 l.
- * packed holds n * k bytes. n % 16 == 0, k % 128 == 0. */
+ * l = 16 g + r holds row 16 f + r, k bytes [128 kt + 32 g, +16) at 16 l and
+ * [128 kt + 32 g + 16, +16) at 1024 + 16 l (two 1 KB planes, one load
+ * instruction each). packed holds n * k bytes. n % 16 == 0, k % 128 == 0. */
 int ff_pack_weight_fp8(const void* w, void* packed, int64_t n, int64_t k, ff_stream_t stream);
 
 /* ff_gemm_fp8_swiglu with an optional packed copy of the same weight

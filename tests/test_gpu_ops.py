@@ -315,20 +315,22 @@ def test_gemm_fp8_swiglu_equals_unfused(gpu, m, i, k):
 
 def test_pack_weight_fp8_layout(gpu):
     """ff_pack_weight_fp8 stores fragment (f, kt) at (f * k/128 + kt) * 2048 with
-    lane l = 16 g + r holding row 16 f + r, k bytes [128 kt + 32 g, +32) at 32 l."""
+    lane l = 16 g + r holding row 16 f + r, k bytes [128 kt + 32 g, +16) at 16 l
+    and the next 16 at 1024 + 16 l."""
     from fastforward_amd._lib import call, ptr, stream
     n, k = 48, 384
     w = torch.randint(0, 256, (n, k), generator=_g(50), dtype=torch.uint8)
     p = torch.empty(n * k, device=DEV, dtype=torch.uint8)
     w_d = w.to(DEV)
     call("ff_pack_weight_fp8", ptr(w_d), ptr(p), n, k, stream())
-    got = p.cpu().numpy().reshape(n // 16, k // 128, 64, 32)
+    got = p.cpu().numpy().reshape(n // 16, k // 128, 2, 64, 16)
     wn = w.numpy()
     for f in range(n // 16):
         for kt in range(k // 128):
             for lane in range(64):
                 r, g = lane % 16, lane // 16
-                assert np.array_equal(got[f, kt, lane], wn[16 * f + r, 128 * kt + 32 * g: 128 * kt + 32 * g + 32])
+                row = wn[16 * f + r, 128 * kt + 32 * g: 128 * kt + 32 * g + 32]
+                assert np.array_equal(got[f, kt, 0, lane], row[:16]) and np.array_equal(got[f, kt, 1, lane], row[16:])
 
 
 @pytest.mark.parametrize("m,i,k", [(576, 12288, 4096), (300, 12288, 2048), (433, 6144, 4096), (3, 12288, 4096),
