@@ -16,6 +16,7 @@ I64 = ctypes.c_int64
 I32 = ctypes.c_int
 F32 = ctypes.c_float
 PI64 = ctypes.POINTER(ctypes.c_int64)
+PI32 = ctypes.POINTER(ctypes.c_int)
 
 # name -> argtypes (restype int unless noted); mirrors include/ff_amd.h
 SIGNATURES = {
@@ -54,6 +55,11 @@ SIGNATURES = {
     "ff_gemm_w4a16_workspace": [I64, I64, I64, PI64],
     "ff_gemm_w4a16_ws": [P, I64, P, P, I64, P, I64, I64, I64, I64, P, I64, P],
     "ff_gemm_w4a16_noalloc": [P, I64, P, P, I64, P, I64, I64, I64, I64, P],
+    "ff_pack_weight_int4": [P, P, I64, I64, P],
+    "ff_gemm_w4a16_pk_workspace": [I64, I64, I64, I64, PI64],
+    "ff_gemm_w4a16_pk": [P, I64, P, P, P, I64, P, I64, I64, I64, I64, P, I64, P],
+    "ff_gemm_w4a16_swiglu_fits": [I64, I64, I64, I64, PI32],
+    "ff_gemm_w4a16_swiglu_pk": [P, I64, P, P, I64, P, I64, I64, I64, I64, P],
     "ff_embed": [P, P, P, I64, I64, I64, P],
     "ff_gather_rows": [P, I64, P, P, I64, I64, I64, I64, P],
     "ff_scatter_rows": [P, P, I64, I64, I64, P],

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/ff_amd.h"
 
 namespace ff {
@@ -51,6 +53,34 @@ __device__ __forceinline__ void wait_vmcnt() {
 // Workgroup barrier without a memory fence; this wave's LDS reads complete first.
 __device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
 
+// ------------------------------------------------------------------ buffer loads
+
+typedef int i32x4v __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource over `bytes` bytes (stride 0, 32-bit data format); loads
+// beyond the range return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// 16 / 4 bytes at byte offset voff + soff of the resource; ordinary
+// compiler-visible loads, so the compiler's wait counts are exact.
+__device__ __forceinline__ i32x4v bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+}
+__device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+}
+
+// f(integral_constant<int, I>) for I = B .. N-1, unrolled at compile time.
+template <int B, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < N) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, N>(f);
+  }
+}
+
 // ------------------------------------------------------------------ bf16
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
@@ -77,6 +107,11 @@ __device__ __forceinline__ void unpack8(const u32x4 v, float* f) {
   f[2] = __uint_as_float(v.y << 16); f[3] = __uint_as_float(v.y & 0xFFFF0000u);
   f[4] = __uint_as_float(v.z << 16); f[5] = __uint_as_float(v.z & 0xFFFF0000u);
   f[6] = __uint_as_float(v.w << 16); f[7] = __uint_as_float(v.w & 0xFFFF0000u);
+}
+
+// 4 bf16 (8 bytes) from 4 fp32 values, low to high.
+__device__ __forceinline__ u32x2 pack4_bf16(float a, float b, float c, float d) {
+  return u32x2{pack_bf16x2(a, b), pack_bf16x2(c, d)};
 }
 
 __device__ __forceinline__ u32x4 pack8(const float* f) {

@@ -59,29 +59,10 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kXcds = 8;
 
-typedef int i32x4v __attribute__((ext_vector_type(4)));
-
-template <int I, int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    static_for<I + 1, N>(f);
-  }
-}
-
 constexpr int lcm3(int a, int b, int c) {
   int l = a;
   while (l % b || l % c) l += a;
   return l;
-}
-
-// Raw buffer resource over `bytes` bytes (stride 0, 32-bit data format).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
-
-__device__ __forceinline__ i32x4v bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
 }
 
 // acc += A . B^T for one 16 x 16 x 128 e4m3 tile (A rows index the result's
@@ -247,11 +228,6 @@ __device__ __forceinline__ void pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], uint
 template <int BM, int G>
 constexpr int pk_smem() {
   return 2 * G * BM * 128;
-}
-
-// 4 bf16 (8 bytes) from 4 fp32 values, low to high.
-__device__ __forceinline__ u32x2 pack4_bf16(float a, float b, float c, float d) {
-  return u32x2{pack_bf16x2(a, b), pack_bf16x2(c, d)};
 }
 
 // Gate/up: BM tokens x (BN/2 gate + BN/2 up channels), BN = 4 CW; wave w takes

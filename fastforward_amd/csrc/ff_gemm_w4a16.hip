@@ -89,14 +89,6 @@ __device__ __forceinline__ u32x4 dequant8_exact(uint32_t w, float s, float z) {
   return r;
 }
 
-template <int I, int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    static_for<I + 1, N>(f);
-  }
-}
-
 template <int BM, int CW, int S>
 struct W4Cfg {
   static constexpr int BN = 4 * CW;
@@ -450,6 +442,565 @@ extern "C" int ff_gemm_w4a16_ws(const void* x, int64_t ldx, const void* packed, 
                                 void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, void* workspace,
                                 int64_t workspace_bytes, ff_stream_t stream) {
   return gemm_w4a16(x, ldx, packed, scales, group, y, ldy, m, n, k, workspace, workspace_bytes, stream);
+}
+
+// ------------------------------------------------------------------ packed-weight kernels
+//
+// The weight is repacked once (ff_pack_weight_int4) into MFMA fragment order:
+// the 16 rows x 128 k of fragment (f, kt) are the 1 KB at (f K/128 + kt) 1024;
+// lane l = 16 g + r holds row 16 f + r, the packed bytes of k = 128 kt + 64 h +
+// 16 g + [0, 16) for h = 0, 1 (8 bytes each, source byte order, each nibble
+// q stored as q ^ 8) at 16 l. One
+// 16-byte buffer load per lane moves a fragment (1 KB of whole cache lines per
+// instruction) straight into registers; dword 2 h + t of a lane feeds MFMA
+// (h, t) of the step, k = 128 kt + 64 h + 16 g + 8 t + [0, 8) -- the k
+// assignment and MFMA order of the LDS-staged kernel above, so that unsplit
+// products are bit-identical between the two.
+//
+// A workgroup of 4 waves owns BM tokens x 4 CW weight rows and wave w owns all
+// BM tokens x CW rows, so each weight is dequantised once per workgroup by the
+// wave that owns it, in registers. The bf16 activations go global -> registers
+// -> LDS: two 128-k stages and one barrier per step; each 256-byte row sits as
+// two 128-byte halves, each half in the FP8 GEMM's swizzled layout (1 KB
+// blocks of 8 rows, 16-byte chunk c of row r at slot c ^ ((r % 16) / 2)).
+// The weight fragment is the MFMA's first operand, so the accumulator holds the
+// transposed tile: lane 16 g + r of fragment (i, j) holds token 16 i + r,
+// weight rows 16 j + 4 g .. + 3, and the epilogues store 8-byte row pieces
+// from registers. The (s, z) pairs come from their [K/group, N] layout as
+// 4-byte loads (group a power of two >= 32, so a lane's 16 k share a group).
+// The fragments store each nibble q as q ^ 8, so that one v_cvt_off_f32_i4 per
+// weight gives (q - 8) / 16 and one fma the exactly rounded (q - 8) s + z
+// (dequant8_off): the same values as the kernel above, with no inexact-z8 case.
+
+namespace {
+
+constexpr int kPkStep = 128;  // k per step
+
+// (q - 8) / 16 from the low 4 bits of byte B of x, read as a signed 4-bit value
+// (the packed fragments store q ^ 8): v_cvt_off_f32_i4 maps 4-bit two's
+// complement n to n / 16, exactly.
+template <int B>
+__device__ __forceinline__ float cvt_off_byte(uint32_t x) {
+  float f;
+  if constexpr (B == 0) asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(f) : "v"(x));
+  if constexpr (B == 1) asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(f) : "v"(x));
+  if constexpr (B == 2) asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(f) : "v"(x));
+  if constexpr (B == 3) asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(f) : "v"(x));
+  return f;
+}
+
+// 8 nibbles of one fragment dword (stored q ^ 8; k order: byte b high nibble,
+// byte b low nibble) -> 8 bf16 of bf16((q - 8) s + z), as the MFMA operand.
+// fma((q - 8) / 16, 16 s, z) forms the exact product (q - 8) s (4-bit by 8-bit
+// significands) and rounds once: the value of dequant8_exact for every (s, z),
+// at the cost of dequant8 and without its z8 condition. s16 = 16 s.
+__device__ __forceinline__ u32x4 dequant8_off(uint32_t w, float s16, float z) {
+  const uint32_t hi = w >> 4;
+  u32x4 r;
+  r.x = pack_bf16x2(fmaf(cvt_off_byte<0>(hi), s16, z), fmaf(cvt_off_byte<0>(w), s16, z));
+  r.y = pack_bf16x2(fmaf(cvt_off_byte<1>(hi), s16, z), fmaf(cvt_off_byte<1>(w), s16, z));
+  r.z = pack_bf16x2(fmaf(cvt_off_byte<2>(hi), s16, z), fmaf(cvt_off_byte<2>(w), s16, z));
+  r.w = pack_bf16x2(fmaf(cvt_off_byte<3>(hi), s16, z), fmaf(cvt_off_byte<3>(w), s16, z));
+  return r;
+}
+
+// dequant8_off in 7 pieces of 2-3 VALU instructions, to be spread between MFMAs
+// (same operations, same values): w, s16, z set by the caller, r the result.
+struct DqPieces {
+  uint32_t w, hi;
+  float s16, z;
+  float f[8], y[8];
+  u32x4 r;
+  template <int P>
+  __device__ __forceinline__ void piece() {
+    if constexpr (P == 0) {
+      hi = w >> 4;
+      f[0] = cvt_off_byte<0>(hi);
+      f[1] = cvt_off_byte<0>(w);
+    } else if constexpr (P == 1) {
+      y[0] = fmaf(f[0], s16, z);
+      y[1] = fmaf(f[1], s16, z);
+      f[2] = cvt_off_byte<1>(hi);
+    } else if constexpr (P == 2) {
+      f[3] = cvt_off_byte<1>(w);
+      y[2] = fmaf(f[2], s16, z);
+      y[3] = fmaf(f[3], s16, z);
+    } else if constexpr (P == 3) {
+      r.x = pack_bf16x2(y[0], y[1]);
+      r.y = pack_bf16x2(y[2], y[3]);
+      f[4] = cvt_off_byte<2>(hi);
+    } else if constexpr (P == 4) {
+      f[5] = cvt_off_byte<2>(w);
+      y[4] = fmaf(f[4], s16, z);
+      y[5] = fmaf(f[5], s16, z);
+    } else if constexpr (P == 5) {
+      f[6] = cvt_off_byte<3>(hi);
+      f[7] = cvt_off_byte<3>(w);
+      y[6] = fmaf(f[6], s16, z);
+    } else {
+      y[7] = fmaf(f[7], s16, z);
+      r.z = pack_bf16x2(y[4], y[5]);
+      r.w = pack_bf16x2(y[6], y[7]);
+    }
+  }
+};
+
+// acc += A . B for one 16 x 16 x 32 bf16 tile, accumulator tied in place in
+// AGPRs (as the packed FP8 kernel: with the builtin the compiler moves every
+// accumulator between AGPRs and VGPRs at the loop edge). The compiler does not
+// see this asm as an MFMA, so it inserts none of the MFMA's wait states:
+// FRESH marks an MFMA whose A operand (dequantised weights) VALU has just
+// written, which needs 2 wait states after that write; the s_nop gives 5. The
+// other hazards are covered by s_nop at the loop's ends.
+template <bool FRESH>
+__device__ __forceinline__ void mfma_bf16_acc(f32x4& acc, const u32x4& a, const i32x4v& b) {
+  const i32x4v av = __builtin_bit_cast(i32x4v, a);
+  if constexpr (FRESH)
+    asm volatile("s_nop 4\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(av), "v"(b));
+  else
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(av), "v"(b));
+}
+
+__global__ __launch_bounds__(kThreads) void pack_int4_kernel(const uint8_t* __restrict__ src,
+                                                             uint8_t* __restrict__ dst, int64_t n, int64_t k) {
+  const int64_t kt_n = k / kPkStep;
+  const int64_t lanes = (n / 16) * kt_n * 64;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < lanes; i += (int64_t)gridDim.x * blockDim.x) {
+    const int l = (int)(i & 63);
+    const int64_t f = i >> 6;  // fragment f16 * kt_n + kt
+    const int64_t kt = f % kt_n, f16 = f / kt_n;
+    const int64_t row = f16 * 16 + (l & 15);
+    const uint8_t* s = src + row * (k / 2) + kt * 64 + 8 * (l >> 4);
+    const u32x2 a = *reinterpret_cast<const u32x2*>(s), b = *reinterpret_cast<const u32x2*>(s + 32);
+    constexpr uint32_t kFlip = 0x88888888u;  // nibble q stored as q ^ 8: its signed 4-bit value is q - 8
+    *reinterpret_cast<u32x4*>(dst + f * 1024 + 16 * l) = u32x4{a.x ^ kFlip, a.y ^ kFlip, b.x ^ kFlip, b.y ^ kFlip};
+  }
+}
+
+// acc (BM x 4 CW tile, wave w owning all BM rows x CW weight rows, transposed
+// layout) = sum over k steps [kt0, kt0 + nk) of A . B^T. sB[j]: byte offset of
+// this wave's weight fragment row j at k step 0; colS[j]: the weight row whose
+// (s, z) this lane reads for fragment j. nk even, kt0 even.
+template <int BM, int CW>
+__device__ __forceinline__ void w4pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], uint8_t* smem,
+                                              const bf16_t* __restrict__ x, int64_t ldx, int M, int m0,
+                                              const uint8_t* __restrict__ wp, uint32_t wbytes,
+                                              const uint32_t (&sB)[CW / 16], const uint32_t* __restrict__ sz,
+                                              uint32_t szbytes, const uint32_t (&colS)[CW / 16], int N, int gshift,
+                                              int kt0, int nk) {
+  constexpr int RA = BM / 16, TJ = CW / 16;
+  constexpr int A_CHUNKS = BM * 16;  // 16-byte chunks of one A stage (BM rows x 256 bytes)
+  constexpr int FULL = A_CHUNKS / kThreads, REM = A_CHUNKS % kThreads;
+  constexpr int NA = FULL + (REM ? 1 : 0);
+  constexpr int HALF = BM * 128;  // one 128-byte half of every row of a stage
+  constexpr int STAGE = 2 * HALF;
+  static_assert(A_CHUNKS >= kThreads, "at least one full activation round");
+  static_assert(RA >= 6, "a group's MFMAs carry the next group's 7 dequantisation pieces");
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int kend = kt0 + nk;
+
+  // Activations: chunk c = tid + 256 i is row c / 16, chunk c % 16 (a partial
+  // last round is moved back over the last 256 chunks, loading and storing the
+  // overlap twice with the same bytes, so nothing is predicated).
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(x, (uint32_t)((int64_t)M * ldx * 2));
+  uint32_t voffA[NA];
+  int dstA[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int c = i < FULL ? tid + kThreads * i : A_CHUNKS - kThreads + tid;
+    const int row = c >> 4, ch = c & 15;
+    voffA[i] = (uint32_t)min(m0 + row, M - 1) * (uint32_t)(2 * ldx) + 16 * ch;
+    dstA[i] = (ch >> 3) * HALF + (row >> 3) * 1024 + 128 * (row & 7) + 16 * ((ch & 7) ^ ((row & 15) >> 1));
+  }
+  i32x4v ast[NA];
+  auto loadA = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) ast[i] = bload16(rA, voffA[i], (uint32_t)kt * 256u);
+  };
+  auto writeA = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) *reinterpret_cast<i32x4v*>(smem + buf * STAGE + dstA[i]) = ast[i];
+  };
+
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(wp, wbytes);
+  const __amdgpu_buffer_rsrc_t rS = make_rsrc(sz, szbytes);
+  const uint32_t voffB = 16u * (uint32_t)lane;
+  i32x4v bq[2][TJ];
+  uint32_t sq[2][TJ][2];  // (s, z) of halves h = 0, 1
+  auto loadB = [&](int kt, auto SLOT) {
+    constexpr int slot = decltype(SLOT)::value;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      bq[slot][j] = bload16(rB, voffB, sB[j] + (uint32_t)kt * 1024u);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t gi = (uint32_t)(kPkStep * kt + 64 * h + 16 * g) >> gshift;
+        sq[slot][j][h] = bload4(rS, (gi * (uint32_t)N + colS[j]) * 4u, 0);
+      }
+    }
+  };
+
+#pragma unroll
+  for (int i = 0; i < RA; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // W4_PIN: every accumulator through an asm barrier (each is zeroed before it).
+  // W4_NOPS: wait states between VALU writes / MFMA results and their readers.
+#define W4_PIN()                                      \
+  do {                                                \
+    _Pragma("unroll") for (int i_ = 0; i_ < RA; ++i_) \
+    _Pragma("unroll") for (int j_ = 0; j_ < TJ; ++j_) \
+      asm volatile("" : "+a"(acc[i_][j_]));           \
+  } while (0)
+#define W4_NOPS() asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(acc[RA - 1][TJ - 1]))
+  W4_PIN();
+  W4_NOPS();
+
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  loadA(kt0);
+  loadB(kt0, I0{});
+  writeA(0);
+  loadA(min(kt0 + 1, kend - 1));
+  loadB(min(kt0 + 1, kend - 1), I1{});
+
+  const int frag = 128 * (r16 & 7) + 1024 * (r16 >> 3);
+  const int cA[2] = {16 * ((2 * g) ^ (r16 >> 1)), 16 * ((2 * g + 1) ^ (r16 >> 1))};
+  for (int kb = kt0; kb < kend; kb += 2) {
+    static_for<0, 2>([&](auto U_) {
+      constexpr int u = decltype(U_)::value;
+      const int kt = kb + u;
+      // stage u (written during the previous step) is visible; stage u ^ 1, read
+      // in the previous step, is free for step kt + 1
+      __syncthreads();
+      writeA(u ^ 1);
+      loadA(min(kt + 2, kend - 1));
+      float sv[TJ][2], zv[TJ][2];  // 16 s and z of fragment j, half h
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          sv[j][h] = 16.f * bf16_to_f32(sq[u][j][h] & 0xFFFFu);
+          zv[j][h] = bf16_to_f32(sq[u][j][h] >> 16);
+        }
+      // The step's MFMAs as 4 TJ groups g = (substep s = g / TJ, fragment j =
+      // g % TJ), each RA MFMAs on one dequantised weight fragment. The wave
+      // issues in order and the matrix core runs an MFMA for 16 cycles, so the
+      // next group's dequantisation (and, before a new substep, its A
+      // fragments) is spread between this group's MFMAs, a few VALU
+      // instructions after each, where it runs under them.
+      const uint8_t* st = smem + u * STAGE + frag;
+      constexpr int NG = 4 * TJ;
+      i32x4v a[2][RA];
+      auto readA = [&](int sub, int i, i32x4v& dst) {
+        dst = *reinterpret_cast<const i32x4v*>(st + (sub >> 1) * HALF + 2 * i * 1024 + cA[sub & 1]);
+      };
+      auto start = [&](DqPieces& d, int sub, int j) {
+        d.w = (uint32_t)bq[u][j][sub];
+        d.s16 = sv[j][sub >> 1];
+        d.z = zv[j][sub >> 1];
+      };
+#pragma unroll
+      for (int i = 0; i < RA; ++i) readA(0, i, a[0][i]);
+      DqPieces d0;
+      start(d0, 0, 0);
+      static_for<0, 7>([&](auto P_) { d0.template piece<decltype(P_)::value>(); });
+      u32x4 bcur = d0.r;
+      static_for<0, NG>([&](auto G_) {
+        constexpr int gg = decltype(G_)::value, sub = gg / TJ, j = gg % TJ;
+        constexpr int gn = gg + 1, subn = gn / TJ, jn = gn % TJ;
+        constexpr bool more = gn < NG;
+        DqPieces d;
+        if constexpr (more) start(d, subn, jn);
+        static_for<0, RA>([&](auto I_) {
+          constexpr int i = decltype(I_)::value;
+          // the step's first operands were written just above; every later
+          // group's were finished three MFMAs before its first one
+          mfma_bf16_acc<gg == 0 && i == 0>(acc[i][j], bcur, a[sub & 1][i]);
+          if constexpr (more) {
+            if constexpr (i < 6) d.template piece<i>();
+            if constexpr (i == 5) d.template piece<6>();
+            if constexpr (jn == 0) readA(subn, i, a[subn & 1][i]);
+          }
+          __builtin_amdgcn_sched_barrier(0);  // keep this placement: the scheduler would cluster the VALU
+        });
+        if constexpr (more) bcur = d.r;
+      });
+      loadB(min(kt + 2, kend - 1), U_);
+    });
+  }
+  W4_NOPS();
+  W4_PIN();
+#undef W4_PIN
+#undef W4_NOPS
+}
+
+// y = bf16(acc) for one BM x 4 CW tile in the transposed accumulator layout
+// (lane 16 g + r of fragment (i, j): token m0 + 16 i + r, columns n0 + wave CW +
+// 16 j + 4 g .. + 3), 8-byte row pieces.
+template <int BM, int CW>
+__device__ __forceinline__ void w4pk_store(const f32x4 (&acc)[BM / 16][CW / 16], bf16_t* __restrict__ y,
+                                           int64_t ldy, int M, int m0, int n0) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < CW / 16; ++j) {
+    const int col = n0 + wave * CW + 16 * j + 4 * g;
+#pragma unroll
+    for (int i = 0; i < BM / 16; ++i) {
+      const int m = m0 + 16 * i + r16;
+      if (m < M)
+        *reinterpret_cast<u32x2*>(y + (int64_t)m * ldy + col) =
+            pack4_bf16(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+    }
+  }
+}
+
+// Plain y = bf16(x . W^T) with k split `splits` ways (pairs of k steps dealt
+// evenly). splits == 1 stores y; otherwise each split stores its fp32 partial
+// tile in accumulator order (f32x4 (i, j) of thread t at ((tile splits + split)
+// RA TJ + i TJ + j) 256 + t) and w4pk_reduce_kernel adds them.
+// SWIGLU: the weight is [gate (half rows); up (half rows)]; wave w takes gate
+// channels [w CW/2, (w + 1) CW/2) of the tile's BN/2 and the matching up
+// channels as fragments j = 2 t (gate) and 2 t + 1 (up), and stores
+// h = bf16(bf16(silu(g)) * u) into y (M, half) with g, u = bf16(acc).
+template <int BM, int CW, bool SWIGLU>
+__global__ __launch_bounds__(kThreads, 1) void gemm_w4a16_pk_kernel(
+    const bf16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ wp, const uint32_t* __restrict__ sz,
+    int gshift, bf16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int tiles_m, int tiles_n, int splits,
+    f32x4* __restrict__ part) {
+  constexpr int RA = BM / 16, TJ = CW / 16, BN = 4 * CW, CH = BN / 2, WCH = CW / 2;
+  constexpr int SMEM = 2 * BM * 256;
+  static_assert(SMEM <= 160 * 1024, "LDS budget");
+  static_assert(!SWIGLU || TJ % 2 == 0, "gate/up fragment pairs");
+  __shared__ __align__(1024) uint8_t smem[SMEM];
+
+  const int nblk = tiles_m * tiles_n * splits;
+  const int b = blockIdx.x;
+  int logical = b;
+  if (nblk % kXcds == 0) logical = (b % kXcds) * (nblk / kXcds) + b / kXcds;  // one XCD walks a tile range
+  const int tm = logical % tiles_m, rest = logical / tiles_m;                 // M fastest: L2 shares weights
+  const int split = rest % splits, tn = rest / splits;
+  const int m0 = tm * BM;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int KT = K / kPkStep, kp = KT / 2;
+  const int p0 = (int)((int64_t)kp * split / splits), p1 = (int)((int64_t)kp * (split + 1) / splits);
+  const int half = N / 2;
+
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  uint32_t sB[TJ], colS[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int row = SWIGLU ? (j & 1 ? half : 0) + tn * CH + wave_s * WCH + 16 * (j >> 1)
+                           : tn * BN + wave_s * CW + 16 * j;
+    sB[j] = (uint32_t)(row / 16) * (uint32_t)KT * 1024u;
+    colS[j] = (uint32_t)(row + r16);
+  }
+  f32x4 acc[RA][TJ];
+  w4pk_mainloop<BM, CW>(acc, smem, x, ldx, M, m0, wp, (uint32_t)((int64_t)N * K / 2), sB, sz,
+                        (uint32_t)((int64_t)(K >> gshift) * N * 4), colS, N, gshift, 2 * p0, 2 * (p1 - p0));
+
+  if constexpr (SWIGLU) {
+    const int c_base = tn * CH + wave * WCH + 4 * g;
+#pragma unroll
+    for (int i = 0; i < RA; ++i) {
+      const int m = m0 + 16 * i + r16;
+#pragma unroll
+      for (int t = 0; t < TJ / 2; ++t) {
+        float hv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float gv = round_bf16(acc[i][2 * t][r]);
+          const float uv = round_bf16(acc[i][2 * t + 1][r]);
+          hv[r] = round_bf16(round_bf16(silu(gv)) * uv);
+        }
+        if (m < M)
+          *reinterpret_cast<u32x2*>(y + (int64_t)m * ldy + c_base + 16 * t) = pack4_bf16(hv[0], hv[1], hv[2], hv[3]);
+      }
+    }
+  } else {
+    if (splits > 1) {
+      f32x4* mine = part + ((int64_t)(tn * tiles_m + tm) * splits + split) * (RA * TJ * kThreads) + tid;
+#pragma unroll
+      for (int i = 0; i < RA; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) mine[(i * TJ + j) * kThreads] = acc[i][j];
+    } else {
+      w4pk_store<BM, CW>(acc, y, ldy, M, m0, tn * BN);
+    }
+  }
+}
+
+// y for the tiles of a split launch, one workgroup per (tile, 16-row group i):
+// the partials of each accumulator added in split order 0, 1, .. (whatever
+// order the splits finished in), then rounded to bf16.
+template <int BM, int CW>
+__global__ __launch_bounds__(kThreads) void w4pk_reduce_kernel(const f32x4* __restrict__ part, int splits,
+                                                               bf16_t* __restrict__ y, int64_t ldy, int M,
+                                                               int tiles_m) {
+  constexpr int RA = BM / 16, TJ = CW / 16, BN = 4 * CW;
+  const int tile = blockIdx.x / RA, i = blockIdx.x % RA;
+  const int tm = tile % tiles_m, tn = tile / tiles_m;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const f32x4* tp = part + (int64_t)tile * splits * (RA * TJ * kThreads) + i * TJ * kThreads + tid;
+  f32x4 t[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) t[j] = tp[j * kThreads];
+  for (int s2 = 1; s2 < splits; ++s2)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) t[j] = t[j] + tp[((int64_t)s2 * RA * TJ + j) * kThreads];
+  const int m = tm * BM + 16 * i + r16;
+  if (m >= M) return;
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int col = tn * BN + wave * CW + 16 * j + 4 * g;
+    *reinterpret_cast<u32x2*>(y + (int64_t)m * ldy + col) = pack4_bf16(t[j][0], t[j][1], t[j][2], t[j][3]);
+  }
+}
+
+// Plans of the packed path. Plain: 144 x 384 tiles (CW 96) when they fill the
+// GPU unsplit; otherwise 144 x 256 tiles (CW 64) with k split until about one
+// workgroup per CU (at most 8 ways, at least one pair of k steps each). SwiGLU:
+// 144 x (192 gate + 192 up) tiles when the channels divide, else 144 x (128 +
+// 128). Shapes outside the packed path's limits are reported as not fitting.
+constexpr int kW4BM = 144;
+
+struct W4PkPlan {
+  int cw = 0;      // 0: the packed path does not take this shape
+  int splits = 1;
+};
+
+bool w4pk_common_fits(int64_t m, int64_t k, int64_t group) {
+  return m > 4 && k % (2 * kPkStep) == 0 && group >= 32 && (group & (group - 1)) == 0 && k % group == 0 &&
+         m < (1 << 24) && k < (1 << 24);
+}
+
+int w4_gshift(int64_t group) {
+  int s = 0;
+  while ((int64_t(1) << s) < group) ++s;
+  return s;
+}
+
+W4PkPlan w4pk_plan(int64_t m, int64_t n, int64_t k, int64_t group) {
+  W4PkPlan p;
+  if (!w4pk_common_fits(m, k, group) || n % 16 || n * k / 2 >= (int64_t(1) << 31) ||
+      (k / group) * n * 4 >= (int64_t(1) << 31) || m * k * 2 >= (int64_t(1) << 31))
+    return p;
+  const int64_t tm = (m + kW4BM - 1) / kW4BM;
+  if (n % 384 == 0 && tm * (n / 384) >= 192) {
+    p.cw = 96;
+    return p;
+  }
+  if (n % 256) return p;
+  const int64_t tiles = tm * (n / 256), pairs = k / (2 * kPkStep);
+  int64_t s = 1;
+  if (const int f = ff_tuning(FF_TUNE_W4A16_SPLITS)) s = f;
+  else if (tiles < 192) s = 256 / tiles;
+  p.cw = 64;
+  p.splits = (int)std::max<int64_t>(1, std::min<int64_t>({s, 8, pairs}));
+  return p;
+}
+
+int w4pk_swiglu_cw(int64_t m, int64_t i, int64_t k, int64_t group) {
+  if (!w4pk_common_fits(m, k, group) || 2 * i * k / 2 >= (int64_t(1) << 31) ||
+      (k / group) * 2 * i * 4 >= (int64_t(1) << 31) || m * k * 2 >= (int64_t(1) << 31))
+    return 0;
+  if (i % 192 == 0) return 96;
+  if (i % 128 == 0) return 64;
+  return 0;
+}
+
+int64_t w4pk_workspace(int64_t m, int64_t n, int64_t k, int64_t group) {
+  const W4PkPlan p = w4pk_plan(m, n, k, group);
+  if (p.cw == 0 || p.splits <= 1) return 0;
+  return (m + kW4BM - 1) / kW4BM * (n / (4 * p.cw)) * p.splits * kW4BM * 4 * p.cw * 4;
+}
+
+template <int CW, bool SWIGLU>
+void launch_w4pk(const void* x, int64_t ldx, const void* frag, const void* scales, int gshift, void* y, int64_t ldy,
+                 int m, int n, int k, int splits, void* ws, hipStream_t s) {
+  const int tiles_m = (m + kW4BM - 1) / kW4BM;
+  const int tiles_n = n / (4 * CW);  // SWIGLU: n = 2 half rows, 2 CW channels of each half per tile
+  hipLaunchKernelGGL((gemm_w4a16_pk_kernel<kW4BM, CW, SWIGLU>), dim3((unsigned)(tiles_m * tiles_n * splits)),
+                     dim3(kThreads), 0, s, (const bf16_t*)x, ldx, (const uint8_t*)frag, (const uint32_t*)scales,
+                     gshift, (bf16_t*)y, ldy, m, n, k, tiles_m, tiles_n, splits, (f32x4*)ws);
+  if (!SWIGLU && splits > 1)
+    hipLaunchKernelGGL((w4pk_reduce_kernel<kW4BM, CW>), dim3((unsigned)(tiles_m * tiles_n * (kW4BM / 16))),
+                       dim3(kThreads), 0, s, (const f32x4*)ws, splits, (bf16_t*)y, ldy, m, tiles_m);
+}
+
+}  // namespace
+
+extern "C" int ff_pack_weight_int4(const void* packed, void* frag, int64_t n, int64_t k, ff_stream_t stream) {
+  FF_REQUIRE(packed && frag, "ff_pack_weight_int4: null pointer");
+  FF_REQUIRE(n > 0 && n % 16 == 0 && k > 0 && k % kPkStep == 0 && n * k < (int64_t(1) << 40),
+             "ff_pack_weight_int4: bad sizes (n %% 16, k %% 128)");
+  FF_REQUIRE(ff_aligned(packed, 8) && ff_aligned(frag, 16), "ff_pack_weight_int4: alignment");
+  const int64_t lanes = (n / 16) * (k / kPkStep) * 64;
+  const int64_t blocks = (lanes + kThreads - 1) / kThreads;
+  hipLaunchKernelGGL(pack_int4_kernel, dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const uint8_t*)packed, (uint8_t*)frag, n, k);
+  FF_LAUNCH_CHECK("ff_pack_weight_int4");
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_w4a16_pk_workspace(int64_t m, int64_t n, int64_t k, int64_t group, int64_t* bytes) {
+  FF_REQUIRE(bytes && m >= 0 && n > 0 && k > 0 && group > 0, "ff_gemm_w4a16_pk_workspace: bad arguments");
+  int64_t other = 0;
+  ff_gemm_w4a16_workspace(m, n, k, &other);
+  *bytes = std::max(w4pk_workspace(m, n, k, group), other);
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_w4a16_pk(const void* x, int64_t ldx, const void* packed, const void* frag, const void* scales,
+                                int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, void* workspace,
+                                int64_t workspace_bytes, ff_stream_t stream) {
+  const W4PkPlan p = frag ? w4pk_plan(m, n, k, group) : W4PkPlan{};
+  if (p.cw == 0 || ldx % 8 || ldy % 8 || ldx < k || ldy < n || m * ldx * 2 >= (int64_t(1) << 31) ||
+      !ff_aligned(x, 16) || !ff_aligned(frag, 16) || !ff_aligned(scales, 4) || !ff_aligned(y, 8))
+    return gemm_w4a16(x, ldx, packed, scales, group, y, ldy, m, n, k, workspace, workspace_bytes, stream);
+  const int64_t need = w4pk_workspace(m, n, k, group);
+  FF_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && ff_aligned(workspace, 16)),
+             "ff_gemm_w4a16_pk: workspace of %lld bytes (16-byte aligned) required", (long long)need);
+  const hipStream_t s = (hipStream_t)stream;
+  const int gs = w4_gshift(group);
+  if (p.cw == 96)
+    launch_w4pk<96, false>(x, ldx, frag, scales, gs, y, ldy, (int)m, (int)n, (int)k, 1, nullptr, s);
+  else
+    launch_w4pk<64, false>(x, ldx, frag, scales, gs, y, ldy, (int)m, (int)n, (int)k, p.splits, workspace, s);
+  FF_LAUNCH_CHECK("ff_gemm_w4a16_pk");
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_w4a16_swiglu_fits(int64_t m, int64_t i, int64_t k, int64_t group, int* fits) {
+  FF_REQUIRE(fits, "ff_gemm_w4a16_swiglu_fits: null pointer");
+  *fits = w4pk_swiglu_cw(m, i, k, group) != 0;
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_w4a16_swiglu_pk(const void* x, int64_t ldx, const void* frag, const void* scales,
+                                       int64_t group, void* h, int64_t ldh, int64_t m, int64_t i, int64_t k,
+                                       ff_stream_t stream) {
+  FF_REQUIRE(x && frag && scales && h, "ff_gemm_w4a16_swiglu_pk: null pointer");
+  const int cw = w4pk_swiglu_cw(m, i, k, group);
+  FF_REQUIRE(cw != 0, "ff_gemm_w4a16_swiglu_pk: m=%lld i=%lld k=%lld group=%lld is outside the fused kernel's "
+             "shapes (m > 4, i %% 128, k %% 256, group a power of two >= 32 dividing k)",
+             (long long)m, (long long)i, (long long)k, (long long)group);
+  FF_REQUIRE(ldx % 8 == 0 && ldx >= k && ldh % 4 == 0 && ldh >= i && m * ldx * 2 < (int64_t(1) << 31),
+             "ff_gemm_w4a16_swiglu_pk: bad strides");
+  FF_REQUIRE(ff_aligned(x, 16) && ff_aligned(frag, 16) && ff_aligned(scales, 4) && ff_aligned(h, 8),
+             "ff_gemm_w4a16_swiglu_pk: alignment (x, frag 16 bytes; h 8)");
+  const hipStream_t s = (hipStream_t)stream;
+  const int gs = w4_gshift(group);
+  if (cw == 96)
+    launch_w4pk<96, true>(x, ldx, frag, scales, gs, h, ldh, (int)m, (int)(2 * i), (int)k, 1, nullptr, s);
+  else
+    launch_w4pk<64, true>(x, ldx, frag, scales, gs, h, ldh, (int)m, (int)(2 * i), (int)k, 1, nullptr, s);
+  FF_LAUNCH_CHECK("ff_gemm_w4a16_swiglu_pk");
+  return FF_OK;
 }
 
 // ------------------------------------------------------------------ allocation-free variant

@@ -202,6 +202,16 @@ class Int4:
         self.scales = torch.empty((k // group, n, 2), device=w.device, dtype=BF16)
         call("ff_quant_weight_int4", ptr(w), ptr(self.packed), ptr(self.scales), n, k, group,
              1 if symmetric else 0, stream())
+        self.frag = None
+
+    def pack(self):
+        """Add the MFMA-fragment copy of the nibbles (ff_pack_weight_int4) that the
+        packed kernels read; ``packed`` stays for the shapes they do not take."""
+        n, k = self.weight.shape
+        if self.frag is None and n % 16 == 0 and k % 128 == 0:
+            self.frag = torch.empty_like(self.packed)
+            call("ff_pack_weight_int4", ptr(self.packed), ptr(self.frag), n, k, stream())
+        return self
 
     def __call__(self, x, out=None):
         flat = _rows(x)
@@ -211,8 +221,41 @@ class Int4:
         n = self.weight.shape[0]
         y = torch.empty((m, n), device=x.device, dtype=BF16) if out is None else out
         need = ctypes.c_int64(0)
+        if self.frag is not None:
+            call("ff_gemm_w4a16_pk_workspace", m, n, k, self.group, ctypes.byref(need))
+            ws = torch.empty(need.value, device=x.device, dtype=torch.uint8) if need.value else None
+            call("ff_gemm_w4a16_pk", ptr(flat), flat.stride(0), ptr(self.packed), ptr(self.frag), ptr(self.scales),
+                 self.group, ptr(y), y.stride(0), m, n, k, ptr(ws), need.value, stream())
+            return y
         call("ff_gemm_w4a16_workspace", m, n, k, ctypes.byref(need))
         ws = torch.empty(need.value, device=x.device, dtype=torch.uint8) if need.value else None
         call("ff_gemm_w4a16_ws", ptr(flat), flat.stride(0), ptr(self.packed), ptr(self.scales), self.group,
              ptr(y), y.stride(0), m, n, k, ptr(ws), need.value, stream())
         return y
+
+    def swiglu_fits(self, m):
+        """Whether ``swiglu`` runs the fused kernel for ``m`` rows."""
+        if self.frag is None:
+            return False
+        n, k = self.weight.shape
+        ok = ctypes.c_int(0)
+        call("ff_gemm_w4a16_swiglu_fits", m, n // 2, k, self.group, ctypes.byref(ok))
+        return bool(ok.value)
+
+    def swiglu(self, x):
+        """swiglu(g, u) for [g, u] = self(x).chunk(2, -1) (gate rows first): one
+        fused launch where the packed kernel takes the shape (ff_gemm_w4a16_swiglu_pk,
+        the same bits), else the GEMM and ``ops.swiglu``."""
+        flat = _rows(x)
+        if flat.stride(-1) != 1 or flat.stride(0) % 8:
+            flat = flat.contiguous()
+        m, k = flat.shape
+        i = self.weight.shape[0] // 2
+        if not self.swiglu_fits(m):
+            from . import ops
+            g, u = self(x).chunk(2, -1)
+            return ops.swiglu(g, u)
+        h = torch.empty((m, i), device=x.device, dtype=BF16)
+        call("ff_gemm_w4a16_swiglu_pk", ptr(flat), flat.stride(0), ptr(self.frag), ptr(self.scales), self.group,
+             ptr(h), i, m, i, k, stream())
+        return h.reshape(*x.shape[:-1], i)

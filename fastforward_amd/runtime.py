@@ -25,7 +25,7 @@ import torch
 
 from . import ops
 from ._lib import call, ptr, stream
-from .linear import FP8Linear, Linear, StaticFP8Linear, gemm_pk_workspace
+from .linear import FP8Linear, Int4, Linear, StaticFP8Linear, gemm_pk_workspace
 
 BF16 = torch.bfloat16
 E4M3 = torch.float8_e4m3fn
@@ -229,6 +229,11 @@ class Runtime:
                 L.o.pack()
                 L.gateup.pack()
                 L.down.pack()
+        else:
+            for L in weights.layers:  # fragment copies of the int4 weights for the packed W4A16 kernels
+                for op in (L.qkv, L.o, L.gateup, L.down):
+                    if isinstance(op, Int4):
+                        op.pack()
         T, H, D = tokens, cfg.hidden, cfg.head_dim
         e = lambda *s, dt=BF16: torch.empty(s, device=dev, dtype=dt)  # noqa: E731
         # activations: aliased into the shared arena when one is given
@@ -459,8 +464,7 @@ class Runtime:
             lw = L[j]
             attn = self._attention_generic(lw, normalized, cos, sin)
             residual, post = ops.add_rms(h, attn, None, lw.post_norm)
-            g, u = Linear.apply(post, lw.gateup).chunk(2, -1)
-            value = Linear.apply(ops.swiglu(g, u), lw.down)
+            value = Linear.apply(self._swiglu(post, lw.gateup), lw.down)
             deep = self.deep[j] if j < len(self.deep) else None
             h, normalized = ops.add_rms(residual, value, deep, L[j + 1].input_norm, self.image_start,
                                         self.nv if deep is not None else 0)
@@ -477,13 +481,22 @@ class Runtime:
         value = Linear.apply(out.reshape(1, 1, -1), lw.o)
         hp = self._index_rows(h[0], self.pick, dim1=True)           # h.index_select(1, pick)
         residual, post = ops.add_rms(hp, value, None, lw.post_norm)
-        g, u = Linear.apply(post[0], lw.gateup).chunk(2, -1)
-        mlp = Linear.apply(ops.swiglu(g, u), lw.down)
+        mlp = Linear.apply(self._swiglu(post[0], lw.gateup), lw.down)
         y = torch.empty((1, w.head.shape[0]), device=self.dev, dtype=torch.float32)
         call("ff_lm_readout", ptr(residual), ptr(mlp), ptr(w.norm.weight), ptr(w.head), ptr(y), cfg.hidden,
              w.head.shape[0], float(w.norm.variance_epsilon), stream())
         self.logits.copy_(y[0])
         return self.logits
+
+    @staticmethod
+    def _swiglu(x, op):
+        """swiglu(g, u) for [g, u] = Linear.apply(x, op).chunk(2, -1)
+        (scaled_qwen_runtime.py:174-176): one fused launch for a packed Int4
+        gate/up whose shape the kernel takes (the same bits), else the two ops."""
+        if isinstance(op, Int4) and op.swiglu_fits(x.numel() // x.shape[-1]):
+            return op.swiglu(x)
+        g, u = Linear.apply(x, op).chunk(2, -1)
+        return ops.swiglu(g, u)
 
     def _attention_generic(self, lw, x, cos, sin):
         cfg = self.cfg

@@ -289,6 +289,43 @@ int ff_gemm_w4a16_noalloc(const void* x, int64_t ldx, const void* packed, const 
                           int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
                           ff_stream_t stream);
 
+/* Setup-time copy of an int4 weight in MFMA fragment order for the packed
+ * kernels below (no reference counterpart: the reference repacks its Int4
+ * weights once for its library kernel, _family/night_runtime.py:27). packed
+ * (n, k/2) in the ff_quant_weight_int4 layout; frag receives n * k / 2 bytes:
+ * the 16 rows x 128 k of fragment (f, kt) at (f k/128 + kt) * 1024, lane
+ * l = 16 g + r holding row 16 f + r, the bytes of k = 128 kt + 64 h + 16 g +
+ * [0, 16) for h = 0, 1 at 16 l, each nibble q stored as q ^ 8. n % 16 == 0,
+ * k % 128 == 0. */
+int ff_pack_weight_int4(const void* packed, void* frag, int64_t n, int64_t k, ff_stream_t stream);
+
+/* ff_gemm_w4a16_ws with the fragment copy (ff_pack_weight_int4 of packed): the
+ * weights are read from frag straight into registers (Int4.__call__,
+ * _family/night_runtime.py:31-42). The same dequantised values and, unsplit,
+ * the same bits as ff_gemm_w4a16; where it splits K (grids that would leave
+ * CUs idle) the fp32 partials go to the workspace and a second launch adds them
+ * in split order. Shapes the packed kernel does not take (m <= 4, k % 256,
+ * group not a power of two >= 32, n % 256 unless the 144 x 384 tiles fill the
+ * GPU) and a null frag run ff_gemm_w4a16_ws. ff_gemm_w4a16_pk_workspace stores
+ * the bytes either path wants; workspace 16-byte aligned; calls that overlap
+ * must not share it. */
+int ff_gemm_w4a16_pk_workspace(int64_t m, int64_t n, int64_t k, int64_t group, int64_t* bytes);
+int ff_gemm_w4a16_pk(const void* x, int64_t ldx, const void* packed, const void* frag, const void* scales,
+                     int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, void* workspace,
+                     int64_t workspace_bytes, ff_stream_t stream);
+
+/* Gate/up W4A16 GEMM with SwiGLU in its epilogue: h (m, i) = bf16(bf16(silu(g))
+ * * u) with g, u = bf16 of x @ dequant(W)^T for W = [gate (i rows); up (i rows)]
+ * (frag: ff_pack_weight_int4 of the (2 i, k) weight; scales [k/group, 2 i, 2]).
+ * No reference counterpart as one op: Int4.__call__ (_family/night_runtime.py:
+ * 31-42) then swiglu (_legacy/search_kernels.py:8-23), the same bits.
+ * ff_gemm_w4a16_swiglu_fits (no GPU needed) reports whether the kernel takes
+ * the shape (m > 4, i % 128, k % 256, group a power of two >= 32 dividing k);
+ * other shapes are rejected with FF_EINVAL. h row stride ldh (multiple of 4). */
+int ff_gemm_w4a16_swiglu_fits(int64_t m, int64_t i, int64_t k, int64_t group, int* fits);
+int ff_gemm_w4a16_swiglu_pk(const void* x, int64_t ldx, const void* frag, const void* scales, int64_t group,
+                            void* h, int64_t ldh, int64_t m, int64_t i, int64_t k, ff_stream_t stream);
+
 /* Embedding gather h[t] = table[ids[t]] (scaled_qwen_runtime.py:145
  * embed_tokens). Ids outside [0, vocab) read row 0 (the host validates ids). */
 int ff_embed(const int64_t* ids, const void* table, void* out, int64_t t, int64_t h,

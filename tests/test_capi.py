@@ -70,3 +70,22 @@ def test_tuning_knobs_validate_without_a_gpu(lib_path):
     text = "".join(open(os.path.join(ROOT, "fastforward_amd", "csrc", f)).read()
                    for f in os.listdir(os.path.join(ROOT, "fastforward_amd", "csrc")))
     assert "getenv" not in text
+
+
+def test_w4a16_swiglu_shape_query_without_a_gpu(lib_path):
+    """ff_gemm_w4a16_swiglu_fits answers on the host: m > 4, i % 128, k % 256 and a
+    power-of-two group >= 32 dividing k."""
+    import ctypes
+    from fastforward_amd import _lib
+    _lib.load()
+
+    def fits(m, i, k, group):
+        ok = ctypes.c_int(-1)
+        _lib.call("ff_gemm_w4a16_swiglu_fits", m, i, k, group, ctypes.byref(ok))
+        return ok.value
+
+    assert fits(576, 12288, 4096, 128) == 1 and fits(320, 6144, 2048, 32) == 1 and fits(100, 640, 1024, 64) == 1
+    assert fits(4, 12288, 4096, 128) == 0          # the tail's rows take the GEMV-sized path
+    assert fits(576, 12288 + 64, 4096, 128) == 0   # i % 128
+    assert fits(576, 12288, 4096 + 128, 128) == 0  # k % 256
+    assert fits(576, 12288, 4096, 96) == 0         # group not a power of two

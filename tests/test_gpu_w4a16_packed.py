@@ -1,0 +1,137 @@
+"""The W4A16 kernels on fragment-packed int4 weights (ff_pack_weight_int4,
+ff_gemm_w4a16_pk, ff_gemm_w4a16_swiglu_pk) against the LDS-staged kernel and
+the oracle's exact dequantisation (Int4, _family/night_runtime.py:15-42).
+
+Bars: where neither kernel splits k, the packed kernel runs the same MFMAs on
+the same dequantised values in the same k order, so the bits are equal; with a
+k split only the fp32 order of adding the partials differs (|difference| <= 1
+bf16 ulp + 2^-21 sum |x w|, under 1% of outputs differing). Every shape is also held to the fp64 product
+with the exactly dequantised weight (relative RMS <= 5e-3, worst element <=
+0.05 of the output RMS), as the LDS-staged kernel's tests are."""
+import pytest
+import torch
+
+import oracle.ops as O
+from helpers import bf16_ulps
+
+pytestmark = pytest.mark.gpu
+
+BF16 = torch.bfloat16
+DEV = "cuda"
+
+FF_TUNE_W4A16_SPLITS = 4
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+@pytest.fixture
+def tuning(gpu):
+    from fastforward_amd._lib import call
+    used = []
+
+    def set_(knob, value):
+        used.append(knob)
+        call("ff_set_tuning", knob, value)
+    yield set_
+    for knob in used:
+        call("ff_set_tuning", knob, 0)
+
+
+def _unsplit_lds(op, x, tuning):
+    """The LDS-staged kernel (ff_gemm_w4a16_ws) with k unsplit."""
+    frag, op.frag = op.frag, None
+    tuning(FF_TUNE_W4A16_SPLITS, 1)
+    try:
+        return op(x)
+    finally:
+        op.frag = frag
+        tuning(FF_TUNE_W4A16_SPLITS, 0)
+
+
+def _pk_splits(m, n, k):
+    """Splits the packed plan takes (mirrors w4pk_plan for the tested shapes)."""
+    tm = (m + 143) // 144
+    if n % 384 == 0 and tm * (n // 384) >= 192:
+        return 1
+    tiles = tm * (n // 256)
+    s = 1 if tiles >= 192 else 256 // tiles
+    return max(1, min(s, 8, k // 256))
+
+
+SHAPES = [(576, 4096, 24576), (576, 4096, 6144), (576, 12288, 4096), (576, 4096, 4096), (320, 2048, 6144),
+          (100, 1024, 512), (1, 12288, 4096)]
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES)
+@pytest.mark.parametrize("sym,group", [(True, 128), (False, 32)])
+def test_w4a16_packed_vs_lds_kernel_and_exact(gpu, tuning, m, k, n, sym, group):
+    from fastforward_amd.linear import Int4
+    x = torch.randn(m, k, generator=_g(70)).to(BF16)
+    w = (torch.randn(n, k, generator=_g(71)) * 0.02).to(BF16)
+    op = Int4(w.to(DEV), group=group, symmetric=sym).pack()
+    xd = x.to(DEV)
+    outs = [op(xd) for _ in range(3)]
+    assert all(torch.equal(outs[0], o) for o in outs[1:])
+    dq = O.int4_dequant(op.packed.cpu(), op.scales.cpu(), group).double()
+    if m <= 4:  # the packed entry hands these rows to the LDS-staged kernel as it is
+        frag, op.frag = op.frag, None
+        assert torch.equal(outs[0], op(xd))
+        op.frag = frag
+        ref = None
+    else:
+        ref = _unsplit_lds(op, xd, tuning)
+    if ref is None:
+        pass
+    elif _pk_splits(m, n, k) == 1:
+        assert torch.equal(outs[0], ref), (m, k, n)
+    else:
+        # adding the splits' partials reassociates the fp32 sum: an absolute
+        # error of a few fp32 ulps of sum |x w|, plus each side's bf16 rounding
+        got, want = outs[0].cpu().double(), ref.cpu().double()
+        mag = torch.maximum(got.abs(), want.abs()).clamp_min(2.0 ** -126)
+        ulp = torch.exp2(torch.floor(torch.log2(mag)) - 7)
+        scale = x.double().abs() @ dq.abs().T
+        assert bool(((got - want).abs() <= ulp + 2.0 ** -21 * scale).all())
+        assert float((bf16_ulps(outs[0], ref) > 0).float().mean()) < 0.01
+    y = outs[0].cpu().double()
+    exact = x.double() @ dq.T
+    rms = exact.pow(2).mean().sqrt()
+    assert float((y - exact).pow(2).mean().sqrt() / rms) <= 5e-3
+    assert float((y - exact).abs().max() / rms) <= 0.05
+
+
+@pytest.mark.parametrize("n,k", [(256, 256), (256, 512)])
+def test_w4a16_packed_dequant_bit_exact_via_one_hot(gpu, n, k):
+    """x = rows of the identity, so y[r, c] = bf16((q-8)*s + z) for k = r exactly,
+    unsplit (k 256) and split in two (k 512; each output has one nonzero
+    product, so adding the partials is exact). Columns 0-39 hold 64.0 in their
+    first 32 k: the asymmetric quantizer stores s = bf16(1e-6), z = 64 there,
+    where z - 8s is not exact in fp32 (the case the LDS-staged kernel routes to
+    its exact form; the packed kernel's v_cvt_off form is exact throughout)."""
+    from fastforward_amd.linear import Int4
+    w = (torch.randn(n, k, generator=_g(72)) * 0.02).to(BF16)
+    w[:40, :32] = 64.0
+    for sym, group in ((True, 128), (False, 32)):
+        op = Int4(w.to(DEV), group=group, symmetric=sym).pack()
+        y = op(torch.eye(k, dtype=BF16, device=DEV)).cpu()
+        dq = O.int4_dequant(op.packed.cpu(), op.scales.cpu(), group).to(BF16)
+        assert torch.equal(y, dq.T.contiguous()), (sym, group)
+
+
+@pytest.mark.parametrize("m,k,i", [(576, 4096, 12288), (320, 2048, 6144), (100, 1024, 640)])
+@pytest.mark.parametrize("sym,group", [(True, 128), (False, 32)])
+def test_w4a16_swiglu_packed_equals_unfused(gpu, tuning, m, k, i, sym, group):
+    """ff_gemm_w4a16_swiglu_pk == ops.swiglu of the unsplit gate/up product, bit
+    for bit (144 x 384 and 144 x 256 tiles; ragged m)."""
+    from fastforward_amd import ops
+    from fastforward_amd.linear import Int4
+    x = torch.randn(m, k, generator=_g(73)).to(BF16).to(DEV)
+    w = (torch.randn(2 * i, k, generator=_g(74)) * 0.02).to(BF16)
+    op = Int4(w.to(DEV), group=group, symmetric=sym).pack()
+    assert op.swiglu_fits(m)
+    h = op.swiglu(x)
+    g, u = _unsplit_lds(op, x, tuning).chunk(2, -1)
+    assert torch.equal(h, ops.swiglu(g, u))
+    assert torch.equal(h, op.swiglu(x))
