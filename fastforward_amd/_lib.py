@@ -60,6 +60,8 @@ SIGNATURES = {
     "ff_gemm_w4a16_pk": [P, I64, P, P, P, I64, P, I64, I64, I64, I64, P, I64, P],
     "ff_gemm_w4a16_swiglu_fits": [I64, I64, I64, I64, PI32],
     "ff_gemm_w4a16_swiglu_pk": [P, I64, P, P, I64, P, I64, I64, I64, I64, P],
+    "ff_gemm_w4a16_qkv_workspace": [I64, I64, I64, I64, I64, PI64],
+    "ff_gemm_w4a16_qkv": [P, I64, P, P, I64, I64, I64, I64, I64, P, P, F32, F32, P, P, P, P, P, I64, P, I64, P],
     "ff_embed": [P, P, P, I64, I64, I64, P],
     "ff_gather_rows": [P, I64, P, P, I64, I64, I64, I64, P],
     "ff_scatter_rows": [P, P, I64, I64, I64, P],

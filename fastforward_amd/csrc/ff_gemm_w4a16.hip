@@ -47,6 +47,7 @@
 #include <type_traits>
 
 #include "ff_common.h"
+#include "ff_rope.h"
 
 using namespace ff;
 
@@ -758,9 +759,10 @@ __device__ __forceinline__ void w4pk_store(const f32x4 (&acc)[BM / 16][CW / 16],
 }
 
 // Plain y = bf16(x . W^T) with k split `splits` ways (pairs of k steps dealt
-// evenly). splits == 1 stores y; otherwise each split stores its fp32 partial
-// tile in accumulator order (f32x4 (i, j) of thread t at ((tile splits + split)
-// RA TJ + i TJ + j) 256 + t) and w4pk_reduce_kernel adds them.
+// evenly). With part null (then splits == 1) it stores y; otherwise each split
+// stores its fp32 partial tile in accumulator order (f32x4 (i, j) of thread t
+// at ((tile splits + split) RA TJ + i TJ + j) 256 + t) and a reduction kernel
+// (w4pk_reduce_kernel, w4pk_qkv_kernel) adds them.
 // SWIGLU: the weight is [gate (half rows); up (half rows)]; wave w takes gate
 // channels [w CW/2, (w + 1) CW/2) of the tile's BN/2 and the matching up
 // channels as fragments j = 2 t (gate) and 2 t + 1 (up), and stores
@@ -821,7 +823,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_w4a16_pk_kernel(
       }
     }
   } else {
-    if (splits > 1) {
+    if (part != nullptr) {
       f32x4* mine = part + ((int64_t)(tn * tiles_m + tm) * splits + split) * (RA * TJ * kThreads) + tid;
 #pragma unroll
       for (int i = 0; i < RA; ++i)
@@ -926,7 +928,8 @@ void launch_w4pk(const void* x, int64_t ldx, const void* frag, const void* scale
   const int tiles_n = n / (4 * CW);  // SWIGLU: n = 2 half rows, 2 CW channels of each half per tile
   hipLaunchKernelGGL((gemm_w4a16_pk_kernel<kW4BM, CW, SWIGLU>), dim3((unsigned)(tiles_m * tiles_n * splits)),
                      dim3(kThreads), 0, s, (const bf16_t*)x, ldx, (const uint8_t*)frag, (const uint32_t*)scales,
-                     gshift, (bf16_t*)y, ldy, m, n, k, tiles_m, tiles_n, splits, (f32x4*)ws);
+                     gshift, (bf16_t*)y, ldy, m, n, k, tiles_m, tiles_n, splits,
+                     !SWIGLU && splits > 1 ? (f32x4*)ws : nullptr);
   if (!SWIGLU && splits > 1)
     hipLaunchKernelGGL((w4pk_reduce_kernel<kW4BM, CW>), dim3((unsigned)(tiles_m * tiles_n * (kW4BM / 16))),
                        dim3(kThreads), 0, s, (const f32x4*)ws, splits, (bf16_t*)y, ldy, m, tiles_m);
@@ -1000,6 +1003,164 @@ extern "C" int ff_gemm_w4a16_swiglu_pk(const void* x, int64_t ldx, const void* f
   else
     launch_w4pk<64, true>(x, ldx, frag, scales, gs, h, ldh, (int)m, (int)(2 * i), (int)k, 1, nullptr, s);
   FF_LAUNCH_CHECK("ff_gemm_w4a16_swiglu_pk");
+  return FF_OK;
+}
+
+// ------------------------------------------------------------------ fused QKV
+//
+// ff_gemm_w4a16_qkv: the packed GEMM of the QKV weight on 144 x 256 tiles (two
+// heads of 128 per tile), its fp32 partials always going to the workspace, then
+// w4pk_qkv_kernel per (tile, 16-token group): the partials added in split
+// order and rounded to bf16 (the values of ff_gemm_w4a16_pk), staged in LDS,
+// then q/k heads through the per-head RMSNorm + rotary of qk_pair (rope_row_pre,
+// the routine of ff_qkv_post) stored head-major, v heads stored transposed
+// (hk, 128, t_pad) with zeros for tokens >= m.
+
+namespace {
+
+struct W4Qkv {
+  const bf16_t* qn;  // q_norm weight (128)
+  const bf16_t* kn;  // k_norm weight (128)
+  float eps_q, eps_k;
+  const bf16_t* cos;  // (m, 128)
+  const bf16_t* sin;
+  bf16_t* yq;  // (hq, m, 128)
+  bf16_t* yk;  // (hk, m, 128)
+  bf16_t* vt;  // (hk, 128, t_pad)
+  int hq, hk, t_pad;
+};
+
+template <int BM>
+__global__ __launch_bounds__(kThreads) void w4pk_qkv_kernel(const f32x4* __restrict__ part, int splits, int M,
+                                                            int tiles_m, W4Qkv qe) {
+  constexpr int CW = 64, RA = BM / 16, TJ = CW / 16, BN = 4 * CW, LD = BN + 8;
+  __shared__ __align__(16) bf16_t tile[16 * LD];
+  const int t_idx = blockIdx.x / RA, i = blockIdx.x % RA;
+  const int tm = t_idx % tiles_m, tn = t_idx / tiles_m;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int m0 = tm * BM + 16 * i;
+  const f32x4* tp = part + (int64_t)t_idx * splits * (RA * TJ * kThreads) + i * TJ * kThreads + tid;
+  f32x4 t[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) t[j] = tp[j * kThreads];
+  for (int s2 = 1; s2 < splits; ++s2)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) t[j] = t[j] + tp[((int64_t)s2 * RA * TJ + j) * kThreads];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j)
+    *reinterpret_cast<u32x2*>(tile + r16 * LD + wave * CW + 16 * j + 4 * g) =
+        pack4_bf16(t[j][0], t[j][1], t[j][2], t[j][3]);
+  __syncthreads();
+  const int head0 = tn * 2;
+  // q / k rows: 16-lane group grp takes token grp of both heads (as ff_qkv_post)
+  const int grp = tid >> 4, jl = tid & 15;
+#pragma unroll
+  for (int hl = 0; hl < 2; ++hl) {
+    const int head = head0 + hl;
+    if (head >= qe.hq + qe.hk) continue;
+    const bool isq = head < qe.hq;
+    const int m = m0 + grp;
+    const bool valid = m < M;
+    const int mm = valid ? m : M - 1;
+    float wv[8];
+    unpack8(*reinterpret_cast<const u32x4*>((isq ? qe.qn : qe.kn) + 8 * jl), wv);
+    const u32x4 cs = *reinterpret_cast<const u32x4*>(qe.cos + (size_t)mm * kHeadDim + 8 * jl);
+    const u32x4 sn = *reinterpret_cast<const u32x4*>(qe.sin + (size_t)mm * kHeadDim + 8 * jl);
+    bf16_t* dst = (isq ? qe.yq + (size_t)head * M * kHeadDim : qe.yk + (size_t)(head - qe.hq) * M * kHeadDim) +
+                  (size_t)mm * kHeadDim;
+    rope_row_pre(tile + grp * LD + hl * kHeadDim, wv, isq ? qe.eps_q : qe.eps_k, cs, sn, dst, jl, valid);
+  }
+  // v heads: thread (d, token half) writes 8 consecutive tokens of row d
+#pragma unroll
+  for (int hl = 0; hl < 2; ++hl) {
+    const int head = head0 + hl;
+    if (head < qe.hq + qe.hk) continue;
+    const int hv = head - qe.hq - qe.hk;
+    const int d = tid >> 1, t0 = 8 * (tid & 1);
+    const int tok = m0 + t0;
+    if (tok >= qe.t_pad) continue;
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = tok + e < M ? bf16_to_f32(tile[(t0 + e) * LD + hl * kHeadDim + d]) : 0.f;
+    *reinterpret_cast<u32x4*>(qe.vt + ((size_t)hv * kHeadDim + d) * qe.t_pad + tok) = pack8(f);
+  }
+}
+
+// vt[:, :, t0 .. t_pad) = 0 for the tokens no tile covers (t_pad > tiles_m * BM).
+__global__ __launch_bounds__(kThreads) void vt_zero_tail_kernel(bf16_t* __restrict__ vt, int rows, int t_pad,
+                                                                int t0) {
+  const int64_t n = (int64_t)rows * (t_pad - t0);
+  for (int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+    vt[(i / (t_pad - t0)) * t_pad + t0 + i % (t_pad - t0)] = 0;
+}
+
+// Splits of the QKV GEMM: the 144 x 256 tiles of w4pk_plan, k split until
+// about one workgroup per CU.
+int w4pk_qkv_splits(int64_t m, int64_t n, int64_t k) {
+  const int64_t tiles = (m + kW4BM - 1) / kW4BM * (n / 256), pairs = k / (2 * kPkStep);
+  int64_t s = tiles >= 192 ? 1 : 256 / tiles;
+  if (const int f = ff_tuning(FF_TUNE_W4A16_SPLITS)) s = f;
+  return (int)std::max<int64_t>(1, std::min<int64_t>({s, 8, pairs}));
+}
+
+bool w4pk_qkv_fits(int64_t m, int64_t k, int64_t hq, int64_t hk, int64_t group) {
+  const int64_t n = (hq + 2 * hk) * kHeadDim;
+  return w4pk_common_fits(m, k, group) && hq > 0 && hk > 0 && n % 256 == 0 && n * k / 2 < (int64_t(1) << 31) &&
+         (k / group) * n * 4 < (int64_t(1) << 31) && m * k * 2 < (int64_t(1) << 31);
+}
+
+}  // namespace
+
+extern "C" int ff_gemm_w4a16_qkv_workspace(int64_t m, int64_t k, int64_t hq, int64_t hk, int64_t group,
+                                           int64_t* bytes) {
+  FF_REQUIRE(bytes && m >= 0 && k > 0 && hq > 0 && hk > 0 && group > 0, "ff_gemm_w4a16_qkv_workspace: bad arguments");
+  const int64_t n = (hq + 2 * hk) * kHeadDim;
+  *bytes = w4pk_qkv_fits(m, k, hq, hk, group)
+               ? (m + kW4BM - 1) / kW4BM * (n / 256) * w4pk_qkv_splits(m, n, k) * kW4BM * 256 * 4
+               : 0;
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_w4a16_qkv(const void* x, int64_t ldx, const void* frag, const void* scales, int64_t group,
+                                 int64_t m, int64_t k, int64_t hq, int64_t hk, const void* q_norm, const void* k_norm,
+                                 float eps_q, float eps_k, const void* cos, const void* sin, void* yq, void* yk,
+                                 void* vt, int64_t t_pad, void* workspace, int64_t workspace_bytes,
+                                 ff_stream_t stream) {
+  FF_REQUIRE(x && frag && scales && q_norm && k_norm && cos && sin && yq && yk && vt,
+             "ff_gemm_w4a16_qkv: null pointer");
+  FF_REQUIRE(w4pk_qkv_fits(m, k, hq, hk, group),
+             "ff_gemm_w4a16_qkv: m=%lld k=%lld hq=%lld hk=%lld group=%lld outside the kernel's shapes (m > 4, "
+             "k %% 256, 2 (hq + 2 hk) heads per 256 columns, group a power of two >= 32 dividing k)",
+             (long long)m, (long long)k, (long long)hq, (long long)hk, (long long)group);
+  FF_REQUIRE(ldx % 8 == 0 && ldx >= k && m * ldx * 2 < (int64_t(1) << 31) && t_pad >= m && t_pad % 64 == 0 &&
+                 t_pad < (1 << 30),
+             "ff_gemm_w4a16_qkv: bad strides or t_pad");
+  FF_REQUIRE(ff_aligned(x, 16) && ff_aligned(frag, 16) && ff_aligned(scales, 4) && ff_aligned(q_norm, 16) &&
+                 ff_aligned(k_norm, 16) && ff_aligned(cos, 16) && ff_aligned(sin, 16) && ff_aligned(yq, 16) &&
+                 ff_aligned(yk, 16) && ff_aligned(vt, 16),
+             "ff_gemm_w4a16_qkv: operands must be 16-byte aligned");
+  int64_t need = 0;
+  ff_gemm_w4a16_qkv_workspace(m, k, hq, hk, group, &need);
+  FF_REQUIRE(workspace && workspace_bytes >= need && ff_aligned(workspace, 16),
+             "ff_gemm_w4a16_qkv: workspace of %lld bytes (16-byte aligned) required", (long long)need);
+  const int64_t n = (hq + 2 * hk) * kHeadDim;
+  const int splits = w4pk_qkv_splits(m, n, k);
+  const int tiles_m = (int)((m + kW4BM - 1) / kW4BM), tiles_n = (int)(n / 256);
+  const hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL((gemm_w4a16_pk_kernel<kW4BM, 64, false>), dim3((unsigned)(tiles_m * tiles_n * splits)),
+                     dim3(kThreads), 0, s, (const bf16_t*)x, ldx, (const uint8_t*)frag, (const uint32_t*)scales,
+                     w4_gshift(group), nullptr, 0, (int)m, (int)n, (int)k, tiles_m, tiles_n, splits,
+                     (f32x4*)workspace);
+  const W4Qkv qe{(const bf16_t*)q_norm, (const bf16_t*)k_norm, eps_q, eps_k, (const bf16_t*)cos,
+                 (const bf16_t*)sin, (bf16_t*)yq, (bf16_t*)yk, (bf16_t*)vt, (int)hq, (int)hk, (int)t_pad};
+  hipLaunchKernelGGL((w4pk_qkv_kernel<kW4BM>), dim3((unsigned)(tiles_m * tiles_n * (kW4BM / 16))), dim3(kThreads),
+                     0, s, (const f32x4*)workspace, splits, (int)m, tiles_m, qe);
+  const int covered = tiles_m * kW4BM;
+  if (t_pad > covered)
+    hipLaunchKernelGGL(vt_zero_tail_kernel, dim3(64), dim3(kThreads), 0, s, (bf16_t*)vt, (int)(hk * kHeadDim),
+                       (int)t_pad, covered);
+  FF_LAUNCH_CHECK("ff_gemm_w4a16_qkv");
   return FF_OK;
 }
 

@@ -233,6 +233,33 @@ class Int4:
              ptr(y), y.stride(0), m, n, k, ptr(ws), need.value, stream())
         return y
 
+    def qkv(self, x, hq, hk, q_norm, k_norm, cos, sin):
+        """The QKV linear with qk_pair and the V transpose in one op
+        (ff_gemm_w4a16_qkv): x (1, T, H) -> yq (1, hq, T, 128), yk (1, hk, T, 128),
+        vt (hk, 128, t_pad), t_pad; None where the packed kernel does not take
+        the shape (the caller then runs the separate ops)."""
+        if self.frag is None:
+            return None
+        flat = _rows(x)
+        if flat.stride(-1) != 1 or flat.stride(0) % 8:
+            flat = flat.contiguous()
+        m, k = flat.shape
+        need = ctypes.c_int64(0)
+        call("ff_gemm_w4a16_qkv_workspace", m, k, hq, hk, self.group, ctypes.byref(need))
+        if need.value == 0:
+            return None
+        d, tp = 128, (m + 63) // 64 * 64
+        yq = torch.empty((1, hq, m, d), device=x.device, dtype=BF16)
+        yk = torch.empty((1, hk, m, d), device=x.device, dtype=BF16)
+        vt = torch.empty((hk, d, tp), device=x.device, dtype=BF16)
+        ws = torch.empty(need.value, device=x.device, dtype=torch.uint8)
+        cos2, sin2 = cos.reshape(-1, d).contiguous(), sin.reshape(-1, d).contiguous()
+        call("ff_gemm_w4a16_qkv", ptr(flat), flat.stride(0), ptr(self.frag), ptr(self.scales), self.group, m, k,
+             hq, hk, ptr(q_norm.weight), ptr(k_norm.weight), float(q_norm.variance_epsilon),
+             float(k_norm.variance_epsilon), ptr(cos2), ptr(sin2), ptr(yq), ptr(yk), ptr(vt), tp, ptr(ws),
+             need.value, stream())
+        return yq, yk, vt, tp
+
     def swiglu_fits(self, m):
         """Whether ``swiglu`` runs the fused kernel for ``m`` rows."""
         if self.frag is None:

@@ -472,12 +472,21 @@ class Runtime:
                 trace.append(h[0].clone())
         lw = L[-1]
         x = ops.fast_norm(h, lw.input_norm)
-        q, k, v = Linear.apply(x, lw.qkv).split([HQ * D, HK * D, HK * D], -1)
-        shape = (*x.shape[:-1], -1, D)
-        q, k = ops.qk_pair(q.view(shape), k.view(shape), lw.q_norm, lw.k_norm, cos, sin)
-        v = v.view(shape).transpose(1, 2)
-        query = self._index_rows(q[0], self.pick)[None]            # q.index_select(2, pick)
-        out = ops.attention_direct(query, k, v, cfg.scaling, positions=self.pick)
+        fused = lw.qkv.qkv(x, HQ, HK, lw.q_norm, lw.k_norm, cos, sin) if isinstance(lw.qkv, Int4) else None
+        if fused is not None:
+            # the picked query row read in place (gather_q), K/V for every token
+            q, k, vt, tp = fused
+            t = x.shape[-2]
+            out = torch.empty((1, 1, HQ, D), device=x.device, dtype=x.dtype)
+            call("ff_attention_vt", ptr(q), ptr(k), ptr(vt), ptr(self.pick), 1, ptr(out), 1, t, tp, HQ, HK, D,
+                 float(cfg.scaling), stream())
+        else:
+            q, k, v = Linear.apply(x, lw.qkv).split([HQ * D, HK * D, HK * D], -1)
+            shape = (*x.shape[:-1], -1, D)
+            q, k = ops.qk_pair(q.view(shape), k.view(shape), lw.q_norm, lw.k_norm, cos, sin)
+            v = v.view(shape).transpose(1, 2)
+            query = self._index_rows(q[0], self.pick)[None]        # q.index_select(2, pick)
+            out = ops.attention_direct(query, k, v, cfg.scaling, positions=self.pick)
         value = Linear.apply(out.reshape(1, 1, -1), lw.o)
         hp = self._index_rows(h[0], self.pick, dim1=True)           # h.index_select(1, pick)
         residual, post = ops.add_rms(hp, value, None, lw.post_norm)
@@ -501,6 +510,16 @@ class Runtime:
     def _attention_generic(self, lw, x, cos, sin):
         cfg = self.cfg
         HQ, HK, D = cfg.heads, cfg.kv_heads, cfg.head_dim
+        fused = lw.qkv.qkv(x, HQ, HK, lw.q_norm, lw.k_norm, cos, sin) if isinstance(lw.qkv, Int4) else None
+        if fused is not None:
+            # packed Int4 QKV: GEMM + qk_pair + V transpose in one op (the same bits),
+            # then the attention kernel attention_direct runs on that layout
+            yq, yk, vt, tp = fused
+            t = x.shape[-2]
+            out = torch.empty((1, t, HQ, D), device=x.device, dtype=x.dtype)
+            call("ff_attention_vt", ptr(yq), ptr(yk), ptr(vt), None, 0, ptr(out), t, t, tp, HQ, HK, D,
+                 float(cfg.scaling), stream())
+            return Linear.apply(out.reshape(*x.shape[:-1], -1), lw.o)
         q, k, v = Linear.apply(x, lw.qkv).split([HQ * D, HK * D, HK * D], -1)
         shape = (*x.shape[:-1], -1, D)
         q, k = ops.qk_pair(q.view(shape), k.view(shape), lw.q_norm, lw.k_norm, cos, sin)

@@ -326,6 +326,21 @@ int ff_gemm_w4a16_swiglu_fits(int64_t m, int64_t i, int64_t k, int64_t group, in
 int ff_gemm_w4a16_swiglu_pk(const void* x, int64_t ldx, const void* frag, const void* scales, int64_t group,
                             void* h, int64_t ldh, int64_t m, int64_t i, int64_t k, ff_stream_t stream);
 
+/* W4A16 QKV GEMM + q/k norm + rotary + V transpose (no reference counterpart as
+ * one op: the QKV Int4.__call__ (_family/night_runtime.py:31-42) followed by
+ * qk_pair and the V transpose of attention_direct, scaled_qwen_runtime.py:
+ * 165-171; the same bits). frag / scales / group: the (hq + 2 hk) * 128 x k
+ * Int4 weight with its fragment copy. Writes yq (hq, m, 128), yk (hk, m, 128)
+ * (per-head RMSNorm with q_norm / k_norm, then rotary with cos / sin (m, 128))
+ * and vt (hk, 128, t_pad) with zeros for tokens in [m, t_pad); head dim 128.
+ * workspace: ff_gemm_w4a16_qkv_workspace bytes (0 there: shape not taken --
+ * m > 4, k % 256, group a power of two >= 32 dividing k), 16-byte aligned. */
+int ff_gemm_w4a16_qkv_workspace(int64_t m, int64_t k, int64_t hq, int64_t hk, int64_t group, int64_t* bytes);
+int ff_gemm_w4a16_qkv(const void* x, int64_t ldx, const void* frag, const void* scales, int64_t group, int64_t m,
+                      int64_t k, int64_t hq, int64_t hk, const void* q_norm, const void* k_norm, float eps_q,
+                      float eps_k, const void* cos, const void* sin, void* yq, void* yk, void* vt, int64_t t_pad,
+                      void* workspace, int64_t workspace_bytes, ff_stream_t stream);
+
 /* Embedding gather h[t] = table[ids[t]] (scaled_qwen_runtime.py:145
  * embed_tokens). Ids outside [0, vocab) read row 0 (the host validates ids). */
 int ff_embed(const int64_t* ids, const void* table, void* out, int64_t t, int64_t h,

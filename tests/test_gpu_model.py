@@ -198,7 +198,8 @@ def test_fused_static_path_equals_reference_op_sequence(gpu):
     assert torch.equal(z1, z2), (z1, z2)
 
 
-@pytest.mark.parametrize("mode,path", [("fp8", "fused"), ("fp8", "generic"), ("fp8_static", "fused_static")])
+@pytest.mark.parametrize("mode,path", [("fp8", "fused"), ("fp8", "generic"), ("fp8_static", "fused_static"),
+                                       ("w4a16", "generic")])
 def test_graph_replays_equal_eager(gpu, mode, path):
     from fastforward_amd.runtime import Runtime
     from fastforward_amd.synthetic import make_model, make_request

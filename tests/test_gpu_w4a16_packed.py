@@ -135,3 +135,32 @@ def test_w4a16_swiglu_packed_equals_unfused(gpu, tuning, m, k, i, sym, group):
     g, u = _unsplit_lds(op, x, tuning).chunk(2, -1)
     assert torch.equal(h, ops.swiglu(g, u))
     assert torch.equal(h, op.swiglu(x))
+
+
+@pytest.mark.parametrize("m,k,hq,hk", [(576, 4096, 32, 8), (320, 2048, 16, 8), (144, 1024, 8, 4), (100, 1024, 8, 2)])
+@pytest.mark.parametrize("sym,group", [(True, 128), (False, 32)])
+def test_w4a16_qkv_fused_equals_unfused(gpu, m, k, hq, hk, sym, group):
+    """Int4.qkv (ff_gemm_w4a16_qkv) == the packed QKV GEMM, qk_pair and the V
+    transpose of attention_direct (ff_v_transpose), bit for bit, with zeros in
+    V^T for the padded tokens (m = 144: t_pad 192 lies beyond the last tile)."""
+    from fastforward_amd import ops
+    from fastforward_amd._lib import call, ptr, stream
+    from fastforward_amd.linear import Int4
+    d = 128
+    n = (hq + 2 * hk) * d
+    x = torch.randn(1, m, k, generator=_g(75)).to(BF16).to(DEV)
+    w = (torch.randn(n, k, generator=_g(76)) * 0.02).to(BF16)
+    op = Int4(w.to(DEV), group=group, symmetric=sym).pack()
+    qn = ops.RMSNorm((1 + 0.2 * torch.randn(d, generator=_g(77))).to(BF16).to(DEV), 1e-6)
+    kn = ops.RMSNorm((1 + 0.2 * torch.randn(d, generator=_g(78))).to(BF16).to(DEV), 1e-6)
+    ang = torch.randn(m, d, generator=_g(79)) * 3
+    cos, sin = ang.cos().to(BF16).to(DEV)[None], ang.sin().to(BF16).to(DEV)[None]
+    yq, yk, vt, tp = op.qkv(x, hq, hk, qn, kn, cos, sin)
+    q, kk, v = op(x).reshape(1, m, n).split([hq * d, hk * d, hk * d], -1)
+    rq, rk = ops.qk_pair(q.view(1, m, hq, d), kk.view(1, m, hk, d), qn, kn, cos, sin)
+    assert torch.equal(yq, rq) and torch.equal(yk, rk)
+    vv = v.view(1, m, hk, d).transpose(1, 2)
+    rvt = torch.full((hk, d, tp), float("nan"), device=DEV, dtype=BF16)
+    call("ff_v_transpose", ptr(vv), vv.stride(2), vv.stride(1), ptr(rvt), m, tp, hk, d, stream())
+    assert torch.equal(vt, rvt)
+    assert int(vt[:, :, m:].abs().sum()) == 0
