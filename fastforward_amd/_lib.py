@@ -56,8 +56,9 @@ SIGNATURES = {
     "ff_gemm_w4a16_ws": [P, I64, P, P, I64, P, I64, I64, I64, I64, P, I64, P],
     "ff_gemm_w4a16_noalloc": [P, I64, P, P, I64, P, I64, I64, I64, I64, P],
     "ff_pack_weight_int4": [P, P, I64, I64, P],
+    "ff_pack_scales_int4": [P, P, I64, I64, I64, P],
     "ff_gemm_w4a16_pk_workspace": [I64, I64, I64, I64, PI64],
-    "ff_gemm_w4a16_pk": [P, I64, P, P, P, I64, P, I64, I64, I64, I64, P, I64, P],
+    "ff_gemm_w4a16_pk": [P, I64, P, P, P, P, I64, P, I64, I64, I64, I64, P, I64, P],
     "ff_gemm_w4a16_swiglu_fits": [I64, I64, I64, I64, PI32],
     "ff_gemm_w4a16_swiglu_pk": [P, I64, P, P, I64, P, I64, I64, I64, I64, P],
     "ff_gemm_w4a16_qkv_workspace": [I64, I64, I64, I64, I64, PI64],

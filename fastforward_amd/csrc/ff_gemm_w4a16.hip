@@ -467,8 +467,10 @@ extern "C" int ff_gemm_w4a16_ws(const void* x, int64_t ldx, const void* packed, 
 // The weight fragment is the MFMA's first operand, so the accumulator holds the
 // transposed tile: lane 16 g + r of fragment (i, j) holds token 16 i + r,
 // weight rows 16 j + 4 g .. + 3, and the epilogues store 8-byte row pieces
-// from registers. The (s, z) pairs come from their [K/group, N] layout as
-// 4-byte loads (group a power of two >= 32, so a lane's 16 k share a group).
+// from registers. The (s, z) pairs come as fp32 (16 s, z) from the copy
+// ff_pack_scales_int4 makes at setup ([K/group, N] order, one 8-byte load per
+// lane, fragment and half step; group a power of two >= 32, so a lane's 16 k
+// share a group).
 // The fragments store each nibble q as q ^ 8, so that one v_cvt_off_f32_i4 per
 // weight gives (q - 8) / 16 and one fma the exactly rounded (q - 8) s + z
 // (dequant8_off): the same values as the kernel above, with no inexact-z8 case.
@@ -505,8 +507,9 @@ __device__ __forceinline__ u32x4 dequant8_off(uint32_t w, float s16, float z) {
   return r;
 }
 
-// dequant8_off in 7 pieces of 2-3 VALU instructions, to be spread between MFMAs
-// (same operations, same values): w, s16, z set by the caller, r the result.
+// dequant8_off in 7 pieces of 3 VALU instructions, to be spread between MFMAs
+// (same operations, same values): w (fragment dword), s16 = 16 s and z set by
+// the caller (the fp32 pair of ff_pack_scales_int4), r the result.
 struct DqPieces {
   uint32_t w, hi;
   float s16, z;
@@ -549,17 +552,14 @@ struct DqPieces {
 // acc += A . B for one 16 x 16 x 32 bf16 tile, accumulator tied in place in
 // AGPRs (as the packed FP8 kernel: with the builtin the compiler moves every
 // accumulator between AGPRs and VGPRs at the loop edge). The compiler does not
-// see this asm as an MFMA, so it inserts none of the MFMA's wait states:
-// FRESH marks an MFMA whose A operand (dequantised weights) VALU has just
-// written, which needs 2 wait states after that write; the s_nop gives 5. The
-// other hazards are covered by s_nop at the loop's ends.
-template <bool FRESH>
+// see this asm as an MFMA, so it inserts none of the MFMA's wait states: the
+// main loop places every VALU write of an A operand (the dequantised weights)
+// at least two MFMAs, or a barrier, before the MFMA that reads it (2 wait
+// states are needed), and the accumulator hazards are covered by s_nop at the
+// loop's ends.
 __device__ __forceinline__ void mfma_bf16_acc(f32x4& acc, const u32x4& a, const i32x4v& b) {
   const i32x4v av = __builtin_bit_cast(i32x4v, a);
-  if constexpr (FRESH)
-    asm volatile("s_nop 4\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(av), "v"(b));
-  else
-    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(av), "v"(b));
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(av), "v"(b));
 }
 
 __global__ __launch_bounds__(kThreads) void pack_int4_kernel(const uint8_t* __restrict__ src,
@@ -586,7 +586,7 @@ template <int BM, int CW>
 __device__ __forceinline__ void w4pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], uint8_t* smem,
                                               const bf16_t* __restrict__ x, int64_t ldx, int M, int m0,
                                               const uint8_t* __restrict__ wp, uint32_t wbytes,
-                                              const uint32_t (&sB)[CW / 16], const uint32_t* __restrict__ sz,
+                                              const uint32_t (&sB)[CW / 16], const float* __restrict__ sz,
                                               uint32_t szbytes, const uint32_t (&colS)[CW / 16], int N, int gshift,
                                               int kt0, int nk) {
   constexpr int RA = BM / 16, TJ = CW / 16;
@@ -596,7 +596,7 @@ __device__ __forceinline__ void w4pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], ui
   constexpr int HALF = BM * 128;  // one 128-byte half of every row of a stage
   constexpr int STAGE = 2 * HALF;
   static_assert(A_CHUNKS >= kThreads, "at least one full activation round");
-  static_assert(RA >= 6, "a group's MFMAs carry the next group's 7 dequantisation pieces");
+  static_assert(RA >= 9, "a group's MFMAs carry the next group's 7 dequantisation pieces, 2 MFMAs before its use");
   const int tid = threadIdx.x, lane = tid & 63;
   const int r16 = lane & 15, g = lane >> 4;
   const int kend = kt0 + nk;
@@ -615,31 +615,36 @@ __device__ __forceinline__ void w4pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], ui
     dstA[i] = (ch >> 3) * HALF + (row >> 3) * 1024 + 128 * (row & 7) + 16 * ((ch & 7) ^ ((row & 15) >> 1));
   }
   i32x4v ast[NA];
+  auto loadA1 = [&](int kt, int i) { ast[i] = bload16(rA, voffA[i], (uint32_t)kt * 256u); };
+  auto writeA1 = [&](int buf, int i) { *reinterpret_cast<i32x4v*>(smem + buf * STAGE + dstA[i]) = ast[i]; };
   auto loadA = [&](int kt) {
 #pragma unroll
-    for (int i = 0; i < NA; ++i) ast[i] = bload16(rA, voffA[i], (uint32_t)kt * 256u);
+    for (int i = 0; i < NA; ++i) loadA1(kt, i);
   };
   auto writeA = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < NA; ++i) *reinterpret_cast<i32x4v*>(smem + buf * STAGE + dstA[i]) = ast[i];
+    for (int i = 0; i < NA; ++i) writeA1(buf, i);
   };
 
   const __amdgpu_buffer_rsrc_t rB = make_rsrc(wp, wbytes);
   const __amdgpu_buffer_rsrc_t rS = make_rsrc(sz, szbytes);
   const uint32_t voffB = 16u * (uint32_t)lane;
   i32x4v bq[2][TJ];
-  uint32_t sq[2][TJ][2];  // (s, z) of halves h = 0, 1
-  auto loadB = [&](int kt, auto SLOT) {
+  float sq[2][TJ][2][2];  // (16 s, z) of halves h = 0, 1
+  auto loadB1 = [&](int kt, auto SLOT, int j) {
     constexpr int slot = decltype(SLOT)::value;
+    bq[slot][j] = bload16(rB, voffB, sB[j] + (uint32_t)kt * 1024u);
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      bq[slot][j] = bload16(rB, voffB, sB[j] + (uint32_t)kt * 1024u);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint32_t gi = (uint32_t)(kPkStep * kt + 64 * h + 16 * g) >> gshift;
-        sq[slot][j][h] = bload4(rS, (gi * (uint32_t)N + colS[j]) * 4u, 0);
-      }
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t gi = (uint32_t)(kPkStep * kt + 64 * h + 16 * g) >> gshift;
+      const i32x2v v = bload8(rS, (gi * (uint32_t)N + colS[j]) * 8u, 0);
+      sq[slot][j][h][0] = __int_as_float(v.x);
+      sq[slot][j][h][1] = __int_as_float(v.y);
     }
+  };
+  auto loadB = [&](int kt, auto SLOT) {
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) loadB1(kt, SLOT, j);
   };
 
 #pragma unroll
@@ -668,6 +673,17 @@ __device__ __forceinline__ void w4pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], ui
 
   const int frag = 128 * (r16 & 7) + 1024 * (r16 >> 3);
   const int cA[2] = {16 * ((2 * g) ^ (r16 >> 1)), 16 * ((2 * g + 1) ^ (r16 >> 1))};
+  // The first fragment of every step is dequantised in the step before (the
+  // first step's here).
+  u32x4 bfirst;
+  {
+    DqPieces d0;
+    d0.w = (uint32_t)bq[0][0][0];
+    d0.s16 = sq[0][0][0][0];
+    d0.z = sq[0][0][0][1];
+    static_for<0, 7>([&](auto P_) { d0.template piece<decltype(P_)::value>(); });
+    bfirst = d0.r;
+  }
   for (int kb = kt0; kb < kend; kb += 2) {
     static_for<0, 2>([&](auto U_) {
       constexpr int u = decltype(U_)::value;
@@ -675,60 +691,56 @@ __device__ __forceinline__ void w4pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], ui
       // stage u (written during the previous step) is visible; stage u ^ 1, read
       // in the previous step, is free for step kt + 1
       __syncthreads();
-      writeA(u ^ 1);
-      loadA(min(kt + 2, kend - 1));
-      float sv[TJ][2], zv[TJ][2];  // 16 s and z of fragment j, half h
-#pragma unroll
-      for (int j = 0; j < TJ; ++j)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          sv[j][h] = 16.f * bf16_to_f32(sq[u][j][h] & 0xFFFFu);
-          zv[j][h] = bf16_to_f32(sq[u][j][h] >> 16);
-        }
+      const int kta = min(kt + 2, kend - 1);  // the step whose activations and weights are loaded here
       // The step's MFMAs as 4 TJ groups g = (substep s = g / TJ, fragment j =
       // g % TJ), each RA MFMAs on one dequantised weight fragment. The wave
       // issues in order and the matrix core runs an MFMA for 16 cycles, so the
-      // next group's dequantisation (and, before a new substep, its A
-      // fragments) is spread between this group's MFMAs, a few VALU
-      // instructions after each, where it runs under them.
+      // next group's dequantisation (the last group: the next step's first) and,
+      // before a new substep, its A fragments are spread between this group's
+      // MFMAs, a few VALU instructions after each, where they run under them.
       const uint8_t* st = smem + u * STAGE + frag;
       constexpr int NG = 4 * TJ;
       i32x4v a[2][RA];
       auto readA = [&](int sub, int i, i32x4v& dst) {
         dst = *reinterpret_cast<const i32x4v*>(st + (sub >> 1) * HALF + 2 * i * 1024 + cA[sub & 1]);
       };
-      auto start = [&](DqPieces& d, int sub, int j) {
-        d.w = (uint32_t)bq[u][j][sub];
-        d.s16 = sv[j][sub >> 1];
-        d.z = zv[j][sub >> 1];
-      };
 #pragma unroll
       for (int i = 0; i < RA; ++i) readA(0, i, a[0][i]);
-      DqPieces d0;
-      start(d0, 0, 0);
-      static_for<0, 7>([&](auto P_) { d0.template piece<decltype(P_)::value>(); });
-      u32x4 bcur = d0.r;
+      u32x4 bcur = bfirst;
       static_for<0, NG>([&](auto G_) {
         constexpr int gg = decltype(G_)::value, sub = gg / TJ, j = gg % TJ;
         constexpr int gn = gg + 1, subn = gn / TJ, jn = gn % TJ;
-        constexpr bool more = gn < NG;
+        constexpr bool in_step = gn < NG;
         DqPieces d;
-        if constexpr (more) start(d, subn, jn);
+        if constexpr (in_step) {
+          d.w = (uint32_t)bq[u][jn][subn];
+          d.s16 = sq[u][jn][subn >> 1][0];
+          d.z = sq[u][jn][subn >> 1][1];
+        } else {  // the next step's first fragment (its registers were loaded a step ago)
+          d.w = (uint32_t)bq[u ^ 1][0][0];
+          d.s16 = sq[u ^ 1][0][0][0];
+          d.z = sq[u ^ 1][0][0][1];
+        }
         static_for<0, RA>([&](auto I_) {
           constexpr int i = decltype(I_)::value;
-          // the step's first operands were written just above; every later
-          // group's were finished three MFMAs before its first one
-          mfma_bf16_acc<gg == 0 && i == 0>(acc[i][j], bcur, a[sub & 1][i]);
-          if constexpr (more) {
-            if constexpr (i < 6) d.template piece<i>();
-            if constexpr (i == 5) d.template piece<6>();
-            if constexpr (jn == 0) readA(subn, i, a[subn & 1][i]);
-          }
+          mfma_bf16_acc(acc[i][j], bcur, a[sub & 1][i]);
+          if constexpr (i < 7) d.template piece<i>();
+          if constexpr (in_step && jn == 0) readA(subn, i, a[subn & 1][i]);
+          // The step's memory work, one instruction group per MFMA slot: the
+          // activation staging (each chunk written to stage u ^ 1, then its
+          // register reloaded for step kt + 2) over the first groups, and each
+          // weight fragment's refill for step kt + 2 once its last use (the
+          // dequantisation of group 3 TJ + j, run during group 3 TJ + j - 1)
+          // is behind.
+          constexpr int slot = gg * RA + i;
+          if constexpr (slot < NA) writeA1(u ^ 1, slot);
+          if constexpr (slot >= NA && slot < 2 * NA) loadA1(kta, slot - NA);
+          if constexpr (gg >= 3 * TJ && i == RA - 1) loadB1(kta, U_, gg - 3 * TJ);
           __builtin_amdgcn_sched_barrier(0);  // keep this placement: the scheduler would cluster the VALU
         });
-        if constexpr (more) bcur = d.r;
+        if constexpr (in_step) bcur = d.r;
+        else bfirst = d.r;
       });
-      loadB(min(kt + 2, kend - 1), U_);
     });
   }
   W4_NOPS();
@@ -769,7 +781,7 @@ __device__ __forceinline__ void w4pk_store(const f32x4 (&acc)[BM / 16][CW / 16],
 // h = bf16(bf16(silu(g)) * u) into y (M, half) with g, u = bf16(acc).
 template <int BM, int CW, bool SWIGLU>
 __global__ __launch_bounds__(kThreads, 1) void gemm_w4a16_pk_kernel(
-    const bf16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ wp, const uint32_t* __restrict__ sz,
+    const bf16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ wp, const float* __restrict__ sz,
     int gshift, bf16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int tiles_m, int tiles_n, int splits,
     f32x4* __restrict__ part) {
   constexpr int RA = BM / 16, TJ = CW / 16, BN = 4 * CW, CH = BN / 2, WCH = CW / 2;
@@ -802,7 +814,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_w4a16_pk_kernel(
   }
   f32x4 acc[RA][TJ];
   w4pk_mainloop<BM, CW>(acc, smem, x, ldx, M, m0, wp, (uint32_t)((int64_t)N * K / 2), sB, sz,
-                        (uint32_t)((int64_t)(K >> gshift) * N * 4), colS, N, gshift, 2 * p0, 2 * (p1 - p0));
+                        (uint32_t)((int64_t)(K >> gshift) * N * 8), colS, N, gshift, 2 * p0, 2 * (p1 - p0));
 
   if constexpr (SWIGLU) {
     const int c_base = tn * CH + wave * WCH + 4 * g;
@@ -889,7 +901,7 @@ int w4_gshift(int64_t group) {
 W4PkPlan w4pk_plan(int64_t m, int64_t n, int64_t k, int64_t group) {
   W4PkPlan p;
   if (!w4pk_common_fits(m, k, group) || n % 16 || n * k / 2 >= (int64_t(1) << 31) ||
-      (k / group) * n * 4 >= (int64_t(1) << 31) || m * k * 2 >= (int64_t(1) << 31))
+      (k / group) * n * 8 >= (int64_t(1) << 31) || m * k * 2 >= (int64_t(1) << 31))
     return p;
   const int64_t tm = (m + kW4BM - 1) / kW4BM;
   if (n % 384 == 0 && tm * (n / 384) >= 192) {
@@ -908,7 +920,7 @@ W4PkPlan w4pk_plan(int64_t m, int64_t n, int64_t k, int64_t group) {
 
 int w4pk_swiglu_cw(int64_t m, int64_t i, int64_t k, int64_t group) {
   if (!w4pk_common_fits(m, k, group) || 2 * i * k / 2 >= (int64_t(1) << 31) ||
-      (k / group) * 2 * i * 4 >= (int64_t(1) << 31) || m * k * 2 >= (int64_t(1) << 31))
+      (k / group) * 2 * i * 8 >= (int64_t(1) << 31) || m * k * 2 >= (int64_t(1) << 31))
     return 0;
   if (i % 192 == 0) return 96;
   if (i % 128 == 0) return 64;
@@ -922,12 +934,12 @@ int64_t w4pk_workspace(int64_t m, int64_t n, int64_t k, int64_t group) {
 }
 
 template <int CW, bool SWIGLU>
-void launch_w4pk(const void* x, int64_t ldx, const void* frag, const void* scales, int gshift, void* y, int64_t ldy,
+void launch_w4pk(const void* x, int64_t ldx, const void* frag, const void* fscales, int gshift, void* y, int64_t ldy,
                  int m, int n, int k, int splits, void* ws, hipStream_t s) {
   const int tiles_m = (m + kW4BM - 1) / kW4BM;
   const int tiles_n = n / (4 * CW);  // SWIGLU: n = 2 half rows, 2 CW channels of each half per tile
   hipLaunchKernelGGL((gemm_w4a16_pk_kernel<kW4BM, CW, SWIGLU>), dim3((unsigned)(tiles_m * tiles_n * splits)),
-                     dim3(kThreads), 0, s, (const bf16_t*)x, ldx, (const uint8_t*)frag, (const uint32_t*)scales,
+                     dim3(kThreads), 0, s, (const bf16_t*)x, ldx, (const uint8_t*)frag, (const float*)fscales,
                      gshift, (bf16_t*)y, ldy, m, n, k, tiles_m, tiles_n, splits,
                      !SWIGLU && splits > 1 ? (f32x4*)ws : nullptr);
   if (!SWIGLU && splits > 1)
@@ -950,6 +962,33 @@ extern "C" int ff_pack_weight_int4(const void* packed, void* frag, int64_t n, in
   return FF_OK;
 }
 
+namespace {
+
+// (s, z) bf16 pairs -> (16 s, z) fp32 pairs, same [k/group, n] order.
+__global__ __launch_bounds__(kThreads) void pack_scales_int4_kernel(const uint32_t* __restrict__ sz,
+                                                                    float* __restrict__ out, int64_t pairs) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < pairs; i += (int64_t)gridDim.x * blockDim.x) {
+    const uint32_t v = sz[i];
+    out[2 * i] = 16.f * bf16_to_f32(v & 0xFFFFu);
+    out[2 * i + 1] = __uint_as_float(v & 0xFFFF0000u);
+  }
+}
+
+}  // namespace
+
+extern "C" int ff_pack_scales_int4(const void* scales, void* frag_scales, int64_t n, int64_t k, int64_t group,
+                                   ff_stream_t stream) {
+  FF_REQUIRE(scales && frag_scales, "ff_pack_scales_int4: null pointer");
+  FF_REQUIRE(n > 0 && k > 0 && group > 0 && k % group == 0 && (k / group) * n < (int64_t(1) << 40),
+             "ff_pack_scales_int4: bad sizes");
+  FF_REQUIRE(ff_aligned(scales, 4) && ff_aligned(frag_scales, 8), "ff_pack_scales_int4: alignment");
+  const int64_t pairs = (k / group) * n, blocks = (pairs + kThreads - 1) / kThreads;
+  hipLaunchKernelGGL(pack_scales_int4_kernel, dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const uint32_t*)scales, (float*)frag_scales, pairs);
+  FF_LAUNCH_CHECK("ff_pack_scales_int4");
+  return FF_OK;
+}
+
 extern "C" int ff_gemm_w4a16_pk_workspace(int64_t m, int64_t n, int64_t k, int64_t group, int64_t* bytes) {
   FF_REQUIRE(bytes && m >= 0 && n > 0 && k > 0 && group > 0, "ff_gemm_w4a16_pk_workspace: bad arguments");
   int64_t other = 0;
@@ -959,11 +998,11 @@ extern "C" int ff_gemm_w4a16_pk_workspace(int64_t m, int64_t n, int64_t k, int64
 }
 
 extern "C" int ff_gemm_w4a16_pk(const void* x, int64_t ldx, const void* packed, const void* frag, const void* scales,
-                                int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, void* workspace,
-                                int64_t workspace_bytes, ff_stream_t stream) {
-  const W4PkPlan p = frag ? w4pk_plan(m, n, k, group) : W4PkPlan{};
+                                const void* frag_scales, int64_t group, void* y, int64_t ldy, int64_t m, int64_t n,
+                                int64_t k, void* workspace, int64_t workspace_bytes, ff_stream_t stream) {
+  const W4PkPlan p = frag && frag_scales ? w4pk_plan(m, n, k, group) : W4PkPlan{};
   if (p.cw == 0 || ldx % 8 || ldy % 8 || ldx < k || ldy < n || m * ldx * 2 >= (int64_t(1) << 31) ||
-      !ff_aligned(x, 16) || !ff_aligned(frag, 16) || !ff_aligned(scales, 4) || !ff_aligned(y, 8))
+      !ff_aligned(x, 16) || !ff_aligned(frag, 16) || !ff_aligned(frag_scales, 8) || !ff_aligned(y, 8))
     return gemm_w4a16(x, ldx, packed, scales, group, y, ldy, m, n, k, workspace, workspace_bytes, stream);
   const int64_t need = w4pk_workspace(m, n, k, group);
   FF_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && ff_aligned(workspace, 16)),
@@ -971,9 +1010,9 @@ extern "C" int ff_gemm_w4a16_pk(const void* x, int64_t ldx, const void* packed, 
   const hipStream_t s = (hipStream_t)stream;
   const int gs = w4_gshift(group);
   if (p.cw == 96)
-    launch_w4pk<96, false>(x, ldx, frag, scales, gs, y, ldy, (int)m, (int)n, (int)k, 1, nullptr, s);
+    launch_w4pk<96, false>(x, ldx, frag, frag_scales, gs, y, ldy, (int)m, (int)n, (int)k, 1, nullptr, s);
   else
-    launch_w4pk<64, false>(x, ldx, frag, scales, gs, y, ldy, (int)m, (int)n, (int)k, p.splits, workspace, s);
+    launch_w4pk<64, false>(x, ldx, frag, frag_scales, gs, y, ldy, (int)m, (int)n, (int)k, p.splits, workspace, s);
   FF_LAUNCH_CHECK("ff_gemm_w4a16_pk");
   return FF_OK;
 }
@@ -984,24 +1023,24 @@ extern "C" int ff_gemm_w4a16_swiglu_fits(int64_t m, int64_t i, int64_t k, int64_
   return FF_OK;
 }
 
-extern "C" int ff_gemm_w4a16_swiglu_pk(const void* x, int64_t ldx, const void* frag, const void* scales,
+extern "C" int ff_gemm_w4a16_swiglu_pk(const void* x, int64_t ldx, const void* frag, const void* frag_scales,
                                        int64_t group, void* h, int64_t ldh, int64_t m, int64_t i, int64_t k,
                                        ff_stream_t stream) {
-  FF_REQUIRE(x && frag && scales && h, "ff_gemm_w4a16_swiglu_pk: null pointer");
+  FF_REQUIRE(x && frag && frag_scales && h, "ff_gemm_w4a16_swiglu_pk: null pointer");
   const int cw = w4pk_swiglu_cw(m, i, k, group);
   FF_REQUIRE(cw != 0, "ff_gemm_w4a16_swiglu_pk: m=%lld i=%lld k=%lld group=%lld is outside the fused kernel's "
              "shapes (m > 4, i %% 128, k %% 256, group a power of two >= 32 dividing k)",
              (long long)m, (long long)i, (long long)k, (long long)group);
   FF_REQUIRE(ldx % 8 == 0 && ldx >= k && ldh % 4 == 0 && ldh >= i && m * ldx * 2 < (int64_t(1) << 31),
              "ff_gemm_w4a16_swiglu_pk: bad strides");
-  FF_REQUIRE(ff_aligned(x, 16) && ff_aligned(frag, 16) && ff_aligned(scales, 4) && ff_aligned(h, 8),
-             "ff_gemm_w4a16_swiglu_pk: alignment (x, frag 16 bytes; h 8)");
+  FF_REQUIRE(ff_aligned(x, 16) && ff_aligned(frag, 16) && ff_aligned(frag_scales, 8) && ff_aligned(h, 8),
+             "ff_gemm_w4a16_swiglu_pk: alignment (x, frag 16 bytes; frag_scales, h 8)");
   const hipStream_t s = (hipStream_t)stream;
   const int gs = w4_gshift(group);
   if (cw == 96)
-    launch_w4pk<96, true>(x, ldx, frag, scales, gs, h, ldh, (int)m, (int)(2 * i), (int)k, 1, nullptr, s);
+    launch_w4pk<96, true>(x, ldx, frag, frag_scales, gs, h, ldh, (int)m, (int)(2 * i), (int)k, 1, nullptr, s);
   else
-    launch_w4pk<64, true>(x, ldx, frag, scales, gs, h, ldh, (int)m, (int)(2 * i), (int)k, 1, nullptr, s);
+    launch_w4pk<64, true>(x, ldx, frag, frag_scales, gs, h, ldh, (int)m, (int)(2 * i), (int)k, 1, nullptr, s);
   FF_LAUNCH_CHECK("ff_gemm_w4a16_swiglu_pk");
   return FF_OK;
 }
@@ -1107,7 +1146,7 @@ int w4pk_qkv_splits(int64_t m, int64_t n, int64_t k) {
 bool w4pk_qkv_fits(int64_t m, int64_t k, int64_t hq, int64_t hk, int64_t group) {
   const int64_t n = (hq + 2 * hk) * kHeadDim;
   return w4pk_common_fits(m, k, group) && hq > 0 && hk > 0 && n % 256 == 0 && n * k / 2 < (int64_t(1) << 31) &&
-         (k / group) * n * 4 < (int64_t(1) << 31) && m * k * 2 < (int64_t(1) << 31);
+         (k / group) * n * 8 < (int64_t(1) << 31) && m * k * 2 < (int64_t(1) << 31);
 }
 
 }  // namespace
@@ -1122,12 +1161,12 @@ extern "C" int ff_gemm_w4a16_qkv_workspace(int64_t m, int64_t k, int64_t hq, int
   return FF_OK;
 }
 
-extern "C" int ff_gemm_w4a16_qkv(const void* x, int64_t ldx, const void* frag, const void* scales, int64_t group,
+extern "C" int ff_gemm_w4a16_qkv(const void* x, int64_t ldx, const void* frag, const void* frag_scales, int64_t group,
                                  int64_t m, int64_t k, int64_t hq, int64_t hk, const void* q_norm, const void* k_norm,
                                  float eps_q, float eps_k, const void* cos, const void* sin, void* yq, void* yk,
                                  void* vt, int64_t t_pad, void* workspace, int64_t workspace_bytes,
                                  ff_stream_t stream) {
-  FF_REQUIRE(x && frag && scales && q_norm && k_norm && cos && sin && yq && yk && vt,
+  FF_REQUIRE(x && frag && frag_scales && q_norm && k_norm && cos && sin && yq && yk && vt,
              "ff_gemm_w4a16_qkv: null pointer");
   FF_REQUIRE(w4pk_qkv_fits(m, k, hq, hk, group),
              "ff_gemm_w4a16_qkv: m=%lld k=%lld hq=%lld hk=%lld group=%lld outside the kernel's shapes (m > 4, "
@@ -1136,7 +1175,7 @@ extern "C" int ff_gemm_w4a16_qkv(const void* x, int64_t ldx, const void* frag, c
   FF_REQUIRE(ldx % 8 == 0 && ldx >= k && m * ldx * 2 < (int64_t(1) << 31) && t_pad >= m && t_pad % 64 == 0 &&
                  t_pad < (1 << 30),
              "ff_gemm_w4a16_qkv: bad strides or t_pad");
-  FF_REQUIRE(ff_aligned(x, 16) && ff_aligned(frag, 16) && ff_aligned(scales, 4) && ff_aligned(q_norm, 16) &&
+  FF_REQUIRE(ff_aligned(x, 16) && ff_aligned(frag, 16) && ff_aligned(frag_scales, 8) && ff_aligned(q_norm, 16) &&
                  ff_aligned(k_norm, 16) && ff_aligned(cos, 16) && ff_aligned(sin, 16) && ff_aligned(yq, 16) &&
                  ff_aligned(yk, 16) && ff_aligned(vt, 16),
              "ff_gemm_w4a16_qkv: operands must be 16-byte aligned");
@@ -1149,7 +1188,7 @@ extern "C" int ff_gemm_w4a16_qkv(const void* x, int64_t ldx, const void* frag, c
   const int tiles_m = (int)((m + kW4BM - 1) / kW4BM), tiles_n = (int)(n / 256);
   const hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL((gemm_w4a16_pk_kernel<kW4BM, 64, false>), dim3((unsigned)(tiles_m * tiles_n * splits)),
-                     dim3(kThreads), 0, s, (const bf16_t*)x, ldx, (const uint8_t*)frag, (const uint32_t*)scales,
+                     dim3(kThreads), 0, s, (const bf16_t*)x, ldx, (const uint8_t*)frag, (const float*)frag_scales,
                      w4_gshift(group), nullptr, 0, (int)m, (int)n, (int)k, tiles_m, tiles_n, splits,
                      (f32x4*)workspace);
   const W4Qkv qe{(const bf16_t*)q_norm, (const bf16_t*)k_norm, eps_q, eps_k, (const bf16_t*)cos,

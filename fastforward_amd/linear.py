@@ -202,15 +202,22 @@ class Int4:
         self.scales = torch.empty((k // group, n, 2), device=w.device, dtype=BF16)
         call("ff_quant_weight_int4", ptr(w), ptr(self.packed), ptr(self.scales), n, k, group,
              1 if symmetric else 0, stream())
-        self.frag = None
+        self.frag = self.frag_scales = None
 
     def pack(self):
-        """Add the MFMA-fragment copy of the nibbles (ff_pack_weight_int4) that the
-        packed kernels read; ``packed`` stays for the shapes they do not take."""
+        """Add the copies the packed kernels read: the nibbles in MFMA-fragment
+        order (ff_pack_weight_int4) and the (s, z) pairs as fp32 (16 s, z)
+        (ff_pack_scales_int4). ``packed`` / ``scales`` stay for the shapes the
+        packed kernels do not take. Weights with a scale of 2^120 or more stay
+        unpacked (16 s must be exact)."""
         n, k = self.weight.shape
         if self.frag is None and n % 16 == 0 and k % 128 == 0:
+            if float(self.scales[..., 0].abs().max()) >= 2.0 ** 120:
+                return self
             self.frag = torch.empty_like(self.packed)
             call("ff_pack_weight_int4", ptr(self.packed), ptr(self.frag), n, k, stream())
+            self.frag_scales = torch.empty(self.scales.shape, device=self.scales.device, dtype=torch.float32)
+            call("ff_pack_scales_int4", ptr(self.scales), ptr(self.frag_scales), n, k, self.group, stream())
         return self
 
     def __call__(self, x, out=None):
@@ -225,7 +232,7 @@ class Int4:
             call("ff_gemm_w4a16_pk_workspace", m, n, k, self.group, ctypes.byref(need))
             ws = torch.empty(need.value, device=x.device, dtype=torch.uint8) if need.value else None
             call("ff_gemm_w4a16_pk", ptr(flat), flat.stride(0), ptr(self.packed), ptr(self.frag), ptr(self.scales),
-                 self.group, ptr(y), y.stride(0), m, n, k, ptr(ws), need.value, stream())
+                 ptr(self.frag_scales), self.group, ptr(y), y.stride(0), m, n, k, ptr(ws), need.value, stream())
             return y
         call("ff_gemm_w4a16_workspace", m, n, k, ctypes.byref(need))
         ws = torch.empty(need.value, device=x.device, dtype=torch.uint8) if need.value else None
@@ -254,7 +261,7 @@ class Int4:
         vt = torch.empty((hk, d, tp), device=x.device, dtype=BF16)
         ws = torch.empty(need.value, device=x.device, dtype=torch.uint8)
         cos2, sin2 = cos.reshape(-1, d).contiguous(), sin.reshape(-1, d).contiguous()
-        call("ff_gemm_w4a16_qkv", ptr(flat), flat.stride(0), ptr(self.frag), ptr(self.scales), self.group, m, k,
+        call("ff_gemm_w4a16_qkv", ptr(flat), flat.stride(0), ptr(self.frag), ptr(self.frag_scales), self.group, m, k,
              hq, hk, ptr(q_norm.weight), ptr(k_norm.weight), float(q_norm.variance_epsilon),
              float(k_norm.variance_epsilon), ptr(cos2), ptr(sin2), ptr(yq), ptr(yk), ptr(vt), tp, ptr(ws),
              need.value, stream())
@@ -283,6 +290,6 @@ class Int4:
             g, u = self(x).chunk(2, -1)
             return ops.swiglu(g, u)
         h = torch.empty((m, i), device=x.device, dtype=BF16)
-        call("ff_gemm_w4a16_swiglu_pk", ptr(flat), flat.stride(0), ptr(self.frag), ptr(self.scales), self.group,
+        call("ff_gemm_w4a16_swiglu_pk", ptr(flat), flat.stride(0), ptr(self.frag), ptr(self.frag_scales), self.group,
              ptr(h), i, m, i, k, stream())
         return h.reshape(*x.shape[:-1], i)

@@ -299,44 +299,52 @@ int ff_gemm_w4a16_noalloc(const void* x, int64_t ldx, const void* packed, const 
  * k % 128 == 0. */
 int ff_pack_weight_int4(const void* packed, void* frag, int64_t n, int64_t k, ff_stream_t stream);
 
-/* ff_gemm_w4a16_ws with the fragment copy (ff_pack_weight_int4 of packed): the
- * weights are read from frag straight into registers (Int4.__call__,
+/* Setup-time copy of the (scale, zero) pairs for the packed kernels: scales
+ * [k/group, n, 2] bf16 -> frag_scales [k/group, n, 2] fp32 holding (16 s, z)
+ * (16 s is exact for |s| < 2^124; larger scales must stay on ff_gemm_w4a16). */
+int ff_pack_scales_int4(const void* scales, void* frag_scales, int64_t n, int64_t k, int64_t group,
+                        ff_stream_t stream);
+
+/* ff_gemm_w4a16_ws with the fragment copies (ff_pack_weight_int4 of packed and
+ * ff_pack_scales_int4 of scales): the weights are read from frag straight into
+ * registers (Int4.__call__,
  * _family/night_runtime.py:31-42). The same dequantised values and, unsplit,
  * the same bits as ff_gemm_w4a16; where it splits K (grids that would leave
  * CUs idle) the fp32 partials go to the workspace and a second launch adds them
  * in split order. Shapes the packed kernel does not take (m <= 4, k % 256,
  * group not a power of two >= 32, n % 256 unless the 144 x 384 tiles fill the
- * GPU) and a null frag run ff_gemm_w4a16_ws. ff_gemm_w4a16_pk_workspace stores
+ * GPU) and a null frag run ff_gemm_w4a16_ws on packed / scales. ff_gemm_w4a16_pk_workspace stores
  * the bytes either path wants; workspace 16-byte aligned; calls that overlap
  * must not share it. */
 int ff_gemm_w4a16_pk_workspace(int64_t m, int64_t n, int64_t k, int64_t group, int64_t* bytes);
 int ff_gemm_w4a16_pk(const void* x, int64_t ldx, const void* packed, const void* frag, const void* scales,
-                     int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, void* workspace,
-                     int64_t workspace_bytes, ff_stream_t stream);
+                     const void* frag_scales, int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
+                     void* workspace, int64_t workspace_bytes, ff_stream_t stream);
 
 /* Gate/up W4A16 GEMM with SwiGLU in its epilogue: h (m, i) = bf16(bf16(silu(g))
  * * u) with g, u = bf16 of x @ dequant(W)^T for W = [gate (i rows); up (i rows)]
- * (frag: ff_pack_weight_int4 of the (2 i, k) weight; scales [k/group, 2 i, 2]).
+ * (frag / frag_scales: ff_pack_weight_int4 / ff_pack_scales_int4 of the
+ * (2 i, k) weight and its [k/group, 2 i, 2] scales).
  * No reference counterpart as one op: Int4.__call__ (_family/night_runtime.py:
  * 31-42) then swiglu (_legacy/search_kernels.py:8-23), the same bits.
  * ff_gemm_w4a16_swiglu_fits (no GPU needed) reports whether the kernel takes
  * the shape (m > 4, i % 128, k % 256, group a power of two >= 32 dividing k);
  * other shapes are rejected with FF_EINVAL. h row stride ldh (multiple of 4). */
 int ff_gemm_w4a16_swiglu_fits(int64_t m, int64_t i, int64_t k, int64_t group, int* fits);
-int ff_gemm_w4a16_swiglu_pk(const void* x, int64_t ldx, const void* frag, const void* scales, int64_t group,
+int ff_gemm_w4a16_swiglu_pk(const void* x, int64_t ldx, const void* frag, const void* frag_scales, int64_t group,
                             void* h, int64_t ldh, int64_t m, int64_t i, int64_t k, ff_stream_t stream);
 
 /* W4A16 QKV GEMM + q/k norm + rotary + V transpose (no reference counterpart as
  * one op: the QKV Int4.__call__ (_family/night_runtime.py:31-42) followed by
  * qk_pair and the V transpose of attention_direct, scaled_qwen_runtime.py:
- * 165-171; the same bits). frag / scales / group: the (hq + 2 hk) * 128 x k
- * Int4 weight with its fragment copy. Writes yq (hq, m, 128), yk (hk, m, 128)
+ * 165-171; the same bits). frag / frag_scales / group: the fragment copies of
+ * the (hq + 2 hk) * 128 x k Int4 weight. Writes yq (hq, m, 128), yk (hk, m, 128)
  * (per-head RMSNorm with q_norm / k_norm, then rotary with cos / sin (m, 128))
  * and vt (hk, 128, t_pad) with zeros for tokens in [m, t_pad); head dim 128.
  * workspace: ff_gemm_w4a16_qkv_workspace bytes (0 there: shape not taken --
  * m > 4, k % 256, group a power of two >= 32 dividing k), 16-byte aligned. */
 int ff_gemm_w4a16_qkv_workspace(int64_t m, int64_t k, int64_t hq, int64_t hk, int64_t group, int64_t* bytes);
-int ff_gemm_w4a16_qkv(const void* x, int64_t ldx, const void* frag, const void* scales, int64_t group, int64_t m,
+int ff_gemm_w4a16_qkv(const void* x, int64_t ldx, const void* frag, const void* frag_scales, int64_t group, int64_t m,
                       int64_t k, int64_t hq, int64_t hk, const void* q_norm, const void* k_norm, float eps_q,
                       float eps_k, const void* cos, const void* sin, void* yq, void* yk, void* vt, int64_t t_pad,
                       void* workspace, int64_t workspace_bytes, ff_stream_t stream);
