@@ -875,6 +875,117 @@ __global__ __launch_bounds__(kThreads) void w4pk_reduce_kernel(const f32x4* __re
   }
 }
 
+// Rows m <= 4 (the pick-only tail) on the packed copies: a workgroup of 4 waves
+// owns 16 weight rows (one fragment row block; SWIGLU: 16 gate rows and the 16
+// matching up rows) and its waves take every 4th 128-k step. Lane (g, r)
+// dequantises its 32 nibbles of the fragment to the bf16 weights the tile
+// kernels use (dequant8_off) and accumulates their products with the bf16 x
+// pairs on v_dot2_f32_bf16 in fp32; the 4 lanes of a row, then the 4 waves in
+// order, are added at the end and rounded to bf16 (SWIGLU: h = bf16(bf16(silu(
+// bf16(g))) * bf16(u))). Only the fp32 order of the sum differs from the tile
+// kernels.
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, a), __builtin_bit_cast(bf16x2v, b), c, false);
+}
+
+template <int M, bool SWIGLU>
+__global__ __launch_bounds__(kThreads) void gemv_w4pk_kernel(const bf16_t* __restrict__ x, int64_t ldx,
+                                                             const uint8_t* __restrict__ wp,
+                                                             const float* __restrict__ fs, int gshift,
+                                                             bf16_t* __restrict__ y, int64_t ldy, int N, int K) {
+  constexpr int NF = SWIGLU ? 2 : 1;  // fragments per k step: the rows (gate), and the up rows
+  __shared__ float red[4][NF][M][16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int KT = K / kPkStep;
+  const int half = N / 2;
+  int rowb[NF];
+  rowb[0] = 16 * blockIdx.x;
+  if constexpr (SWIGLU) rowb[NF - 1] = half + 16 * blockIdx.x;
+  const __amdgpu_buffer_rsrc_t rX = make_rsrc(x, (uint32_t)((int64_t)M * ldx * 2));
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(wp, (uint32_t)((int64_t)N * K / 2));
+  const __amdgpu_buffer_rsrc_t rS = make_rsrc(fs, (uint32_t)((int64_t)(K >> gshift) * N * 8));
+  float acc[NF][M];
+#pragma unroll
+  for (int f = 0; f < NF; ++f)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[f][m] = 0.f;
+  for (int kt = wave; kt < KT; kt += 4) {
+    i32x4v xv[M][2][2];  // row m, half h, 8 k each: k = 128 kt + 64 h + 16 g + [0, 16)
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          xv[m][h][c] = bload16(rX, (uint32_t)(m * ldx + kPkStep * kt + 64 * h + 16 * g + 8 * c) * 2u, 0);
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const i32x4v w = bload16(rB, 16u * (uint32_t)lane, (uint32_t)((rowb[f] / 16) * KT + kt) * 1024u);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t gi = (uint32_t)(kPkStep * kt + 64 * h + 16 * g) >> gshift;
+        const i32x2v sz = bload8(rS, (gi * (uint32_t)N + (uint32_t)(rowb[f] + r16)) * 8u, 0);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const u32x4 b = dequant8_off((uint32_t)w[2 * h + t], __int_as_float(sz.x), __int_as_float(sz.y));
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            const i32x4v xx = xv[m][h][t];
+            acc[f][m] = dot2_bf16(b.x, (uint32_t)xx.x, acc[f][m]);
+            acc[f][m] = dot2_bf16(b.y, (uint32_t)xx.y, acc[f][m]);
+            acc[f][m] = dot2_bf16(b.z, (uint32_t)xx.z, acc[f][m]);
+            acc[f][m] = dot2_bf16(b.w, (uint32_t)xx.w, acc[f][m]);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int f = 0; f < NF; ++f)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float v = acc[f][m];
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      if (g == 0) red[wave][f][m][r16] = v;
+    }
+  __syncthreads();
+  if (tid < 16 * M) {
+    const int m = tid / 16, r = tid % 16;
+    float sum[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) sum[f] = ((red[0][f][m][r] + red[1][f][m][r]) + red[2][f][m][r]) + red[3][f][m][r];
+    float out = sum[0];
+    if constexpr (SWIGLU) out = round_bf16(round_bf16(silu(round_bf16(sum[0]))) * round_bf16(sum[NF - 1]));
+    y[(int64_t)m * ldy + 16 * blockIdx.x + r] = (bf16_t)f32_to_bf16(out);
+  }
+}
+
+template <bool SWIGLU>
+void launch_gemv_w4pk(const void* x, int64_t ldx, const void* frag, const void* fscales, int gshift, void* y,
+                      int64_t ldy, int m, int n, int k, hipStream_t s) {
+  const int blocks = SWIGLU ? n / 32 : n / 16;
+#define FF_GEMV_W4(MM)                                                                                          \
+  case MM:                                                                                                      \
+    hipLaunchKernelGGL((gemv_w4pk_kernel<MM, SWIGLU>), dim3((unsigned)blocks), dim3(kThreads), 0, s,             \
+                       (const bf16_t*)x, ldx, (const uint8_t*)frag, (const float*)fscales, gshift, (bf16_t*)y, ldy, \
+                       n, k);                                                                                   \
+    break;
+  switch (m) { FF_GEMV_W4(1) FF_GEMV_W4(2) FF_GEMV_W4(3) FF_GEMV_W4(4) }
+#undef FF_GEMV_W4
+}
+
+// Shapes the packed GEMV takes: 1 <= m <= 4, n % 16 (SWIGLU: the 2 i rows,
+// i % 16), k % 128, a power-of-two group >= 32 dividing k.
+bool w4pk_gemv_fits(int64_t m, int64_t n, int64_t k, int64_t group) {
+  return m >= 1 && m <= 4 && n > 0 && n % 16 == 0 && k % kPkStep == 0 && group >= 32 && (group & (group - 1)) == 0 &&
+         k % group == 0 && n * k / 2 < (int64_t(1) << 31) && (k / group) * n * 8 < (int64_t(1) << 31) &&
+         k < (1 << 24);
+}
+
 // Plans of the packed path. Plain: 144 x 384 tiles (CW 96) when they fill the
 // GPU unsplit; otherwise 144 x 256 tiles (CW 64) with k split until about one
 // workgroup per CU (at most 8 ways, at least one pair of k steps each). SwiGLU:
@@ -1000,6 +1111,15 @@ extern "C" int ff_gemm_w4a16_pk_workspace(int64_t m, int64_t n, int64_t k, int64
 extern "C" int ff_gemm_w4a16_pk(const void* x, int64_t ldx, const void* packed, const void* frag, const void* scales,
                                 const void* frag_scales, int64_t group, void* y, int64_t ldy, int64_t m, int64_t n,
                                 int64_t k, void* workspace, int64_t workspace_bytes, ff_stream_t stream) {
+  if (frag && frag_scales && w4pk_gemv_fits(m, n, k, group) && ldx % 8 == 0 && ldx >= k && ldy >= n &&
+      m * ldx * 2 < (int64_t(1) << 31) && ff_aligned(x, 16) && ff_aligned(frag, 16) && ff_aligned(frag_scales, 8) &&
+      ff_aligned(y, 2)) {
+    FF_REQUIRE(y, "ff_gemm_w4a16_pk: null pointer");
+    launch_gemv_w4pk<false>(x, ldx, frag, frag_scales, w4_gshift(group), y, ldy, (int)m, (int)n, (int)k,
+                            (hipStream_t)stream);
+    FF_LAUNCH_CHECK("ff_gemm_w4a16_pk");
+    return FF_OK;
+  }
   const W4PkPlan p = frag && frag_scales ? w4pk_plan(m, n, k, group) : W4PkPlan{};
   if (p.cw == 0 || ldx % 8 || ldy % 8 || ldx < k || ldy < n || m * ldx * 2 >= (int64_t(1) << 31) ||
       !ff_aligned(x, 16) || !ff_aligned(frag, 16) || !ff_aligned(frag_scales, 8) || !ff_aligned(y, 8))
@@ -1019,7 +1139,7 @@ extern "C" int ff_gemm_w4a16_pk(const void* x, int64_t ldx, const void* packed, 
 
 extern "C" int ff_gemm_w4a16_swiglu_fits(int64_t m, int64_t i, int64_t k, int64_t group, int* fits) {
   FF_REQUIRE(fits, "ff_gemm_w4a16_swiglu_fits: null pointer");
-  *fits = w4pk_swiglu_cw(m, i, k, group) != 0;
+  *fits = w4pk_swiglu_cw(m, i, k, group) != 0 || (i % 16 == 0 && w4pk_gemv_fits(m, 2 * i, k, group));
   return FF_OK;
 }
 
@@ -1028,16 +1148,19 @@ extern "C" int ff_gemm_w4a16_swiglu_pk(const void* x, int64_t ldx, const void* f
                                        ff_stream_t stream) {
   FF_REQUIRE(x && frag && frag_scales && h, "ff_gemm_w4a16_swiglu_pk: null pointer");
   const int cw = w4pk_swiglu_cw(m, i, k, group);
-  FF_REQUIRE(cw != 0, "ff_gemm_w4a16_swiglu_pk: m=%lld i=%lld k=%lld group=%lld is outside the fused kernel's "
-             "shapes (m > 4, i %% 128, k %% 256, group a power of two >= 32 dividing k)",
-             (long long)m, (long long)i, (long long)k, (long long)group);
+  const bool gemv = cw == 0 && i % 16 == 0 && w4pk_gemv_fits(m, 2 * i, k, group);
+  FF_REQUIRE(cw != 0 || gemv, "ff_gemm_w4a16_swiglu_pk: m=%lld i=%lld k=%lld group=%lld is outside the fused "
+             "kernels' shapes (m > 4: i %% 128, k %% 256; m <= 4: i %% 16, k %% 128; group a power of two >= 32 "
+             "dividing k)", (long long)m, (long long)i, (long long)k, (long long)group);
   FF_REQUIRE(ldx % 8 == 0 && ldx >= k && ldh % 4 == 0 && ldh >= i && m * ldx * 2 < (int64_t(1) << 31),
              "ff_gemm_w4a16_swiglu_pk: bad strides");
   FF_REQUIRE(ff_aligned(x, 16) && ff_aligned(frag, 16) && ff_aligned(frag_scales, 8) && ff_aligned(h, 8),
              "ff_gemm_w4a16_swiglu_pk: alignment (x, frag 16 bytes; frag_scales, h 8)");
   const hipStream_t s = (hipStream_t)stream;
   const int gs = w4_gshift(group);
-  if (cw == 96)
+  if (gemv)
+    launch_gemv_w4pk<true>(x, ldx, frag, frag_scales, gs, h, ldh, (int)m, (int)(2 * i), (int)k, s);
+  else if (cw == 96)
     launch_w4pk<96, true>(x, ldx, frag, frag_scales, gs, h, ldh, (int)m, (int)(2 * i), (int)k, 1, nullptr, s);
   else
     launch_w4pk<64, true>(x, ldx, frag, frag_scales, gs, h, ldh, (int)m, (int)(2 * i), (int)k, 1, nullptr, s);

@@ -311,9 +311,11 @@ int ff_pack_scales_int4(const void* scales, void* frag_scales, int64_t n, int64_
  * _family/night_runtime.py:31-42). The same dequantised values and, unsplit,
  * the same bits as ff_gemm_w4a16; where it splits K (grids that would leave
  * CUs idle) the fp32 partials go to the workspace and a second launch adds them
- * in split order. Shapes the packed kernel does not take (m <= 4, k % 256,
- * group not a power of two >= 32, n % 256 unless the 144 x 384 tiles fill the
- * GPU) and a null frag run ff_gemm_w4a16_ws on packed / scales. ff_gemm_w4a16_pk_workspace stores
+ * in split order. Rows m <= 4 (n % 16, k % 128) run a GEMV on the same
+ * copies: the same bf16 weights, summed in another fp32 order. Shapes neither
+ * takes (k % 256 for m > 4, group not a power of two >= 32, n % 256 unless the
+ * 144 x 384 tiles fill the GPU) and a null frag run ff_gemm_w4a16_ws on
+ * packed / scales. ff_gemm_w4a16_pk_workspace stores
  * the bytes either path wants; workspace 16-byte aligned; calls that overlap
  * must not share it. */
 int ff_gemm_w4a16_pk_workspace(int64_t m, int64_t n, int64_t k, int64_t group, int64_t* bytes);
@@ -327,9 +329,10 @@ int ff_gemm_w4a16_pk(const void* x, int64_t ldx, const void* packed, const void*
  * (2 i, k) weight and its [k/group, 2 i, 2] scales).
  * No reference counterpart as one op: Int4.__call__ (_family/night_runtime.py:
  * 31-42) then swiglu (_legacy/search_kernels.py:8-23), the same bits.
- * ff_gemm_w4a16_swiglu_fits (no GPU needed) reports whether the kernel takes
- * the shape (m > 4, i % 128, k % 256, group a power of two >= 32 dividing k);
- * other shapes are rejected with FF_EINVAL. h row stride ldh (multiple of 4). */
+ * ff_gemm_w4a16_swiglu_fits (no GPU needed) reports whether a kernel takes the
+ * shape (m > 4: the tile kernel, i % 128, k % 256; 1 <= m <= 4: the GEMV,
+ * i % 16, k % 128; group a power of two >= 32 dividing k); other shapes are
+ * rejected with FF_EINVAL. h row stride ldh (multiple of 4). */
 int ff_gemm_w4a16_swiglu_fits(int64_t m, int64_t i, int64_t k, int64_t group, int* fits);
 int ff_gemm_w4a16_swiglu_pk(const void* x, int64_t ldx, const void* frag, const void* frag_scales, int64_t group,
                             void* h, int64_t ldh, int64_t m, int64_t i, int64_t k, ff_stream_t stream);

@@ -73,8 +73,8 @@ def test_tuning_knobs_validate_without_a_gpu(lib_path):
 
 
 def test_w4a16_swiglu_shape_query_without_a_gpu(lib_path):
-    """ff_gemm_w4a16_swiglu_fits answers on the host: m > 4, i % 128, k % 256 and a
-    power-of-two group >= 32 dividing k."""
+    """ff_gemm_w4a16_swiglu_fits answers on the host: m > 4 with i % 128 and k % 256,
+    or m <= 4 with i % 16 and k % 128; a power-of-two group >= 32 dividing k."""
     import ctypes
     from fastforward_amd import _lib
     _lib.load()
@@ -85,7 +85,8 @@ def test_w4a16_swiglu_shape_query_without_a_gpu(lib_path):
         return ok.value
 
     assert fits(576, 12288, 4096, 128) == 1 and fits(320, 6144, 2048, 32) == 1 and fits(100, 640, 1024, 64) == 1
-    assert fits(4, 12288, 4096, 128) == 0          # the tail's rows take the GEMV-sized path
+    assert fits(4, 12288, 4096, 128) == 1 and fits(1, 16, 128, 32) == 1  # the tail's rows: the packed GEMV
+    assert fits(1, 8, 128, 32) == 0                # the GEMV takes 16-row blocks
     assert fits(576, 12288 + 64, 4096, 128) == 0   # i % 128
     assert fits(576, 12288, 4096 + 128, 128) == 0  # k % 256
     assert fits(576, 12288, 4096, 96) == 0         # group not a power of two

@@ -4,8 +4,10 @@ the oracle's exact dequantisation (Int4, _family/night_runtime.py:15-42).
 
 Bars: where neither kernel splits k, the packed kernel runs the same MFMAs on
 the same dequantised values in the same k order, so the bits are equal; with a
-k split only the fp32 order of adding the partials differs (|difference| <= 1
-bf16 ulp + 2^-21 sum |x w|, under 1% of outputs differing). Every shape is also held to the fp64 product
+k split, or on the single-row GEMV (m <= 4: the same bf16 weights, summed on
+v_dot2_f32_bf16 in another fp32 order), only the order of the fp32 sum
+differs (|difference| <= 1 bf16 ulp + 2^-21 sum |x w|, under 1% of outputs
+differing). Every shape is also held to the fp64 product
 with the exactly dequantised weight (relative RMS <= 5e-3, worst element <=
 0.05 of the output RMS), as the LDS-staged kernel's tests are."""
 import pytest
@@ -61,7 +63,7 @@ def _pk_splits(m, n, k):
 
 
 SHAPES = [(576, 4096, 24576), (576, 4096, 6144), (576, 12288, 4096), (576, 4096, 4096), (320, 2048, 6144),
-          (100, 1024, 512), (1, 12288, 4096)]
+          (100, 1024, 512), (1, 12288, 4096), (1, 4096, 4096), (3, 4096, 1040), (4, 1024, 16)]
 
 
 @pytest.mark.parametrize("m,k,n", SHAPES)
@@ -75,16 +77,8 @@ def test_w4a16_packed_vs_lds_kernel_and_exact(gpu, tuning, m, k, n, sym, group):
     outs = [op(xd) for _ in range(3)]
     assert all(torch.equal(outs[0], o) for o in outs[1:])
     dq = O.int4_dequant(op.packed.cpu(), op.scales.cpu(), group).double()
-    if m <= 4:  # the packed entry hands these rows to the LDS-staged kernel as it is
-        frag, op.frag = op.frag, None
-        assert torch.equal(outs[0], op(xd))
-        op.frag = frag
-        ref = None
-    else:
-        ref = _unsplit_lds(op, xd, tuning)
-    if ref is None:
-        pass
-    elif _pk_splits(m, n, k) == 1:
+    ref = _unsplit_lds(op, xd, tuning)
+    if m > 4 and _pk_splits(m, n, k) == 1:
         assert torch.equal(outs[0], ref), (m, k, n)
     else:
         # adding the splits' partials reassociates the fp32 sum: an absolute
@@ -118,6 +112,35 @@ def test_w4a16_packed_dequant_bit_exact_via_one_hot(gpu, n, k):
         y = op(torch.eye(k, dtype=BF16, device=DEV)).cpu()
         dq = O.int4_dequant(op.packed.cpu(), op.scales.cpu(), group).to(BF16)
         assert torch.equal(y, dq.T.contiguous()), (sym, group)
+
+
+@pytest.mark.parametrize("m,k,i", [(1, 4096, 12288), (3, 1024, 656)])
+@pytest.mark.parametrize("sym,group", [(True, 128), (False, 32)])
+def test_w4a16_swiglu_gemv_vs_exact(gpu, m, k, i, sym, group):
+    """The tail's fused gate/up + SwiGLU (single-row GEMV on the packed copies)
+    against the fp64 product with the dequantised weights rounded to bf16 (the
+    MFMA operand; the oracle's bf16-weight form), SwiGLU in fp64: relative RMS
+    <= 5e-3, and per element |h - want| <= 2^-6 |want| + 1e-3 RMS (h rounds g,
+    u, silu(g) and the product to bf16, about 4 ulps of its own size); the
+    unfused ops (tile kernel + swiglu) meet the same bar."""
+    from fastforward_amd import ops
+    from fastforward_amd.linear import Int4
+    x = torch.randn(m, k, generator=_g(80)).to(BF16)
+    w = (torch.randn(2 * i, k, generator=_g(81)) * 0.02).to(BF16)
+    op = Int4(w.to(DEV), group=group, symmetric=sym).pack()
+    assert op.swiglu_fits(m)
+    h = op.swiglu(x.to(DEV)).cpu().double()
+    dq = O.int4_dequant(op.packed.cpu(), op.scales.cpu(), group).to(BF16).double()
+    gu = x.double() @ dq.T
+    g, u = gu[:, :i], gu[:, i:]
+    want = g / (1 + torch.exp(-g)) * u
+    rms = want.pow(2).mean().sqrt()
+    bound = 2.0 ** -6 * want.abs() + 1e-3 * rms
+    assert float((h - want).pow(2).mean().sqrt() / rms) <= 5e-3
+    assert bool(((h - want).abs() <= bound).all())
+    gg, uu = op(x.to(DEV)).chunk(2, -1)
+    unf = ops.swiglu(gg, uu).cpu().double()
+    assert bool(((unf - want).abs() <= bound).all())
 
 
 @pytest.mark.parametrize("m,k,i", [(576, 4096, 12288), (320, 2048, 6144), (100, 1024, 640)])
