@@ -92,15 +92,17 @@ def option_ids_from_tokenizer(path, n=8):
     return [tok.encode(" " + chr(ord("A") + i), add_special_tokens=False).ids[0] for i in range(n)]
 
 
-def _linear(w, mode, static_bound):
+def _linear(w, mode, static_bound, oracle=False):
+    """One linear of the ``mode`` bank; ``oracle`` (int4 banks) keeps the fp32
+    dequantised weight for the first-call operator check (``Int4``)."""
     if mode == "fp8":
         return FP8Linear(w)
     if mode == "fp8_static":
         return RuntimeScaleLinear(w, 448.0 / static_bound)
     if mode == "w4a16":
-        return Int4(w)
+        return Int4(w, oracle=oracle)
     if mode == "int4":      # the reference's asymmetric group-32 quantizer
-        return Int4(w, group=32, symmetric=False)
+        return Int4(w, group=32, symmetric=False, oracle=oracle)
     raise ValueError(f"unknown linear mode {mode!r}")
 
 
@@ -116,9 +118,13 @@ def load_lm(path, cfg, option_ids, mode="fp8", device="cuda", static_bound=8.0, 
     layers = []
 
     def lin(w, j, role):
+        # the middle layer's int4 QKV carries the operator check, as pack_release
+        # builds it (_family/night_runtime.py:77)
+        oracle = j == cfg.layers // 2 and role == "qkv"
         if mode in MIXED_MODES:
-            return _linear(w, "int4" if bank_of(mode, j, cfg.layers, role) == "int4" else fp8_bank, static_bound)
-        return _linear(w, mode, static_bound)
+            bank = "int4" if bank_of(mode, j, cfg.layers, role) == "int4" else fp8_bank
+            return _linear(w, bank, static_bound, oracle)
+        return _linear(w, mode, static_bound, oracle)
     for j in range(cfg.layers):
         q = f"{p}layers.{j}."
         ops = {}

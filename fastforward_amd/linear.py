@@ -173,6 +173,30 @@ class StaticFP8Linear:
         return y
 
 
+def parity(op, x):
+    """``parity`` (_family/depth_fp8.py:29-37) for a static-scale linear and an
+    activation x: the e4m3 codes of the runtime-scale cast (ff_quant_static_fp8,
+    the cast the fused producers share) against an independent cast of the
+    same formula (torch: e4m3(clamp(x * inverse_scale, +-448)), round to nearest
+    even), byte for byte, and the op's output against the GEMM on those codes.
+    Returns {shape, inverse_scale, quant_bytes_exact, output_exact}; asserts both."""
+    flat = _rows(x).contiguous()
+    m, k = flat.shape
+    n = op.weight.shape[0]
+    q = torch.empty((m, k), device=flat.device, dtype=E4M3)
+    call("ff_quant_static_fp8", ptr(flat), ptr(q), m, m, k, float(op.inverse_scale), stream())
+    ref = (flat.float() * float(op.inverse_scale)).clamp(-448., 448.).to(E4M3)
+    exact = torch.equal(q.view(torch.uint8), ref.view(torch.uint8))
+    new = op(flat)
+    prev = torch.empty((m, n), device=flat.device, dtype=BF16)
+    call("ff_gemm_fp8", ptr(ref), ptr(op.input_scale), 0, ptr(op.weight), ptr(op.weight_scale), 0, ptr(prev), n, m, n,
+         k, stream())
+    result = dict(shape=[m, k], inverse_scale=op.inverse_scale, quant_bytes_exact=exact,
+                  output_exact=torch.equal(new.reshape(m, n), prev))
+    assert exact and result["output_exact"], result
+    return result
+
+
 class RuntimeScaleLinear(StaticFP8Linear):
     """``RuntimeScaleLinear`` (_family/depth_fp8.py:22-26): the activation multiplier is
     read at call time, so ``select`` can change it without re-building the op.
@@ -189,9 +213,15 @@ class RuntimeScaleLinear(StaticFP8Linear):
 class Int4:
     """W4A16 linear (_family/night_runtime.py:15-42). ``symmetric=True`` (default,
     group 128) stores s = bf16(amax/7) and z = 0; ``symmetric=False`` is the
-    reference's asymmetric min/max quantizer (group 32 there)."""
+    reference's asymmetric min/max quantizer (group 32 there).
 
-    def __init__(self, w, group=128, symmetric=True):
+    ``oracle=True`` keeps the fp32 dequantised weight ((q - 8) s + z) until the
+    first call, which checks its first output row against that weight in fp32:
+    ``operator_check`` = {passed: relative RMS <= 0.01, relative_rms, max_abs,
+    shape}, asserted (the reference's setup-time check, :28-41). The first call
+    must be eager (the check reads the result on the host)."""
+
+    def __init__(self, w, group=128, symmetric=True, oracle=False):
         n, k = w.shape
         assert n % 8 == 0 and k % 128 == 0 and k % group == 0
         w = w.detach().to(BF16).contiguous()
@@ -203,6 +233,21 @@ class Int4:
         call("ff_quant_weight_int4", ptr(w), ptr(self.packed), ptr(self.scales), n, k, group,
              1 if symmetric else 0, stream())
         self.frag = self.frag_scales = None
+        self.oracle = self.operator_check = None
+        if oracle:
+            q = torch.stack((self.packed >> 4, self.packed & 15), -1).reshape(n, k).float()
+            s, z = self.scales.float().permute(2, 1, 0)                      # (n, k / group) each
+            self.oracle = ((q.reshape(n, -1, group) - 8) * s[..., None] + z[..., None]).reshape(n, k)
+
+    def _check(self, flat, y):
+        """The first-call operator check against the fp32 dequantised weight."""
+        reference = torch.nn.functional.linear(flat[:1].float(), self.oracle)
+        delta = y[:1].float() - reference
+        rms = float(delta.square().mean().sqrt() / (reference.square().mean().sqrt() + 1e-12))
+        self.operator_check = dict(passed=rms <= .01, relative_rms=rms, max_abs=float(delta.abs().max()),
+                                   shape=list(flat.shape))
+        self.oracle = None
+        assert self.operator_check["passed"], self.operator_check
 
     def pack(self):
         """Add the copies the packed kernels read: the nibbles in MFMA-fragment
@@ -233,11 +278,13 @@ class Int4:
             ws = torch.empty(need.value, device=x.device, dtype=torch.uint8) if need.value else None
             call("ff_gemm_w4a16_pk", ptr(flat), flat.stride(0), ptr(self.packed), ptr(self.frag), ptr(self.scales),
                  ptr(self.frag_scales), self.group, ptr(y), y.stride(0), m, n, k, ptr(ws), need.value, stream())
-            return y
-        call("ff_gemm_w4a16_workspace", m, n, k, ctypes.byref(need))
-        ws = torch.empty(need.value, device=x.device, dtype=torch.uint8) if need.value else None
-        call("ff_gemm_w4a16_ws", ptr(flat), flat.stride(0), ptr(self.packed), ptr(self.scales), self.group,
-             ptr(y), y.stride(0), m, n, k, ptr(ws), need.value, stream())
+        else:
+            call("ff_gemm_w4a16_workspace", m, n, k, ctypes.byref(need))
+            ws = torch.empty(need.value, device=x.device, dtype=torch.uint8) if need.value else None
+            call("ff_gemm_w4a16_ws", ptr(flat), flat.stride(0), ptr(self.packed), ptr(self.scales), self.group,
+                 ptr(y), y.stride(0), m, n, k, ptr(ws), need.value, stream())
+        if self.oracle is not None:
+            self._check(flat, y)
         return y
 
     def qkv(self, x, hq, hk, q_norm, k_norm, cos, sin):
@@ -250,6 +297,8 @@ class Int4:
         flat = _rows(x)
         if flat.stride(-1) != 1 or flat.stride(0) % 8:
             flat = flat.contiguous()
+        if self.oracle is not None:
+            self(flat[:1])  # the first-call operator check, on the GEMM alone
         m, k = flat.shape
         need = ctypes.c_int64(0)
         call("ff_gemm_w4a16_qkv_workspace", m, k, hq, hk, self.group, ctypes.byref(need))
@@ -283,6 +332,8 @@ class Int4:
         flat = _rows(x)
         if flat.stride(-1) != 1 or flat.stride(0) % 8:
             flat = flat.contiguous()
+        if self.oracle is not None:
+            self(flat[:1])  # the first-call operator check, on the GEMM alone
         m, k = flat.shape
         i = self.weight.shape[0] // 2
         if not self.swiglu_fits(m):

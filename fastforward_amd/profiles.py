@@ -58,3 +58,59 @@ def apply_profile(weights, bounds):
     if n == 0:
         raise ValueError("the model has no static FP8 linears to calibrate")
     return n
+
+
+def model_parity(cfg, weights, ids, pos, pick, profiles=None):
+    """``model_parity`` (_family/depth_fp8.py:40-62): one step of the
+    reference's op sequence (the generic path) with the static FP8 linears of
+    the middle layer (every role) and of the final layer (gate/up, down)
+    observed, then ``linear.parity`` for each observed (op, activation) under
+    every calibration variant of ``profiles`` ({variant: {"j:role": bound}};
+    None: the ops' current scales). The ops' scales are restored afterwards.
+    Returns the checks {role, variant, shape, inverse_scale, quant_bytes_exact,
+    output_exact}; ``parity`` asserts each."""
+    import torch
+    from .linear import parity
+    from .runtime import Runtime
+    captured = {}
+
+    class Observe:
+        def __init__(self, op, key):
+            self.op, self.key = op, key
+
+        def __getattr__(self, name):
+            return getattr(self.op, name)
+
+        def __call__(self, x):
+            captured[self.key] = (self.op, x.detach().clone())
+            return self.op(x)
+
+    layers = weights.layers
+    mid, final = len(layers) // 2, len(layers) - 1
+    originals = []
+    for j in sorted({mid, final}):
+        for attr, role in ROLE_KEYS.items():
+            op = getattr(layers[j], attr)
+            if isinstance(op, StaticFP8Linear) and (j == mid or role in ("gateup", "down")):
+                originals.append((layers[j], attr, op))
+                setattr(layers[j], attr, Observe(op, f"{j}:{role}"))
+    try:
+        rt = Runtime(cfg, weights, len(ids), path="generic")
+        rt.set_inputs(ids, pos, pick)
+        rt.step()
+        torch.cuda.synchronize()
+    finally:
+        for layer, attr, op in originals:
+            setattr(layer, attr, op)
+    checks = []
+    for key, (op, x) in captured.items():
+        inverse, scale = op.inverse_scale, op.input_scale.clone()
+        try:
+            for name, bounds in (profiles or {"anchor": None}).items():
+                if bounds is not None:
+                    op.set_bound(float(bounds[key]))
+                checks.append(dict(role=key, variant=name, **parity(op, x)))
+        finally:
+            op.inverse_scale = inverse
+            op.input_scale.copy_(scale)
+    return checks

@@ -112,6 +112,28 @@ def test_loaded_mixed_banks(gpu, tmp_path, mode):
 
 
 @pytest.mark.gpu
+def test_loaded_int4_operator_check(gpu, tmp_path):
+    """Loaded in the int4 mode, the middle layer's QKV (and only it) keeps the
+    fp32 dequantised weight, as pack_release builds it; the step's first call
+    runs the operator check on the loaded weights and passes."""
+    from fastforward_amd.checkpoint import load_pretrained
+    from fastforward_amd.runtime import Runtime
+    from fastforward_amd.synthetic import make_request
+    m, path = _tiny_hf(tmp_path, seed=4, layers=4)
+    lm, lw, _, _, _ = load_pretrained(path, option_ids=list(range(10, 18)), mode="int4")
+    mid = lm.layers // 2
+    assert lw.layers[mid].qkv.oracle is not None
+    assert all(getattr(L, r).oracle is None for j, L in enumerate(lw.layers) for r in ("qkv", "o", "gateup", "down")
+               if (j, r) != (mid, "qkv"))
+    rt = Runtime(lm, lw, 64)
+    rt.set_inputs(*make_request(lm, 64, 2, 2, seed=1))
+    rt.step()
+    torch.cuda.synchronize()
+    chk = lw.layers[mid].qkv.operator_check
+    assert chk is not None and chk["passed"] and chk["relative_rms"] <= 0.01, chk
+
+
+@pytest.mark.gpu
 def test_image_step_on_loaded_weights_matches_transformers(gpu, tmp_path):
     from fastforward_amd.checkpoint import load_pretrained
     from fastforward_amd.pipeline import ImageStep
