@@ -176,6 +176,52 @@ __device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
 // SiLU as the reference writes it: g / (1 + exp(-g)), correctly rounded divide.
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
+// bf16(silu(g)) for a bf16 g, given as its 16 bits b, without evaluating exp
+// and the divide per element: |g| in [2^-8, 128) (bits & 0x7FFF in [kSiluLo,
+// kSiluHi)) reads a table of round_bf16(silu(g)) that silu_table_fill writes
+// with the function above (one entry per bf16 value of that range and sign, so
+// the result is the same bits by construction). Outside it:
+// * |g| < 2^-8 (zero and subnormals included): exp(-g) is within 2^-8 of 1 and
+//   silu(g) = g/2 (1 + g/2 + O(g^3)) is less than a quarter bf16 ulp from g/2,
+//   so the result is round_bf16(g / 2);
+// * |g| >= 128: for g > 0, 1 + exp(-g) rounds to 1 and the result is g; for
+//   g < 0, exp(-g) overflows to inf and g / inf = -0 (NaN for g = -inf); both
+//   are g * (g > 0 ? 1 : 0), and NaN stays NaN.
+// Every bf16 pattern is compared with the exact form through the fused SwiGLU
+// GEMM epilogues in the tests.
+constexpr uint32_t kSiluLo = 0x3B80u, kSiluHi = 0x4300u, kSiluSpan = kSiluHi - kSiluLo;
+constexpr int kSiluEntries = 2 * (int)kSiluSpan;  // positive g, then negative g
+
+// NT threads (a divisor of kSiluEntries) fill the table; the entries of one
+// thread are independent, so the unrolled loop overlaps their exp / divide
+// latencies.
+template <int NT>
+__device__ __forceinline__ void silu_table_fill(uint16_t* tab, int tid) {
+  static_assert(kSiluEntries % NT == 0, "whole rounds");
+#pragma unroll
+  for (int c = 0; c < kSiluEntries / NT; ++c) {
+    const int e = tid + c * NT;
+    const uint32_t neg = e >= (int)kSiluSpan;
+    const uint32_t bits = (neg << 15) | (kSiluLo + (uint32_t)e - neg * kSiluSpan);
+    tab[e] = (uint16_t)f32_to_bf16(silu(bf16_to_f32(bits)));
+  }
+}
+
+// The table read for g (its bits b) and the result from it: split so that a
+// caller can issue many reads before it needs the first.
+__device__ __forceinline__ uint32_t silu_bf16_read(uint32_t b, const uint16_t* tab) {
+  const uint32_t a = b & 0x7FFFu, neg = b >> 15;
+  const uint32_t ia = min(max(a, kSiluLo), kSiluHi - 1u);
+  return tab[ia - kSiluLo + neg * kSiluSpan];
+}
+__device__ __forceinline__ float silu_bf16_finish(uint32_t b, uint32_t t) {
+  const uint32_t a = b & 0x7FFFu, neg = b >> 15;
+  const float g = bf16_to_f32(b);
+  const float small = round_bf16(g * 0.5f);
+  const float big = g * (neg ? 0.0f : 1.0f);
+  return a < kSiluLo ? small : (a >= kSiluHi ? big : bf16_to_f32(t));
+}
+
 // Per-token quantisation of 8 values: clamp(x / scale, +-448) -> e4m3, r = 1/scale.
 __device__ __forceinline__ u32x2 quant8(const float* x, float scale, float r) {
   float v[8];

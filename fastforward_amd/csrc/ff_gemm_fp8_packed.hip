@@ -92,12 +92,14 @@ __global__ __launch_bounds__(kThreads) void pack_fp8_kernel(const uint8_t* __res
 // of lane 16 g + r is tokens 16 i + r, weight rows 16 j + 4 g .. + 3) = sum over k steps
 // [kt0, kt0 + nk) of A . B^T. sB[j] is the byte offset of this wave's weight
 // fragment row j at k step 0. P = weight register stages, D = activation
-// register stages, G = k steps per barrier; nk % lcm(P, D, 2G) == 0.
-template <int BM, int CW, int P, int D, int G>
+// register stages, G = k steps per barrier; nk % lcm(P, D, 2G) == 0. pre()
+// runs once the first activation loads are issued, while they are in flight
+// (VALU work of the epilogue that does not depend on the product).
+template <int BM, int CW, int P, int D, int G, typename Pre>
 __device__ __forceinline__ void pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], uint8_t* smem,
                                             const uint8_t* __restrict__ qa, int M, int K, int m0,
                                             const uint8_t* __restrict__ qwp, uint32_t wbytes,
-                                            const uint32_t (&sB)[CW / 16], int kt0, int nk) {
+                                            const uint32_t (&sB)[CW / 16], int kt0, int nk, Pre&& pre) {
   constexpr int RA = BM / 16, TJ = CW / 16;
   constexpr int A_CHUNKS = BM * 8;  // 16-byte chunks of one A stage
   constexpr int FULL = A_CHUNKS / kThreads, REM = A_CHUNKS % kThreads;
@@ -177,6 +179,11 @@ __device__ __forceinline__ void pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], uint
   static_for<0, G>([&](auto S_) {
     constexpr int s = decltype(S_)::value;
     loadA(min(kt0 + s, kend - 1), I0{});
+    if constexpr (s == 0) {
+      __builtin_amdgcn_sched_barrier(0);
+      pre();
+      __builtin_amdgcn_sched_barrier(0);
+    }
     writeA(I0{}, std::integral_constant<int, s>{});
   });
   static_for<0, (D > P ? D : P)>([&](auto S_) {
@@ -250,6 +257,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
   static_assert(TJ % 2 == 0 && CH % 64 == 0, "gate/up fragment pairs; whole 64-channel row-max blocks");
   __shared__ __align__(1024) uint8_t smem[SMEM];
   __shared__ float pm16[BM][Q16];  // max |h| per token and 16-channel block of the tile
+  __shared__ uint16_t silu_tab[kSiluEntries];
 
   const int nblk = tiles_m * tiles_n;
   const int b = blockIdx.x;
@@ -271,10 +279,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
     sB[j] = (uint32_t)(row / 16) * (uint32_t)KT * 2048u;
   }
   f32x4 acc[RA][TJ];
-  pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)(2 * half) * (uint32_t)K, sB, 0, KT);
+  pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)(2 * half) * (uint32_t)K, sB, 0, KT,
+                               [&] { silu_table_fill<kThreads>(silu_tab, tid); });
 
   // g, u = bf16((acc * sa) * sw); h = bf16(bf16(silu(g)) * u), in registers:
   // lane 16 g + r holds token 16 i + r, channels c + 4 g .. + 3 of block t.
+  // bf16(silu(g)) comes from the table filled in the prologue (written before
+  // the main loop's first barrier). The row maximum is taken over |h| before
+  // the rounding: bf16 rounding is monotonic and odd, so rounding the maximum
+  // gives the maximum of the rounded values.
   const int c_base = tn * CH + wave * WCH + 4 * g;
   float swg[TT][4], swu[TT][4];
 #pragma unroll
@@ -284,29 +297,51 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
       swg[t][r] = sw[SQ ? 0 : c_base + 16 * t + r];
       swu[t][r] = sw[SQ ? 0 : half + c_base + 16 * t + r];
     }
+  // First every g of the tile and its table read (the reads are all in flight
+  // before the first result is needed), then h.
+  uint32_t gp[RA][TT][2], tv[RA][TT][4];
+  float sav[RA];
+#pragma unroll
+  for (int i = 0; i < RA; ++i) {
+    sav[i] = sa[SQ ? 0 : min(m0 + 16 * i + r16, M - 1)];
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; r += 2) {
+        const uint32_t p = pack_bf16x2((acc[i][2 * t][r] * sav[i]) * swg[t][r],
+                                       (acc[i][2 * t][r + 1] * sav[i]) * swg[t][r + 1]);
+        gp[i][t][r / 2] = p;
+        tv[i][t][r] = silu_bf16_read(p & 0xFFFFu, silu_tab);
+        tv[i][t][r + 1] = silu_bf16_read(p >> 16, silu_tab);
+      }
+  }
 #pragma unroll
   for (int i = 0; i < RA; ++i) {
     const int tl = 16 * i + r16, m = m0 + tl;
-    const float sav = sa[SQ ? 0 : min(m, M - 1)];
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
       float hv[4], mx = 0.f;
+      uint32_t up[2];
+#pragma unroll
+      for (int r = 0; r < 4; r += 2)
+        up[r / 2] = pack_bf16x2((acc[i][2 * t + 1][r] * sav[i]) * swu[t][r],
+                                (acc[i][2 * t + 1][r + 1] * sav[i]) * swu[t][r + 1]);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float gv = round_bf16((acc[i][2 * t][r] * sav) * swg[t][r]);
-        const float uv = round_bf16((acc[i][2 * t + 1][r] * sav) * swu[t][r]);
-        hv[r] = round_bf16(round_bf16(silu(gv)) * uv);
+        const uint32_t gb = r & 1 ? gp[i][t][r / 2] >> 16 : gp[i][t][r / 2] & 0xFFFFu;
+        const float uv = r & 1 ? __uint_as_float(up[r / 2] & 0xFFFF0000u) : __uint_as_float(up[r / 2] << 16);
+        hv[r] = silu_bf16_finish(gb, tv[i][t][r]) * uv;
         mx = fmaxf(mx, fabsf(hv[r]));
       }
       if constexpr (SQ) {
         if (m < M)
-          *reinterpret_cast<uint32_t*>(hq + (int64_t)m * ldh + c_base + 16 * t) =
-              quant4_static(hv[0], hv[1], hv[2], hv[3], qinv);
+          *reinterpret_cast<uint32_t*>(hq + (int64_t)m * ldh + c_base + 16 * t) = quant4_static(
+              round_bf16(hv[0]), round_bf16(hv[1]), round_bf16(hv[2]), round_bf16(hv[3]), qinv);
         continue;
       }
       if (m < M)
         *reinterpret_cast<u32x2*>(h + (int64_t)m * ldh + c_base + 16 * t) = pack4_bf16(hv[0], hv[1], hv[2], hv[3]);
-      mx = max_rows(mx);  // over the 4 lanes of this token: 16 channels
+      mx = max_rows(round_bf16(mx));  // over the 4 lanes of this token: 16 channels
       if (g == 0) pm16[tl][wave * TT + t] = mx;
     }
   }
@@ -386,7 +421,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_split_packed_kernel(
 #pragma unroll
   for (int j = 0; j < TJ; ++j) sB[j] = (uint32_t)((n0 + wave_s * CW + 16 * j) / 16) * (uint32_t)KT * 2048u;
   f32x4 acc[RA][TJ];
-  pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, split * nk, nk);
+  pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, split * nk, nk, [] {});
   if constexpr (S > 1) {
     f32x4* mine = part + ((int64_t)(tn * tiles_m + tm) * S + split) * (RA * TJ * kThreads) + tid;
 #pragma unroll

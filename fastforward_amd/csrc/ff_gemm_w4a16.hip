@@ -582,13 +582,13 @@ __global__ __launch_bounds__(kThreads) void pack_int4_kernel(const uint8_t* __re
 // layout) = sum over k steps [kt0, kt0 + nk) of A . B^T. sB[j]: byte offset of
 // this wave's weight fragment row j at k step 0; colS[j]: the weight row whose
 // (s, z) this lane reads for fragment j. nk even, kt0 even.
-template <int BM, int CW>
+template <int BM, int CW, typename Pre>
 __device__ __forceinline__ void w4pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], uint8_t* smem,
                                               const bf16_t* __restrict__ x, int64_t ldx, int M, int m0,
                                               const uint8_t* __restrict__ wp, uint32_t wbytes,
                                               const uint32_t (&sB)[CW / 16], const float* __restrict__ sz,
                                               uint32_t szbytes, const uint32_t (&colS)[CW / 16], int N, int gshift,
-                                              int kt0, int nk) {
+                                              int kt0, int nk, Pre&& pre) {
   constexpr int RA = BM / 16, TJ = CW / 16;
   constexpr int A_CHUNKS = BM * 16;  // 16-byte chunks of one A stage (BM rows x 256 bytes)
   constexpr int FULL = A_CHUNKS / kThreads, REM = A_CHUNKS % kThreads;
@@ -667,6 +667,9 @@ __device__ __forceinline__ void w4pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], ui
   using I1 = std::integral_constant<int, 1>;
   loadA(kt0);
   loadB(kt0, I0{});
+  __builtin_amdgcn_sched_barrier(0);
+  pre();  // epilogue set-up that does not depend on the product, while the loads are in flight
+  __builtin_amdgcn_sched_barrier(0);
   writeA(0);
   loadA(min(kt0 + 1, kend - 1));
   loadB(min(kt0 + 1, kend - 1), I1{});
@@ -789,6 +792,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_w4a16_pk_kernel(
   static_assert(SMEM <= 160 * 1024, "LDS budget");
   static_assert(!SWIGLU || TJ % 2 == 0, "gate/up fragment pairs");
   __shared__ __align__(1024) uint8_t smem[SMEM];
+  __shared__ uint16_t silu_tab[SWIGLU ? kSiluEntries : 1];  // bf16(silu(g)) by g (silu_bf16)
 
   const int nblk = tiles_m * tiles_n * splits;
   const int b = blockIdx.x;
@@ -814,21 +818,39 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_w4a16_pk_kernel(
   }
   f32x4 acc[RA][TJ];
   w4pk_mainloop<BM, CW>(acc, smem, x, ldx, M, m0, wp, (uint32_t)((int64_t)N * K / 2), sB, sz,
-                        (uint32_t)((int64_t)(K >> gshift) * N * 8), colS, N, gshift, 2 * p0, 2 * (p1 - p0));
+                        (uint32_t)((int64_t)(K >> gshift) * N * 8), colS, N, gshift, 2 * p0, 2 * (p1 - p0), [&] {
+                          if constexpr (SWIGLU) silu_table_fill<kThreads>(silu_tab, tid);
+                        });
 
   if constexpr (SWIGLU) {
+    // Every g of the tile and its table read first (all in flight before the
+    // first result is needed), then h.
     const int c_base = tn * CH + wave * WCH + 4 * g;
+    uint32_t gp[RA][TJ / 2][2], tv[RA][TJ / 2][4];
+#pragma unroll
+    for (int i = 0; i < RA; ++i)
+#pragma unroll
+      for (int t = 0; t < TJ / 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; r += 2) {
+          const uint32_t p = pack_bf16x2(acc[i][2 * t][r], acc[i][2 * t][r + 1]);
+          gp[i][t][r / 2] = p;
+          tv[i][t][r] = silu_bf16_read(p & 0xFFFFu, silu_tab);
+          tv[i][t][r + 1] = silu_bf16_read(p >> 16, silu_tab);
+        }
 #pragma unroll
     for (int i = 0; i < RA; ++i) {
       const int m = m0 + 16 * i + r16;
 #pragma unroll
       for (int t = 0; t < TJ / 2; ++t) {
         float hv[4];
+        const uint32_t up[2] = {pack_bf16x2(acc[i][2 * t + 1][0], acc[i][2 * t + 1][1]),
+                                pack_bf16x2(acc[i][2 * t + 1][2], acc[i][2 * t + 1][3])};
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float gv = round_bf16(acc[i][2 * t][r]);
-          const float uv = round_bf16(acc[i][2 * t + 1][r]);
-          hv[r] = round_bf16(round_bf16(silu(gv)) * uv);
+          const uint32_t gb = r & 1 ? gp[i][t][r / 2] >> 16 : gp[i][t][r / 2] & 0xFFFFu;
+          const float uv = r & 1 ? __uint_as_float(up[r / 2] & 0xFFFF0000u) : __uint_as_float(up[r / 2] << 16);
+          hv[r] = silu_bf16_finish(gb, tv[i][t][r]) * uv;  // rounded by the store's pack
         }
         if (m < M)
           *reinterpret_cast<u32x2*>(y + (int64_t)m * ldy + c_base + 16 * t) = pack4_bf16(hv[0], hv[1], hv[2], hv[3]);
