@@ -545,6 +545,21 @@ __global__ __launch_bounds__(kThreads, NS == 2 ? 2 : 1) void attention_prefill_k
     if (CAUSAL && (kb >= s_len || kb > wq0 + 16 * QT - 1)) continue;  // wave-uniform: no query of the wave sees it
     const uint8_t* st_base = smem + (ib % NS) * STAGE;
 
+    // Every K fragment of the block is read before the first S MFMA, and every
+    // V^T fragment right after the last one, so that these LDS reads are in
+    // flight together (one latency per group, the V^T reads under the softmax)
+    // instead of a few at a time ahead of each MFMA. The scheduling barriers
+    // keep the compiler from sinking the reads back to their uses. QT = 4 has
+    // no registers for that and reads each fragment ahead of its MFMAs.
+    constexpr bool BATCH = QT <= 2;
+    u32x4 kf[KST][4], vf[2][DTN];
+    if constexpr (BATCH) {
+#pragma unroll
+      for (int st = 0; st < KST; ++st)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kf[st][i] = *reinterpret_cast<const u32x4*>(st_base + koff(i >> 1, i & 1, st));
+      __builtin_amdgcn_sched_barrier(0);
+    }
     f32x4 sc[QT][4];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt)
@@ -554,10 +569,17 @@ __global__ __launch_bounds__(kThreads, NS == 2 ? 2 : 1) void attention_prefill_k
     for (int st = 0; st < KST; ++st)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const u32x4 kf = *reinterpret_cast<const u32x4*>(st_base + koff(i >> 1, i & 1, st));
+        if constexpr (!BATCH) kf[st][i] = *reinterpret_cast<const u32x4*>(st_base + koff(i >> 1, i & 1, st));
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) sc[qt][i] = mfma_bf16(kf, qf[qt][st], sc[qt][i]);
+        for (int qt = 0; qt < QT; ++qt) sc[qt][i] = mfma_bf16(kf[st][i], qf[qt][st], sc[qt][i]);
       }
+    if constexpr (BATCH) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int dt = 0; dt < DTN; ++dt) vf[c][dt] = *reinterpret_cast<const u32x4*>(st_base + voff(dt, c));
+      __builtin_amdgcn_sched_barrier(0);
+    }
     u32x4 pf[QT][2];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
@@ -571,9 +593,9 @@ __global__ __launch_bounds__(kThreads, NS == 2 ? 2 : 1) void attention_prefill_k
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int dt = 0; dt < DTN; ++dt) {
-        const u32x4 vf = *reinterpret_cast<const u32x4*>(st_base + voff(dt, c));
+        if constexpr (!BATCH) vf[c][dt] = *reinterpret_cast<const u32x4*>(st_base + voff(dt, c));
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) o[qt][dt] = mfma_bf16(vf, pf[qt][c], o[qt][dt]);
+        for (int qt = 0; qt < QT; ++qt) o[qt][dt] = mfma_bf16(vf[c][dt], pf[qt][c], o[qt][dt]);
       }
   }
 #pragma unroll
