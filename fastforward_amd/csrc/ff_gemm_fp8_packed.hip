@@ -396,7 +396,7 @@ __device__ __forceinline__ void pk_store_tile(const f32x4 (&acc)[BM / 16][CW / 1
 // of thread t at ((tile S + split) RA TJ + i TJ + j) 256 + t) and
 // split_reduce_kernel, the next launch, adds the partials.
 template <int BM, int CW, int P, int D, int G, int S>
-__global__ __launch_bounds__(kThreads, 1) void gemm_fp8_split_packed_kernel(
+__global__ __launch_bounds__(kThreads, BM < 144 ? 2 : 1) void gemm_fp8_split_packed_kernel(
     const uint8_t* __restrict__ qa, const float* __restrict__ sa, int sa_rows, const uint8_t* __restrict__ qwp,
     const float* __restrict__ sw, int sw_cols, bf16_t* __restrict__ y, int64_t ldy, int M, int N, int K,
     int tiles_m, int tiles_n, f32x4* __restrict__ part) {
@@ -486,12 +486,49 @@ constexpr int kSpU = lcm3(kSpP, kSpD, 2 * kSpG);
 // Splits for an m x n x k plain GEMM on the packed path, 0 if it does not take
 // it: one launch when the tiles fill the GPU, else 4 splits when k is long
 // enough that the extra reduction launch pays off (the 8B down projection,
-// 576 x 4096 x 12288); shorter k stays on the row-major kernels.
+// 576 x 4096 x 12288); shorter k takes small_plan's tiles (below) or the
+// row-major kernels.
 int split_plan(int64_t m, int64_t n, int64_t k) {
   if (m <= 4 || n % kSpBN || k % 128 || m * k >= (int64_t(1) << 31) || n * k >= (int64_t(1) << 31)) return 0;
   const int64_t tiles = (m + kSpBM - 1) / kSpBM * (n / kSpBN), kt = k / 128;
   if (tiles >= 192) return kt % kSpU == 0 ? 1 : 0;
   return kt >= 64 && kt % (4 * kSpU) == 0 ? 4 : 0;
+}
+
+// Unsplit plain GEMMs whose 144 x 256 tiles are too few and whose k is too
+// short to split (the 8B o projection, 576 x 4096 x 4096; a QKV-shaped plain
+// GEMM): smaller packed tiles at two workgroups per CU. BM x 4 CW with BM =
+// 64, CW = 64, else BM = 96, CW = 32, else BM = 64, CW = 32, the first whose
+// grid has 192 .. 512 workgroups. A wave still owns all BM rows of its CW
+// weight rows, so each weight fragment feeds BM / 16 MFMAs and the
+// activations alone go through LDS (the row-major kernels' 2 x 2 waves at 64
+// x 128 read both operands from LDS: 1.8-2.5 us slower at these shapes).
+struct SmallTile {
+  int bm = 0, cw = 0;
+};
+SmallTile small_plan(int64_t m, int64_t n, int64_t k) {
+  SmallTile t;
+  if (m <= 4 || k % (128 * kSpU) || m * k >= (int64_t(1) << 31) || n * k >= (int64_t(1) << 31)) return t;
+  constexpr int cand[3][2] = {{64, 64}, {96, 32}, {64, 32}};
+  for (const auto& c : cand) {
+    if (n % (4 * c[1])) continue;
+    const int64_t tiles = (m + c[0] - 1) / c[0] * (n / (4 * c[1]));
+    if (tiles >= 192 && tiles <= 512) {
+      t.bm = c[0];
+      t.cw = c[1];
+      return t;
+    }
+  }
+  return t;
+}
+
+template <int BM, int CW>
+void launch_small(const void* qa, const float* sa, int sa_rows, const void* qw_packed, const float* sw, int sw_cols,
+                  void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, hipStream_t st) {
+  const int64_t tm = (m + BM - 1) / BM, tn = n / (4 * CW);
+  hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<BM, CW, kSpP, kSpD, kSpG, 1>), dim3((unsigned)(tm * tn)),
+                     dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows, (const uint8_t*)qw_packed, sw, sw_cols,
+                     (bf16_t*)y, ldy, (int)m, (int)n, (int)k, (int)tm, (int)tn, (f32x4*)nullptr);
 }
 
 int64_t split_workspace(int64_t m, int64_t n, int64_t k) {
@@ -569,7 +606,23 @@ extern "C" int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, cons
                         ff_aligned(y, 16)
                     ? split_plan(m, n, k)
                     : 0;
-  if (s == 0) return ff_gemm_fp8(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, stream);
+  if (s == 0) {
+    const SmallTile t = qw_packed && ldy % 8 == 0 && ldy >= n && ff_aligned(qa, 16) && ff_aligned(qw_packed, 16) &&
+                                ff_aligned(y, 16)
+                            ? small_plan(m, n, k)
+                            : SmallTile{};
+    hipStream_t st = (hipStream_t)stream;
+    if (t.bm == 64 && t.cw == 64)
+      launch_small<64, 64>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, st);
+    else if (t.bm == 96)
+      launch_small<96, 32>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, st);
+    else if (t.bm == 64)
+      launch_small<64, 32>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, st);
+    else
+      return ff_gemm_fp8(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, stream);
+    FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
+    return FF_OK;
+  }
   const int64_t need = split_workspace(m, n, k);
   FF_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && ff_aligned(workspace, 16)),
              "ff_gemm_fp8_pk: workspace of %lld bytes (16-byte aligned) required", (long long)need);

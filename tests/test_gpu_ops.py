@@ -358,9 +358,12 @@ def test_gemm_fp8_swiglu_packed_equals_rowmajor(gpu, m, i, k):
     assert torch.equal(h0, h1) and torch.equal(p0, p1)
 
 
-# (m, n, k, splits the packed path takes); 0 = not taken (row-major kernels)
+# (m, n, k, splits the packed path takes); 0 = unsplit on the small packed tiles
+# (576 x 4096 x 4096: 96 x 128; 576 / 500 x 6144 x 4096: 64 x 256, the last
+# tile ragged) or the row-major kernels (too few tiles, 3 rows, n % 128)
 PK_SHAPES = [(576, 4096, 12288, 4), (300, 2048, 8192, 4), (1000, 6144, 8192, 4), (576, 12288, 4096, 1),
-             (576, 4096, 4096, 0), (3, 4096, 4096, 0), (576, 4160, 12288, 0)]
+             (576, 4096, 4096, 0), (576, 6144, 4096, 0), (500, 6144, 4096, 0), (300, 4096, 2048, 0),
+             (3, 4096, 4096, 0), (576, 4160, 12288, 0)]
 
 
 @pytest.mark.parametrize("m,n,k,splits", PK_SHAPES)
