@@ -42,15 +42,19 @@
 //   the epilogue reads them (ACC_NOPS).
 //
 // Packed layout (ff_pack_weight_fp8): fragment (f, kt) of rows [16 f, 16 f + 16)
-// and k bytes [128 kt, 128 kt + 128) is the 2048 bytes at (f * K/128 + kt) * 2048;
-// lane l = 16 g + r holds row 16 f + r, k bytes [128 kt + 32 g, +16) at 16 l and
-// [128 kt + 32 g + 16, +16) at 1024 + 16 l.
+// and k bytes [128 kt, 128 kt + 128) is the 2048 bytes at (kt * N/16 + f) * 2048
+// (k-step major: the fragments every workgroup reads at one k step are
+// contiguous; with the rows' k steps contiguous instead, the loads in flight
+// together sat 64 KB apart and streamed weights from HBM 0.5-2 us slower per
+// GEMM); lane l = 16 g + r holds row 16 f + r, k bytes [128 kt + 32 g, +16) at
+// 16 l and [128 kt + 32 g + 16, +16) at 1024 + 16 l.
 // That is the operand layout of the MFMA for both A and B (the row-major
 // kernels feed the same k range to the same lane).
 #include <stdio.h>
 #include <type_traits>
 
 #include "ff_common.h"
+#include "ff_rope.h"
 
 using namespace ff;
 
@@ -79,9 +83,10 @@ __global__ __launch_bounds__(kThreads) void pack_fp8_kernel(const uint8_t* __res
     const int l = (int)(i & 63);
     const int64_t f = i >> 6;  // fragment index f16 * kt_n + kt
     const int64_t kt = f % kt_n, f16 = f / kt_n;
+    const int64_t nf = n / 16;
     const int64_t row = f16 * 16 + (l & 15);
     const u32x4* src = reinterpret_cast<const u32x4*>(w + row * k + kt * 128 + 32 * (l >> 4));
-    uint8_t* dst = p + f * 2048 + 16 * l;
+    uint8_t* dst = p + (kt * nf + f16) * 2048 + 16 * l;
     *reinterpret_cast<u32x4*>(dst) = src[0];
     *reinterpret_cast<u32x4*>(dst + 1024) = src[1];
   }
@@ -144,14 +149,15 @@ __device__ __forceinline__ void pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], uint
   };
 
   const __amdgpu_buffer_rsrc_t rB = make_rsrc(qwp, wbytes);
+  const uint32_t kstride = wbytes / (uint32_t)(K / 128);
   const uint32_t voffB = 16u * (uint32_t)lane;
   i32x8 bq[P][TJ];
   auto loadB = [&](int kt, auto SLOT) {
     constexpr int slot = decltype(SLOT)::value;
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
-      const i32x4v lo = bload16(rB, voffB, sB[j] + (uint32_t)kt * 2048u);
-      const i32x4v hi = bload16(rB, voffB + 1024u, sB[j] + (uint32_t)kt * 2048u);
+      const i32x4v lo = bload16(rB, voffB, sB[j] + (uint32_t)kt * kstride);
+      const i32x4v hi = bload16(rB, voffB + 1024u, sB[j] + (uint32_t)kt * kstride);
       bq[slot][j] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
     }
   };
@@ -219,8 +225,8 @@ __device__ __forceinline__ void pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], uint
         constexpr int j = decltype(J_)::value;
 #pragma unroll
         for (int i = 0; i < RA; ++i) mfma_acc(acc[i][j], bq[u % P][j], af[i]);
-        const i32x4v lo = bload16(rB, voffB, sB[j] + ktn * 2048u);
-        const i32x4v hi = bload16(rB, voffB + 1024u, sB[j] + ktn * 2048u);
+        const i32x4v lo = bload16(rB, voffB, sB[j] + ktn * kstride);
+        const i32x4v hi = bload16(rB, voffB + 1024u, sB[j] + ktn * kstride);
         bq[u % P][j] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
       });
     });
@@ -276,7 +282,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
     const int row = (j & 1 ? half : 0) + tn * CH + wave_s * WCH + 16 * (j >> 1);
-    sB[j] = (uint32_t)(row / 16) * (uint32_t)KT * 2048u;
+    sB[j] = (uint32_t)(row / 16) * 2048u;
   }
   f32x4 acc[RA][TJ];
   pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)(2 * half) * (uint32_t)K, sB, 0, KT,
@@ -419,7 +425,7 @@ __global__ __launch_bounds__(kThreads, BM < 144 ? 2 : 1) void gemm_fp8_split_pac
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   uint32_t sB[TJ];
 #pragma unroll
-  for (int j = 0; j < TJ; ++j) sB[j] = (uint32_t)((n0 + wave_s * CW + 16 * j) / 16) * (uint32_t)KT * 2048u;
+  for (int j = 0; j < TJ; ++j) sB[j] = (uint32_t)((n0 + wave_s * CW + 16 * j) / 16) * 2048u;
   f32x4 acc[RA][TJ];
   pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, split * nk, nk, [] {});
   if constexpr (S > 1) {
@@ -537,6 +543,128 @@ int64_t split_workspace(int64_t m, int64_t n, int64_t k) {
   return (m + kSpBM - 1) / kSpBM * (n / kSpBN) * s * kSpBM * kSpBN * 4;
 }
 
+// Fused QKV on fragment-packed weights: BM tokens x BN = 4 CW channels (BN /
+// 128 whole heads) per workgroup, the packed main loop at two workgroups per
+// CU. The tile y = bf16((acc * sa) * sw) is written to LDS as a row-major
+// bf16 tile (lane 16 g + r of fragment (i, j) holds token 16 i + r, columns
+// wave CW + 16 j + 4 g .. + 3: one 8-byte store), then each head of the tile
+// gets the epilogue of the row-major QKV kernel, the same code on the same
+// bits: q/k heads the per-head RMSNorm + rotary (rope_row_pre, 16 lanes per
+// token row) stored head-major, v heads stored transposed with zeros for the
+// tokens in [M, t_pad).
+struct PkQkv {
+  const bf16_t* qn;  // q_norm weight (128)
+  const bf16_t* kn;  // k_norm weight (128)
+  float eps_q, eps_k;
+  const bf16_t* cos;  // (M, 128)
+  const bf16_t* sin;
+  bf16_t* yq;  // (hq, M, 128)
+  bf16_t* yk;  // (hk, M, 128)
+  bf16_t* vt;  // (hk, 128, t_pad)
+  int hq, hk, t_pad;
+};
+
+template <int BM, int CW, int P, int D, int G>
+__global__ __launch_bounds__(kThreads, 2) void gemm_fp8_qkv_packed_kernel(
+    const uint8_t* __restrict__ qa, const float* __restrict__ sa, int sa_rows, const uint8_t* __restrict__ qwp,
+    const float* __restrict__ sw, int sw_cols, int M, int N, int K, int tiles_m, int tiles_n, PkQkv qe) {
+  constexpr int BN = 4 * CW, RA = BM / 16, TJ = CW / 16;
+  static_assert(BN % kHeadDim == 0, "whole heads per tile");
+  constexpr int HPT = BN / kHeadDim;         // heads per tile
+  constexpr int LD = BN + 8;                 // bf16 row pitch of the LDS tile
+  constexpr int ROWS = BM / (kThreads / 16);  // token rows per 16-lane group
+  constexpr int SMEM_LOOP = pk_smem<BM, G>(), SMEM_TILE = BM * LD * 2;
+  constexpr int SMEM = SMEM_LOOP > SMEM_TILE ? SMEM_LOOP : SMEM_TILE;
+  static_assert(SMEM <= 80 * 1024, "two workgroups per CU");
+  __shared__ __align__(1024) uint8_t smem[SMEM];
+
+  const int nblk = tiles_m * tiles_n;
+  const int b = blockIdx.x;
+  int logical = b;
+  if (nblk % kXcds == 0) logical = (b % kXcds) * (nblk / kXcds) + b / kXcds;
+  const int tm = logical % tiles_m, tn = logical / tiles_m;  // M fastest: L2 shares weights
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int KT = K / 128;
+
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  uint32_t sB[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) sB[j] = (uint32_t)((n0 + wave_s * CW + 16 * j) / 16) * 2048u;
+  f32x4 acc[RA][TJ];
+  pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, 0, KT, [] {});
+
+  // The epilogue's global loads (norm weights, this thread's cos / sin rows)
+  // are issued before the tile is staged.
+  const int jr = tid & 15, grp = tid >> 4;
+  float rope_w[HPT][8];
+  u32x4 rope_c[ROWS], rope_s[ROWS];
+#pragma unroll
+  for (int hh = 0; hh < HPT; ++hh) {
+    const int head = tn * HPT + hh;
+    if (head < qe.hq + qe.hk) unpack8(*reinterpret_cast<const u32x4*>((head < qe.hq ? qe.qn : qe.kn) + 8 * jr), rope_w[hh]);
+  }
+#pragma unroll
+  for (int p = 0; p < ROWS; ++p) {
+    const int mm = min(m0 + grp + p * (kThreads / 16), M - 1);
+    rope_c[p] = *reinterpret_cast<const u32x4*>(qe.cos + (size_t)mm * kHeadDim + 8 * jr);
+    rope_s[p] = *reinterpret_cast<const u32x4*>(qe.sin + (size_t)mm * kHeadDim + 8 * jr);
+  }
+
+  __syncthreads();  // every wave's last activation-stage reads are done before the tile overwrites them
+  bf16_t* tile = reinterpret_cast<bf16_t*>(smem);
+  float sav[RA];
+#pragma unroll
+  for (int i = 0; i < RA; ++i) sav[i] = sa[sa_rows ? min(m0 + 16 * i + r16, M - 1) : 0];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int col = wave * CW + 16 * j + 4 * g;
+    float swv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) swv[r] = sw[sw_cols ? n0 + col + r : 0];
+#pragma unroll
+    for (int i = 0; i < RA; ++i)
+      *reinterpret_cast<u32x2*>(tile + (16 * i + r16) * LD + col) =
+          pack4_bf16((acc[i][j][0] * sav[i]) * swv[0], (acc[i][j][1] * sav[i]) * swv[1],
+                     (acc[i][j][2] * sav[i]) * swv[2], (acc[i][j][3] * sav[i]) * swv[3]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int hh = 0; hh < HPT; ++hh) {
+    const int head = tn * HPT + hh;
+    if (head < qe.hq + qe.hk) {
+      const bool isq = head < qe.hq;
+      const int hx = isq ? head : head - qe.hq;
+      const float eps = isq ? qe.eps_q : qe.eps_k;
+      bf16_t* dst = (isq ? qe.yq : qe.yk) + (size_t)hx * M * kHeadDim;
+#pragma unroll
+      for (int p = 0; p < ROWS; ++p) {
+        const int rl = grp + p * (kThreads / 16);
+        const int m = m0 + rl;
+        const bool valid = m < M;
+        const int mm = valid ? m : M - 1;
+        rope_row_pre(tile + rl * LD + hh * kHeadDim, rope_w[hh], eps, rope_c[p], rope_s[p],
+                     dst + (size_t)mm * kHeadDim, jr, valid);
+      }
+    } else {
+      const int hv = head - qe.hq - qe.hk;
+      for (int c = tid; c < kHeadDim * (BM / 8); c += kThreads) {
+        const int d = c % kHeadDim, t0 = (c / kHeadDim) * 8;
+        const int tok = m0 + t0;
+        if (tok >= qe.t_pad) continue;
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = (tok + e < M) ? bf16_to_f32(tile[(t0 + e) * LD + hh * kHeadDim + d]) : 0.f;
+        *reinterpret_cast<u32x4*>(qe.vt + ((size_t)hv * kHeadDim + d) * qe.t_pad + tok) = pack8(f);
+      }
+    }
+  }
+}
+
+// Fused QKV tile: 64 tokens x 256 channels (two heads).
+constexpr int kQkBM = 64, kQkCW = 64;
+
 }  // namespace
 
 extern "C" int ff_pack_weight_fp8(const void* w, void* packed, int64_t n, int64_t k, ff_stream_t stream) {
@@ -643,5 +771,30 @@ extern "C" int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, cons
                        (const f32x4*)part, sa, sa_rows, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)tiles_m);
   }
   FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_fp8_qkv_pk(const void* qa, const float* sa, int sa_rows, const void* qw, const void* qw_packed,
+                                  const float* sw, int sw_cols, int64_t m, int64_t k, int64_t hq, int64_t hk,
+                                  const void* q_norm, const void* k_norm, float eps_q, float eps_k, const void* cos,
+                                  const void* sin, void* yq, void* yk, void* vt, int64_t t_pad, ff_stream_t stream) {
+  const int64_t n = (hq + 2 * hk) * kHeadDim;
+  const int64_t tiles_m = (m + kQkBM - 1) / kQkBM, tiles_n = n / (4 * kQkCW), tiles = tiles_m * tiles_n;
+  const bool fits = qw_packed && m > 4 && hq > 0 && hk > 0 && hq % hk == 0 && n % (4 * kQkCW) == 0 &&
+                    k > 0 && k % (128 * kSpU) == 0 && tiles >= 192 && tiles <= 512 && t_pad >= m && t_pad % 64 == 0 &&
+                    t_pad <= tiles_m * kQkBM && m * k < (int64_t(1) << 31) && n * k < (int64_t(1) << 31) &&
+                    ff_aligned(qa, 16) && ff_aligned(qw_packed, 16) && ff_aligned(cos, 16) && ff_aligned(sin, 16) &&
+                    ff_aligned(q_norm, 16) && ff_aligned(k_norm, 16) && ff_aligned(yq, 16) && ff_aligned(yk, 16) &&
+                    ff_aligned(vt, 16);
+  if (!fits)
+    return ff_gemm_fp8_qkv(qa, sa, sa_rows, qw, sw, sw_cols, m, k, hq, hk, q_norm, k_norm, eps_q, eps_k, cos, sin, yq,
+                           yk, vt, t_pad, stream);
+  FF_REQUIRE(sa && sw && q_norm && k_norm && yq && yk && vt, "ff_gemm_fp8_qkv_pk: null pointer");
+  PkQkv qe{(const bf16_t*)q_norm, (const bf16_t*)k_norm, eps_q, eps_k, (const bf16_t*)cos, (const bf16_t*)sin,
+           (bf16_t*)yq, (bf16_t*)yk, (bf16_t*)vt, (int)hq, (int)hk, (int)t_pad};
+  hipLaunchKernelGGL((gemm_fp8_qkv_packed_kernel<kQkBM, kQkCW, kSpP, kSpD, kSpG>), dim3((unsigned)tiles),
+                     dim3(kThreads), 0, (hipStream_t)stream, (const uint8_t*)qa, sa, sa_rows, (const uint8_t*)qw_packed,
+                     sw, sw_cols, (int)m, (int)n, (int)k, (int)tiles_m, (int)tiles_n, qe);
+  FF_LAUNCH_CHECK("ff_gemm_fp8_qkv_pk");
   return FF_OK;
 }

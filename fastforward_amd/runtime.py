@@ -226,6 +226,7 @@ class Runtime:
                                 else "StaticFP8Linear / RuntimeScaleLinear (calibrated per-tensor)") + " weights")
         if self.path in ("fused", "fused_static"):
             for L in weights.layers:  # MFMA-fragment copies for the packed tile kernels (once per weight)
+                L.qkv.pack()
                 L.o.pack()
                 L.gateup.pack()
                 L.down.pack()
@@ -351,10 +352,10 @@ class Runtime:
         T, Tp, H, D = self.T, self.Tp, cfg.hidden, cfg.head_dim
         HQ, HK = cfg.heads, cfg.kv_heads
         # QKV GEMM with q/k norm + rotary and the V transpose in its epilogue
-        call("ff_gemm_fp8_qkv", ptr(self.xq), ptr(self.xs), 1, ptr(lw.qkv.weight), ptr(lw.qkv.scale), 1, T, H, HQ, HK,
-             ptr(lw.q_norm.weight), ptr(lw.k_norm.weight), float(lw.q_norm.variance_epsilon),
-             float(lw.k_norm.variance_epsilon), ptr(self.cos), ptr(self.sin), ptr(self.yq), ptr(self.yk),
-             ptr(self.vt), Tp, s)
+        call("ff_gemm_fp8_qkv_pk", ptr(self.xq), ptr(self.xs), 1, ptr(lw.qkv.weight), ptr(lw.qkv.packed),
+             ptr(lw.qkv.scale), 1, T, H, HQ, HK, ptr(lw.q_norm.weight), ptr(lw.k_norm.weight),
+             float(lw.q_norm.variance_epsilon), float(lw.k_norm.variance_epsilon), ptr(self.cos), ptr(self.sin),
+             ptr(self.yq), ptr(self.yk), ptr(self.vt), Tp, s)
         if tail:
             call("ff_attention_vt", ptr(self.yq), ptr(self.yk), ptr(self.vt), ptr(self.pick), 1, ptr(self.attn),
                  1, T, Tp, HQ, HK, D, float(cfg.scaling), s)
@@ -434,8 +435,8 @@ class Runtime:
     def _qkv_static(self, lw, m, s):
         cfg = self.cfg
         op = lw.qkv
-        call("ff_gemm_fp8_qkv", ptr(self.xq), ptr(op.input_scale), 0, ptr(op.weight), ptr(op.weight_scale), 0, m,
-             cfg.hidden, cfg.heads, cfg.kv_heads, ptr(lw.q_norm.weight), ptr(lw.k_norm.weight),
+        call("ff_gemm_fp8_qkv_pk", ptr(self.xq), ptr(op.input_scale), 0, ptr(op.weight), ptr(op.packed),
+             ptr(op.weight_scale), 0, m, cfg.hidden, cfg.heads, cfg.kv_heads, ptr(lw.q_norm.weight), ptr(lw.k_norm.weight),
              float(lw.q_norm.variance_epsilon), float(lw.k_norm.variance_epsilon), ptr(self.cos), ptr(self.sin),
              ptr(self.yq), ptr(self.yk), ptr(self.vt), self.Tp, s)
 

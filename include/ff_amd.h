@@ -168,9 +168,10 @@ int ff_gemm_fp8_swiglu(const void* qa, const float* sa, const void* qw, const fl
                        int64_t ldh, float* pmax, int64_t m, int64_t i, int64_t k, ff_stream_t stream);
 
 /* Setup-time repack of e4m3 weights w (n, k) row-major into the MFMA fragment
- * layout read by ff_gemm_fp8_swiglu_pk (no reference counterpart: a storage
- * layout of this library): fragment (f, kt), rows [16 f, 16 f + 16) x k bytes
- * [128 kt, 128 kt + 128), is the 2048 bytes at (f * k/128 + kt) * 2048; lane
+ * layout read by ff_gemm_fp8_swiglu_pk, ff_gemm_fp8_pk and ff_gemm_fp8_qkv_pk
+ * (no reference counterpart: a storage layout of this library): fragment (f,
+ * kt), rows [16 f, 16 f + 16) x k bytes [128 kt, 128 kt + 128), is the 2048
+ * bytes at (kt * n/16 + f) * 2048 (k-step major); lane
  * l = 16 g + r holds row 16 f + r, k bytes [128 kt + 32 g, +16) at 16 l and
  * [128 kt + 32 g + 16, +16) at 1024 + 16 l (two 1 KB planes, one load
  * instruction each). packed holds n * k bytes. n % 16 == 0, k % 128 == 0. */
@@ -214,6 +215,16 @@ int ff_gemm_fp8_qkv(const void* qa, const float* sa, int sa_rows, const void* qw
                     int64_t m, int64_t k, int64_t hq, int64_t hk, const void* q_norm, const void* k_norm,
                     float eps_q, float eps_k, const void* cos, const void* sin, void* yq, void* yk, void* vt,
                     int64_t t_pad, ff_stream_t stream);
+/* ff_gemm_fp8_qkv on the MFMA-fragment copy of qw (ff_pack_weight_fp8):
+ * 64-token x 256-channel tiles (two heads) when m > 4, (hq + 2 hk) is even, k
+ * % 512 == 0, the grid has 192..512 tiles and t_pad <= the tiles' token range
+ * (the 8B step's 576 x 4096 x 6144); the same bits as ff_gemm_fp8_qkv, which
+ * it calls for every other shape (qw_packed may then be NULL). Same
+ * reference replacement as ff_gemm_fp8_qkv. */
+int ff_gemm_fp8_qkv_pk(const void* qa, const float* sa, int sa_rows, const void* qw, const void* qw_packed,
+                       const float* sw, int sw_cols, int64_t m, int64_t k, int64_t hq, int64_t hk,
+                       const void* q_norm, const void* k_norm, float eps_q, float eps_k, const void* cos,
+                       const void* sin, void* yq, void* yk, void* vt, int64_t t_pad, ff_stream_t stream);
 
 /* Static-scale (calibrated) FP8 producers of the step, no reference counterpart
  * as separate ops: each is the op it extends followed by the runtime-scale cast

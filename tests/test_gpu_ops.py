@@ -314,7 +314,7 @@ def test_gemm_fp8_swiglu_equals_unfused(gpu, m, i, k):
 
 
 def test_pack_weight_fp8_layout(gpu):
-    """ff_pack_weight_fp8 stores fragment (f, kt) at (f * k/128 + kt) * 2048 with
+    """ff_pack_weight_fp8 stores fragment (f, kt) at (kt * n/16 + f) * 2048 with
     lane l = 16 g + r holding row 16 f + r, k bytes [128 kt + 32 g, +16) at 16 l
     and the next 16 at 1024 + 16 l."""
     from fastforward_amd._lib import call, ptr, stream
@@ -323,7 +323,7 @@ def test_pack_weight_fp8_layout(gpu):
     p = torch.empty(n * k, device=DEV, dtype=torch.uint8)
     w_d = w.to(DEV)
     call("ff_pack_weight_fp8", ptr(w_d), ptr(p), n, k, stream())
-    got = p.cpu().numpy().reshape(n // 16, k // 128, 2, 64, 16)
+    got = p.cpu().numpy().reshape(k // 128, n // 16, 2, 64, 16).transpose(1, 0, 2, 3, 4)
     wn = w.numpy()
     for f in range(n // 16):
         for kt in range(k // 128):
@@ -672,6 +672,48 @@ def test_gemm_fp8_qkv_equals_unfused(gpu, t, k, hq, hk):
          1e-6, 1e-6, ptr(cos), ptr(sin), ptr(yq), ptr(yk), ptr(vt), tp, stream())
     assert torch.equal(yq, rq) and torch.equal(yk, rk)
     assert torch.equal(vt, rv)
+
+
+@pytest.mark.parametrize("t,k,hq,hk,static", [(576, 4096, 32, 8, False), (500, 4096, 32, 8, False),
+                                               (1024, 4096, 32, 8, False), (576, 4096, 32, 8, True),
+                                               (300, 2048, 16, 8, False), (3, 4096, 32, 8, False)])
+def test_gemm_fp8_qkv_packed_equals_rowmajor(gpu, t, k, hq, hk, static):
+    """ff_gemm_fp8_qkv_pk (64-token x two-head tiles on the packed weight: 576,
+    ragged 500 and 1024 tokens at 32/8 heads, per-token and per-tensor scales)
+    equals ff_gemm_fp8_qkv bit for bit, V^T zero padding included; shapes
+    outside its plan (300 tokens at 16/8 heads: 80 tiles; 3 tokens) run
+    ff_gemm_fp8_qkv itself."""
+    from fastforward_amd._lib import call, ptr, stream
+    d = 128
+    tp, n = (t + 63) // 64 * 64, (hq + 2 * hk) * d
+    qa = torch.randint(0, 126, (t, k), generator=_g(84), dtype=torch.uint8)
+    qa[torch.rand(t, k, generator=_g(85)) < 0.5] |= 0x80
+    qw = torch.randint(0, 126, (n, k), generator=_g(86), dtype=torch.uint8)
+    qw[torch.rand(n, k, generator=_g(87)) < 0.5] |= 0x80
+    qa_d, qw_d = qa.to(DEV), qw.to(DEV)
+    packed = torch.empty_like(qw_d)
+    call("ff_pack_weight_fp8", ptr(qw_d), ptr(packed), n, k, stream())
+    if static:
+        sa, sw = torch.tensor([0.011], device=DEV), torch.tensor([0.0007], device=DEV)
+    else:
+        sa = (torch.rand(t, generator=_g(88)) * 0.02 + 0.001).to(DEV)
+        sw = (torch.rand(n, generator=_g(89)) * 0.001 + 1e-4).to(DEV)
+    qn, _ = _norm_module(d, 90, 0.3)
+    kn, _ = _norm_module(d, 91, 0.3)
+    ang = torch.randn(t, d, generator=_g(92)) * 3
+    cos, sin = ang.cos().to(BF16).to(DEV), ang.sin().to(BF16).to(DEV)
+    outs = []
+    for entry in ("ff_gemm_fp8_qkv", "ff_gemm_fp8_qkv_pk"):
+        yq = torch.full((hq, t, d), float("nan"), device=DEV, dtype=BF16)
+        yk = torch.full((hk, t, d), float("nan"), device=DEV, dtype=BF16)
+        vt = torch.full((hk, d, tp), float("nan"), device=DEV, dtype=BF16)
+        w = [ptr(qw_d)] + ([ptr(packed)] if entry.endswith("pk") else [])
+        call(entry, ptr(qa_d), ptr(sa), 0 if static else 1, *w, ptr(sw), 0 if static else 1, t, k, hq, hk,
+             ptr(qn.weight), ptr(kn.weight), 1e-6, 1e-6, ptr(cos), ptr(sin), ptr(yq), ptr(yk), ptr(vt), tp, stream())
+        outs.append((yq, yk, vt))
+    (q0, k0, v0), (q1, k1, v1) = outs
+    assert not torch.isnan(q0.float()).any() and not torch.isnan(v0.float()).any()
+    assert torch.equal(q1, q0) and torch.equal(k1, k0) and torch.equal(v1, v0)
 
 
 # ------------------------------------------------------------------ static-scale (calibrated) producers
