@@ -448,7 +448,9 @@ extern "C" int ff_gemm_w4a16_ws(const void* x, int64_t ldx, const void* packed, 
 // ------------------------------------------------------------------ packed-weight kernels
 //
 // The weight is repacked once (ff_pack_weight_int4) into MFMA fragment order:
-// the 16 rows x 128 k of fragment (f, kt) are the 1 KB at (f K/128 + kt) 1024;
+// the 16 rows x 128 k of fragment (f, kt) are the 1 KB at (kt N/16 + f) 1024
+// (k-step major: the fragments all workgroups load at one k step are
+// contiguous, which streams weights from HBM faster than 32 KB-strided loads);
 // lane l = 16 g + r holds row 16 f + r, the packed bytes of k = 128 kt + 64 h +
 // 16 g + [0, 16) for h = 0, 1 (8 bytes each, source byte order, each nibble
 // q stored as q ^ 8) at 16 l. One
@@ -571,10 +573,12 @@ __global__ __launch_bounds__(kThreads) void pack_int4_kernel(const uint8_t* __re
     const int64_t f = i >> 6;  // fragment f16 * kt_n + kt
     const int64_t kt = f % kt_n, f16 = f / kt_n;
     const int64_t row = f16 * 16 + (l & 15);
+    const int64_t nf = n / 16;
     const uint8_t* s = src + row * (k / 2) + kt * 64 + 8 * (l >> 4);
     const u32x2 a = *reinterpret_cast<const u32x2*>(s), b = *reinterpret_cast<const u32x2*>(s + 32);
     constexpr uint32_t kFlip = 0x88888888u;  // nibble q stored as q ^ 8: its signed 4-bit value is q - 8
-    *reinterpret_cast<u32x4*>(dst + f * 1024 + 16 * l) = u32x4{a.x ^ kFlip, a.y ^ kFlip, b.x ^ kFlip, b.y ^ kFlip};
+    *reinterpret_cast<u32x4*>(dst + (kt * nf + f16) * 1024 + 16 * l) =
+        u32x4{a.x ^ kFlip, a.y ^ kFlip, b.x ^ kFlip, b.y ^ kFlip};
   }
 }
 
@@ -629,11 +633,12 @@ __device__ __forceinline__ void w4pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], ui
   const __amdgpu_buffer_rsrc_t rB = make_rsrc(wp, wbytes);
   const __amdgpu_buffer_rsrc_t rS = make_rsrc(sz, szbytes);
   const uint32_t voffB = 16u * (uint32_t)lane;
+  const uint32_t kstride = (uint32_t)N * 64u;  // bytes per k step: N / 16 fragments of 1 KB
   i32x4v bq[2][TJ];
   float sq[2][TJ][2][2];  // (16 s, z) of halves h = 0, 1
   auto loadB1 = [&](int kt, auto SLOT, int j) {
     constexpr int slot = decltype(SLOT)::value;
-    bq[slot][j] = bload16(rB, voffB, sB[j] + (uint32_t)kt * 1024u);
+    bq[slot][j] = bload16(rB, voffB, sB[j] + (uint32_t)kt * kstride);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const uint32_t gi = (uint32_t)(kPkStep * kt + 64 * h + 16 * g) >> gshift;
@@ -813,7 +818,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_w4a16_pk_kernel(
   for (int j = 0; j < TJ; ++j) {
     const int row = SWIGLU ? (j & 1 ? half : 0) + tn * CH + wave_s * WCH + 16 * (j >> 1)
                            : tn * BN + wave_s * CW + 16 * j;
-    sB[j] = (uint32_t)(row / 16) * (uint32_t)KT * 1024u;
+    sB[j] = (uint32_t)(row / 16) * 1024u;
     colS[j] = (uint32_t)(row + r16);
   }
   f32x4 acc[RA][TJ];
@@ -945,7 +950,7 @@ __global__ __launch_bounds__(kThreads) void gemv_w4pk_kernel(const bf16_t* __res
           xv[m][h][c] = bload16(rX, (uint32_t)(m * ldx + kPkStep * kt + 64 * h + 16 * g + 8 * c) * 2u, 0);
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
-      const i32x4v w = bload16(rB, 16u * (uint32_t)lane, (uint32_t)((rowb[f] / 16) * KT + kt) * 1024u);
+      const i32x4v w = bload16(rB, 16u * (uint32_t)lane, (uint32_t)(kt * (N / 16) + rowb[f] / 16) * 1024u);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const uint32_t gi = (uint32_t)(kPkStep * kt + 64 * h + 16 * g) >> gshift;

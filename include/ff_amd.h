@@ -304,7 +304,7 @@ int ff_gemm_w4a16_noalloc(const void* x, int64_t ldx, const void* packed, const 
  * kernels below (no reference counterpart: the reference repacks its Int4
  * weights once for its library kernel, _family/night_runtime.py:27). packed
  * (n, k/2) in the ff_quant_weight_int4 layout; frag receives n * k / 2 bytes:
- * the 16 rows x 128 k of fragment (f, kt) at (f k/128 + kt) * 1024, lane
+ * the 16 rows x 128 k of fragment (f, kt) at (kt n/16 + f) * 1024, lane
  * l = 16 g + r holding row 16 f + r, the bytes of k = 128 kt + 64 h + 16 g +
  * [0, 16) for h = 0, 1 at 16 l, each nibble q stored as q ^ 8. n % 16 == 0,
  * k % 128 == 0. */

@@ -10,6 +10,7 @@ differs (|difference| <= 1 bf16 ulp + 2^-21 sum |x w|, under 1% of outputs
 differing). Every shape is also held to the fp64 product
 with the exactly dequantised weight (relative RMS <= 5e-3, worst element <=
 0.05 of the output RMS), as the LDS-staged kernel's tests are."""
+import numpy as np
 import pytest
 import torch
 
@@ -60,6 +61,28 @@ def _pk_splits(m, n, k):
     tiles = tm * (n // 256)
     s = 1 if tiles >= 192 else 256 // tiles
     return max(1, min(s, 8, k // 256))
+
+
+def test_pack_weight_int4_layout(gpu):
+    """ff_pack_weight_int4 stores fragment (f, kt) at (kt * n/16 + f) * 1024 with
+    lane l = 16 g + r holding row 16 f + r, the packed bytes of k = 128 kt +
+    64 h + 16 g + [0, 16) for h = 0, 1 (8 bytes each), every nibble q as q ^ 8."""
+    from fastforward_amd._lib import call, ptr, stream
+    n, k = 48, 384
+    src = torch.randint(0, 256, (n, k // 2), generator=_g(69), dtype=torch.uint8)
+    frag = torch.empty(n * k // 2, device=DEV, dtype=torch.uint8)
+    src_d = src.to(DEV)
+    call("ff_pack_weight_int4", ptr(src_d), ptr(frag), n, k, stream())
+    got = frag.cpu().numpy().reshape(k // 128, n // 16, 64, 16)
+    s = src.numpy() ^ 0x88
+    for f in range(n // 16):
+        for kt in range(k // 128):
+            for lane in range(64):
+                r, g = lane % 16, lane // 16
+                row = s[16 * f + r]
+                want = np.concatenate([row[64 * kt + 8 * g: 64 * kt + 8 * g + 8],
+                                       row[64 * kt + 32 + 8 * g: 64 * kt + 32 + 8 * g + 8]])
+                assert np.array_equal(got[kt, f, lane], want), (f, kt, lane)
 
 
 SHAPES = [(576, 4096, 24576), (576, 4096, 6144), (576, 12288, 4096), (576, 4096, 4096), (320, 2048, 6144),
