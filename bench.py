@@ -29,8 +29,8 @@ PEAK_FP8_TFLOPS = 5000.0      # MI355X dense fp8 MFMA
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 GEMM_KERNELS = ("FP8 GEMM launches of the step: gemm_fp8_swiglu_packed_kernel (gate/up), "
-                "gemm_fp8_split_packed_kernel + split_reduce_kernel (down), gemm_fp8_kernel (qkv with its "
-                "epilogue, o), gemv_fp8 kernels (the tail's single row)")
+                "gemm_fp8_split_packed_kernel + split_reduce_kernel (down; 96 x 128 tiles unsplit for o), "
+                "gemm_fp8_qkv_packed_kernel (qkv with its epilogue), gemv_fp8 kernels (the tail's single row)")
 MICRO_SHAPES = [(320, 2048, 6144), (320, 6144, 2048), (576, 4096, 12288), (576, 12288, 4096),
                 (1024, 5120, 25600)]
 
@@ -80,18 +80,19 @@ def gemm_buffers(cfg, role, n, m, T):
 
 def launch_gemm(cfg, role, lw, q, s, m, b):
     """One FP8 GEMM launch as the step issues it: the QKV projection with its
-    q/k norm + rotary + V^T epilogue (ff_gemm_fp8_qkv), the gate/up projection
-    with its SwiGLU epilogue (ff_gemm_fp8_swiglu_pk: packed weights), o and down through
-    ``FP8Linear.gemm`` (ff_gemm_fp8_pk: the k-split packed kernel and its reduction for
-    down, the row-major kernel for o, the GEMV kernels for the tail's single row)."""
+    q/k norm + rotary + V^T epilogue (ff_gemm_fp8_qkv_pk: packed weights), the
+    gate/up projection with its SwiGLU epilogue (ff_gemm_fp8_swiglu_pk), o and down
+    through ``FP8Linear.gemm`` (ff_gemm_fp8_pk: the k-split packed kernel and its
+    reduction for down, the small packed tiles for o, the GEMV kernels for the
+    tail's single row)."""
     from fastforward_amd._lib import call, ptr, stream
     op = getattr(lw, role)
     n, k = op.weight.shape
     if role == "qkv":
-        call("ff_gemm_fp8_qkv", ptr(q), ptr(s), 1, ptr(op.weight), ptr(op.scale), 1, m, k, cfg.heads, cfg.kv_heads,
-             ptr(lw.q_norm.weight), ptr(lw.k_norm.weight), float(lw.q_norm.variance_epsilon),
-             float(lw.k_norm.variance_epsilon), ptr(b["cos"]), ptr(b["sin"]), ptr(b["yq"]), ptr(b["yk"]),
-             ptr(b["vt"]), b["Tp"], stream())
+        call("ff_gemm_fp8_qkv_pk", ptr(q), ptr(s), 1, ptr(op.weight), ptr(op.packed), ptr(op.scale), 1, m, k,
+             cfg.heads, cfg.kv_heads, ptr(lw.q_norm.weight), ptr(lw.k_norm.weight),
+             float(lw.q_norm.variance_epsilon), float(lw.k_norm.variance_epsilon), ptr(b["cos"]), ptr(b["sin"]),
+             ptr(b["yq"]), ptr(b["yk"]), ptr(b["vt"]), b["Tp"], stream())
     elif role == "gateup":
         call("ff_gemm_fp8_swiglu_pk", ptr(q), ptr(s), ptr(op.weight), ptr(op.packed), ptr(op.scale), ptr(b["out"]),
              n // 2, ptr(b["pmax"]), m, n // 2, k, stream())
@@ -385,7 +386,7 @@ def main():
     log(f"building {cfg.name} fp8 (random init, seed 0)")
     w = make_model(cfg, mode=args.linear if args.profile else "fp8", seed=0, n_options=8)
     for L in w.layers:  # as Runtime does: the packed tile kernels read these copies
-        for op in (L.o, L.gateup, L.down):
+        for op in (L.qkv, L.o, L.gateup, L.down):
             if hasattr(op, "pack"):
                 op.pack()
     ids, pos, pick = make_request(cfg, T, *grid, seed=0)
