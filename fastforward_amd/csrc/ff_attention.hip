@@ -264,31 +264,78 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(
 //   pass 1: every wave computes its blocks' scores and each block's max per
 //           query into LDS; the running max after block b of the sequential
 //           walk is the prefix max pm[b] = max(bmax[0..b]), one scan per query;
-//   pass 2: every wave recomputes its blocks' scores (same instructions, same
-//           bits) and forms p = exp(s - pm[b]) with the running max the
-//           sequential walk would hold at block b, so bf16(p) -- the rounding
-//           the output depends on -- is identical. Its partial den and
-//           acc = sum bf16(p).V are kept in the frame of its latest pm and
-//           rescaled as pm grows, like the one-pass kernels' alpha.
+//   pass 2: every wave forms p = exp(s - pm[b]) for its blocks with the
+//           running max the sequential walk would hold at block b, so bf16(p)
+//           -- the rounding the output depends on -- is identical. Its partial
+//           den and acc = sum bf16(p).V are kept in the frame of its latest pm
+//           and rescaled as pm grows, like the one-pass kernels' alpha.
 // The waves' partials are merged in LDS in the frame of the final max
 // M = pm[last]: den = sum_w den_w 2^((pm_w - M) log2e scale), acc likewise,
 // out = acc / den. Only the fp32 order of the rescales differs from the
 // one-pass kernels (a factor 2^((pm_b - M) c2) per wave instead of a product of
 // per-block alphas).
+//
+// The kernel is a chain of dependent memory latencies, so its loads are issued
+// as early as their addresses allow: the K fragments of a wave's first two
+// blocks (all of them up to 1024 keys) at entry, beside the positions and
+// before q, whose address may depend on the positions; their V^T fragments
+// before the prefix-max scan. Those blocks keep their scores in registers
+// from pass 1 to pass 2; blocks past the first two (t > 1024) recompute them
+// from K in pass 2 with the same instructions, hence the same bits.
 constexpr int kDecodeWaves = 8;
 constexpr int kDecodeMaxBlocks = 256;  // 64-key blocks the LDS block maxima hold (t <= 16384)
 
-// Scores of one 64-key block (kb) for the lane's query, masked past lim
-// (the routine of softmax_block's mask), and the block max over the tile's rows
-// of this lane's query (reduced over the 4 key groups).
-__device__ __forceinline__ float decode_block_scores(const bf16_t* __restrict__ kp, const u32x4 (&qf)[4], int kb,
-                                                    int kend, int t, int r16, int g, int lim, f32x4 (&sc)[4]) {
-  score_chunk(kp, qf, kb, t, r16, g, sc[0], sc[1]);
-  if (kb + 32 < kend) {
-    score_chunk(kp, qf, kb + 32, t, r16, g, sc[2], sc[3]);
-  } else {
-    sc[2] = sc[3] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+// Maximum over the 16 lanes of each row of 16: quad_perm swaps (lane ^ 1,
+// lane ^ 2), then row_half_mirror (lane i with 7 - i of each half row) and
+// row_mirror (lane i with 15 - i).
+__device__ __forceinline__ int max_row16(int x) {
+  x = max(x, __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x141, 0xF, 0xF, false));
+  return max(x, __builtin_amdgcn_update_dpp(x, x, 0x140, 0xF, 0xF, false));
+}
+
+// The 16 K fragments of 64-key block kb in the order the S MFMAs take them:
+// kf[4 * (2c + tt) + st] is what score_chunk reads for chunk kb + 32c, tile tt,
+// step st.
+__device__ __forceinline__ void load_block_k(const bf16_t* __restrict__ kp, int kb, int t, int r16, int g,
+                                             u32x4 (&kf)[16]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int key = min(kb + 32 * (i >> 1) + 8 * (r16 >> 2) + 4 * (i & 1) + (r16 & 3), t - 1);
+    const bf16_t* kr = kp + (int64_t)key * D;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) kf[4 * i + st] = *reinterpret_cast<const u32x4*>(kr + 32 * st + 8 * g);
   }
+}
+
+// V^T fragments of block kb: vf[c][dt] feeds the P.V MFMA of chunk c, d tile dt
+// (keys kb + 32c + 8g .. +7 of d row 16 dt + r16; t_pad >= kb + 64 keeps both
+// chunks in bounds).
+__device__ __forceinline__ void load_block_v(const bf16_t* __restrict__ vp, int kb, int t_pad, int r16, int g,
+                                             u32x4 (&vf)[2][8]) {
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      vf[c][dt] = *reinterpret_cast<const u32x4*>(vp + (int64_t)(16 * dt + r16) * t_pad + kb + 32 * c + 8 * g);
+}
+
+// Scores of one 64-key block (kb) for the lane's query from its K fragments
+// (score_chunk's arithmetic), the second 32-key chunk dropped when no visible
+// key reaches it, masked past lim (the routine of softmax_block's mask); returns
+// the block max over the tile's rows of this lane's query (reduced over the 4
+// key groups).
+__device__ __forceinline__ float decode_scores(const u32x4 (&kf)[16], const u32x4 (&qf)[4], int kb, int kend,
+                                               int lim, f32x4 (&sc)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 4; ++st) a = mfma_bf16(kf[4 * i + st], qf[st], a);
+    sc[i] = a;
+  }
+  if (!(kb + 32 < kend)) sc[2] = sc[3] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -298,6 +345,39 @@ __device__ __forceinline__ float decode_block_scores(const bf16_t* __restrict__ 
 #pragma unroll
   for (int i = 1; i < 4; ++i) bmax = fmaxf(bmax, fmaxf(fmaxf(sc[i][0], sc[i][1]), fmaxf(sc[i][2], sc[i][3])));
   return max_rows(bmax);
+}
+
+// Pass 2 for one block: P against the sequential running max mnew of the
+// block, this wave's den and acc rescaled into that frame, acc += bf16(P).V.
+__device__ __forceinline__ void decode_accumulate(const f32x4 (&sc)[4], const u32x4 (&vf)[2][8], bool two,
+                                                  float mnew, float c2, float& m, float& den, f32x4 (&o)[8]) {
+  const float mref = mnew == -INFINITY ? 0.f : mnew;  // a fully masked query keeps p = 0
+  const float alpha = __builtin_amdgcn_exp2f((m - mref) * c2);
+  float p[16], psum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float e = __builtin_amdgcn_exp2f((sc[i][r] - mref) * c2);
+      p[4 * i + r] = e;
+      psum += e;
+    }
+  den = den * alpha + psum;
+  m = mnew;
+  u32x4 pf[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    pf[c].x = pack_bf16x2(p[8 * c + 0], p[8 * c + 1]);
+    pf[c].y = pack_bf16x2(p[8 * c + 2], p[8 * c + 3]);
+    pf[c].z = pack_bf16x2(p[8 * c + 4], p[8 * c + 5]);
+    pf[c].w = pack_bf16x2(p[8 * c + 6], p[8 * c + 7]);
+  }
+  rescale(o, alpha);
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    o[dt] = mfma_bf16(vf[0][dt], pf[0], o[dt]);
+    if (two) o[dt] = mfma_bf16(vf[1][dt], pf[1], o[dt]);
+  }
 }
 
 __global__ __launch_bounds__(kDecodeWaves * 64) void attention_decode_kernel(
@@ -312,77 +392,81 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void attention_decode_kernel(
   const int kvh = head / (hq / hk);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r16 = lane & 15, g = lane >> 4;
+  const bf16_t* kp = k + (int64_t)kvh * t * D;
+  const bf16_t* vp = vt + (int64_t)kvh * D * t_pad;
+  // The lane's query position, then the K of blocks b0 = wave and
+  // b1 = wave + 8, then the visible key range: the maximum of
+  // the positions over the 16 lanes of a row (every row holds the same ones).
   const bool qvalid = r16 < s_len;
   const int qrow = qvalid ? r16 : s_len - 1;
   const int pos = (int)positions[qrow];
-  int kend = pos + 1;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) kend = max(kend, __shfl_xor(kend, o, 64));
-  kend = min(kend, t);
+  const int kb0 = wave * 64, kb1 = (wave + kDecodeWaves) * 64;
+  u32x4 kf0[16], kf1[16];  // unconditional (keys clamp to t - 1): no branch splits the loads from the wait
+  load_block_k(kp, kb0, t, r16, g, kf0);
+  load_block_k(kp, kb1, t, r16, g, kf1);
+  const int kend = min(__builtin_amdgcn_readfirstlane(max_row16(pos + 1)), t);
   const int nb = (kend + 63) / 64;  // <= kDecodeMaxBlocks (checked at launch)
   const int64_t qsrc = gather_q ? min(max(pos, 0), t - 1) : qrow;
   const bf16_t* qp = q + ((int64_t)head * (gather_q ? t : s_len) + qsrc) * D;
   u32x4 qf[4];
 #pragma unroll
   for (int st = 0; st < 4; ++st) qf[st] = *reinterpret_cast<const u32x4*>(qp + 32 * st + 8 * g);
-  const bf16_t* kp = k + (int64_t)kvh * t * D;
-  const bf16_t* vp = vt + (int64_t)kvh * D * t_pad;
   const int plim = min(pos, t - 1);
 
-  // pass 1: block maxima, then the running max of the sequential walk
-  for (int kb = wave * 64; kb < kend; kb += kDecodeWaves * 64) {
+  // pass 1: block maxima (scores of the first two blocks kept), then the V^T
+  // loads of those blocks, then the running max of the sequential walk
+  f32x4 sc0[4], sc1[4];
+  const bool has0 = kb0 < kend, has1 = kb1 < kend;  // wave-uniform
+  if (has0) {
+    const float bmax = decode_scores(kf0, qf, kb0, kend, plim - kb0 - 8 * g, sc0);
+    if (g == 0) pm[wave][r16] = bmax;
+  }
+  if (has1) {
+    const float bmax = decode_scores(kf1, qf, kb1, kend, plim - kb1 - 8 * g, sc1);
+    if (g == 0) pm[wave + kDecodeWaves][r16] = bmax;
+  }
+  for (int kb = kb1 + kDecodeWaves * 64; kb < kend; kb += kDecodeWaves * 64) {
+    u32x4 kf[16];
+    load_block_k(kp, kb, t, r16, g, kf);
     f32x4 sc[4];
-    const float bmax = decode_block_scores(kp, qf, kb, kend, t, r16, g, plim - kb - 8 * g, sc);
+    const float bmax = decode_scores(kf, qf, kb, kend, plim - kb - 8 * g, sc);
     if (g == 0) pm[kb / 64][r16] = bmax;
   }
-  __syncthreads();
+  u32x4 vf0[2][8], vf1[2][8];
+  if (has0) load_block_v(vp, kb0, t_pad, r16, g, vf0);
+  if (has1) load_block_v(vp, kb1, t_pad, r16, g, vf1);
+  barrier_lds();  // block maxima written (the V^T loads stay in flight)
+  // prefix max over the blocks, 16 blocks at a time per query
   if (threadIdx.x < 16) {
     float run = -INFINITY;
-    for (int b = 0; b < nb; ++b) {
-      run = fmaxf(run, pm[b][threadIdx.x]);
-      pm[b][threadIdx.x] = run;
+    for (int b0 = 0; b0 < nb; b0 += 16) {
+      float v[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = b0 + j < nb ? pm[b0 + j][threadIdx.x] : -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        run = fmaxf(run, v[j]);
+        if (b0 + j < nb) pm[b0 + j][threadIdx.x] = run;
+      }
     }
   }
-  __syncthreads();
+  barrier_lds();
 
   // pass 2: P against the sequential running max of each block
   f32x4 o[8];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, den = 0.f;  // the frame (a prefix max) of this wave's partials
-  for (int kb = wave * 64; kb < kend; kb += kDecodeWaves * 64) {
-    const bool two = kb + 32 < kend;
+  if (has0) decode_accumulate(sc0, vf0, kb0 + 32 < kend, pm[wave][r16], c2, m, den, o);
+  if (has1) decode_accumulate(sc1, vf1, kb1 + 32 < kend, pm[wave + kDecodeWaves][r16], c2, m, den, o);
+  for (int kb = kb1 + kDecodeWaves * 64; kb < kend; kb += kDecodeWaves * 64) {
+    u32x4 kf[16];
+    u32x4 vf[2][8];
+    load_block_k(kp, kb, t, r16, g, kf);
+    load_block_v(vp, kb, t_pad, r16, g, vf);
     f32x4 sc[4];
-    decode_block_scores(kp, qf, kb, kend, t, r16, g, plim - kb - 8 * g, sc);
-    const float mnew = pm[kb / 64][r16];
-    const float mref = mnew == -INFINITY ? 0.f : mnew;  // a fully masked query keeps p = 0
-    const float alpha = __builtin_amdgcn_exp2f((m - mref) * c2);
-    float p[16], psum = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float e = __builtin_amdgcn_exp2f((sc[i][r] - mref) * c2);
-        p[4 * i + r] = e;
-        psum += e;
-      }
-    den = den * alpha + psum;
-    m = mnew;
-    u32x4 pf[2];
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      pf[c].x = pack_bf16x2(p[8 * c + 0], p[8 * c + 1]);
-      pf[c].y = pack_bf16x2(p[8 * c + 2], p[8 * c + 3]);
-      pf[c].z = pack_bf16x2(p[8 * c + 4], p[8 * c + 5]);
-      pf[c].w = pack_bf16x2(p[8 * c + 6], p[8 * c + 7]);
-    }
-    rescale(o, alpha);
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const bf16_t* vr = vp + (int64_t)(16 * dt + r16) * t_pad + kb + 8 * g;
-      o[dt] = mfma_bf16(*reinterpret_cast<const u32x4*>(vr), pf[0], o[dt]);
-      if (two) o[dt] = mfma_bf16(*reinterpret_cast<const u32x4*>(vr + 32), pf[1], o[dt]);
-    }
+    decode_scores(kf, qf, kb, kend, plim - kb - 8 * g, sc);
+    decode_accumulate(sc, vf, kb + 32 < kend, pm[kb / 64][r16], c2, m, den, o);
   }
   den = sum_rows(den);
   if (g == 0) {

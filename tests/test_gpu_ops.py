@@ -528,11 +528,15 @@ def test_attention_causal(gpu, t, hq, hk):
     assert float((got - want).pow(2).mean().sqrt() / want.pow(2).mean().sqrt()) <= 5e-3
 
 
-@pytest.mark.parametrize("t,hq,hk", [(576, 32, 8), (1000, 64, 8), (129, 16, 4), (17, 8, 2)])
+@pytest.mark.parametrize("t,hq,hk", [(576, 32, 8), (1000, 64, 8), (129, 16, 4), (17, 8, 2), (320, 16, 8),
+                                     (130, 8, 8), (2048, 32, 8)])
 def test_attention_prefill_matches_per_head_kernel(gpu, t, hq, hk):
-    """The grouped prefill kernel (>= 4 query heads per kv head, K/V staged in
-    LDS) and the per-head kernel (taken when positions are given) run the same
-    64-key-block online softmax in the same order: results are bit-identical."""
+    """The grouped prefill kernel (1, 2 or a multiple of 4 query heads per kv
+    head, K/V staged in LDS; one or two query tiles per wave) and the per-head
+    kernel (taken when positions are given) run the same 64-key-block online
+    softmax in the same order: results are bit-identical. With 2 or 1 heads
+    per workgroup the waves hold different query rows and stop at different
+    key blocks."""
     from fastforward_amd import ops
     d = 128
     q = torch.randn(1, hq, t, d, generator=_g(40)).to(BF16).to(DEV)
