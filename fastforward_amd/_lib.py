@@ -44,6 +44,10 @@ SIGNATURES = {
     "ff_gemm_fp8_swiglu_pk": [P, P, P, P, P, P, I64, P, I64, I64, I64, P],
     "ff_gemm_fp8_pk_workspace": [I64, I64, I64, PI64],
     "ff_gemm_fp8_pk": [P, P, I32, P, P, P, I32, P, I64, I64, I64, I64, P, I64, P],
+    "ff_gemm_fp8_pk_add_rms_quant": [P, P, I32, P, P, P, I32, P, I64, I64, I64, P, I64, P, P, P, P, P, P, F32, I64,
+                                     I64, P],
+    "ff_gemm_fp8_pk_add_rms_quant_static": [P, P, I32, P, P, P, I32, P, I64, I64, I64, P, I64, P, P, P, P, P, F32,
+                                            F32, I64, I64, P],
     "ff_quant_rows_pmax": [P, I64, P, I64, P, P, I64, I64, P],
     "ff_gemm_fp8_qkv": [P, P, I32, P, P, I32, I64, I64, I64, I64, P, P, F32, F32, P, P, P, P, P, I64, P],
     "ff_gemm_fp8_qkv_pk": [P, P, I32, P, P, P, I32, I64, I64, I64, I64, P, P, F32, F32, P, P, P, P, P, I64, P],

@@ -368,6 +368,13 @@ namespace ff {
 // Row-major / GEMV form of ff_gemm_fp8_swiglu_static (defined with the row-major kernels).
 int gemm_swiglu_static_rowmajor(const void* qa, const float* sa, const void* qw, const float* sw, void* hq,
                                 int64_t ldh, float inv, int64_t m, int64_t i, int64_t k, hipStream_t s);
+// The split-K launch of ff_gemm_fp8_pk alone (defined with the packed kernels):
+// where ff_gemm_fp8_pk splits this shape, the split GEMM with its fp32 partials
+// row-major in workspace ((*splits, *mp, n), *mp = m rounded up to whole
+// tiles); elsewhere nothing is launched and *splits = 0.
+int gemm_fp8_pk_partials(const void* qa, const float* sa, int sa_rows, const void* qw_packed, const float* sw,
+                         int sw_cols, int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes,
+                         hipStream_t st, int* splits, int64_t* mp);
 }  // namespace ff
 
 #define FF_REQUIRE(cond, ...)          \

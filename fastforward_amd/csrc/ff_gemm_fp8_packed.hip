@@ -398,14 +398,15 @@ __device__ __forceinline__ void pk_store_tile(const f32x4 (&acc)[BM / 16][CW / 1
 
 // Plain y = bf16((A . W^T * sa) * sw) with k split S ways: workgroup (tile,
 // split) runs k steps [split KT/S, (split + 1) KT/S). With S == 1 it stores y;
-// with S > 1 it stores its fp32 partial tile in accumulator order (f32x4 (i, j)
-// of thread t at ((tile S + split) RA TJ + i TJ + j) 256 + t) and
-// split_reduce_kernel, the next launch, adds the partials.
+// with S > 1 it stores its fp32 partial tile row-major over the rows padded to
+// whole tiles, part[(split Mp + row) N + col] (Mp = tiles_m BM), and the next
+// launch adds the partials: split_reduce_kernel, or the add_rms row kernel
+// that takes them in place of its bf16 addend.
 template <int BM, int CW, int P, int D, int G, int S>
 __global__ __launch_bounds__(kThreads, BM < 144 ? 2 : 1) void gemm_fp8_split_packed_kernel(
     const uint8_t* __restrict__ qa, const float* __restrict__ sa, int sa_rows, const uint8_t* __restrict__ qwp,
     const float* __restrict__ sw, int sw_cols, bf16_t* __restrict__ y, int64_t ldy, int M, int N, int K,
-    int tiles_m, int tiles_n, f32x4* __restrict__ part) {
+    int tiles_m, int tiles_n, float* __restrict__ part) {
   constexpr int BN = 4 * CW;
   constexpr int RA = BM / 16, TJ = CW / 16;
   constexpr int SMEM = pk_smem<BM, G>();
@@ -429,52 +430,80 @@ __global__ __launch_bounds__(kThreads, BM < 144 ? 2 : 1) void gemm_fp8_split_pac
   f32x4 acc[RA][TJ];
   pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, split * nk, nk, [] {});
   if constexpr (S > 1) {
-    f32x4* mine = part + ((int64_t)(tn * tiles_m + tm) * S + split) * (RA * TJ * kThreads) + tid;
+    // The partial tile goes out through LDS, GR 16-row groups at a time, so
+    // that every store instruction writes one whole 1 KB row segment (the
+    // accumulators scatter 64 bytes to each of 16 rows). Lane 16 g + r of
+    // fragment (i, j) holds row 16 i + r, columns wave CW + 16 j + 4 g .. + 3.
+    constexpr int LDW = BN + 4;  // floats per staged row; the pad spreads the rows over the banks
+    constexpr int GR = SMEM / (16 * LDW * 4);
+    static_assert(GR >= 1, "one 16-row group fits the LDS");
+    float* stg = reinterpret_cast<float*>(smem);
+    float* dst = part + ((int64_t)split * tiles_m * BM + m0) * N + n0;
+    const int lane = tid & 63;
+    float* mine = stg + (lane & 15) * LDW + wave * CW + 4 * (lane >> 4);
+    static_for<0, (RA + GR - 1) / GR>([&](auto R_) {
+      constexpr int i0 = decltype(R_)::value * GR;
+      constexpr int ng = RA - i0 < GR ? RA - i0 : GR;
+      barrier_lds();  // the stage (main loop or previous round) is no longer read
 #pragma unroll
-    for (int i = 0; i < RA; ++i)
+      for (int ii = 0; ii < ng; ++ii)
 #pragma unroll
-      for (int j = 0; j < TJ; ++j) mine[(i * TJ + j) * kThreads] = acc[i][j];
+        for (int j = 0; j < TJ; ++j) *reinterpret_cast<f32x4*>(mine + ii * 16 * LDW + 16 * j) = acc[i0 + ii][j];
+      barrier_lds();
+#pragma unroll
+      for (int e = tid; e < ng * 16 * (BN / 4); e += kThreads) {
+        const int r = e / (BN / 4), c4 = e % (BN / 4);
+        *reinterpret_cast<f32x4*>(dst + (int64_t)(16 * i0 + r) * N + 4 * c4) =
+            *reinterpret_cast<const f32x4*>(stg + r * LDW + 4 * c4);
+      }
+    });
   } else {
     pk_store_tile<BM, CW>(acc, sa, sa_rows, sw, sw_cols, y, ldy, M, m0, n0);
   }
 }
 
-// y for the tiles of a split launch, one workgroup per (tile, 16-row group i):
-// the S partials of each accumulator added in split order 0, 1, .., S-1
-// (independent of which split finished first), then the epilogue of the
-// unsplit kernel for those 16 rows (transposed accumulator layout: lane
-// 16 g + r holds row r, columns 16 j + 4 g .. + 3 of wave w's CW columns).
-template <int BM, int CW, int S>
-__global__ __launch_bounds__(kThreads) void split_reduce_kernel(
-    const f32x4* __restrict__ part, const float* __restrict__ sa, int sa_rows, const float* __restrict__ sw,
-    int sw_cols, bf16_t* __restrict__ y, int64_t ldy, int M, int tiles_m) {
-  constexpr int RA = BM / 16, TJ = CW / 16, BN = 4 * CW;
-  const int tile = blockIdx.x / RA, i = blockIdx.x % RA;
-  const int tm = tile % tiles_m, tn = tile / tiles_m;
-  const int m0 = tm * BM + 16 * i, n0 = tn * BN;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r16 = lane & 15, g = lane >> 4;
-  const f32x4* tp = part + (int64_t)tile * S * (RA * TJ * kThreads) + tid;
-  f32x4 v[TJ][S];
+// y = bf16((sum_s part_s * sa) * sw) for the rows < M of a split launch's
+// row-major partials, added in split order 0, 1, .., S-1 (the unsplit
+// kernel's arithmetic on the same sums); one thread per 8 columns.
+template <int S>
+__global__ __launch_bounds__(kThreads) void split_reduce_kernel(const float* __restrict__ part, int64_t mp,
+                                                                const float* __restrict__ sa, int sa_rows,
+                                                                const float* __restrict__ sw, int sw_cols,
+                                                                bf16_t* __restrict__ y, int64_t ldy, int M, int N) {
+  const int nc = N / 8;
+  const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int m = (int)(e / nc), col = (int)(e % nc) * 8;
+  if (m >= M) return;
+  f32x4 v[S][2], vs[2];
 #pragma unroll
-  for (int j = 0; j < TJ; ++j)
-#pragma unroll
-    for (int s2 = 0; s2 < S; ++s2) v[j][s2] = tp[((int64_t)s2 * RA * TJ + i * TJ + j) * kThreads];
-  const int m = m0 + r16;
-  const float sav = sa[sa_rows ? min(m, M - 1) : 0];
-#pragma unroll
-  for (int j = 0; j < TJ; ++j) {
-    f32x4 t = v[j][0];
-#pragma unroll
-    for (int s2 = 1; s2 < S; ++s2) t = t + v[j][s2];
-    const int col = n0 + wave * CW + 16 * j + 4 * g;
-    float swv[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) swv[r] = sw[sw_cols ? col + r : 0];
-    if (m < M)
-      *reinterpret_cast<u32x2*>(y + (int64_t)m * ldy + col) =
-          pack4_bf16((t[0] * sav) * swv[0], (t[1] * sav) * swv[1], (t[2] * sav) * swv[2], (t[3] * sav) * swv[3]);
+  for (int s2 = 0; s2 < S; ++s2) {
+    const float* src = part + ((int64_t)s2 * mp + m) * N + col;
+    v[s2][0] = *reinterpret_cast<const f32x4*>(src);
+    v[s2][1] = *reinterpret_cast<const f32x4*>(src + 4);
   }
+  if (sw_cols && ((uintptr_t)sw & 15) == 0) {
+    vs[0] = *reinterpret_cast<const f32x4*>(sw + col);
+    vs[1] = *reinterpret_cast<const f32x4*>(sw + col + 4);
+  } else if (sw_cols) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      vs[0][r] = sw[col + r];
+      vs[1][r] = sw[col + 4 + r];
+    }
+  } else {
+    vs[0] = vs[1] = f32x4{sw[0], sw[0], sw[0], sw[0]};
+  }
+  const float sav = sa[sa_rows ? m : 0];
+  float f[8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    f32x4 t = v[0][h];
+#pragma unroll
+    for (int s2 = 1; s2 < S; ++s2) t = t + v[s2][h];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) f[4 * h + r] = (t[r] * sav) * vs[h][r];
+  }
+  *reinterpret_cast<u32x4*>(y + (int64_t)m * ldy + col) = pack8(f);
 }
 
 // The configuration measured for the 8B gate/up shape (576 x 4096 x 2 x 12288):
@@ -534,7 +563,7 @@ void launch_small(const void* qa, const float* sa, int sa_rows, const void* qw_p
   const int64_t tm = (m + BM - 1) / BM, tn = n / (4 * CW);
   hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<BM, CW, kSpP, kSpD, kSpG, 1>), dim3((unsigned)(tm * tn)),
                      dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows, (const uint8_t*)qw_packed, sw, sw_cols,
-                     (bf16_t*)y, ldy, (int)m, (int)n, (int)k, (int)tm, (int)tn, (f32x4*)nullptr);
+                     (bf16_t*)y, ldy, (int)m, (int)n, (int)k, (int)tm, (int)tn, (float*)nullptr);
 }
 
 int64_t split_workspace(int64_t m, int64_t n, int64_t k) {
@@ -726,20 +755,39 @@ extern "C" int ff_gemm_fp8_pk_workspace(int64_t m, int64_t n, int64_t k, int64_t
   return FF_OK;
 }
 
+namespace ff {
+int gemm_fp8_pk_partials(const void* qa, const float* sa, int sa_rows, const void* qw_packed, const float* sw,
+                         int sw_cols, int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes,
+                         hipStream_t st, int* splits, int64_t* mp) {
+  *splits = 0;
+  *mp = 0;
+  const int s = qw_packed && ff_aligned(qa, 16) && ff_aligned(qw_packed, 16) ? split_plan(m, n, k) : 0;
+  if (s <= 1) return FF_OK;
+  const int64_t need = split_workspace(m, n, k);
+  FF_REQUIRE(workspace && workspace_bytes >= need && ff_aligned(workspace, 16),
+             "ff_gemm_fp8_pk: workspace of %lld bytes (16-byte aligned) required", (long long)need);
+  const int64_t tiles_m = (m + kSpBM - 1) / kSpBM, tiles_n = n / kSpBN;
+  hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<kSpBM, kSpCW, kSpP, kSpD, kSpG, 4>),
+                     dim3((unsigned)(tiles_m * tiles_n * 4)), dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows,
+                     (const uint8_t*)qw_packed, sw, sw_cols, (bf16_t*)nullptr, (int64_t)0, (int)m, (int)n, (int)k,
+                     (int)tiles_m, (int)tiles_n, (float*)workspace);
+  FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
+  *splits = 4;
+  *mp = tiles_m * kSpBM;
+  return FF_OK;
+}
+}  // namespace ff
+
 extern "C" int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, const void* qw, const void* qw_packed,
                               const float* sw, int sw_cols, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
                               void* workspace, int64_t workspace_bytes, ff_stream_t stream) {
   FF_REQUIRE(qa && sa && qw && sw && y, "ff_gemm_fp8_pk: null pointer");
-  const int s = qw_packed && ldy % 8 == 0 && ldy >= n && ff_aligned(qa, 16) && ff_aligned(qw_packed, 16) &&
-                        ff_aligned(y, 16)
-                    ? split_plan(m, n, k)
-                    : 0;
+  const bool pk = qw_packed && ldy % 8 == 0 && ldy >= n && ff_aligned(qa, 16) && ff_aligned(qw_packed, 16) &&
+                  ff_aligned(y, 16);
+  const int s = pk ? split_plan(m, n, k) : 0;
+  hipStream_t st = (hipStream_t)stream;
   if (s == 0) {
-    const SmallTile t = qw_packed && ldy % 8 == 0 && ldy >= n && ff_aligned(qa, 16) && ff_aligned(qw_packed, 16) &&
-                                ff_aligned(y, 16)
-                            ? small_plan(m, n, k)
-                            : SmallTile{};
-    hipStream_t st = (hipStream_t)stream;
+    const SmallTile t = pk ? small_plan(m, n, k) : SmallTile{};
     if (t.bm == 64 && t.cw == 64)
       launch_small<64, 64>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, st);
     else if (t.bm == 96)
@@ -751,25 +799,23 @@ extern "C" int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, cons
     FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
     return FF_OK;
   }
-  const int64_t need = split_workspace(m, n, k);
-  FF_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && ff_aligned(workspace, 16)),
-             "ff_gemm_fp8_pk: workspace of %lld bytes (16-byte aligned) required", (long long)need);
-  const int64_t tiles_m = (m + kSpBM - 1) / kSpBM, tiles_n = n / kSpBN, tiles = tiles_m * tiles_n;
-  f32x4* part = (f32x4*)workspace;
-  hipStream_t st = (hipStream_t)stream;
+  const int64_t tiles_m = (m + kSpBM - 1) / kSpBM, tiles_n = n / kSpBN;
   if (s == 1) {
-    hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<kSpBM, kSpCW, kSpP, kSpD, kSpG, 1>), dim3((unsigned)tiles),
-                       dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows, (const uint8_t*)qw_packed, sw, sw_cols,
-                       (bf16_t*)y, ldy, (int)m, (int)n, (int)k, (int)tiles_m, (int)tiles_n, part);
-  } else {
-    hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<kSpBM, kSpCW, kSpP, kSpD, kSpG, 4>),
-                       dim3((unsigned)(tiles * 4)), dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows,
-                       (const uint8_t*)qw_packed, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)n, (int)k,
-                       (int)tiles_m, (int)tiles_n, part);
-    hipLaunchKernelGGL((split_reduce_kernel<kSpBM, kSpCW, 4>), dim3((unsigned)(tiles * (kSpBM / 16))),
-                       dim3(kThreads), 0, st,
-                       (const f32x4*)part, sa, sa_rows, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)tiles_m);
+    hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<kSpBM, kSpCW, kSpP, kSpD, kSpG, 1>),
+                       dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows,
+                       (const uint8_t*)qw_packed, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)n, (int)k, (int)tiles_m,
+                       (int)tiles_n, (float*)nullptr);
+    FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
+    return FF_OK;
   }
+  int splits = 0;
+  int64_t mp = 0;
+  const int rc = ff::gemm_fp8_pk_partials(qa, sa, sa_rows, qw_packed, sw, sw_cols, m, n, k, workspace,
+                                          workspace_bytes, st, &splits, &mp);
+  if (rc) return rc;
+  const int64_t chunks = m * (n / 8);
+  hipLaunchKernelGGL((split_reduce_kernel<4>), dim3((unsigned)((chunks + kThreads - 1) / kThreads)), dim3(kThreads),
+                     0, st, (const float*)workspace, mp, sa, sa_rows, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)n);
   FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
   return FF_OK;
 }

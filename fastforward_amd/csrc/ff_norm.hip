@@ -16,13 +16,29 @@ namespace {
 // scales[row]) or a static calibrated multiplier (e4m3(clamp(x * sinv, +-448))).
 constexpr int kNoQuant = 0, kDynamic = 1, kStatic = 2;
 
+// The addend of add_rms given as the S fp32 split-K partials of an FP8 GEMM
+// (row-major, (S, mp, h)) instead of bf16: b = bf16((sum_s part_s * sa[row]) *
+// sw[col]), the partials added in split order -- the split GEMM's own
+// reduction, bit for bit -- and stored to y (row stride h) as that GEMM's output.
+struct SplitAddend {
+  const float* part = nullptr;
+  int64_t mp = 0;
+  const float* sa = nullptr;
+  int sa_rows = 0;
+  const float* sw = nullptr;
+  int sw_cols = 0;
+  bf16_t* y = nullptr;
+};
+
 // One workgroup per row, blockDim.x threads (a multiple of 64, <= 1024) with
-// CPT 16-byte chunks each (row_shape picks both from h).
-template <int CPT, bool ADD, bool DEEP, bool WRITE_RES, bool WRITE_OUT, int QUANT>
+// CPT 16-byte chunks each (row_shape picks both from h). SPLIT > 0: the addend
+// b comes from SPLIT split-K partials (sb) instead of the bf16 array b.
+template <int CPT, bool ADD, bool DEEP, bool WRITE_RES, bool WRITE_OUT, int QUANT, int SPLIT = 0>
 __global__ __launch_bounds__(1024) void row_norm_kernel(
     const bf16_t* __restrict__ a, const bf16_t* __restrict__ b, const bf16_t* __restrict__ deep,
     const bf16_t* __restrict__ w, bf16_t* __restrict__ residual, bf16_t* __restrict__ out,
-    uint8_t* __restrict__ q, float* __restrict__ scales, int h, float eps, int start, int nv, float sinv) {
+    uint8_t* __restrict__ q, float* __restrict__ scales, int h, float eps, int start, int nv, float sinv,
+    SplitAddend sb) {
   __shared__ float red[16];
   const int row = blockIdx.x;
   const int nchunk = h >> 3;
@@ -30,13 +46,38 @@ __global__ __launch_bounds__(1024) void row_norm_kernel(
   const size_t base = (size_t)row * h;
   float x[CPT][8];
   u32x4 va[CPT], vb[CPT], vw[CPT];
+  f32x4 vp[CPT][SPLIT > 0 ? SPLIT : 1][2], vs[CPT][2];
+  float sav = 0.f;
+  if constexpr (SPLIT > 0) sav = sb.sa[sb.sa_rows ? row : 0];
   const bool in_deep = DEEP && row >= start && row < start + nv;
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
     const int idx = threadIdx.x + c * nt;
     if (idx < nchunk) {
       va[c] = *reinterpret_cast<const u32x4*>(a + base + (size_t)idx * 8);
-      if (ADD) vb[c] = *reinterpret_cast<const u32x4*>(b + base + (size_t)idx * 8);
+      if constexpr (ADD && SPLIT > 0) {
+#pragma unroll
+        for (int s2 = 0; s2 < SPLIT; ++s2) {
+          const float* src = sb.part + ((int64_t)s2 * sb.mp + row) * h + (size_t)idx * 8;
+          vp[c][s2][0] = *reinterpret_cast<const f32x4*>(src);
+          vp[c][s2][1] = *reinterpret_cast<const f32x4*>(src + 4);
+        }
+        if (sb.sw_cols && ((uintptr_t)sb.sw & 15) == 0) {
+          vs[c][0] = *reinterpret_cast<const f32x4*>(sb.sw + (size_t)idx * 8);
+          vs[c][1] = *reinterpret_cast<const f32x4*>(sb.sw + (size_t)idx * 8 + 4);
+        } else if (sb.sw_cols) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            vs[c][0][r] = sb.sw[(size_t)idx * 8 + r];
+            vs[c][1][r] = sb.sw[(size_t)idx * 8 + 4 + r];
+          }
+        } else {
+          const float s0 = sb.sw[0];
+          vs[c][0] = vs[c][1] = f32x4{s0, s0, s0, s0};
+        }
+      } else if (ADD) {
+        vb[c] = *reinterpret_cast<const u32x4*>(b + base + (size_t)idx * 8);
+      }
       vw[c] = *reinterpret_cast<const u32x4*>(w + (size_t)idx * 8);
     }
   }
@@ -48,7 +89,21 @@ __global__ __launch_bounds__(1024) void row_norm_kernel(
       unpack8(va[c], x[c]);
       if (ADD) {
         float y[8];
-        unpack8(vb[c], y);
+        if constexpr (SPLIT > 0) {
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            f32x4 t = vp[c][0][hh];
+#pragma unroll
+            for (int s2 = 1; s2 < SPLIT; ++s2) t = t + vp[c][s2][hh];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) y[4 * hh + r] = (t[r] * sav) * vs[c][hh][r];
+          }
+          const u32x4 yb = pack8(y);
+          *reinterpret_cast<u32x4*>(sb.y + base + (size_t)idx * 8) = yb;
+          unpack8(yb, y);
+        } else {
+          unpack8(vb[c], y);
+        }
 #pragma unroll
         for (int i = 0; i < 8; ++i) x[c][i] = round_bf16(x[c][i] + y[i]);
       }
@@ -100,19 +155,20 @@ __global__ __launch_bounds__(1024) void row_norm_kernel(
   }
 }
 
-template <bool ADD, bool DEEP, bool WRITE_RES, bool WRITE_OUT, int QUANT>
+template <bool ADD, bool DEEP, bool WRITE_RES, bool WRITE_OUT, int QUANT, int SPLIT = 0>
 int launch_row_norm(const void* a, const void* b, const void* deep, const void* w, void* residual,
                     void* out, void* q, float* scales, int64_t rows, int64_t h, float eps,
-                    int64_t start, int64_t nv, hipStream_t s, const char* name, float sinv = 0.f) {
+                    int64_t start, int64_t nv, hipStream_t s, const char* name, float sinv = 0.f,
+                    SplitAddend sb = SplitAddend{}) {
   int threads, cpt;
   row_shape(h / 8, &threads, &cpt);
   dim3 grid((unsigned)rows), block((unsigned)threads);
-#define FF_ROWNORM_CASE(N)                                                                       \
-  case N:                                                                                        \
-    hipLaunchKernelGGL((row_norm_kernel<N, ADD, DEEP, WRITE_RES, WRITE_OUT, QUANT>), grid, block, \
-                       0, s, (const bf16_t*)a, (const bf16_t*)b, (const bf16_t*)deep,             \
-                       (const bf16_t*)w, (bf16_t*)residual, (bf16_t*)out, (uint8_t*)q, scales,    \
-                       (int)h, eps, (int)start, (int)nv, sinv);                                   \
+#define FF_ROWNORM_CASE(N)                                                                              \
+  case N:                                                                                               \
+    hipLaunchKernelGGL((row_norm_kernel<N, ADD, DEEP, WRITE_RES, WRITE_OUT, QUANT, SPLIT>), grid, block, \
+                       0, s, (const bf16_t*)a, (const bf16_t*)b, (const bf16_t*)deep,                    \
+                       (const bf16_t*)w, (bf16_t*)residual, (bf16_t*)out, (uint8_t*)q, scales,           \
+                       (int)h, eps, (int)start, (int)nv, sinv, sb);                                      \
     break;
   switch (cpt) {
     FF_ROWNORM_CASE(1)
@@ -334,4 +390,77 @@ extern "C" int ff_lm_readout(const void* x, const void* x2, const void* norm_w, 
                        eps);
   FF_LAUNCH_CHECK("ff_lm_readout");
   return FF_OK;
+}
+
+// ---------------------------------------------------------------- GEMM + add_rms
+
+// ff_gemm_fp8_pk into y, then ff_add_rms_quant(a, y, ..) (or its static form).
+// Where the GEMM splits k, the row kernel adds the split partials itself (and
+// stores y) instead of a separate reduction launch; elsewhere the two entry
+// points run as they are.
+namespace {
+template <int QUANT>
+int gemm_add_rms(const char* name, const void* qa, const float* sa, int sa_rows, const void* qw, const void* qw_packed,
+                 const float* sw, int sw_cols, void* y, int64_t m, int64_t n, int64_t k, void* workspace,
+                 int64_t workspace_bytes, const void* a, const void* deep, const void* w, void* residual, void* q,
+                 float* scales, float inv, float eps, int64_t start, int64_t nv, ff_stream_t stream) {
+  int st = check_rows(name, a, m, n);
+  if (st) return st;
+  FF_REQUIRE(qa && sa && qw && sw && y && w && residual && q && (QUANT != kDynamic || scales),
+             "%s: null pointer", name);
+  FF_REQUIRE(ff_aligned(y, 16) && ff_aligned(w, 16) && ff_aligned(residual, 16) && ff_aligned(q, 8),
+             "%s: y, w and residual must be 16-byte aligned, q 8-byte", name);
+  FF_REQUIRE(!deep || (ff_aligned(deep, 16) && nv >= 0 && start >= 0), "%s: bad deep", name);
+  if (m == 0) return FF_OK;
+  hipStream_t s = (hipStream_t)stream;
+  int splits = 0;
+  int64_t mp = 0;
+  st = ff::gemm_fp8_pk_partials(qa, sa, sa_rows, qw_packed, sw, sw_cols, m, n, k, workspace, workspace_bytes, s,
+                                &splits, &mp);
+  if (st) return st;
+  if (splits == 0) {
+    st = ff_gemm_fp8_pk(qa, sa, sa_rows, qw, qw_packed, sw, sw_cols, y, n, m, n, k, workspace, workspace_bytes,
+                        stream);
+    if (st) return st;
+    if constexpr (QUANT == kDynamic)
+      return ff_add_rms_quant(a, y, deep, w, residual, nullptr, q, scales, m, n, eps, start, nv, stream);
+    else
+      return ff_add_rms_quant_static(a, y, deep, w, residual, nullptr, q, inv, m, n, eps, start, nv, stream);
+  }
+  FF_REQUIRE(splits == 4, "%s: unexpected split count %d", name, splits);
+  SplitAddend sb;
+  sb.part = (const float*)workspace;
+  sb.mp = mp;
+  sb.sa = sa;
+  sb.sa_rows = sa_rows;
+  sb.sw = sw;
+  sb.sw_cols = sw_cols;
+  sb.y = (bf16_t*)y;
+  if (deep && nv > 0)
+    return launch_row_norm<true, true, true, false, QUANT, 4>(a, nullptr, deep, w, residual, nullptr, q, scales, m,
+                                                              n, eps, start, nv, s, name, inv, sb);
+  return launch_row_norm<true, false, true, false, QUANT, 4>(a, nullptr, nullptr, w, residual, nullptr, q, scales, m,
+                                                             n, eps, 0, 0, s, name, inv, sb);
+}
+}  // namespace
+
+extern "C" int ff_gemm_fp8_pk_add_rms_quant(const void* qa, const float* sa, int sa_rows, const void* qw,
+                                            const void* qw_packed, const float* sw, int sw_cols, void* y, int64_t m,
+                                            int64_t n, int64_t k, void* workspace, int64_t workspace_bytes,
+                                            const void* a, const void* deep, const void* w, void* residual, void* q,
+                                            float* scales, float eps, int64_t start, int64_t nv, ff_stream_t stream) {
+  return gemm_add_rms<kDynamic>("ff_gemm_fp8_pk_add_rms_quant", qa, sa, sa_rows, qw, qw_packed, sw, sw_cols, y, m, n,
+                                k, workspace, workspace_bytes, a, deep, w, residual, q, scales, 0.f, eps, start, nv,
+                                stream);
+}
+
+extern "C" int ff_gemm_fp8_pk_add_rms_quant_static(const void* qa, const float* sa, int sa_rows, const void* qw,
+                                                   const void* qw_packed, const float* sw, int sw_cols, void* y,
+                                                   int64_t m, int64_t n, int64_t k, void* workspace,
+                                                   int64_t workspace_bytes, const void* a, const void* deep,
+                                                   const void* w, void* residual, void* q, float inv, float eps,
+                                                   int64_t start, int64_t nv, ff_stream_t stream) {
+  return gemm_add_rms<kStatic>("ff_gemm_fp8_pk_add_rms_quant_static", qa, sa, sa_rows, qw, qw_packed, sw, sw_cols, y,
+                               m, n, k, workspace, workspace_bytes, a, deep, w, residual, q, nullptr, inv, eps, start,
+                               nv, stream);
 }

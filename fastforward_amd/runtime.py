@@ -10,7 +10,8 @@ Two step bodies produce identical numbers:
 * ``fused`` (FP8Linear weights): every activation buffer is allocated once per
   token bucket (or laid out in an ``Arena`` that the buckets share); the per-token e4m3 quantization of each GEMM input is fused into
   the kernel that produces it (add_rms, fast_norm, swiglu), and V is written
-  transposed by the q/k-norm + rotary kernel. 10 launches per layer.
+  transposed by the QKV GEMM's epilogue; the down projection's split-K partials
+  are added by the next add_rms launch. 9 launches per layer.
 * ``generic`` (any linear op): the reference's own op sequence through the
   drop-in ops of ``fastforward_amd.ops`` and ``Linear.apply``.
 
@@ -324,12 +325,15 @@ class Runtime:
             self._gemm(self.aq, self.as_, lw.o, self.o, T, s)
             call("ff_add_rms_quant", ptr(h), ptr(self.o), None, ptr(lw.post_norm.weight), ptr(self.res), None,
                  ptr(self.pq), ptr(self.ps), T, H, float(lw.post_norm.variance_epsilon), 0, 0, s)
-            self._mlp_fused(lw, self.pq, self.ps, T, self.dn, s)
+            self._gateup_fused(lw, self.pq, self.ps, T, s)
             nxt = self.h[cur ^ 1]
             deep = self.deep[j] if j < len(self.deep) else None
             nn = L[j + 1].input_norm
-            call("ff_add_rms_quant", ptr(self.res), ptr(self.dn), ptr(deep), ptr(nn.weight), ptr(nxt), None,
-                 ptr(self.xq), ptr(self.xs), T, H, float(nn.variance_epsilon), self.image_start,
+            # down projection + the next layer's add_rms (the split-K partials added by the add_rms launch)
+            dw = lw.down
+            call("ff_gemm_fp8_pk_add_rms_quant", ptr(self.mq), ptr(self.ms), 1, ptr(dw.weight), ptr(dw.packed),
+                 ptr(dw.scale), 1, ptr(self.dn), T, H, I, ptr(self.gws), self.gws.numel(), ptr(self.res), ptr(deep),
+                 ptr(nn.weight), ptr(nxt), ptr(self.xq), ptr(self.xs), float(nn.variance_epsilon), self.image_start,
                  self.nv if deep is not None else 0, s)
             cur ^= 1
             if trace is not None:
@@ -373,12 +377,15 @@ class Runtime:
         call("ff_gemm_fp8_pk", ptr(q), ptr(sc), 1, ptr(op.weight), ptr(op.packed), ptr(op.scale), 1, ptr(out), n,
              m, n, k, ptr(self.gws), self.gws.numel(), s)
 
-    def _mlp_fused(self, lw, q, sc, m, out, s):
+    def _gateup_fused(self, lw, q, sc, m, s):
         I, H = self.cfg.inter, self.cfg.hidden
         # gate/up GEMM with SwiGLU in its epilogue, then per-token quant from its row maxima
         call("ff_gemm_fp8_swiglu_pk", ptr(q), ptr(sc), ptr(lw.gateup.weight), ptr(lw.gateup.packed),
              ptr(lw.gateup.scale), ptr(self.hm), I, ptr(self.pmax), m, I, H, s)
         call("ff_quant_rows_pmax", ptr(self.hm), I, ptr(self.pmax), I // 64, ptr(self.mq), ptr(self.ms), m, I, s)
+
+    def _mlp_fused(self, lw, q, sc, m, out, s):
+        self._gateup_fused(lw, q, sc, m, s)
         self._gemm(self.mq, self.ms, lw.down, out, m, s)
 
     def _step_static(self, trace=None):
@@ -387,8 +394,8 @@ class Runtime:
         bounds): every GEMM input is cast to e4m3 with the consuming linear's
         inverse_scale inside the kernel that produces it (norms, attention, the
         gate/up SwiGLU epilogue), and the GEMMs take the per-tensor
-        input_scale / weight_scale. 7 launches per full layer (8 where the
-        down projection splits k)."""
+        input_scale / weight_scale. 7 launches per full layer; where the down
+        projection splits k its partials are added by the add_rms launch."""
         cfg, w, s = self.cfg, self.w, stream()
         T, Tp, H, D = self.T, self.Tp, cfg.hidden, cfg.head_dim
         HQ, HK, I = cfg.heads, cfg.kv_heads, cfg.inter
@@ -406,13 +413,15 @@ class Runtime:
             self._gemm_static(self.aq, lw.o, self.o, T, s)
             call("ff_add_rms_quant_static", ptr(h), ptr(self.o), None, ptr(lw.post_norm.weight), ptr(self.res), None,
                  ptr(self.pq), float(lw.gateup.inverse_scale), T, H, float(lw.post_norm.variance_epsilon), 0, 0, s)
-            self._mlp_static(lw, T, s)
+            self._gateup_static(lw, T, s)
             nxt = self.h[cur ^ 1]
             deep = self.deep[j] if j < len(self.deep) else None
             nn = L[j + 1].input_norm
-            call("ff_add_rms_quant_static", ptr(self.res), ptr(self.dn), ptr(deep), ptr(nn.weight), ptr(nxt), None,
-                 ptr(self.xq), float(L[j + 1].qkv.inverse_scale), T, H, float(nn.variance_epsilon), self.image_start,
-                 self.nv if deep is not None else 0, s)
+            dw = lw.down
+            call("ff_gemm_fp8_pk_add_rms_quant_static", ptr(self.mq), ptr(dw.input_scale), 0, ptr(dw.weight),
+                 ptr(dw.packed), ptr(dw.weight_scale), 0, ptr(self.dn), T, H, I, ptr(self.gws), self.gws.numel(),
+                 ptr(self.res), ptr(deep), ptr(nn.weight), ptr(nxt), ptr(self.xq), float(L[j + 1].qkv.inverse_scale),
+                 float(nn.variance_epsilon), self.image_start, self.nv if deep is not None else 0, s)
             cur ^= 1
             if trace is not None:
                 trace.append(nxt.clone())
@@ -445,11 +454,14 @@ class Runtime:
         call("ff_gemm_fp8_pk", ptr(q), ptr(op.input_scale), 0, ptr(op.weight), ptr(op.packed), ptr(op.weight_scale),
              0, ptr(out), n, m, n, k, ptr(self.gws), self.gws.numel(), s)
 
-    def _mlp_static(self, lw, m, s):
+    def _gateup_static(self, lw, m, s):
         I, H = self.cfg.inter, self.cfg.hidden
         op = lw.gateup
         call("ff_gemm_fp8_swiglu_static", ptr(self.pq), ptr(op.input_scale), ptr(op.weight), ptr(op.packed),
              ptr(op.weight_scale), ptr(self.mq), I, float(lw.down.inverse_scale), m, I, H, s)
+
+    def _mlp_static(self, lw, m, s):
+        self._gateup_static(lw, m, s)
         self._gemm_static(self.mq, lw.down, self.dn, m, s)
 
     def _step_generic(self, trace=None):

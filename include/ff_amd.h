@@ -203,6 +203,27 @@ int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, const void* qw,
                    const float* sw, int sw_cols, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
                    void* workspace, int64_t workspace_bytes, ff_stream_t stream);
 
+/* Down projection + the next add_rms (no reference counterpart as one op: the
+ * down Linear of scaled_qwen_runtime.py:35-39 followed by the add_rms of
+ * _legacy/lower_kernels.py:7-32 with the per-token quant of
+ * _legacy/fp8_private.py:11-18, or, _static, the runtime-scale cast of
+ * _family/depth_fp8.py:8-19 with multiplier inv): ff_gemm_fp8_pk into y (m, n)
+ * bf16 (row stride n), then ff_add_rms_quant(a, y, deep, w, residual, NULL, q,
+ * scales, m, n, eps, start, nv) (_static: ff_add_rms_quant_static with inv),
+ * bit for bit. Where the GEMM splits k the add_rms launch adds the fp32
+ * partials itself, taking the place of the reduction launch; the workspace is
+ * ff_gemm_fp8_pk_workspace bytes as for ff_gemm_fp8_pk. */
+int ff_gemm_fp8_pk_add_rms_quant(const void* qa, const float* sa, int sa_rows, const void* qw, const void* qw_packed,
+                                 const float* sw, int sw_cols, void* y, int64_t m, int64_t n, int64_t k,
+                                 void* workspace, int64_t workspace_bytes, const void* a, const void* deep,
+                                 const void* w, void* residual, void* q, float* scales, float eps, int64_t start,
+                                 int64_t nv, ff_stream_t stream);
+int ff_gemm_fp8_pk_add_rms_quant_static(const void* qa, const float* sa, int sa_rows, const void* qw,
+                                        const void* qw_packed, const float* sw, int sw_cols, void* y, int64_t m,
+                                        int64_t n, int64_t k, void* workspace, int64_t workspace_bytes,
+                                        const void* a, const void* deep, const void* w, void* residual, void* q,
+                                        float inv, float eps, int64_t start, int64_t nv, ff_stream_t stream);
+
 /* Fused QKV GEMM + q/k norm + rotary + V transpose (no reference counterpart as
  * one op; the same arithmetic as ff_gemm_fp8 on the packed QKV weight followed
  * by ff_qkv_post): qw ((hq + 2 hk) * 128, k) e4m3 with scales sw (per row if

@@ -400,6 +400,55 @@ def test_gemm_fp8_pk_matches_rowmajor(gpu, m, n, k, splits):
                          "gemm_fp8_pk split 4")
 
 
+@pytest.mark.parametrize("m,n,k,static,deep", [(576, 4096, 12288, False, True), (576, 4096, 12288, True, False),
+                                               (500, 4096, 12288, False, False), (300, 2048, 8192, True, True),
+                                               (576, 4096, 4096, False, False), (1, 4096, 12288, False, False),
+                                               (1, 4096, 12288, True, False)])
+def test_gemm_fp8_pk_add_rms_equals_unfused(gpu, m, n, k, static, deep):
+    """ff_gemm_fp8_pk_add_rms_quant(_static) == ff_gemm_fp8_pk followed by
+    ff_add_rms_quant(_static), bit for bit in y, the residual, the e4m3 codes
+    and the scales: on the split shapes the add_rms launch adds the split-K
+    partials itself (500 rows: the last 144-row tile ragged; DeepStack rows
+    inside the range), elsewhere (k = 4096, one row) the two entry points
+    run."""
+    from fastforward_amd._lib import call, ptr, stream
+    from fastforward_amd.linear import FP8Linear, gemm_pk_workspace
+    x = (torch.randn(m, k, generator=_g(64)) * 2).to(BF16).to(DEV)
+    op = FP8Linear((torch.randn(n, k, generator=_g(65)) * 0.03).to(BF16).to(DEV)).pack()
+    qa, sa = op.quantize(x)
+    a = (torch.randn(m, n, generator=_g(66)) * 4).to(BF16).to(DEV)
+    w = (1 + 0.1 * torch.randn(n, generator=_g(67))).to(BF16).to(DEV)
+    dp = (torch.randn(40, n, generator=_g(68))).to(BF16).to(DEV) if deep else None
+    start, nv = (min(10, m - 1), min(40, m - min(10, m - 1))) if deep else (0, 0)
+    ws = torch.full((max(gemm_pk_workspace(m, n, k), 256),), 0xFF, device=DEV, dtype=torch.uint8)
+    inv = 448 / 30.0
+    outs = []
+    for fused in (False, True):
+        y = torch.full((m, n), float("nan"), device=DEV, dtype=BF16)
+        res = torch.full((m, n), float("nan"), device=DEV, dtype=BF16)
+        q = torch.full((m, n), 0x7F, device=DEV, dtype=torch.uint8)
+        sc = torch.full((m,), float("nan"), device=DEV)
+        gemm = [ptr(qa), ptr(sa), 1, ptr(op.weight), ptr(op.packed), ptr(op.scale), 1, ptr(y)]
+        if fused:
+            tail = [ptr(a), ptr(dp), ptr(w), ptr(res), ptr(q)] + ([inv] if static else [ptr(sc)])
+            call("ff_gemm_fp8_pk_add_rms_quant" + ("_static" if static else ""), *gemm, m, n, k, ptr(ws), ws.numel(),
+                 *tail, 1e-6, start, nv, stream())
+        else:
+            call("ff_gemm_fp8_pk", *gemm, n, m, n, k, ptr(ws), ws.numel(), stream())
+            if static:
+                call("ff_add_rms_quant_static", ptr(a), ptr(y), ptr(dp), ptr(w), ptr(res), None, ptr(q), inv, m, n,
+                     1e-6, start, nv, stream())
+            else:
+                call("ff_add_rms_quant", ptr(a), ptr(y), ptr(dp), ptr(w), ptr(res), None, ptr(q), ptr(sc), m, n,
+                     1e-6, start, nv, stream())
+        outs.append((y, res, q, sc))
+    (y0, r0, q0, s0), (y1, r1, q1, s1) = outs
+    assert not torch.isnan(y0.float()).any() and not torch.isnan(r0.float()).any()
+    assert torch.equal(y0, y1) and torch.equal(r0, r1) and torch.equal(q0, q1)
+    if not static:
+        assert torch.equal(s0, s1)
+
+
 def test_gemm_fp8_pk_scalar_scales(gpu):
     """Per-tensor scales (sa_rows = sw_cols = 0) on the split path agree with ff_gemm_fp8."""
     from fastforward_amd._lib import call, ptr, stream
