@@ -64,6 +64,7 @@ SIGNATURES = {
     "ff_pack_scales_int4": [P, P, I64, I64, I64, P],
     "ff_gemm_w4a16_pk_workspace": [I64, I64, I64, I64, PI64],
     "ff_gemm_w4a16_pk": [P, I64, P, P, P, P, I64, P, I64, I64, I64, I64, P, I64, P],
+    "ff_gemm_w4a16_pk_add_rms": [P, I64, P, P, P, P, I64, P, I64, I64, I64, P, I64, P, P, P, P, P, F32, I64, I64, P],
     "ff_gemm_w4a16_swiglu_fits": [I64, I64, I64, I64, PI32],
     "ff_gemm_w4a16_swiglu_pk": [P, I64, P, P, I64, P, I64, I64, I64, I64, P],
     "ff_gemm_w4a16_qkv_workspace": [I64, I64, I64, I64, I64, PI64],

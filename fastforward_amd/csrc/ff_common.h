@@ -85,6 +85,41 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// A BM x 4 CW fp32 accumulator tile of 256 threads (lane 16 g + r of wave w,
+// fragment (i, j): row 16 i + r, columns w CW + 16 j + 4 g .. + 3) stored
+// row-major at dst (row stride ld floats) through the workgroup's LDS (SMEM
+// bytes at smem), a group of 16-row blocks at a time, so that every store
+// instruction writes whole row segments instead of 64 bytes to each of 16
+// rows. Called by every thread; it opens with a barrier, so the caller's LDS
+// may still be in use when it is called.
+template <int BM, int CW, int SMEM>
+__device__ __forceinline__ void store_tile_rows_lds(const f32x4 (&acc)[BM / 16][CW / 16], uint8_t* smem, float* dst,
+                                                    int64_t ld, int tid) {
+  constexpr int RA = BM / 16, TJ = CW / 16, BN = 4 * CW;
+  constexpr int LDW = BN + 4;  // floats per staged row; the pad spreads the rows over the banks
+  constexpr int GR = SMEM / (16 * LDW * 4);
+  static_assert(GR >= 1, "one 16-row group fits the LDS");
+  float* stg = reinterpret_cast<float*>(smem);
+  const int lane = tid & 63, wave = tid >> 6;
+  float* mine = stg + (lane & 15) * LDW + wave * CW + 4 * (lane >> 4);
+  static_for<0, (RA + GR - 1) / GR>([&](auto R_) {
+    constexpr int i0 = decltype(R_)::value * GR;
+    constexpr int ng = RA - i0 < GR ? RA - i0 : GR;
+    barrier_lds();  // the LDS (the caller's, or the previous group's) is no longer read
+#pragma unroll
+    for (int ii = 0; ii < ng; ++ii)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) *reinterpret_cast<f32x4*>(mine + ii * 16 * LDW + 16 * j) = acc[i0 + ii][j];
+    barrier_lds();
+#pragma unroll
+    for (int e = tid; e < ng * 16 * (BN / 4); e += 256) {
+      const int r = e / (BN / 4), c4 = e % (BN / 4);
+      *reinterpret_cast<f32x4*>(dst + (int64_t)(16 * i0 + r) * ld + 4 * c4) =
+          *reinterpret_cast<const f32x4*>(stg + r * LDW + 4 * c4);
+    }
+  });
+}
+
 // ------------------------------------------------------------------ bf16
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
@@ -375,6 +410,12 @@ int gemm_swiglu_static_rowmajor(const void* qa, const float* sa, const void* qw,
 int gemm_fp8_pk_partials(const void* qa, const float* sa, int sa_rows, const void* qw_packed, const float* sw,
                          int sw_cols, int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes,
                          hipStream_t st, int* splits, int64_t* mp);
+// The same for ff_gemm_w4a16_pk (defined with the W4A16 kernels): where it
+// splits k on the packed copies, the split GEMM with its fp32 partials
+// row-major in workspace ((*splits, *mp, n)); elsewhere *splits = 0.
+int gemm_w4a16_pk_partials(const void* x, int64_t ldx, const void* frag, const void* frag_scales, int64_t group,
+                           int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes, hipStream_t st,
+                           int* splits, int64_t* mp);
 }  // namespace ff
 
 #define FF_REQUIRE(cond, ...)          \

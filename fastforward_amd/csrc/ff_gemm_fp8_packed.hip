@@ -430,33 +430,8 @@ __global__ __launch_bounds__(kThreads, BM < 144 ? 2 : 1) void gemm_fp8_split_pac
   f32x4 acc[RA][TJ];
   pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, split * nk, nk, [] {});
   if constexpr (S > 1) {
-    // The partial tile goes out through LDS, GR 16-row groups at a time, so
-    // that every store instruction writes one whole 1 KB row segment (the
-    // accumulators scatter 64 bytes to each of 16 rows). Lane 16 g + r of
-    // fragment (i, j) holds row 16 i + r, columns wave CW + 16 j + 4 g .. + 3.
-    constexpr int LDW = BN + 4;  // floats per staged row; the pad spreads the rows over the banks
-    constexpr int GR = SMEM / (16 * LDW * 4);
-    static_assert(GR >= 1, "one 16-row group fits the LDS");
-    float* stg = reinterpret_cast<float*>(smem);
-    float* dst = part + ((int64_t)split * tiles_m * BM + m0) * N + n0;
-    const int lane = tid & 63;
-    float* mine = stg + (lane & 15) * LDW + wave * CW + 4 * (lane >> 4);
-    static_for<0, (RA + GR - 1) / GR>([&](auto R_) {
-      constexpr int i0 = decltype(R_)::value * GR;
-      constexpr int ng = RA - i0 < GR ? RA - i0 : GR;
-      barrier_lds();  // the stage (main loop or previous round) is no longer read
-#pragma unroll
-      for (int ii = 0; ii < ng; ++ii)
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) *reinterpret_cast<f32x4*>(mine + ii * 16 * LDW + 16 * j) = acc[i0 + ii][j];
-      barrier_lds();
-#pragma unroll
-      for (int e = tid; e < ng * 16 * (BN / 4); e += kThreads) {
-        const int r = e / (BN / 4), c4 = e % (BN / 4);
-        *reinterpret_cast<f32x4*>(dst + (int64_t)(16 * i0 + r) * N + 4 * c4) =
-            *reinterpret_cast<const f32x4*>(stg + r * LDW + 4 * c4);
-      }
-    });
+    // the fp32 partial tile, row-major over the rows padded to whole tiles
+    store_tile_rows_lds<BM, CW, SMEM>(acc, smem, part + ((int64_t)split * tiles_m * BM + m0) * N + n0, N, tid);
   } else {
     pk_store_tile<BM, CW>(acc, sa, sa_rows, sw, sw_cols, y, ldy, M, m0, n0);
   }

@@ -780,14 +780,16 @@ __device__ __forceinline__ void w4pk_store(const f32x4 (&acc)[BM / 16][CW / 16],
 
 // Plain y = bf16(x . W^T) with k split `splits` ways (pairs of k steps dealt
 // evenly). With part null (then splits == 1) it stores y; otherwise each split
-// stores its fp32 partial tile in accumulator order (f32x4 (i, j) of thread t
-// at ((tile splits + split) RA TJ + i TJ + j) 256 + t) and a reduction kernel
-// (w4pk_reduce_kernel, w4pk_qkv_kernel) adds them.
+// stores its fp32 partial tile and a reduction adds them: ROWPART, row-major
+// over the rows padded to whole tiles, part[(split Mp + row) N + col] (Mp =
+// tiles_m BM; w4pk_reduce_kernel or the add_rms row kernel that takes the
+// partials as its addend); else in accumulator order (f32x4 (i, j) of thread t
+// at ((tile splits + split) RA TJ + i TJ + j) 256 + t; w4pk_qkv_kernel).
 // SWIGLU: the weight is [gate (half rows); up (half rows)]; wave w takes gate
 // channels [w CW/2, (w + 1) CW/2) of the tile's BN/2 and the matching up
 // channels as fragments j = 2 t (gate) and 2 t + 1 (up), and stores
 // h = bf16(bf16(silu(g)) * u) into y (M, half) with g, u = bf16(acc).
-template <int BM, int CW, bool SWIGLU>
+template <int BM, int CW, bool SWIGLU, bool ROWPART = false>
 __global__ __launch_bounds__(kThreads, 1) void gemm_w4a16_pk_kernel(
     const bf16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ wp, const float* __restrict__ sz,
     int gshift, bf16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int tiles_m, int tiles_n, int splits,
@@ -862,7 +864,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_w4a16_pk_kernel(
       }
     }
   } else {
-    if (part != nullptr) {
+    if (part != nullptr && ROWPART) {
+      store_tile_rows_lds<BM, CW, SMEM>(acc, smem,
+                                        reinterpret_cast<float*>(part) + ((int64_t)split * tiles_m * BM + m0) * N +
+                                            tn * BN,
+                                        N, tid);
+    } else if (part != nullptr) {
       f32x4* mine = part + ((int64_t)(tn * tiles_m + tm) * splits + split) * (RA * TJ * kThreads) + tid;
 #pragma unroll
       for (int i = 0; i < RA; ++i)
@@ -874,32 +881,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_w4a16_pk_kernel(
   }
 }
 
-// y for the tiles of a split launch, one workgroup per (tile, 16-row group i):
-// the partials of each accumulator added in split order 0, 1, .. (whatever
-// order the splits finished in), then rounded to bf16.
-template <int BM, int CW>
-__global__ __launch_bounds__(kThreads) void w4pk_reduce_kernel(const f32x4* __restrict__ part, int splits,
-                                                               bf16_t* __restrict__ y, int64_t ldy, int M,
-                                                               int tiles_m) {
-  constexpr int RA = BM / 16, TJ = CW / 16, BN = 4 * CW;
-  const int tile = blockIdx.x / RA, i = blockIdx.x % RA;
-  const int tm = tile % tiles_m, tn = tile / tiles_m;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r16 = lane & 15, g = lane >> 4;
-  const f32x4* tp = part + (int64_t)tile * splits * (RA * TJ * kThreads) + i * TJ * kThreads + tid;
-  f32x4 t[TJ];
-#pragma unroll
-  for (int j = 0; j < TJ; ++j) t[j] = tp[j * kThreads];
-  for (int s2 = 1; s2 < splits; ++s2)
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) t[j] = t[j] + tp[((int64_t)s2 * RA * TJ + j) * kThreads];
-  const int m = tm * BM + 16 * i + r16;
+// y = bf16(sum of the splits' row-major partials) for rows < M, added in split
+// order 0, 1, .. (whatever order the splits finished in); one thread per 8
+// columns.
+__global__ __launch_bounds__(kThreads) void w4pk_reduce_kernel(const float* __restrict__ part, int splits, int64_t mp,
+                                                               bf16_t* __restrict__ y, int64_t ldy, int M, int N) {
+  const int nc = N / 8;
+  const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int m = (int)(e / nc), col = (int)(e % nc) * 8;
   if (m >= M) return;
-#pragma unroll
-  for (int j = 0; j < TJ; ++j) {
-    const int col = tn * BN + wave * CW + 16 * j + 4 * g;
-    *reinterpret_cast<u32x2*>(y + (int64_t)m * ldy + col) = pack4_bf16(t[j][0], t[j][1], t[j][2], t[j][3]);
+  const float* src = part + (int64_t)m * N + col;
+  f32x4 t0 = *reinterpret_cast<const f32x4*>(src), t1 = *reinterpret_cast<const f32x4*>(src + 4);
+  for (int s2 = 1; s2 < splits; ++s2) {
+    const float* p = src + (int64_t)s2 * mp * N;
+    t0 = t0 + *reinterpret_cast<const f32x4*>(p);
+    t1 = t1 + *reinterpret_cast<const f32x4*>(p + 4);
   }
+  const float f[8] = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
+  *reinterpret_cast<u32x4*>(y + (int64_t)m * ldy + col) = pack8(f);
 }
 
 // Rows m <= 4 (the pick-only tail) on the packed copies: a workgroup of 4 waves
@@ -1076,13 +1075,15 @@ void launch_w4pk(const void* x, int64_t ldx, const void* frag, const void* fscal
                  int m, int n, int k, int splits, void* ws, hipStream_t s) {
   const int tiles_m = (m + kW4BM - 1) / kW4BM;
   const int tiles_n = n / (4 * CW);  // SWIGLU: n = 2 half rows, 2 CW channels of each half per tile
-  hipLaunchKernelGGL((gemm_w4a16_pk_kernel<kW4BM, CW, SWIGLU>), dim3((unsigned)(tiles_m * tiles_n * splits)),
+  hipLaunchKernelGGL((gemm_w4a16_pk_kernel<kW4BM, CW, SWIGLU, !SWIGLU>), dim3((unsigned)(tiles_m * tiles_n * splits)),
                      dim3(kThreads), 0, s, (const bf16_t*)x, ldx, (const uint8_t*)frag, (const float*)fscales,
                      gshift, (bf16_t*)y, ldy, m, n, k, tiles_m, tiles_n, splits,
                      !SWIGLU && splits > 1 ? (f32x4*)ws : nullptr);
-  if (!SWIGLU && splits > 1)
-    hipLaunchKernelGGL((w4pk_reduce_kernel<kW4BM, CW>), dim3((unsigned)(tiles_m * tiles_n * (kW4BM / 16))),
-                       dim3(kThreads), 0, s, (const f32x4*)ws, splits, (bf16_t*)y, ldy, m, tiles_m);
+  if (!SWIGLU && splits > 1 && y != nullptr) {
+    const int64_t chunks = (int64_t)m * (n / 8);
+    hipLaunchKernelGGL(w4pk_reduce_kernel, dim3((unsigned)((chunks + kThreads - 1) / kThreads)), dim3(kThreads), 0, s,
+                       (const float*)ws, splits, (int64_t)tiles_m * kW4BM, (bf16_t*)y, ldy, m, n);
+  }
 }
 
 }  // namespace
@@ -1134,6 +1135,29 @@ extern "C" int ff_gemm_w4a16_pk_workspace(int64_t m, int64_t n, int64_t k, int64
   *bytes = std::max(w4pk_workspace(m, n, k, group), other);
   return FF_OK;
 }
+
+namespace ff {
+int gemm_w4a16_pk_partials(const void* x, int64_t ldx, const void* frag, const void* frag_scales, int64_t group,
+                           int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes, hipStream_t st,
+                           int* splits, int64_t* mp) {
+  *splits = 0;
+  *mp = 0;
+  if (!frag || !frag_scales || w4pk_gemv_fits(m, n, k, group)) return FF_OK;
+  const W4PkPlan p = w4pk_plan(m, n, k, group);
+  if (p.cw != 64 || p.splits <= 1 || ldx % 8 || ldx < k || m * ldx * 2 >= (int64_t(1) << 31) || !ff_aligned(x, 16) ||
+      !ff_aligned(frag, 16) || !ff_aligned(frag_scales, 8))
+    return FF_OK;
+  const int64_t need = w4pk_workspace(m, n, k, group);
+  FF_REQUIRE(workspace && workspace_bytes >= need && ff_aligned(workspace, 16),
+             "ff_gemm_w4a16_pk: workspace of %lld bytes (16-byte aligned) required", (long long)need);
+  launch_w4pk<64, false>(x, ldx, frag, frag_scales, w4_gshift(group), nullptr, 0, (int)m, (int)n, (int)k, p.splits,
+                         workspace, st);
+  FF_LAUNCH_CHECK("ff_gemm_w4a16_pk");
+  *splits = p.splits;
+  *mp = (m + kW4BM - 1) / kW4BM * kW4BM;
+  return FF_OK;
+}
+}  // namespace ff
 
 extern "C" int ff_gemm_w4a16_pk(const void* x, int64_t ldx, const void* packed, const void* frag, const void* scales,
                                 const void* frag_scales, int64_t group, void* y, int64_t ldy, int64_t m, int64_t n,

@@ -16,14 +16,16 @@ namespace {
 // scales[row]) or a static calibrated multiplier (e4m3(clamp(x * sinv, +-448))).
 constexpr int kNoQuant = 0, kDynamic = 1, kStatic = 2;
 
-// The addend of add_rms given as the S fp32 split-K partials of an FP8 GEMM
-// (row-major, (S, mp, h)) instead of bf16: b = bf16((sum_s part_s * sa[row]) *
-// sw[col]), the partials added in split order -- the split GEMM's own
-// reduction, bit for bit -- and stored to y (row stride h) as that GEMM's output.
+// The addend of add_rms given as the fp32 split-K partials of a GEMM
+// (row-major, (splits, mp, h)) instead of bf16: b = bf16(sum_s part_s), or with
+// scales (an FP8 GEMM) b = bf16((sum_s part_s * sa[row]) * sw[col]); the
+// partials added in split order -- the split GEMM's own reduction, bit for bit
+// -- and b stored to y (row stride h) as that GEMM's output.
 struct SplitAddend {
   const float* part = nullptr;
   int64_t mp = 0;
-  const float* sa = nullptr;
+  int splits = 0;
+  const float* sa = nullptr;  // null: no scales
   int sa_rows = 0;
   const float* sw = nullptr;
   int sw_cols = 0;
@@ -32,7 +34,7 @@ struct SplitAddend {
 
 // One workgroup per row, blockDim.x threads (a multiple of 64, <= 1024) with
 // CPT 16-byte chunks each (row_shape picks both from h). SPLIT > 0: the addend
-// b comes from SPLIT split-K partials (sb) instead of the bf16 array b.
+// b comes from sb.splits <= SPLIT split-K partials instead of the bf16 array b.
 template <int CPT, bool ADD, bool DEEP, bool WRITE_RES, bool WRITE_OUT, int QUANT, int SPLIT = 0>
 __global__ __launch_bounds__(1024) void row_norm_kernel(
     const bf16_t* __restrict__ a, const bf16_t* __restrict__ b, const bf16_t* __restrict__ deep,
@@ -48,7 +50,7 @@ __global__ __launch_bounds__(1024) void row_norm_kernel(
   u32x4 va[CPT], vb[CPT], vw[CPT];
   f32x4 vp[CPT][SPLIT > 0 ? SPLIT : 1][2], vs[CPT][2];
   float sav = 0.f;
-  if constexpr (SPLIT > 0) sav = sb.sa[sb.sa_rows ? row : 0];
+  if constexpr (SPLIT > 0) sav = sb.sa ? sb.sa[sb.sa_rows ? row : 0] : 0.f;
   const bool in_deep = DEEP && row >= start && row < start + nv;
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
@@ -58,11 +60,14 @@ __global__ __launch_bounds__(1024) void row_norm_kernel(
       if constexpr (ADD && SPLIT > 0) {
 #pragma unroll
         for (int s2 = 0; s2 < SPLIT; ++s2) {
-          const float* src = sb.part + ((int64_t)s2 * sb.mp + row) * h + (size_t)idx * 8;
-          vp[c][s2][0] = *reinterpret_cast<const f32x4*>(src);
-          vp[c][s2][1] = *reinterpret_cast<const f32x4*>(src + 4);
+          if (s2 < sb.splits) {
+            const float* src = sb.part + ((int64_t)s2 * sb.mp + row) * h + (size_t)idx * 8;
+            vp[c][s2][0] = *reinterpret_cast<const f32x4*>(src);
+            vp[c][s2][1] = *reinterpret_cast<const f32x4*>(src + 4);
+          }
         }
-        if (sb.sw_cols && ((uintptr_t)sb.sw & 15) == 0) {
+        if (!sb.sa) {
+        } else if (sb.sw_cols && ((uintptr_t)sb.sw & 15) == 0) {
           vs[c][0] = *reinterpret_cast<const f32x4*>(sb.sw + (size_t)idx * 8);
           vs[c][1] = *reinterpret_cast<const f32x4*>(sb.sw + (size_t)idx * 8 + 4);
         } else if (sb.sw_cols) {
@@ -94,9 +99,10 @@ __global__ __launch_bounds__(1024) void row_norm_kernel(
           for (int hh = 0; hh < 2; ++hh) {
             f32x4 t = vp[c][0][hh];
 #pragma unroll
-            for (int s2 = 1; s2 < SPLIT; ++s2) t = t + vp[c][s2][hh];
+            for (int s2 = 1; s2 < SPLIT; ++s2)
+              if (s2 < sb.splits) t = t + vp[c][s2][hh];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) y[4 * hh + r] = (t[r] * sav) * vs[c][hh][r];
+            for (int r = 0; r < 4; ++r) y[4 * hh + r] = sb.sa ? (t[r] * sav) * vs[c][hh][r] : t[r];
           }
           const u32x4 yb = pack8(y);
           *reinterpret_cast<u32x4*>(sb.y + base + (size_t)idx * 8) = yb;
@@ -431,6 +437,7 @@ int gemm_add_rms(const char* name, const void* qa, const float* sa, int sa_rows,
   SplitAddend sb;
   sb.part = (const float*)workspace;
   sb.mp = mp;
+  sb.splits = splits;
   sb.sa = sa;
   sb.sa_rows = sa_rows;
   sb.sw = sw;
@@ -463,4 +470,45 @@ extern "C" int ff_gemm_fp8_pk_add_rms_quant_static(const void* qa, const float* 
   return gemm_add_rms<kStatic>("ff_gemm_fp8_pk_add_rms_quant_static", qa, sa, sa_rows, qw, qw_packed, sw, sw_cols, y,
                                m, n, k, workspace, workspace_bytes, a, deep, w, residual, q, nullptr, inv, eps, start,
                                nv, stream);
+}
+
+// ff_gemm_w4a16_pk into y, then ff_add_rms(a, y, ..), with the split-K
+// partials (where that GEMM splits k on the packed copies) added by the
+// add_rms launch in place of the reduction launch.
+extern "C" int ff_gemm_w4a16_pk_add_rms(const void* x, int64_t ldx, const void* packed, const void* frag,
+                                        const void* scales, const void* frag_scales, int64_t group, void* y, int64_t m,
+                                        int64_t n, int64_t k, void* workspace, int64_t workspace_bytes, const void* a,
+                                        const void* deep, const void* w, void* residual, void* out, float eps,
+                                        int64_t start, int64_t nv, ff_stream_t stream) {
+  const char* name = "ff_gemm_w4a16_pk_add_rms";
+  int st = check_rows(name, a, m, n);
+  if (st) return st;
+  FF_REQUIRE(x && y && w && residual && out, "%s: null pointer", name);
+  FF_REQUIRE(ff_aligned(y, 16) && ff_aligned(w, 16) && ff_aligned(residual, 16) && ff_aligned(out, 16),
+             "%s: y, w, residual and out must be 16-byte aligned", name);
+  FF_REQUIRE(!deep || (ff_aligned(deep, 16) && nv >= 0 && start >= 0), "%s: bad deep", name);
+  if (m == 0) return FF_OK;
+  hipStream_t s = (hipStream_t)stream;
+  int splits = 0;
+  int64_t mp = 0;
+  st = ff::gemm_w4a16_pk_partials(x, ldx, frag, frag_scales, group, m, n, k, workspace, workspace_bytes, s, &splits,
+                                  &mp);
+  if (st) return st;
+  if (splits == 0) {
+    st = ff_gemm_w4a16_pk(x, ldx, packed, frag, scales, frag_scales, group, y, n, m, n, k, workspace, workspace_bytes,
+                          stream);
+    if (st) return st;
+    return ff_add_rms(a, y, deep, w, residual, out, m, n, eps, start, nv, stream);
+  }
+  FF_REQUIRE(splits <= 8, "%s: unexpected split count %d", name, splits);
+  SplitAddend sb;
+  sb.part = (const float*)workspace;
+  sb.mp = mp;
+  sb.splits = splits;
+  sb.y = (bf16_t*)y;
+  if (deep && nv > 0)
+    return launch_row_norm<true, true, true, true, kNoQuant, 8>(a, nullptr, deep, w, residual, out, nullptr, nullptr,
+                                                                m, n, eps, start, nv, s, name, 0.f, sb);
+  return launch_row_norm<true, false, true, true, kNoQuant, 8>(a, nullptr, nullptr, w, residual, out, nullptr, nullptr,
+                                                               m, n, eps, 0, 0, s, name, 0.f, sb);
 }

@@ -287,6 +287,35 @@ class Int4:
             self._check(flat, y)
         return y
 
+    def add_rms(self, x, a, deep, module, start=0, nv=0):
+        """``ops.add_rms(a, self(x), deep, module, start, nv)`` in one op
+        (ff_gemm_w4a16_pk_add_rms: where the packed GEMM splits k, the add_rms
+        launch adds its fp32 partials; the same bits). Returns (residual, out)
+        like ``ops.add_rms``."""
+        from . import ops
+        if self.frag is None:
+            return ops.add_rms(a, self(x), deep, module, start, nv)
+        flat = _rows(x)
+        if flat.stride(-1) != 1 or flat.stride(0) % 8:
+            flat = flat.contiguous()
+        if self.oracle is not None:
+            self(flat[:1])  # the first-call operator check, on the GEMM alone
+        m, k = flat.shape
+        n = self.weight.shape[0]
+        assert a.is_contiguous() and a.dtype == BF16 and a.shape[-1] == n and a.numel() == m * n
+        if deep is not None:
+            assert deep.shape == (nv, n) and deep.is_contiguous()
+        need = ctypes.c_int64(0)
+        call("ff_gemm_w4a16_pk_workspace", m, n, k, self.group, ctypes.byref(need))
+        ws = torch.empty(need.value, device=x.device, dtype=torch.uint8) if need.value else None
+        y = torch.empty((m, n), device=x.device, dtype=BF16)
+        residual, out = torch.empty_like(a), torch.empty_like(a)
+        call("ff_gemm_w4a16_pk_add_rms", ptr(flat), flat.stride(0), ptr(self.packed), ptr(self.frag), ptr(self.scales),
+             ptr(self.frag_scales), self.group, ptr(y), m, n, k, ptr(ws), need.value, ptr(a), ptr(deep),
+             ptr(module.weight), ptr(residual), ptr(out), float(module.variance_epsilon), int(start), int(nv),
+             stream())
+        return residual, out
+
     def qkv(self, x, hq, hk, q_norm, k_norm, cos, sin):
         """The QKV linear with qk_pair and the V transpose in one op
         (ff_gemm_w4a16_qkv): x (1, T, H) -> yq (1, hq, T, 128), yk (1, hk, T, 128),

@@ -476,11 +476,11 @@ class Runtime:
         for j in range(cfg.layers - 1):
             lw = L[j]
             attn = self._attention_generic(lw, normalized, cos, sin)
-            residual, post = ops.add_rms(h, attn, None, lw.post_norm)
-            value = Linear.apply(self._swiglu(post, lw.gateup), lw.down)
+            residual, post = self._linear_add_rms(attn, lw.o, h, None, lw.post_norm)
             deep = self.deep[j] if j < len(self.deep) else None
-            h, normalized = ops.add_rms(residual, value, deep, L[j + 1].input_norm, self.image_start,
-                                        self.nv if deep is not None else 0)
+            h, normalized = self._linear_add_rms(self._swiglu(post, lw.gateup), lw.down, residual, deep,
+                                                 L[j + 1].input_norm, self.image_start,
+                                                 self.nv if deep is not None else 0)
             if trace is not None:
                 trace.append(h[0].clone())
         lw = L[-1]
@@ -511,6 +511,16 @@ class Runtime:
         return self.logits
 
     @staticmethod
+    def _linear_add_rms(x, op, a, deep, module, start=0, nv=0):
+        """add_rms(a, Linear.apply(x, op), deep, module, start, nv)
+        (scaled_qwen_runtime.py:158-162): one fused op for a packed Int4 (the
+        add_rms launch adds the GEMM's split-K partials; the same bits), else
+        the two ops."""
+        if isinstance(op, Int4) and op.frag is not None:
+            return op.add_rms(x, a, deep, module, start, nv)
+        return ops.add_rms(a, Linear.apply(x, op), deep, module, start, nv)
+
+    @staticmethod
     def _swiglu(x, op):
         """swiglu(g, u) for [g, u] = Linear.apply(x, op).chunk(2, -1)
         (scaled_qwen_runtime.py:174-176): one fused launch for a packed Int4
@@ -532,13 +542,13 @@ class Runtime:
             out = torch.empty((1, t, HQ, D), device=x.device, dtype=x.dtype)
             call("ff_attention_vt", ptr(yq), ptr(yk), ptr(vt), None, 0, ptr(out), t, t, tp, HQ, HK, D,
                  float(cfg.scaling), stream())
-            return Linear.apply(out.reshape(*x.shape[:-1], -1), lw.o)
+            return out.reshape(*x.shape[:-1], -1)
         q, k, v = Linear.apply(x, lw.qkv).split([HQ * D, HK * D, HK * D], -1)
         shape = (*x.shape[:-1], -1, D)
         q, k = ops.qk_pair(q.view(shape), k.view(shape), lw.q_norm, lw.k_norm, cos, sin)
         v = v.view(shape).transpose(1, 2)
         out = ops.attention_direct(q, k, v, cfg.scaling)
-        return Linear.apply(out.reshape(*x.shape[:-1], -1), lw.o)
+        return out.reshape(*x.shape[:-1], -1)
 
     def _index_rows(self, x, idx, dim1=False):
         """Rows ``idx`` of x along its token axis on the device (index_select);

@@ -355,6 +355,18 @@ int ff_gemm_w4a16_pk(const void* x, int64_t ldx, const void* packed, const void*
                      const void* frag_scales, int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
                      void* workspace, int64_t workspace_bytes, ff_stream_t stream);
 
+/* An Int4 linear + the add_rms it feeds (no reference counterpart as one op:
+ * Linear.apply of an Int4, _family/night_runtime.py:31-42, followed by the
+ * add_rms of _legacy/lower_kernels.py:7-32): ff_gemm_w4a16_pk into y (m, n)
+ * bf16 (row stride n), then ff_add_rms(a, y, deep, w, residual, out, m, n,
+ * eps, start, nv), bit for bit. Where the GEMM splits k on the packed copies
+ * the add_rms launch adds the fp32 partials itself, taking the place of the
+ * reduction launch; workspace as for ff_gemm_w4a16_pk. */
+int ff_gemm_w4a16_pk_add_rms(const void* x, int64_t ldx, const void* packed, const void* frag, const void* scales,
+                             const void* frag_scales, int64_t group, void* y, int64_t m, int64_t n, int64_t k,
+                             void* workspace, int64_t workspace_bytes, const void* a, const void* deep, const void* w,
+                             void* residual, void* out, float eps, int64_t start, int64_t nv, ff_stream_t stream);
+
 /* Gate/up W4A16 GEMM with SwiGLU in its epilogue: h (m, i) = bf16(bf16(silu(g))
  * * u) with g, u = bf16 of x @ dequant(W)^T for W = [gate (i rows); up (i rows)]
  * (frag / frag_scales: ff_pack_weight_int4 / ff_pack_scales_int4 of the

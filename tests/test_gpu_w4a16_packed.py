@@ -210,3 +210,26 @@ def test_w4a16_qkv_fused_equals_unfused(gpu, m, k, hq, hk, sym, group):
     call("ff_v_transpose", ptr(vv), vv.stride(2), vv.stride(1), ptr(rvt), m, tp, hk, d, stream())
     assert torch.equal(vt, rvt)
     assert int(vt[:, :, m:].abs().sum()) == 0
+
+
+@pytest.mark.parametrize("m,k,n,deep", [(576, 12288, 4096, True), (576, 4096, 4096, False), (500, 12288, 4096, False),
+                                        (320, 6144, 2048, True), (576, 4096, 12288, False), (1, 12288, 4096, False)])
+def test_w4a16_add_rms_equals_unfused(gpu, m, k, n, deep):
+    """Int4.add_rms (ff_gemm_w4a16_pk_add_rms) == ops.add_rms of the packed GEMM's
+    output, bit for bit, residual and normalised rows: where the GEMM splits k
+    (o and down of the 8B step, 500 rows with a ragged last tile, DeepStack
+    rows) the add_rms launch adds the partials; elsewhere (144 x 384 tiles
+    unsplit, the one-row GEMV) the two ops run."""
+    from fastforward_amd import ops
+    from fastforward_amd.linear import Int4
+    x = torch.randn(m, k, generator=_g(80)).to(BF16).to(DEV)
+    w = (torch.randn(n, k, generator=_g(81)) * 0.02).to(BF16)
+    op = Int4(w.to(DEV), group=128, symmetric=True).pack()
+    a = (torch.randn(1, m, n, generator=_g(82)) * 3).to(BF16).to(DEV)
+    norm = ops.RMSNorm((1 + 0.2 * torch.randn(n, generator=_g(83))).to(BF16).to(DEV), 1e-6)
+    start, nv = (min(5, m - 1), min(40, m - min(5, m - 1))) if deep else (0, 0)
+    dp = torch.randn(nv, n, generator=_g(84)).to(BF16).to(DEV) if deep else None
+    r0, o0 = ops.add_rms(a, op(x).reshape(1, m, n), dp, norm, start, nv)
+    r1, o1 = op.add_rms(x, a, dp, norm, start, nv)
+    assert torch.equal(r0, r1) and torch.equal(o0, o1)
+    assert not torch.isnan(o1.float()).any()
