@@ -29,7 +29,8 @@ PEAK_FP8_TFLOPS = 5000.0      # MI355X dense fp8 MFMA
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 GEMM_KERNELS = ("FP8 GEMM launches of the step: gemm_fp8_swiglu_packed_kernel (gate/up), "
-                "gemm_fp8_split_packed_kernel + split_reduce_kernel (down; 96 x 128 tiles unsplit for o), "
+                "gemm_fp8_split_packed_kernel (down, timed with split_reduce_kernel adding its partials, which "
+                "the step's next add_rms launch does; 96 x 128 tiles unsplit for o), "
                 "gemm_fp8_qkv_packed_kernel (qkv with its epilogue), gemv_fp8 kernels (the tail's single row)")
 MICRO_SHAPES = [(320, 2048, 6144), (320, 6144, 2048), (576, 4096, 12288), (576, 12288, 4096),
                 (1024, 5120, 25600)]
@@ -83,8 +84,9 @@ def launch_gemm(cfg, role, lw, q, s, m, b):
     q/k norm + rotary + V^T epilogue (ff_gemm_fp8_qkv_pk: packed weights), the
     gate/up projection with its SwiGLU epilogue (ff_gemm_fp8_swiglu_pk), o and down
     through ``FP8Linear.gemm`` (ff_gemm_fp8_pk: the k-split packed kernel and its
-    reduction for down, the small packed tiles for o, the GEMV kernels for the
-    tail's single row)."""
+    reduction for down -- in the step the next add_rms launch adds the partials
+    -- the small packed tiles for o, the GEMV kernels for the tail's single
+    row)."""
     from fastforward_amd._lib import call, ptr, stream
     op = getattr(lw, role)
     n, k = op.weight.shape
