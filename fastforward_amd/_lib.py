@@ -76,6 +76,8 @@ SIGNATURES = {
     "ff_pack_pixels": [P, P, I64, I64, P],
     "ff_layer_norm": [P, I64, P, P, P, I64, I64, I64, F32, P],
     "ff_gemm_bf16": [P, I64, P, P, P, I64, P, I64, I64, I64, I64, I32, P],
+    "ff_pack_weight_bf16": [P, P, I64, I64, P],
+    "ff_gemm_bf16_pk": [P, I64, P, P, P, P, I64, P, I64, I64, I64, I64, I32, P],
     "ff_vision_rope": [P, P, I64, I64, P, P, P, P, I64, I64, I64, I64, I64, I64, P],
     "ff_vision_vt": [P, I64, I64, P, I64, I64, I64, I64, P],
     "ff_attention_full": [P, P, P, P, I64, I64, I64, I64, F32, P],

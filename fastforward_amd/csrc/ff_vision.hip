@@ -271,6 +271,184 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_bf16_kernel(
   }
 }
 
+// ---------------------------------------------------------------- packed-weight bf16 GEMM
+//
+// The product and epilogue of gemm_bf16_kernel with the weight read from a
+// setup-time copy in MFMA operand order (ff_pack_weight_bf16) straight into
+// registers, so that only the activations go through LDS. A workgroup of 4
+// waves owns BM rows x BN = 4 CW columns; wave w owns columns [w CW, (w + 1)
+// CW) and all BM rows, so each weight fragment feeds BM / 16 MFMAs and each
+// activation fragment read from LDS CW / 16. A step is 128 k (256 bytes of an
+// activation row, halves h = 0, 1); its four MFMAs per (i, j), sub = 2 h + s,
+// take k 128 kt + 64 h + 16 g + 8 s .. + 8 for lane (r, g): the k partition
+// and order of gemm_bf16_kernel's two MFMAs per 64-k stage, so the
+// accumulators and y are bit-identical to it.
+//
+// Activations: two LDS stages of BM rows x 256 bytes, written from registers
+// loaded a step ahead (16-byte chunk c of row r at half c / 8, 1 KB block r / 8,
+// row r % 8, slot (c % 8) ^ ((r % 16) / 2)). Weights: fragment (f, kt) is the 4
+// KB at (kt N / 16 + f) 4096; its sub-block `sub` (1 KB) holds for lane 16 g + r
+// the 16 bytes of row 16 f + r at k 128 kt + 64 (sub / 2) + 16 g + 8 (sub % 2).
+// Each lane holds two steps of fragments in registers; fragment (j, sub) of
+// step kt is reloaded with step kt + 2's right after its MFMAs issue.
+constexpr int kBfStep = 128;  // k per step of the packed kernel
+
+template <int BM, int CW, int ACT, bool RESID>
+__global__ __launch_bounds__(kThreads, 1) void gemm_bf16_pk_kernel(
+    const bf16_t* __restrict__ a, int64_t lda, const uint8_t* __restrict__ wp, const bf16_t* __restrict__ bias,
+    bf16_t* y, int64_t ldy, const bf16_t* resid, int64_t ldr, int M, int N, int K, int tiles_m, int tiles_n) {
+  constexpr int RA = BM / 16, TJ = CW / 16;
+  constexpr int A_CHUNKS = BM * 16;  // 16-byte chunks of one stage
+  constexpr int FULL = A_CHUNKS / kThreads, REM = A_CHUNKS % kThreads;
+  constexpr int NA = FULL + (REM ? 1 : 0);
+  constexpr int HALF = BM * 128, STAGE = 2 * HALF;
+  static_assert(A_CHUNKS >= kThreads, "at least one full activation round");
+  __shared__ __align__(1024) uint8_t smem[2 * STAGE];
+
+  const int nblk = tiles_m * tiles_n;
+  int logical = blockIdx.x;
+  if (nblk % kXcds == 0) logical = (blockIdx.x % kXcds) * (nblk / kXcds) + blockIdx.x / kXcds;
+  const int tm = logical % tiles_m, tn = logical / tiles_m;  // M fastest: an XCD's tiles share weight slabs
+  const int m0 = tm * BM, n0 = tn * 4 * CW;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int KT = K / kBfStep;
+
+  // Activations: chunk c = tid + 256 i is row c / 16, chunk c % 16 (a partial
+  // last round is moved back over the last 256 chunks, writing the overlap
+  // twice with the same bytes); rows past M are clamped (masked at the store).
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(a, (uint32_t)((int64_t)M * lda * 2));
+  uint32_t voffA[NA];
+  int dstA[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int c = i < FULL ? tid + kThreads * i : A_CHUNKS - kThreads + tid;
+    const int row = c >> 4, ch = c & 15;
+    voffA[i] = (uint32_t)min(m0 + row, M - 1) * (uint32_t)(2 * lda) + 16 * ch;
+    dstA[i] = (ch >> 3) * HALF + (row >> 3) * 1024 + 128 * (row & 7) + 16 * ((ch & 7) ^ ((row & 15) >> 1));
+  }
+  i32x4v ast[NA];
+  auto loadA = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) ast[i] = bload16(rA, voffA[i], (uint32_t)kt * 256u);
+  };
+  auto writeA = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) *reinterpret_cast<i32x4v*>(smem + buf * STAGE + dstA[i]) = ast[i];
+  };
+
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(wp, (uint32_t)((int64_t)N * K * 2));
+  const uint32_t kstride = (uint32_t)N * 256u;  // bytes per step: N / 16 fragments of 4 KB
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  uint32_t sB[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) sB[j] = (uint32_t)((n0 + wave_s * CW + 16 * j) / 16) * 4096u;
+  const uint32_t voffB = 16u * (uint32_t)lane;
+  i32x4v bq[2][TJ][4];
+  auto loadB1 = [&](int kt, int slot, int j, int sub) {
+    bq[slot][j][sub] = bload16(rB, voffB + 1024u * (uint32_t)sub, sB[j] + (uint32_t)kt * kstride);
+  };
+  auto loadB = [&](int kt, int slot) {
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) loadB1(kt, slot, j, sub);
+  };
+
+  f32x4 acc[RA][TJ];
+#pragma unroll
+  for (int i = 0; i < RA; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  loadA(0);
+  loadB(0, 0);
+  writeA(0);
+  loadA(min(1, KT - 1));
+  loadB(min(1, KT - 1), 1);
+
+  const int frag = 128 * (r16 & 7) + 1024 * (r16 >> 3);
+  const int cA[2] = {16 * ((2 * g) ^ (r16 >> 1)), 16 * ((2 * g + 1) ^ (r16 >> 1))};
+  for (int kb = 0; kb < KT; kb += 2) {
+    static_for<0, 2>([&](auto U_) {
+      constexpr int u = decltype(U_)::value;
+      const int kt = kb + u;
+      if (kt < KT) {  // uniform: an odd step count ends on u = 0
+        // stage u (written during the previous step) is visible; stage u ^ 1,
+        // read in the previous step, is free for step kt + 1
+        __syncthreads();
+        const int kta = min(kt + 2, KT - 1);
+        writeA(u ^ 1);
+        loadA(kta);
+        const uint8_t* st = smem + u * STAGE + frag;
+        i32x4v af[2][RA];
+#pragma unroll
+        for (int i = 0; i < RA; ++i) af[0][i] = *reinterpret_cast<const i32x4v*>(st + 2 * i * 1024 + cA[0]);
+        static_for<0, 4>([&](auto S_) {
+          constexpr int sub = decltype(S_)::value;
+          if constexpr (sub < 3) {
+#pragma unroll
+            for (int i = 0; i < RA; ++i)
+              af[(sub + 1) & 1][i] =
+                  *reinterpret_cast<const i32x4v*>(st + ((sub + 1) >> 1) * HALF + 2 * i * 1024 + cA[(sub + 1) & 1]);
+          }
+#pragma unroll
+          for (int j = 0; j < TJ; ++j) {
+            const u32x4 b = __builtin_bit_cast(u32x4, bq[u][j][sub]);
+#pragma unroll
+            for (int i = 0; i < RA; ++i) acc[i][j] = mfma_bf16(b, __builtin_bit_cast(u32x4, af[sub & 1][i]), acc[i][j]);
+            loadB1(kta, u, j, sub);
+          }
+        });
+      }
+    });
+  }
+
+  // lane (r16, g) of fragment (i, j): row m0 + 16 i + r16, columns
+  // n0 + wave CW + 16 j + 4 g .. + 3; the epilogue of gemm_bf16_kernel
+#pragma unroll
+  for (int i = 0; i < RA; ++i) {
+    const int m = m0 + 16 * i + r16;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const int n = n0 + wave * CW + 16 * j + 4 * g;
+      const u32x2 bb = *reinterpret_cast<const u32x2*>(bias + n);
+      float v[4] = {bf16_to_f32(bb.x & 0xFFFFu), bf16_to_f32(bb.x >> 16), bf16_to_f32(bb.y & 0xFFFFu),
+                    bf16_to_f32(bb.y >> 16)};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float t = round_bf16(acc[i][j][r] + v[r]);
+        if constexpr (ACT == kGeluTanh) t = round_bf16(gelu_tanh(t));
+        if constexpr (ACT == kGeluErf) t = round_bf16(gelu_erf(t));
+        v[r] = t;
+      }
+      if constexpr (RESID) {
+        const u32x2 rr = *reinterpret_cast<const u32x2*>(resid + (int64_t)m * ldr + n);
+        v[0] += bf16_to_f32(rr.x & 0xFFFFu);
+        v[1] += bf16_to_f32(rr.x >> 16);
+        v[2] += bf16_to_f32(rr.y & 0xFFFFu);
+        v[3] += bf16_to_f32(rr.y >> 16);
+      }
+      *reinterpret_cast<u32x2*>(y + (int64_t)m * ldy + n) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    }
+  }
+}
+
+// Weight copy in the packed kernel's operand order: one thread per 16-byte
+// piece ((kt N/16 + f) 4 + sub) 64 + lane of the output.
+__global__ __launch_bounds__(kThreads) void pack_bf16_kernel(const bf16_t* __restrict__ w, uint8_t* __restrict__ dst,
+                                                             int64_t n, int64_t k) {
+  const int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x;
+  if (i >= n * k / 8) return;
+  const int lane = (int)(i & 63), sub = (int)((i >> 6) & 3);
+  const int64_t rest = i >> 8, nf = n / 16;
+  const int64_t f = rest % nf, kt = rest / nf;
+  const int64_t row = 16 * f + (lane & 15);
+  const int64_t kk = kBfStep * kt + 64 * (sub >> 1) + 16 * (lane >> 4) + 8 * (sub & 1);
+  *reinterpret_cast<u32x4*>(dst + i * 16) = *reinterpret_cast<const u32x4*>(w + row * k + kk);
+}
+
 // ---------------------------------------------------------------- vision rotary
 //
 // y = bf16(x * cos + rotate_half(x) * sin) in fp32 for q and k of every
@@ -426,6 +604,40 @@ int launch_gemm(const void* a, int64_t lda, const void* w, const void* bias, voi
   return FF_OK;
 }
 
+// Tile of the packed kernel for an m x n GEMM: the first (BM, CW) of
+// (128, 48), (64, 64), (64, 48), (64, 32) whose BN = 4 CW divides n and whose
+// grid of 192 .. 256 workgroups runs in one round at one workgroup per CU; 0
+// if none (the LDS-staged kernel then runs). Grids past one round lose to it:
+// the tower's qkv (288 tiles of 128 x 192) took 43.7 us against 28.5, fc1
+// (544 of 64 x 256) 69.2 against 51.0; one-round grids win: proj / fc2 (192
+// of 64 x 192) 30.1 against 32.9 us, the merger's fc1 50.8 against 57.1 and
+// fc2 (256 of 64 x 128) 33.4 against 37.2. (128, 64) would spill: two steps
+// of its weight fragments, two sets of activation fragments and the staging
+// registers exceed the 256 VGPRs.
+int bf16pk_tile(int64_t m, int64_t n) {
+  constexpr int cand[4][2] = {{128, 48}, {64, 64}, {64, 48}, {64, 32}};
+  for (int c = 0; c < 4; ++c) {
+    if (n % (4 * cand[c][1])) continue;
+    const int64_t tiles = (m + cand[c][0] - 1) / cand[c][0] * (n / (4 * cand[c][1]));
+    if (tiles >= 192 && tiles <= 256) return c + 1;
+  }
+  return 0;
+}
+
+template <int BM, int CW>
+void launch_gemm_pk(const void* a, int64_t lda, const void* wp, const void* bias, void* y, int64_t ldy,
+                    const void* resid, int64_t ldr, int64_t m, int64_t n, int64_t k, int act, hipStream_t st) {
+  const int tiles_m = (int)((m + BM - 1) / BM), tiles_n = (int)(n / (4 * CW));
+  const dim3 grid((unsigned)(tiles_m * tiles_n)), block(kThreads);
+#define FF_G(ACT, RES)                                                                                         \
+  if (act == ACT && (resid != nullptr) == RES)                                                                 \
+    hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, CW, ACT, RES>), grid, block, 0, st, (const bf16_t*)a, lda,     \
+                       (const uint8_t*)wp, (const bf16_t*)bias, (bf16_t*)y, ldy, (const bf16_t*)resid, ldr,    \
+                       (int)m, (int)n, (int)k, tiles_m, tiles_n);
+  FF_G(kActNone, false) FF_G(kActNone, true) FF_G(kGeluTanh, false) FF_G(kGeluErf, false)
+#undef FF_G
+}
+
 }  // namespace
 
 extern "C" int ff_pack_pixels(const void* rgb, void* out, int64_t height, int64_t width, ff_stream_t stream) {
@@ -486,6 +698,45 @@ extern "C" int ff_gemm_bf16(const void* a, int64_t lda, const void* w, const voi
   else
     launch_gemm<64, 128, 3, 2>(a, lda, w, bias, y, ldy, resid, ldr, m, n, k, act, st);
   FF_LAUNCH_CHECK("ff_gemm_bf16");
+  return FF_OK;
+}
+
+extern "C" int ff_pack_weight_bf16(const void* w, void* packed, int64_t n, int64_t k, ff_stream_t stream) {
+  FF_REQUIRE(w && packed, "ff_pack_weight_bf16: null pointer");
+  FF_REQUIRE(n > 0 && k > 0 && n % 16 == 0 && k % kBfStep == 0, "ff_pack_weight_bf16: n %% 16, k %% 128 (n=%lld k=%lld)",
+             (long long)n, (long long)k);
+  FF_REQUIRE(ff_aligned(w, 16) && ff_aligned(packed, 16), "ff_pack_weight_bf16: alignment");
+  const int64_t pieces = n * k / 8;
+  hipLaunchKernelGGL(pack_bf16_kernel, dim3((unsigned)((pieces + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const bf16_t*)w, (uint8_t*)packed, n, k);
+  FF_LAUNCH_CHECK("ff_pack_weight_bf16");
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_bf16_pk(const void* a, int64_t lda, const void* w, const void* w_packed, const void* bias,
+                               void* y, int64_t ldy, const void* resid, int64_t ldr, int64_t m, int64_t n, int64_t k,
+                               int act, ff_stream_t stream) {
+  const int tile = w_packed && k % kBfStep == 0 && ff_aligned(w_packed, 16) && ff_aligned(a, 16) &&
+                           m * lda * 2 < (int64_t(1) << 31) && n * k * 2 < (int64_t(1) << 31)
+                       ? bf16pk_tile(m, n)
+                       : 0;
+  if (tile == 0) return ff_gemm_bf16(a, lda, w, bias, y, ldy, resid, ldr, m, n, k, act, stream);
+  FF_REQUIRE(a && w && bias && y, "ff_gemm_bf16_pk: null pointer");
+  FF_REQUIRE(m > 0 && lda >= k && ldy >= n && lda % 8 == 0 && ldy % 4 == 0 && (!resid || (ldr >= n && ldr % 4 == 0)),
+             "ff_gemm_bf16_pk: bad sizes m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
+  FF_REQUIRE(act == kActNone || act == kGeluTanh || act == kGeluErf, "ff_gemm_bf16_pk: act %d unknown", act);
+  FF_REQUIRE(!resid || act == kActNone, "ff_gemm_bf16_pk: a residual add takes no activation");
+  FF_REQUIRE(ff_aligned(bias, 8) && ff_aligned(y, 8) && (!resid || ff_aligned(resid, 8)), "ff_gemm_bf16_pk: alignment");
+  hipStream_t st = (hipStream_t)stream;
+  if (tile == 1)
+    launch_gemm_pk<128, 48>(a, lda, w_packed, bias, y, ldy, resid, ldr, m, n, k, act, st);
+  else if (tile == 2)
+    launch_gemm_pk<64, 64>(a, lda, w_packed, bias, y, ldy, resid, ldr, m, n, k, act, st);
+  else if (tile == 3)
+    launch_gemm_pk<64, 48>(a, lda, w_packed, bias, y, ldy, resid, ldr, m, n, k, act, st);
+  else
+    launch_gemm_pk<64, 32>(a, lda, w_packed, bias, y, ldy, resid, ldr, m, n, k, act, st);
+  FF_LAUNCH_CHECK("ff_gemm_bf16_pk");
   return FF_OK;
 }
 

@@ -66,9 +66,32 @@ VISION_PRESETS = {
 
 @dataclass
 class Lin:
-    """A bf16 linear: weight (n, k) and bias (n,) on the device."""
+    """A bf16 linear: weight (n, k) and bias (n,) on the device, and once
+    ``pack`` has run the weight's copy in the packed GEMM's operand order
+    (ff_pack_weight_bf16; ``linear`` then reads it, the same bits)."""
     w: torch.Tensor
     b: torch.Tensor
+    p: torch.Tensor = None
+
+    def pack(self):
+        n, k = self.w.shape
+        if self.p is None and n % 16 == 0 and k % 128 == 0:
+            self.p = torch.empty_like(self.w)
+            call("ff_pack_weight_bf16", ptr(self.w), ptr(self.p), n, k, stream())
+        return self
+
+
+def pack_linears(obj):
+    """``Lin.pack`` on every linear reachable from a weights object (dataclass
+    fields, lists and tuples)."""
+    if isinstance(obj, Lin):
+        obj.pack()
+    elif isinstance(obj, (list, tuple)):
+        for o in obj:
+            pack_linears(o)
+    elif hasattr(obj, "__dataclass_fields__"):
+        for f in obj.__dataclass_fields__:
+            pack_linears(getattr(obj, f))
 
 
 @dataclass
@@ -242,8 +265,8 @@ def linear(x, lin, act=ACT_NONE, resid=None, out=None):
     m, k = x.shape
     n = lin.w.shape[0]
     y = torch.empty((m, n), device=x.device, dtype=BF16) if out is None else out
-    call("ff_gemm_bf16", ptr(x), x.stride(0), ptr(lin.w), ptr(lin.b), ptr(y), y.stride(0), ptr(resid),
-         0 if resid is None else resid.stride(0), m, n, k, act, stream())
+    call("ff_gemm_bf16_pk", ptr(x), x.stride(0), ptr(lin.w), ptr(lin.p), ptr(lin.b), ptr(y), y.stride(0),
+         ptr(resid), 0 if resid is None else resid.stride(0), m, n, k, act, stream())
     return y
 
 
@@ -300,6 +323,7 @@ class VisionRuntime:
         if gh % cfg.merge or gw % cfg.merge:
             raise ValueError("the patch grid must be a whole number of merge blocks")
         self.cfg, self.w = cfg, weights
+        pack_linears(weights)  # packed weight copies for the packed GEMM (once per weights object)
         self.gh, self.gw = gh, gw
         n = gh * gw
         self.n, self.nm = n, n // cfg.merge ** 2

@@ -455,6 +455,24 @@ int ff_layer_norm(const void* x, int64_t x_rs, const void* w, const void* b, voi
 int ff_gemm_bf16(const void* a, int64_t lda, const void* w, const void* bias, void* y, int64_t ldy,
                  const void* resid, int64_t ldr, int64_t m, int64_t n, int64_t k, int act, ff_stream_t stream);
 
+/* Setup-time repack of bf16 weights w (n, k) row-major into the operand order
+ * of ff_gemm_bf16_pk (no reference counterpart: a storage layout of this
+ * library): fragment (f, kt), rows [16 f, 16 f + 16) x k [128 kt, 128 kt +
+ * 128), is the 4 KB at (kt * n/16 + f) * 4096; its sub-block s (1 KB at s *
+ * 1024) holds for lane l = 16 g + r the 16 bytes of row 16 f + r at k 128 kt +
+ * 64 (s / 2) + 16 g + 8 (s % 2). packed holds 2 n k bytes. n % 16 == 0,
+ * k % 128 == 0. */
+int ff_pack_weight_bf16(const void* w, void* packed, int64_t n, int64_t k, ff_stream_t stream);
+/* ff_gemm_bf16 with the weight read from its packed copy (ff_pack_weight_bf16
+ * of w) straight into the matrix-core operands: the same products in the same
+ * order, so the same bits. Taken when w_packed is given, k % 128 == 0 and a
+ * tile of 128 x 192, 64 x 256, 64 x 192 or 64 x 128 divides n and gives a grid
+ * of 192..256 workgroups; otherwise this is ff_gemm_bf16 on w (w_packed may be
+ * NULL). Same reference replacement as ff_gemm_bf16. */
+int ff_gemm_bf16_pk(const void* a, int64_t lda, const void* w, const void* w_packed, const void* bias, void* y,
+                    int64_t ldy, const void* resid, int64_t ldr, int64_t m, int64_t n, int64_t k, int act,
+                    ff_stream_t stream);
+
 /* vision_rope (_legacy/search_kernels.py:111-134): yq/yk = bf16(x * cos +
  * rotate_half(x) * sin) in fp32, cos/sin (n, hd) fp32. q, k with token stride
  * x_ts and head stride x_hs (views of the packed qkv output); outputs with

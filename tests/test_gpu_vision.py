@@ -125,6 +125,61 @@ def test_gemm_bf16_residual_in_place(gpu):
     _assert_within(hd.cpu(), want, bound, "gemm_bf16 residual")
 
 
+# (m, k, n, act, resid): proj / fc2 of the tower with the residual add in place
+# (64 x 192 tiles), the patch embedding, the mergers' fc1 + GELU (64 x 192) and
+# fc2 (64 x 128), the 128 x 192 and 64 x 256 tiles (GELU-tanh) at row counts
+# whose grids they fill, ragged row counts and an odd number of 128-k steps
+# (k 1152); the tower's qkv and fc1 (grids past one round), n = 1000 and 1000
+# rows fall back to the LDS-staged kernel.
+PK_VISION = [(2048, 1152, 1152, 0, True), (2048, 4352, 1152, 0, True), (2048, 1536, 1152, 0, False),
+             (512, 4608, 4608, 2, False), (512, 4608, 4096, 0, False), (1536, 1152, 3456, 0, False),
+             (1024, 1152, 4096, 1, False), (2000, 4352, 1152, 0, True), (2048, 1152, 3456, 0, False),
+             (2048, 1152, 4352, 1, False), (600, 1152, 1000, 0, False)]
+
+
+@pytest.mark.parametrize("m,k,n,act,resid", PK_VISION)
+def test_gemm_bf16_packed_equals_rowmajor(gpu, m, k, n, act, resid):
+    """linear() on a packed Lin (ff_gemm_bf16_pk: weights from the operand-order
+    copy straight into the MFMA operands) == the LDS-staged kernel on the
+    row-major weight, bit for bit, with every epilogue (bias, GELU-tanh,
+    GELU-erf, residual add in place)."""
+    from fastforward_amd.vision import Lin, linear
+    x = torch.randn(m, k, generator=_g(m + n)).to(BF16).to(DEV)
+    w = (torch.randn(n, k, generator=_g(k)) * 0.03).to(BF16).to(DEV)
+    b = (torch.randn(n, generator=_g(n + 2)) * 0.1).to(BF16).to(DEV)
+    h = torch.randn(m, n, generator=_g(n + 3)).to(BF16).to(DEV) if resid else None
+    outs = []
+    for lin in (Lin(w, b), Lin(w, b).pack()):
+        if resid:
+            y = h.clone()
+            linear(x, lin, act=act, resid=y, out=y)
+        else:
+            y = linear(x, lin, act=act)
+        outs.append(y)
+    assert (outs[1] is not None) and not torch.isnan(outs[1].float()).any()
+    assert torch.equal(outs[0], outs[1])
+
+
+def test_pack_weight_bf16_layout(gpu):
+    """ff_pack_weight_bf16: fragment (f, kt) at (kt n/16 + f) 4 KB, sub-block s,
+    lane 16 g + r: row 16 f + r, k 128 kt + 64 (s / 2) + 16 g + 8 (s % 2) .. + 8."""
+    from fastforward_amd._lib import call, ptr, stream
+    n, k = 48, 384
+    w = torch.randint(-30000, 30000, (n, k), generator=_g(90), dtype=torch.int16)
+    p = torch.empty(n * k, device=DEV, dtype=torch.int16)
+    wd = w.to(DEV)
+    call("ff_pack_weight_bf16", ptr(wd), ptr(p), n, k, stream())
+    got = p.cpu().numpy().reshape(k // 128, n // 16, 4, 64, 8)
+    wn = w.numpy()
+    for kt in range(k // 128):
+        for f in range(n // 16):
+            for s in range(4):
+                for lane in range(64):
+                    r, g = lane % 16, lane // 16
+                    k0 = 128 * kt + 64 * (s // 2) + 16 * g + 8 * (s % 2)
+                    assert np.array_equal(got[kt, f, s, lane], wn[16 * f + r, k0:k0 + 8]), (kt, f, s, lane)
+
+
 def test_vision_rope_bit_exact_and_padded_layout(gpu):
     from fastforward_amd._lib import call, ptr, stream
     from fastforward_amd.vision import VISION_PRESETS, rope_tables, vision_rope
