@@ -322,9 +322,13 @@ class Runtime:
             lw = L[j]
             h = self.h[cur]
             self._attention_fused(lw, s)
-            self._gemm(self.aq, self.as_, lw.o, self.o, T, s)
-            call("ff_add_rms_quant", ptr(h), ptr(self.o), None, ptr(lw.post_norm.weight), ptr(self.res), None,
-                 ptr(self.pq), ptr(self.ps), T, H, float(lw.post_norm.variance_epsilon), 0, 0, s)
+            # o projection + the post-attention add_rms: where o splits k (the 32B shape) the add_rms
+            # launch adds its partials; elsewhere the two launches as they are
+            ow = lw.o
+            call("ff_gemm_fp8_pk_add_rms_quant", ptr(self.aq), ptr(self.as_), 1, ptr(ow.weight), ptr(ow.packed),
+                 ptr(ow.scale), 1, ptr(self.o), T, H, HQ * D, ptr(self.gws), self.gws.numel(), ptr(h), None,
+                 ptr(lw.post_norm.weight), ptr(self.res), ptr(self.pq), ptr(self.ps),
+                 float(lw.post_norm.variance_epsilon), 0, 0, s)
             self._gateup_fused(lw, self.pq, self.ps, T, s)
             nxt = self.h[cur ^ 1]
             deep = self.deep[j] if j < len(self.deep) else None
@@ -410,9 +414,11 @@ class Runtime:
             self._qkv_static(lw, T, s)
             call("ff_attention_vt_q", ptr(self.yq), ptr(self.yk), ptr(self.vt), ptr(self.aq),
                  float(lw.o.inverse_scale), T, T, Tp, HQ, HK, D, float(cfg.scaling), s)
-            self._gemm_static(self.aq, lw.o, self.o, T, s)
-            call("ff_add_rms_quant_static", ptr(h), ptr(self.o), None, ptr(lw.post_norm.weight), ptr(self.res), None,
-                 ptr(self.pq), float(lw.gateup.inverse_scale), T, H, float(lw.post_norm.variance_epsilon), 0, 0, s)
+            ow = lw.o
+            call("ff_gemm_fp8_pk_add_rms_quant_static", ptr(self.aq), ptr(ow.input_scale), 0, ptr(ow.weight),
+                 ptr(ow.packed), ptr(ow.weight_scale), 0, ptr(self.o), T, H, HQ * D, ptr(self.gws),
+                 self.gws.numel(), ptr(h), None, ptr(lw.post_norm.weight), ptr(self.res), ptr(self.pq),
+                 float(lw.gateup.inverse_scale), float(lw.post_norm.variance_epsilon), 0, 0, s)
             self._gateup_static(lw, T, s)
             nxt = self.h[cur ^ 1]
             deep = self.deep[j] if j < len(self.deep) else None
