@@ -78,7 +78,7 @@ def _by_grid(path, counters=None):
 def step_table(db, fetch_csv, write_csv, mfma_csv, fetch_factor, write_factor, xcds=8, simds=1024,
                skip=("at::native", "__amd_rocclr", "weight_quant_kernel", "row_amax_kernel", "channel_scale_kernel",
                      "int4_quant_kernel", "pack_fp8_kernel", "pack_int4_kernel", "pack_scales_int4_kernel",
-                     "tensor_scale_kernel")):
+                     "pack_bf16_kernel", "tensor_scale_kernel")):
     con = sqlite3.connect(db)
     dur = collections.defaultdict(list)
     for name, gx, gy, gz, wx, start, end in con.execute(
