@@ -493,7 +493,8 @@ int ff_vision_vt(const void* v, int64_t v_ts, int64_t v_hs, void* vt, int64_t n,
 /* ff_vision_rope + ff_vision_vt on the packed qkv output of a vision block in
  * one launch (no reference counterpart as one op): qkv (n, 3, heads, hd)
  * contiguous -> yq, yk (heads, n, 128) rotated and zero-padded, vt (heads,
- * 128, t_pad) zero-padded. hd % 8 == 0, hd <= 128, t_pad % 64 == 0. */
+ * 128, t_pad) zero-padded. hd % 8 == 0, hd <= 128, t_pad % 64 == 0; every
+ * pointer 16-byte aligned. */
 int ff_vision_qkv(const void* qkv, const float* cos, const float* sin, void* yq, void* yk, void* vt,
                   int64_t n, int64_t t_pad, int64_t heads, int64_t hd, ff_stream_t stream);
 
