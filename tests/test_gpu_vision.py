@@ -16,7 +16,8 @@ Tolerances (stated per op):
   to bf16 inside the online softmax; the oracle is exact fp64).
 * whole tower (teacher-forced per block and end to end over 3 blocks):
   relative L2 <= 1% per block output, <= 2% for the merged and DeepStack
-  features.
+  features; the full 27-block 8B tower teacher-forced to the same bars per
+  block and merger, and end to end within 3%.
 """
 import numpy as np
 import pytest
@@ -368,12 +369,19 @@ def test_vision_graph_replays_equal_eager(gpu):
             assert torch.equal(m, em) and all(torch.equal(a, b) for a, b in zip(d, ed))
 
 
-def test_vision_8b_shape_two_blocks(gpu):
-    """The 8B tower's real widths (1152 hidden, 16 heads of 72, MLP 4304 padded to
-    4352, 4608-wide mergers) on a 16 x 32 patch grid, two blocks, against the oracle."""
-    from fastforward_amd.vision import VISION_PRESETS, VisionConfig, VisionRuntime, make_vision
-    base = VISION_PRESETS["qwen3vl-8b"]
-    cfg = VisionConfig("8b-2", 2, base.hidden, base.heads, base.inter, base.out_hidden, (0,))
+@pytest.mark.timeout(600)
+def test_vision_8b_full_depth(gpu):
+    """The whole 8B tower (27 blocks, 1152 hidden, 16 heads of 72, MLP 4304 padded
+    to 4352, 4608-wide mergers, DeepStack after blocks 8, 16 and 24) on a 16 x 32
+    patch grid. Teacher-forced: every block, given the GPU's own input to it,
+    within 1% relative L2 of the oracle's block; every DeepStack merger and the
+    final merger, given the GPU's block output, within 2%. End to end (the
+    oracle's own tower from the same pixels): printed per block, and the merged
+    and DeepStack features within 3%: the 27 residual updates each differ by
+    <= 0.3% (the teacher-forced figures of this shape), as independent roundings
+    that add in quadrature, sqrt(27) x 0.3% ~ 1.6%, and the bar is twice that."""
+    from fastforward_amd.vision import VISION_PRESETS, VisionRuntime, make_vision
+    cfg = VISION_PRESETS["qwen3vl-8b"]
     w = make_vision(cfg, seed=2)
     gh, gw = 16, 32
     rt = VisionRuntime(cfg, w, gh, gw)
@@ -383,9 +391,32 @@ def test_vision_8b_shape_two_blocks(gpu):
     trace = []
     merged, deep = rt.step(trace)
     torch.cuda.synchronize()
+    trace = [t.cpu() for t in trace]
+    merged, deep = merged.cpu(), [d.cpu() for d in deep]
+    del rt
     shape, ow = _to_oracle(cfg, w)
+    del w
+    torch.cuda.empty_cache()
+    cos, sin = OV.rope_cos_sin(shape, gh, gw)
+    pixels = OV.pack_pixels(rgb)
+    h0 = OV.linear(pixels, ow.patch_w, ow.patch_b)
+    h0 = OV.bf16(h0.to(F32) + OV.pos_embeds(shape, ow.pos_embed, gh, gw).to(F32)).to(BF16)
+    hin = [h0] + trace
+    for j in range(cfg.depth):
+        got = _rel_l2(trace[j], OV.block(shape, ow.blocks[j], hin[j], cos, sin))
+        print(f"8b vision block {j}: teacher-forced rel L2 {got:.2e}", flush=True)
+        assert got <= 1e-2, f"teacher-forced block {j}: {got:.3e}"
+    for k, j in enumerate(cfg.deepstack):
+        got = _rel_l2(deep[k], OV.merge(shape, ow.deep[k], trace[j]))
+        print(f"8b vision deepstack merger {k} (block {j}): teacher-forced rel L2 {got:.2e}", flush=True)
+        assert got <= 2e-2
+    got = _rel_l2(merged, OV.merge(shape, ow.merger, trace[-1]))
+    print(f"8b vision merger: teacher-forced rel L2 {got:.2e}", flush=True)
+    assert got <= 2e-2
     otrace = []
-    omerged, odeep = OV.tower(shape, ow, OV.pack_pixels(rgb), gh, gw, otrace)
-    for j, (a, b) in enumerate(zip(trace, otrace)):
-        assert _rel_l2(a, b) <= 1e-2, f"block {j}: {_rel_l2(a, b):.3e}"
-    assert _rel_l2(merged, omerged) <= 2e-2 and _rel_l2(deep[0], odeep[0]) <= 2e-2
+    omerged, odeep = OV.tower(shape, ow, pixels, gh, gw, otrace)
+    print("8b vision end to end per block: " + " ".join(f"{_rel_l2(a, b):.1e}" for a, b in zip(trace, otrace)),
+          flush=True)
+    ends = [_rel_l2(merged, omerged)] + [_rel_l2(a, b) for a, b in zip(deep, odeep)]
+    print(f"8b vision end to end merged / deepstack: {ends}", flush=True)
+    assert max(ends) <= 3e-2
