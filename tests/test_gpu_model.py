@@ -333,8 +333,8 @@ def test_full_model_vs_oracle(gpu, preset, tokens, grid, choices, mode):
 def test_32b_shape_on_one_gpu(gpu):
     """The 32B shape (64 layers, hidden 5120, 64/8 heads with HQ*D = 8192 != H,
     MLP 25600, 1024 tokens on a 30x32 image grid, 2 choices, FP8): graph replay
-    equals the eager step; first, second and second-to-last layers and the tail
-    teacher-forced against the oracle (only those layers are copied to the host)."""
+    equals the eager step; every layer and the tail teacher-forced against the
+    oracle (the FP8 codes of all 64 layers, 31 GB, copied to the host)."""
     from fastforward_amd.runtime import PRESETS, Runtime
     from fastforward_amd.synthetic import make_model, make_request
     cfg = PRESETS["qwen3vl-32b"]
@@ -350,6 +350,5 @@ def test_32b_shape_on_one_gpu(gpu):
     assert torch.equal(z_graph, z_eager)
     del rt
     torch.cuda.empty_cache()
-    z, _, _ = _check_teacher_forced(cfg, w, "fp8", ids, pos, pick, (0, 1, cfg.layers - 2), "qwen3vl-32b fp8",
-                                    copy_all=False)
+    z, _, _ = _check_teacher_forced(cfg, w, "fp8", ids, pos, pick, range(cfg.layers - 1), "qwen3vl-32b fp8")
     assert torch.equal(z, z_eager.cpu())
