@@ -174,28 +174,43 @@ def test_mixed_bank_model_teacher_forced(gpu, mode):
                           tail_tol=TINY_TAIL_TOL["fp8"])
 
 
-def test_fused_path_equals_reference_op_sequence(gpu):
+def _wide(layers=2):
+    """The 8B layer widths (hidden 4096, 32/8 heads of 128, MLP 12288) with a
+    small vocabulary: the packed GEMMs, their k splits and the fused add_rms
+    launches at their real shapes."""
+    from fastforward_amd.runtime import LMConfig
+    return LMConfig("wide", layers, 4096, 32, 8, 128, 12288, 1000)
+
+
+# (config, tokens, image grid): 333 tokens leave a ragged last tile of 45
+# rows in the 144-row GEMM tiles and of 13 rows in the 64-row qkv tiles.
+FUSED_CASES = [(_tiny, 4, 130, (5, 5)), (_wide, 2, 333, (8, 8))]
+
+
+@pytest.mark.parametrize("make_cfg,layers,tokens,grid", FUSED_CASES, ids=["tiny-130", "wide-333"])
+def test_fused_path_equals_reference_op_sequence(gpu, make_cfg, layers, tokens, grid):
     from fastforward_amd.synthetic import make_model, make_request
-    cfg = _tiny(4)
+    cfg = make_cfg(layers)
     w = make_model(cfg, mode="fp8", seed=2, norm_jitter=0.2)
-    ids, pos, pick = make_request(cfg, 130, 5, 5, seed=2)
-    _, z1 = _run(cfg, w, 130, ids, pos, pick, path="fused")
-    _, z2 = _run(cfg, w, 130, ids, pos, pick, path="generic")
+    ids, pos, pick = make_request(cfg, tokens, *grid, seed=2)
+    rt1, z1 = _run(cfg, w, tokens, ids, pos, pick, path="fused")
+    _, z2 = _run(cfg, w, tokens, ids, pos, pick, path="generic")
     assert torch.equal(z1, z2), (z1, z2)
 
 
-def test_fused_static_path_equals_reference_op_sequence(gpu):
+@pytest.mark.parametrize("make_cfg,layers,tokens,grid", FUSED_CASES, ids=["tiny-130", "wide-333"])
+def test_fused_static_path_equals_reference_op_sequence(gpu, make_cfg, layers, tokens, grid):
     """Static-scale linears (RuntimeScaleLinear, _family/depth_fp8.py:22-26):
     the fused step, whose producers cast to e4m3 with the consumer's
     inverse_scale, equals the reference's op sequence (quantize_runtime +
     _scaled_mm per linear) bit for bit."""
     from fastforward_amd.synthetic import make_model, make_request
-    cfg = _tiny(4)
+    cfg = make_cfg(layers)
     w = make_model(cfg, mode="fp8_static", seed=2, norm_jitter=0.2)
-    ids, pos, pick = make_request(cfg, 130, 5, 5, seed=2)
-    rt1, z1 = _run(cfg, w, 130, ids, pos, pick)
+    ids, pos, pick = make_request(cfg, tokens, *grid, seed=2)
+    rt1, z1 = _run(cfg, w, tokens, ids, pos, pick)
     assert rt1.path == "fused_static"
-    _, z2 = _run(cfg, w, 130, ids, pos, pick, path="generic")
+    _, z2 = _run(cfg, w, tokens, ids, pos, pick, path="generic")
     assert torch.equal(z1, z2), (z1, z2)
 
 
