@@ -777,7 +777,14 @@ static int attention_vt(const void* q, const void* k, const void* vt, const int6
   if (!positions && s == t && hpw) {
     // ff_set_tuning(FF_TUNE_ATTN_QT, 1 | 2 | 4) overrides the query tiles per wave.
     const int qt_env = ff_tuning(FF_TUNE_ATTN_QT);
-    const int qt = (qt_env == 1 || qt_env == 2 || qt_env == 4) ? qt_env : (s <= 1024 ? 1 : (s <= 2048 ? 2 : 4));
+    // One query tile per wave while the grid at one tile stays under 1024
+    // workgroups: 32/8 heads at 1040 / 1536 tokens take 22.6 / 37.0 us with one
+    // tile and 28.6 / 41.9 us with two; at 2048 tokens (1024 workgroups) two
+    // tiles are ahead, 57.4 against 59.6 us (88.5 against 104.2 with 64/8 heads).
+    const int64_t wg1 = (s + 64 / hpw - 1) / (64 / hpw) * (hq / hpw);  // 16 (4 / hpw) queries x hpw heads each
+    const int qt = (qt_env == 1 || qt_env == 2 || qt_env == 4)
+                       ? qt_env
+                       : (s <= 1024 || (s <= 2048 && wg1 < 1024) ? 1 : (s <= 2048 ? 2 : 4));
     // ff_set_tuning(FF_TUNE_ATTN_NS, 2 | 3) overrides the number of K/V LDS stages.
     const int ns_env = ff_tuning(FF_TUNE_ATTN_NS);
     // Two stages run at two workgroups per CU, which fits the registers of

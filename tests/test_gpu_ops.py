@@ -578,7 +578,7 @@ def test_attention_causal(gpu, t, hq, hk):
 
 
 @pytest.mark.parametrize("t,hq,hk", [(576, 32, 8), (1000, 64, 8), (129, 16, 4), (17, 8, 2), (320, 16, 8),
-                                     (130, 8, 8), (2048, 32, 8)])
+                                     (130, 8, 8), (1536, 32, 8), (1100, 16, 8), (2048, 32, 8)])
 def test_attention_prefill_matches_per_head_kernel(gpu, t, hq, hk):
     """The grouped prefill kernel (1, 2 or a multiple of 4 query heads per kv
     head, K/V staged in LDS; one or two query tiles per wave) and the per-head
