@@ -487,6 +487,30 @@ constexpr int kPkBM = 144, kPkCW = 96, kPkP = 2, kPkD = 2, kPkG = 2;
 constexpr int kPkCH = 2 * kPkCW;
 constexpr int kPkKAlign = 128 * lcm3(kPkP, kPkD, 2 * kPkG);  // k multiple of the unrolled k steps
 
+// Row-tile height of the packed gate/up GEMM for m tokens and tiles_n column
+// tiles: the candidate whose grid takes the fewest row steps per CU, counted as
+// rounds of 256 workgroups (one per CU) x (BM + 16) rows (the 16 stand for the
+// per-tile prologue and the lower operand reuse of shorter tiles), ties to the
+// taller tile; 0 when no candidate gives 192 or more workgroups (the row-major
+// kernel runs then). 8B gate/up (64 column tiles): 576 tokens 144 x 384 tiles
+// in one round; 640 tokens 80 (two rounds of 80 against two of 144); 176 and
+// 320 tokens 80; 2048 tokens 128.
+int swiglu_bm(int64_t m, int64_t tiles_n) {
+  constexpr int cand[5] = {144, 128, 112, 96, 80};
+  int best = 0;
+  int64_t best_cost = 0;
+  for (const int bm : cand) {
+    const int64_t tiles = (m + bm - 1) / bm * tiles_n;
+    if (tiles < 192) continue;
+    const int64_t cost = (tiles + 255) / 256 * (bm + 16);
+    if (best == 0 || cost < best_cost) {
+      best = bm;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
 // Plain GEMM: 144 x 256 tiles, k split so that about 256 workgroups run (the
 // 8B o and down projections: 4 x 16 tiles, 4 splits).
 constexpr int kSpBM = 144, kSpCW = 64, kSpP = 2, kSpD = 2, kSpG = 2;
@@ -502,7 +526,22 @@ int split_plan(int64_t m, int64_t n, int64_t k) {
   if (m <= 4 || n % kSpBN || k % 128 || m * k >= (int64_t(1) << 31) || n * k >= (int64_t(1) << 31)) return 0;
   const int64_t tiles = (m + kSpBM - 1) / kSpBM * (n / kSpBN), kt = k / 128;
   if (tiles >= 192) return kt % kSpU == 0 ? 1 : 0;
-  return kt >= 64 && kt % (4 * kSpU) == 0 ? 4 : 0;
+  if (kt < 64) return 0;
+  // The split count with the fewest k steps per CU: rounds of 256 workgroups
+  // (one per CU) x kt / S steps each, ties to fewer splits (less partial
+  // traffic). 8B down (k = 12288): 576 tokens 4 splits in one round, 640
+  // tokens 3 in one round (4 would take two), 1152 tokens 2.
+  int best = 0;
+  int64_t best_steps = 0;
+  for (int sp = 2; sp <= 4; ++sp) {
+    if (kt % (sp * kSpU)) continue;
+    const int64_t steps = (tiles * sp + 255) / 256 * (kt / sp);
+    if (best == 0 || steps < best_steps) {
+      best = sp;
+      best_steps = steps;
+    }
+  }
+  return best;
 }
 
 // Unsplit plain GEMMs whose 144 x 256 tiles are too few and whose k is too
@@ -688,16 +727,21 @@ extern "C" int ff_gemm_fp8_swiglu_pk(const void* qa, const float* sa, const void
                                      const float* sw, void* h, int64_t ldh, float* pmax, int64_t m, int64_t i,
                                      int64_t k, ff_stream_t stream) {
   FF_REQUIRE(qa && sa && qw && sw && h && pmax, "ff_gemm_fp8_swiglu_pk: null pointer");
-  const int64_t tiles_m = (m + kPkBM - 1) / kPkBM, tiles_n = i / kPkCH;
-  const bool packed_fits = qw_packed && m > 4 && i % kPkCH == 0 && k % kPkKAlign == 0 && ldh % 8 == 0 &&
-                           ldh >= i && m * k < (int64_t(1) << 31) && 2 * i * k < (int64_t(1) << 31) &&
-                           tiles_m * tiles_n >= 192 && ff_aligned(qa, 16) && ff_aligned(qw_packed, 16) &&
-                           ff_aligned(h, 16);
+  const int64_t tiles_n = i / kPkCH;
+  const int bm = i % kPkCH == 0 ? swiglu_bm(m, tiles_n) : 0;
+  const bool packed_fits = qw_packed && bm && m > 4 && k % kPkKAlign == 0 && ldh % 8 == 0 && ldh >= i &&
+                           m * k < (int64_t(1) << 31) && 2 * i * k < (int64_t(1) << 31) && ff_aligned(qa, 16) &&
+                           ff_aligned(qw_packed, 16) && ff_aligned(h, 16);
   if (!packed_fits) return ff_gemm_fp8_swiglu(qa, sa, qw, sw, h, ldh, pmax, m, i, k, stream);
-  hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<kPkBM, kPkCW, kPkP, kPkD, kPkG>),
-                     dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads), 0, (hipStream_t)stream,
-                     (const uint8_t*)qa, sa, (const uint8_t*)qw_packed, sw, (bf16_t*)h, ldh, pmax, (int)m, (int)i,
-                     (int)k, (int)tiles_m, (int)tiles_n, nullptr, 0.f);
+  const int64_t tiles_m = (m + bm - 1) / bm;
+#define FF_SWIGLU(BM)                                                                                               \
+  if (bm == BM)                                                                                                     \
+    hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<BM, kPkCW, kPkP, kPkD, kPkG>),                                \
+                       dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads), 0, (hipStream_t)stream,                 \
+                       (const uint8_t*)qa, sa, (const uint8_t*)qw_packed, sw, (bf16_t*)h, ldh, pmax, (int)m,        \
+                       (int)i, (int)k, (int)tiles_m, (int)tiles_n, nullptr, 0.f);
+  FF_SWIGLU(144) FF_SWIGLU(128) FF_SWIGLU(112) FF_SWIGLU(96) FF_SWIGLU(80)
+#undef FF_SWIGLU
   FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu_pk");
   return FF_OK;
 }
@@ -711,15 +755,20 @@ extern "C" int ff_gemm_fp8_swiglu_static(const void* qa, const float* sa, const 
              "ff_gemm_fp8_swiglu_static: bad sizes (i %% 64, k %% 128, ldh %% 8)");
   FF_REQUIRE(ff_aligned(qa, 16) && ff_aligned(qw, 16) && ff_aligned(hq, 16),
              "ff_gemm_fp8_swiglu_static: operands must be 16-byte aligned");
-  const int64_t tiles_m = (m + kPkBM - 1) / kPkBM, tiles_n = i / kPkCH;
-  const bool packed_fits = qw_packed && m > 4 && i % kPkCH == 0 && k % kPkKAlign == 0 &&
-                           m * k < (int64_t(1) << 31) && 2 * i * k < (int64_t(1) << 31) &&
-                           tiles_m * tiles_n >= 192 && ff_aligned(qw_packed, 16);
+  const int64_t tiles_n = i / kPkCH;
+  const int bm = i % kPkCH == 0 ? swiglu_bm(m, tiles_n) : 0;
+  const bool packed_fits = qw_packed && bm && m > 4 && k % kPkKAlign == 0 && m * k < (int64_t(1) << 31) &&
+                           2 * i * k < (int64_t(1) << 31) && ff_aligned(qw_packed, 16);
   if (!packed_fits) return gemm_swiglu_static_rowmajor(qa, sa, qw, sw, hq, ldh, inv, m, i, k, (hipStream_t)stream);
-  hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<kPkBM, kPkCW, kPkP, kPkD, kPkG, true>),
-                     dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads), 0, (hipStream_t)stream,
-                     (const uint8_t*)qa, sa, (const uint8_t*)qw_packed, sw, nullptr, ldh, nullptr, (int)m, (int)i,
-                     (int)k, (int)tiles_m, (int)tiles_n, (uint8_t*)hq, inv);
+  const int64_t tiles_m = (m + bm - 1) / bm;
+#define FF_SWIGLU(BM)                                                                                               \
+  if (bm == BM)                                                                                                     \
+    hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<BM, kPkCW, kPkP, kPkD, kPkG, true>),                          \
+                       dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads), 0, (hipStream_t)stream,                 \
+                       (const uint8_t*)qa, sa, (const uint8_t*)qw_packed, sw, nullptr, ldh, nullptr, (int)m, (int)i, \
+                       (int)k, (int)tiles_m, (int)tiles_n, (uint8_t*)hq, inv);
+  FF_SWIGLU(144) FF_SWIGLU(128) FF_SWIGLU(112) FF_SWIGLU(96) FF_SWIGLU(80)
+#undef FF_SWIGLU
   FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu_static");
   return FF_OK;
 }
@@ -742,12 +791,16 @@ int gemm_fp8_pk_partials(const void* qa, const float* sa, int sa_rows, const voi
   FF_REQUIRE(workspace && workspace_bytes >= need && ff_aligned(workspace, 16),
              "ff_gemm_fp8_pk: workspace of %lld bytes (16-byte aligned) required", (long long)need);
   const int64_t tiles_m = (m + kSpBM - 1) / kSpBM, tiles_n = n / kSpBN;
-  hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<kSpBM, kSpCW, kSpP, kSpD, kSpG, 4>),
-                     dim3((unsigned)(tiles_m * tiles_n * 4)), dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows,
-                     (const uint8_t*)qw_packed, sw, sw_cols, (bf16_t*)nullptr, (int64_t)0, (int)m, (int)n, (int)k,
-                     (int)tiles_m, (int)tiles_n, (float*)workspace);
+#define FF_SPLIT(S)                                                                                                 \
+  if (s == S)                                                                                                       \
+    hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<kSpBM, kSpCW, kSpP, kSpD, kSpG, S>),                           \
+                       dim3((unsigned)(tiles_m * tiles_n * S)), dim3(kThreads), 0, st, (const uint8_t*)qa, sa,      \
+                       sa_rows, (const uint8_t*)qw_packed, sw, sw_cols, (bf16_t*)nullptr, (int64_t)0, (int)m,       \
+                       (int)n, (int)k, (int)tiles_m, (int)tiles_n, (float*)workspace);
+  FF_SPLIT(2) FF_SPLIT(3) FF_SPLIT(4)
+#undef FF_SPLIT
   FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
-  *splits = 4;
+  *splits = s;
   *mp = tiles_m * kSpBM;
   return FF_OK;
 }
@@ -789,8 +842,13 @@ extern "C" int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, cons
                                           workspace_bytes, st, &splits, &mp);
   if (rc) return rc;
   const int64_t chunks = m * (n / 8);
-  hipLaunchKernelGGL((split_reduce_kernel<4>), dim3((unsigned)((chunks + kThreads - 1) / kThreads)), dim3(kThreads),
-                     0, st, (const float*)workspace, mp, sa, sa_rows, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)n);
+  const dim3 rgrid((unsigned)((chunks + kThreads - 1) / kThreads));
+#define FF_REDUCE(S)                                                                                                \
+  if (splits == S)                                                                                                  \
+    hipLaunchKernelGGL((split_reduce_kernel<S>), rgrid, dim3(kThreads), 0, st, (const float*)workspace, mp, sa,     \
+                       sa_rows, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)n);
+  FF_REDUCE(2) FF_REDUCE(3) FF_REDUCE(4)
+#undef FF_REDUCE
   FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
   return FF_OK;
 }

@@ -433,7 +433,7 @@ int gemm_add_rms(const char* name, const void* qa, const float* sa, int sa_rows,
     else
       return ff_add_rms_quant_static(a, y, deep, w, residual, nullptr, q, inv, m, n, eps, start, nv, stream);
   }
-  FF_REQUIRE(splits == 4, "%s: unexpected split count %d", name, splits);
+  FF_REQUIRE(splits >= 2 && splits <= 4, "%s: unexpected split count %d", name, splits);
   SplitAddend sb;
   sb.part = (const float*)workspace;
   sb.mp = mp;

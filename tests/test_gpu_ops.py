@@ -333,10 +333,13 @@ def test_pack_weight_fp8_layout(gpu):
                 assert np.array_equal(got[f, kt, 0, lane], row[:16]) and np.array_equal(got[f, kt, 1, lane], row[16:])
 
 
+# 12288 channels (64 column tiles) take row tiles of 144 (576 tokens), 80 (176),
+# 112 (400), 96 (700) and 128 (1000)
 @pytest.mark.parametrize("m,i,k", [(576, 12288, 4096), (300, 12288, 2048), (433, 6144, 4096), (3, 12288, 4096),
-                                   (576, 4096, 4096)])
+                                   (576, 4096, 4096), (176, 12288, 4096), (400, 12288, 4096), (700, 12288, 4096),
+                                   (1000, 12288, 4096)])
 def test_gemm_fp8_swiglu_packed_equals_rowmajor(gpu, m, i, k):
-    """The gate/up GEMM on the packed weight copy (144 x 384 tiles, weights
+    """The gate/up GEMM on the packed weight copy (BM x 384 tiles, BM = 80..144 by grid, weights
     straight into the MFMA operands) gives the same bits as ff_gemm_fp8_swiglu on
     the row-major weight, SwiGLU output and row maxima, including a ragged last
     token tile; shapes it does not take (3 rows, i % 192 != 0, too few tiles)
@@ -362,6 +365,7 @@ def test_gemm_fp8_swiglu_packed_equals_rowmajor(gpu, m, i, k):
 # (576 x 4096 x 4096: 96 x 128; 576 / 500 x 6144 x 4096: 64 x 256, the last
 # tile ragged) or the row-major kernels (too few tiles, 3 rows, n % 128)
 PK_SHAPES = [(576, 4096, 12288, 4), (300, 2048, 8192, 4), (1000, 6144, 8192, 4), (576, 12288, 4096, 1),
+             (640, 4096, 12288, 3), (1152, 4096, 12288, 2),
              (576, 4096, 4096, 0), (576, 6144, 4096, 0), (500, 6144, 4096, 0), (300, 4096, 2048, 0),
              (3, 4096, 4096, 0), (576, 4160, 12288, 0)]
 
@@ -403,7 +407,8 @@ def test_gemm_fp8_pk_matches_rowmajor(gpu, m, n, k, splits):
 @pytest.mark.parametrize("m,n,k,static,deep", [(576, 4096, 12288, False, True), (576, 4096, 12288, True, False),
                                                (500, 4096, 12288, False, False), (300, 2048, 8192, True, True),
                                                (576, 4096, 4096, False, False), (1, 4096, 12288, False, False),
-                                               (1, 4096, 12288, True, False)])
+                                               (1, 4096, 12288, True, False), (640, 4096, 12288, False, True),
+                                               (1152, 4096, 12288, True, False)])
 def test_gemm_fp8_pk_add_rms_equals_unfused(gpu, m, n, k, static, deep):
     """ff_gemm_fp8_pk_add_rms_quant(_static) == ff_gemm_fp8_pk followed by
     ff_add_rms_quant(_static), bit for bit in y, the residual, the e4m3 codes
@@ -823,7 +828,8 @@ def test_attention_q_equals_unfused(gpu, t, hq, hk):
         call("ff_attention_vt_q", ptr(q), ptr(k), ptr(vt), ptr(got), inv, 1, t, tp, hq, hk, d, d ** -0.5, stream())
 
 
-@pytest.mark.parametrize("m,i,k", [(576, 12288, 4096), (320, 6144, 2048), (1, 12288, 4096), (3, 640, 256)])
+@pytest.mark.parametrize("m,i,k", [(576, 12288, 4096), (320, 6144, 2048), (1, 12288, 4096), (3, 640, 256),
+                                   (640, 12288, 4096), (176, 12288, 4096)])
 def test_gemm_swiglu_static_equals_unfused(gpu, m, i, k):
     """ff_gemm_fp8_swiglu_static (packed tile, row-major tile and GEMV by shape)
     equals ff_gemm_fp8 with per-tensor scales, then swiglu, then the static cast,
