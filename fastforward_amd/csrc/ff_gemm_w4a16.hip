@@ -1070,19 +1070,29 @@ int64_t w4pk_workspace(int64_t m, int64_t n, int64_t k, int64_t group) {
   return (m + kW4BM - 1) / kW4BM * (n / (4 * p.cw)) * p.splits * kW4BM * 4 * p.cw * 4;
 }
 
-template <int CW, bool SWIGLU>
+// Row-tile height of the packed SwiGLU GEMM with 96-channel wave tiles: 160
+// where it keeps the grid in one round of 256 workgroups that 144 would spill
+// into a second (the 8B gate/up at 577..640 and 1153..1280 tokens), counted as
+// rounds x (BM + 16) rows per CU; 144 otherwise. 160 rows is the most the
+// accumulators fit (240 of 256 AGPRs), and the main loop needs at least 144.
+int w4_swiglu_bm(int64_t m, int64_t tiles_n) {
+  const auto cost = [&](int bm) { return ((m + bm - 1) / bm * tiles_n + 255) / 256 * (bm + 16); };
+  return cost(160) < cost(kW4BM) ? 160 : kW4BM;
+}
+
+template <int CW, bool SWIGLU, int BM = kW4BM>
 void launch_w4pk(const void* x, int64_t ldx, const void* frag, const void* fscales, int gshift, void* y, int64_t ldy,
                  int m, int n, int k, int splits, void* ws, hipStream_t s) {
-  const int tiles_m = (m + kW4BM - 1) / kW4BM;
+  const int tiles_m = (m + BM - 1) / BM;
   const int tiles_n = n / (4 * CW);  // SWIGLU: n = 2 half rows, 2 CW channels of each half per tile
-  hipLaunchKernelGGL((gemm_w4a16_pk_kernel<kW4BM, CW, SWIGLU, !SWIGLU>), dim3((unsigned)(tiles_m * tiles_n * splits)),
+  hipLaunchKernelGGL((gemm_w4a16_pk_kernel<BM, CW, SWIGLU, !SWIGLU>), dim3((unsigned)(tiles_m * tiles_n * splits)),
                      dim3(kThreads), 0, s, (const bf16_t*)x, ldx, (const uint8_t*)frag, (const float*)fscales,
                      gshift, (bf16_t*)y, ldy, m, n, k, tiles_m, tiles_n, splits,
                      !SWIGLU && splits > 1 ? (f32x4*)ws : nullptr);
   if (!SWIGLU && splits > 1 && y != nullptr) {
     const int64_t chunks = (int64_t)m * (n / 8);
     hipLaunchKernelGGL(w4pk_reduce_kernel, dim3((unsigned)((chunks + kThreads - 1) / kThreads)), dim3(kThreads), 0, s,
-                       (const float*)ws, splits, (int64_t)tiles_m * kW4BM, (bf16_t*)y, ldy, m, n);
+                       (const float*)ws, splits, (int64_t)tiles_m * BM, (bf16_t*)y, ldy, m, n);
   }
 }
 
@@ -1211,6 +1221,8 @@ extern "C" int ff_gemm_w4a16_swiglu_pk(const void* x, int64_t ldx, const void* f
   const int gs = w4_gshift(group);
   if (gemv)
     launch_gemv_w4pk<true>(x, ldx, frag, frag_scales, gs, h, ldh, (int)m, (int)(2 * i), (int)k, s);
+  else if (cw == 96 && w4_swiglu_bm(m, 2 * i / 384) == 160)
+    launch_w4pk<96, true, 160>(x, ldx, frag, frag_scales, gs, h, ldh, (int)m, (int)(2 * i), (int)k, 1, nullptr, s);
   else if (cw == 96)
     launch_w4pk<96, true>(x, ldx, frag, frag_scales, gs, h, ldh, (int)m, (int)(2 * i), (int)k, 1, nullptr, s);
   else

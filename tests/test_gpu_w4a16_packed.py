@@ -166,7 +166,8 @@ def test_w4a16_swiglu_gemv_vs_exact(gpu, m, k, i, sym, group):
     assert bool(((unf - want).abs() <= bound).all())
 
 
-@pytest.mark.parametrize("m,k,i", [(576, 4096, 12288), (320, 2048, 6144), (100, 1024, 640)])
+# 576 tokens: 144-row tiles; 640: 160-row tiles (one round of 256 workgroups)
+@pytest.mark.parametrize("m,k,i", [(576, 4096, 12288), (640, 4096, 12288), (320, 2048, 6144), (100, 1024, 640)])
 @pytest.mark.parametrize("sym,group", [(True, 128), (False, 32)])
 def test_w4a16_swiglu_packed_equals_unfused(gpu, tuning, m, k, i, sym, group):
     """ff_gemm_w4a16_swiglu_pk == ops.swiglu of the unsplit gate/up product, bit
