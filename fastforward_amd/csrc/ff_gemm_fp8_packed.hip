@@ -527,13 +527,14 @@ int split_plan(int64_t m, int64_t n, int64_t k) {
   const int64_t tiles = (m + kSpBM - 1) / kSpBM * (n / kSpBN), kt = k / 128;
   if (tiles >= 192) return kt % kSpU == 0 ? 1 : 0;
   if (kt < 64) return 0;
-  // The split count with the fewest k steps per CU: rounds of 256 workgroups
-  // (one per CU) x kt / S steps each, ties to fewer splits (less partial
-  // traffic). 8B down (k = 12288): 576 tokens 4 splits in one round, 640
-  // tokens 3 in one round (4 would take two), 1152 tokens 2.
+  // The split count (2, 3, 4 or 8) with the fewest k steps per CU: rounds of
+  // 256 workgroups (one per CU) x kt / S steps each, ties to fewer splits
+  // (less partial traffic). 8B down (k = 12288): 176 tokens 8 splits, 576
+  // tokens 4 in one round, 640 tokens 3 in one round (4 would take two),
+  // 1152 tokens 2.
   int best = 0;
   int64_t best_steps = 0;
-  for (int sp = 2; sp <= 4; ++sp) {
+  for (int sp = 2; sp <= 8; sp += sp < 4 ? 1 : 4) {
     if (kt % (sp * kSpU)) continue;
     const int64_t steps = (tiles * sp + 255) / 256 * (kt / sp);
     if (best == 0 || steps < best_steps) {
@@ -797,7 +798,7 @@ int gemm_fp8_pk_partials(const void* qa, const float* sa, int sa_rows, const voi
                        dim3((unsigned)(tiles_m * tiles_n * S)), dim3(kThreads), 0, st, (const uint8_t*)qa, sa,      \
                        sa_rows, (const uint8_t*)qw_packed, sw, sw_cols, (bf16_t*)nullptr, (int64_t)0, (int)m,       \
                        (int)n, (int)k, (int)tiles_m, (int)tiles_n, (float*)workspace);
-  FF_SPLIT(2) FF_SPLIT(3) FF_SPLIT(4)
+  FF_SPLIT(2) FF_SPLIT(3) FF_SPLIT(4) FF_SPLIT(8)
 #undef FF_SPLIT
   FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
   *splits = s;
@@ -847,7 +848,7 @@ extern "C" int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, cons
   if (splits == S)                                                                                                  \
     hipLaunchKernelGGL((split_reduce_kernel<S>), rgrid, dim3(kThreads), 0, st, (const float*)workspace, mp, sa,     \
                        sa_rows, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)n);
-  FF_REDUCE(2) FF_REDUCE(3) FF_REDUCE(4)
+  FF_REDUCE(2) FF_REDUCE(3) FF_REDUCE(4) FF_REDUCE(8)
 #undef FF_REDUCE
   FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
   return FF_OK;

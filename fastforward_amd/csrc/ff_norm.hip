@@ -433,7 +433,7 @@ int gemm_add_rms(const char* name, const void* qa, const float* sa, int sa_rows,
     else
       return ff_add_rms_quant_static(a, y, deep, w, residual, nullptr, q, inv, m, n, eps, start, nv, stream);
   }
-  FF_REQUIRE(splits >= 2 && splits <= 4, "%s: unexpected split count %d", name, splits);
+  FF_REQUIRE(splits >= 2 && splits <= 8, "%s: unexpected split count %d", name, splits);
   SplitAddend sb;
   sb.part = (const float*)workspace;
   sb.mp = mp;
@@ -444,10 +444,16 @@ int gemm_add_rms(const char* name, const void* qa, const float* sa, int sa_rows,
   sb.sw_cols = sw_cols;
   sb.y = (bf16_t*)y;
   if (deep && nv > 0)
-    return launch_row_norm<true, true, true, false, QUANT, 4>(a, nullptr, deep, w, residual, nullptr, q, scales, m,
-                                                              n, eps, start, nv, s, name, inv, sb);
-  return launch_row_norm<true, false, true, false, QUANT, 4>(a, nullptr, nullptr, w, residual, nullptr, q, scales, m,
-                                                             n, eps, 0, 0, s, name, inv, sb);
+    return splits > 4 ? launch_row_norm<true, true, true, false, QUANT, 8>(a, nullptr, deep, w, residual, nullptr, q,
+                                                                          scales, m, n, eps, start, nv, s, name, inv,
+                                                                          sb)
+                      : launch_row_norm<true, true, true, false, QUANT, 4>(a, nullptr, deep, w, residual, nullptr, q,
+                                                                          scales, m, n, eps, start, nv, s, name, inv,
+                                                                          sb);
+  return splits > 4 ? launch_row_norm<true, false, true, false, QUANT, 8>(a, nullptr, nullptr, w, residual, nullptr, q,
+                                                                         scales, m, n, eps, 0, 0, s, name, inv, sb)
+                    : launch_row_norm<true, false, true, false, QUANT, 4>(a, nullptr, nullptr, w, residual, nullptr, q,
+                                                                         scales, m, n, eps, 0, 0, s, name, inv, sb);
 }
 }  // namespace
 

@@ -365,7 +365,7 @@ def test_gemm_fp8_swiglu_packed_equals_rowmajor(gpu, m, i, k):
 # (576 x 4096 x 4096: 96 x 128; 576 / 500 x 6144 x 4096: 64 x 256, the last
 # tile ragged) or the row-major kernels (too few tiles, 3 rows, n % 128)
 PK_SHAPES = [(576, 4096, 12288, 4), (300, 2048, 8192, 4), (1000, 6144, 8192, 4), (576, 12288, 4096, 1),
-             (640, 4096, 12288, 3), (1152, 4096, 12288, 2),
+             (640, 4096, 12288, 3), (1152, 4096, 12288, 2), (176, 4096, 12288, 8),
              (576, 4096, 4096, 0), (576, 6144, 4096, 0), (500, 6144, 4096, 0), (300, 4096, 2048, 0),
              (3, 4096, 4096, 0), (576, 4160, 12288, 0)]
 
@@ -408,7 +408,8 @@ def test_gemm_fp8_pk_matches_rowmajor(gpu, m, n, k, splits):
                                                (500, 4096, 12288, False, False), (300, 2048, 8192, True, True),
                                                (576, 4096, 4096, False, False), (1, 4096, 12288, False, False),
                                                (1, 4096, 12288, True, False), (640, 4096, 12288, False, True),
-                                               (1152, 4096, 12288, True, False)])
+                                               (1152, 4096, 12288, True, False), (176, 4096, 12288, False, True),
+                                               (176, 4096, 12288, True, False)])
 def test_gemm_fp8_pk_add_rms_equals_unfused(gpu, m, n, k, static, deep):
     """ff_gemm_fp8_pk_add_rms_quant(_static) == ff_gemm_fp8_pk followed by
     ff_add_rms_quant(_static), bit for bit in y, the residual, the e4m3 codes
