@@ -569,6 +569,19 @@ SmallTile small_plan(int64_t m, int64_t n, int64_t k) {
       return t;
     }
   }
+  // Short m (no candidate reaches 192 workgroups): the candidate with the
+  // most workgroups, if it has at least 64 (the row-major kernel's 64 x 128
+  // tiles give no more).
+  int64_t most = 63;
+  for (const auto& c : cand) {
+    if (n % (4 * c[1])) continue;
+    const int64_t tiles = (m + c[0] - 1) / c[0] * (n / (4 * c[1]));
+    if (tiles > most && tiles <= 512) {
+      most = tiles;
+      t.bm = c[0];
+      t.cw = c[1];
+    }
+  }
   return t;
 }
 
