@@ -341,6 +341,46 @@ def cpu_baseline(cfg, w, ids, pos, pick, T, layers_sample):
                        f"sample wall time {t2 - t0:.1f} s")
 
 
+def cpu_layer_2b(reps=5, warmup=2):
+    """The CPU reference configuration: one Qwen3-VL-2B-shaped decoder layer
+    (hidden 2048, 16/8 heads, head_dim 128, MLP 6144, q/k eps 1e-6, rope theta
+    5e6, M-RoPE [24, 20, 20]) over 320 tokens (4 text + 16 x 16 image grid + 60
+    text), causal, batch 1, through the oracle's restatement of the reference's
+    op sequence with unquantised linears: fp32 arithmetic with the reference's
+    bf16 rounding points, weights N(0, 0.02) and hidden states N(0, 1) (seeded).
+    Median of ``reps`` runs after ``warmup``, on every core of this host."""
+    from oracle import model as omodel
+    from oracle import ops as O
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    H, HQ, HK, D, I, T = 2048, 16, 8, 128, 6144, 320
+    g = torch.Generator().manual_seed(0)
+    lin = lambda rows, cols: dict(kind="bf16", w=(torch.randn(rows, cols, generator=g) * 0.02).to(torch.bfloat16))  # noqa: E731
+    shape = omodel.Shape(layers=2, hidden=H, heads=HQ, kv_heads=HK, head_dim=D, inter=I, vocab=151936)
+    one = torch.ones(H, dtype=torch.bfloat16)
+    layer = omodel.Layer(input_norm=one, post_norm=one, q_norm=torch.ones(D, dtype=torch.bfloat16),
+                         k_norm=torch.ones(D, dtype=torch.bfloat16), qkv=lin((HQ + 2 * HK) * D, H),
+                         o=lin(H, HQ * D), gateup=lin(2 * I, H), down=lin(H, I))
+    h = torch.randn(1, T, H, generator=g).to(torch.bfloat16)
+    pos = O.mrope_positions(4, 16, 16, T)
+    times = []
+    for i in range(warmup + reps):
+        t0 = time.perf_counter()
+        cos, sin = O.mrope_cos_sin(pos, shape.theta, D, shape.sections)
+        x = O.fast_norm(h, layer.input_norm, shape.eps)
+        attn = omodel.attention_block(shape, layer, x, cos, sin)
+        res, post = O.add_rms(h, attn, None, layer.post_norm, shape.eps)
+        out = O.add_rms(res, omodel.mlp(layer, post), None, layer.input_norm, shape.eps)
+        times.append(time.perf_counter() - t0)
+        del out
+    ms = sorted(times[warmup:])[reps // 2] * 1e3
+    flop = 2.0 * T * H * ((HQ + 2 * HK) * D + HQ * D + 3 * I) + 4.0 * HQ * D * T * (T + 1) / 2
+    return dict(value=round(ms, 2), unit="ms per decoder layer", gflops=round(flop / ms / 1e6, 1), cores=n,
+                kind="port", workload="one Qwen3-VL-2B-shaped decoder layer, 320 tokens (16x16 image grid + "
+                                      "64 text), causal, oracle op formulation in fp32 with bf16 rounding points, "
+                                      f"median of {reps} after {warmup} warm-ups")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -415,6 +455,8 @@ def main():
     if not args.no_cpu:
         log("cpu baseline")
         cpu = cpu_baseline(cfg, w, ids, pos, pick, T, args.cpu_layers)
+        cpu["layer_2b_320_fp32"] = cpu_layer_2b()
+        log(f"cpu 2B layer {cpu['layer_2b_320_fp32']['value']} ms")
     del rt
     if not args.no_extras:
         extras.update(vision_extras(cfg, w, T, grid, args))

@@ -1438,11 +1438,10 @@ extern "C" int ff_gemm_w4a16_noalloc(const void* x, int64_t ldx, const void* pac
                                      int64_t group, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
                                      ff_stream_t stream) {
   FF_REQUIRE(m >= 0 && n > 0 && k > 0, "ff_gemm_w4a16_noalloc: bad sizes");
+  // the workspace entry point's own size, so both take the same split
   int64_t need = 0;
-  if (k % (2 * KSTAGE) == 0) {
-    const int splits = pick_w4_splits(pick_w4_tile(m, n), m, n, k);
-    need = splits > 1 ? (int64_t)splits * m * n * 4 : 0;
-  }
+  const int rc = ff_gemm_w4a16_workspace(m, n, k, &need);
+  if (rc != FF_OK) return rc;
   FF_REQUIRE(need <= kScratchBytes,
              "ff_gemm_w4a16_noalloc: this %lld x %lld x %lld product needs %lld bytes of split-K scratch; the "
              "static scratch holds %lld (use ff_gemm_w4a16_ws with a workspace)",

@@ -299,7 +299,9 @@ class Int4:
         if flat.stride(-1) != 1 or flat.stride(0) % 8:
             flat = flat.contiguous()
         if self.oracle is not None:
-            self(flat[:1])  # the first-call operator check, on the GEMM alone
+            # the first-call operator check on row 0 of the full-m product: ff_gemm_w4a16_pk
+            # runs the packed tile kernel the fused op runs (a one-row call would take the GEMV)
+            self(flat)
         m, k = flat.shape
         n = self.weight.shape[0]
         assert a.is_contiguous() and a.dtype == BF16 and a.shape[-1] == n and a.numel() == m * n
@@ -327,7 +329,9 @@ class Int4:
         if flat.stride(-1) != 1 or flat.stride(0) % 8:
             flat = flat.contiguous()
         if self.oracle is not None:
-            self(flat[:1])  # the first-call operator check, on the GEMM alone
+            # the first-call operator check on row 0 of the full-m product: ff_gemm_w4a16_pk
+            # runs the packed tile kernel the fused op runs (a one-row call would take the GEMV)
+            self(flat)
         m, k = flat.shape
         need = ctypes.c_int64(0)
         call("ff_gemm_w4a16_qkv_workspace", m, k, hq, hk, self.group, ctypes.byref(need))
@@ -362,7 +366,9 @@ class Int4:
         if flat.stride(-1) != 1 or flat.stride(0) % 8:
             flat = flat.contiguous()
         if self.oracle is not None:
-            self(flat[:1])  # the first-call operator check, on the GEMM alone
+            # the first-call operator check on row 0 of the full-m product: ff_gemm_w4a16_pk
+            # runs the packed tile kernel the fused op runs (a one-row call would take the GEMV)
+            self(flat)
         m, k = flat.shape
         i = self.weight.shape[0] // 2
         if not self.swiglu_fits(m):

@@ -152,12 +152,14 @@ def test_step_gateup_swiglu_vs_oracle(gpu, preset, rows):
 @pytest.mark.parametrize("preset", list(SHAPES))
 def test_step_qkv_epilogue_vs_oracle(gpu, preset):
     """The QKV GEMM with the per-head q/k RMSNorm, the M-RoPE rotary and the V
-    transpose in its epilogue (ff_gemm_fp8_qkv, the step's launch). The GEMM
-    part: the raw product of the same codes (ff_gemm_fp8, the same tile) meets
-    the plain-GEMM bar against the exact product, and V^T is exactly its V
-    columns (the fused kernel sums the same values); V^T padding is zero. The
-    epilogue: q and k equal the oracle's qk_pair of that raw product within the
-    rotary-term bar of the module docstring."""
+    transpose in its epilogue: ff_gemm_fp8_qkv_pk (the step's launch, packed
+    weights) gives the same bits as ff_gemm_fp8_qkv (row-major weights), which
+    is checked here. The GEMM part: the raw product of the same codes
+    (ff_gemm_fp8, the same tile) meets the plain-GEMM bar against the exact
+    product, and V^T is exactly its V columns (the fused kernel sums the same
+    values); V^T padding is zero. The epilogue: q and k equal the oracle's
+    qk_pair of that raw product within the rotary-term bar of the module
+    docstring."""
     from fastforward_amd._lib import call, ptr, stream
     from fastforward_amd.ops import RMSNorm
     t, h, hq, hk, _ = SHAPES[preset]
@@ -178,6 +180,12 @@ def test_step_qkv_epilogue_vs_oracle(gpu, preset):
     vt = torch.full((hk, D, tp), float("nan"), device=DEV, dtype=BF16)
     call("ff_gemm_fp8_qkv", ptr(qa_d), ptr(sa_d), 1, ptr(op.weight), ptr(op.scale), 1, t, h, hq, hk, ptr(qn_d.weight),
          ptr(kn_d.weight), 1e-6, 1e-6, ptr(cos_d), ptr(sin_d), ptr(yq), ptr(yk), ptr(vt), tp, stream())
+    # the step's launch on the packed copy: the same bits
+    pq, pk_, pv = (torch.full_like(b, float("nan")) for b in (yq, yk, vt))
+    call("ff_gemm_fp8_qkv_pk", ptr(qa_d), ptr(sa_d), 1, ptr(op.weight), ptr(op.packed), ptr(op.scale), 1, t, h,
+         hq, hk, ptr(qn_d.weight), ptr(kn_d.weight), 1e-6, 1e-6, ptr(cos_d), ptr(sin_d), ptr(pq), ptr(pk_), ptr(pv),
+         tp, stream())
+    assert torch.equal(pq, yq) and torch.equal(pk_, yk) and torch.equal(pv, vt), f"{preset}: packed != row-major"
     raw = torch.empty(t, n, device=DEV, dtype=BF16)
     call("ff_gemm_fp8", ptr(qa_d), ptr(sa_d), 1, ptr(op.weight), ptr(op.scale), 1, ptr(raw), n, t, n, h, stream())
     raw = raw.cpu()

@@ -2,7 +2,8 @@
 workspace entry point it mirrors (ff_gemm_w4a16_ws given the bytes
 ff_gemm_w4a16_workspace asks for): bit-identical outputs on consecutive calls
 that share the static scratch, the second with a smaller input, plus a tail
-row; a split that would exceed the scratch is rejected."""
+row; a split that would exceed the scratch is rejected; captured in a hipGraph,
+every replay equals the eager call."""
 import ctypes
 
 import pytest
@@ -66,3 +67,37 @@ def test_noalloc_rejects_a_split_beyond_the_scratch(gpu):
     # and the default choice for the same product runs
     y_ws, y_na, _ = _both(x, op)
     assert torch.equal(y_ws, y_na)
+
+
+def test_noalloc_under_graph_capture(gpu):
+    """The use the entry point exists for: captured in a hipGraph (no allocation,
+    no memset node), each replay equals the workspace entry point's eager call
+    on the inputs the replay read, with other eager work and synchronisations
+    between the replays."""
+    from fastforward_amd._lib import call, ptr, stream
+    m, k, n = 576, 4096, 6144
+    x, op = _case(m, k, n, 128, True, 5)
+    y = torch.full((m, n), float("nan"), device=DEV, dtype=BF16)
+    g = torch.Generator().manual_seed(6)
+    inputs = [torch.randn(m, k, generator=g).to(BF16).to(DEV) for _ in range(3)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):   # eager call first: the scratch address is taken outside the capture
+        call("ff_gemm_w4a16_noalloc", ptr(x), k, ptr(op.packed), ptr(op.scales), op.group, ptr(y), n, m, n, k,
+             stream())
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call("ff_gemm_w4a16_noalloc", ptr(x), k, ptr(op.packed), ptr(op.scales), op.group, ptr(y), n, m, n, k,
+             stream())
+    for rep, xi in enumerate(inputs + inputs[:1]):
+        x.copy_(xi)
+        y.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = y.clone()
+        y_ws, y_na, need = _both(x, op)      # eager calls between the replays (they reuse the scratch)
+        assert need > 0
+        assert torch.equal(got, y_ws), f"replay {rep} differs from the eager workspace call"
+        assert torch.equal(y_na, y_ws)
