@@ -484,8 +484,14 @@ __global__ __launch_bounds__(kThreads) void split_reduce_kernel(const float* __r
 // The configuration measured for the 8B gate/up shape (576 x 4096 x 2 x 12288):
 // 144 x 384 tiles, one workgroup per CU (4 x 64 = 256 workgroups).
 constexpr int kPkBM = 144, kPkCW = 96, kPkP = 2, kPkD = 2, kPkG = 2;
-constexpr int kPkCH = 2 * kPkCW;
 constexpr int kPkKAlign = 128 * lcm3(kPkP, kPkD, 2 * kPkG);  // k multiple of the unrolled k steps
+
+// Wave width CW of the packed gate/up tile (CW / 2 gate + CW / 2 up channels
+// per wave, 2 CW channels of h per workgroup) for MLP width i: 96 (192-channel
+// tiles) where i allows it, else 64 (128-channel tiles: the 32B shape's 25600
+// and the 4B shape's 9728 channels); 0 when neither divides i (the row-major
+// kernel runs then).
+int swiglu_cw(int64_t i) { return i % 192 == 0 ? 96 : (i % 128 == 0 ? 64 : 0); }
 
 // Row-tile height of the packed gate/up GEMM for m tokens and tiles_n column
 // tiles: the candidate whose grid takes the fewest row steps per CU, counted as
@@ -522,9 +528,15 @@ constexpr int kSpU = lcm3(kSpP, kSpD, 2 * kSpG);
 // enough that the extra reduction launch pays off (the 8B down projection,
 // 576 x 4096 x 12288); shorter k takes small_plan's tiles (below) or the
 // row-major kernels.
+// Row-tile height of the plain packed GEMM: 144, or 80 when FF_TUNE_FP8_SPLIT_BM
+// asks for it (80-row tiles at two workgroups per CU take half the k splits of
+// the 144-row ones on the same grid).
+int split_bm() { return ff_tuning(FF_TUNE_FP8_SPLIT_BM) == 80 ? 80 : kSpBM; }
+
 int split_plan(int64_t m, int64_t n, int64_t k) {
   if (m <= 4 || n % kSpBN || k % 128 || m * k >= (int64_t(1) << 31) || n * k >= (int64_t(1) << 31)) return 0;
-  const int64_t tiles = (m + kSpBM - 1) / kSpBM * (n / kSpBN), kt = k / 128;
+  const int bm = split_bm();
+  const int64_t tiles = (m + bm - 1) / bm * (n / kSpBN), kt = k / 128;
   if (tiles >= 192) return kt % kSpU == 0 ? 1 : 0;
   if (kt < 64) return 0;
   // The split count (2, 3, 4 or 8) with the fewest k steps per CU: rounds of
@@ -595,9 +607,33 @@ void launch_small(const void* qa, const float* sa, int sa_rows, const void* qw_p
 }
 
 int64_t split_workspace(int64_t m, int64_t n, int64_t k) {
-  const int s = split_plan(m, n, k);
+  const int s = split_plan(m, n, k), bm = split_bm();
   if (s <= 1) return 0;
-  return (m + kSpBM - 1) / kSpBM * (n / kSpBN) * s * kSpBM * kSpBN * 4;
+  return (m + bm - 1) / bm * (n / kSpBN) * s * bm * kSpBN * 4;
+}
+
+// The plain packed kernel at row tile BM with S k splits (S == 1: y directly).
+template <int BM, int S>
+void launch_split(const void* qa, const float* sa, int sa_rows, const void* qw_packed, const float* sw, int sw_cols,
+                  void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, void* part, hipStream_t st) {
+  const int64_t tiles_m = (m + BM - 1) / BM, tiles_n = n / kSpBN;
+  hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<BM, kSpCW, kSpP, kSpD, kSpG, S>),
+                     dim3((unsigned)(tiles_m * tiles_n * S)), dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows,
+                     (const uint8_t*)qw_packed, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)n, (int)k, (int)tiles_m,
+                     (int)tiles_n, (float*)part);
+}
+
+template <int BM>
+void launch_splits(int s, const void* qa, const float* sa, int sa_rows, const void* qw_packed, const float* sw,
+                   int sw_cols, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, void* part, hipStream_t st) {
+  switch (s) {
+    case 1: launch_split<BM, 1>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
+    case 2: launch_split<BM, 2>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
+    case 3: launch_split<BM, 3>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
+    case 4: launch_split<BM, 4>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
+    case 8: launch_split<BM, 8>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
+    default: break;
+  }
 }
 
 // Fused QKV on fragment-packed weights: BM tokens x BN = 4 CW channels (BN /
@@ -741,20 +777,22 @@ extern "C" int ff_gemm_fp8_swiglu_pk(const void* qa, const float* sa, const void
                                      const float* sw, void* h, int64_t ldh, float* pmax, int64_t m, int64_t i,
                                      int64_t k, ff_stream_t stream) {
   FF_REQUIRE(qa && sa && qw && sw && h && pmax, "ff_gemm_fp8_swiglu_pk: null pointer");
-  const int64_t tiles_n = i / kPkCH;
-  const int bm = i % kPkCH == 0 ? swiglu_bm(m, tiles_n) : 0;
+  const int cw = swiglu_cw(i);
+  const int64_t tiles_n = cw ? i / (2 * cw) : 0;
+  const int bm = cw ? swiglu_bm(m, tiles_n) : 0;
   const bool packed_fits = qw_packed && bm && m > 4 && k % kPkKAlign == 0 && ldh % 8 == 0 && ldh >= i &&
                            m * k < (int64_t(1) << 31) && 2 * i * k < (int64_t(1) << 31) && ff_aligned(qa, 16) &&
                            ff_aligned(qw_packed, 16) && ff_aligned(h, 16);
   if (!packed_fits) return ff_gemm_fp8_swiglu(qa, sa, qw, sw, h, ldh, pmax, m, i, k, stream);
   const int64_t tiles_m = (m + bm - 1) / bm;
-#define FF_SWIGLU(BM)                                                                                               \
-  if (bm == BM)                                                                                                     \
-    hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<BM, kPkCW, kPkP, kPkD, kPkG>),                                \
+#define FF_SWIGLU(BM, CW)                                                                                           \
+  if (bm == BM && cw == CW)                                                                                         \
+    hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<BM, CW, kPkP, kPkD, kPkG>),                                   \
                        dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads), 0, (hipStream_t)stream,                 \
                        (const uint8_t*)qa, sa, (const uint8_t*)qw_packed, sw, (bf16_t*)h, ldh, pmax, (int)m,        \
                        (int)i, (int)k, (int)tiles_m, (int)tiles_n, nullptr, 0.f);
-  FF_SWIGLU(144) FF_SWIGLU(128) FF_SWIGLU(112) FF_SWIGLU(96) FF_SWIGLU(80)
+  FF_SWIGLU(144, 96) FF_SWIGLU(128, 96) FF_SWIGLU(112, 96) FF_SWIGLU(96, 96) FF_SWIGLU(80, 96)
+  FF_SWIGLU(144, 64) FF_SWIGLU(128, 64) FF_SWIGLU(112, 64) FF_SWIGLU(96, 64) FF_SWIGLU(80, 64)
 #undef FF_SWIGLU
   FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu_pk");
   return FF_OK;
@@ -769,19 +807,21 @@ extern "C" int ff_gemm_fp8_swiglu_static(const void* qa, const float* sa, const 
              "ff_gemm_fp8_swiglu_static: bad sizes (i %% 64, k %% 128, ldh %% 8)");
   FF_REQUIRE(ff_aligned(qa, 16) && ff_aligned(qw, 16) && ff_aligned(hq, 16),
              "ff_gemm_fp8_swiglu_static: operands must be 16-byte aligned");
-  const int64_t tiles_n = i / kPkCH;
-  const int bm = i % kPkCH == 0 ? swiglu_bm(m, tiles_n) : 0;
+  const int cw = swiglu_cw(i);
+  const int64_t tiles_n = cw ? i / (2 * cw) : 0;
+  const int bm = cw ? swiglu_bm(m, tiles_n) : 0;
   const bool packed_fits = qw_packed && bm && m > 4 && k % kPkKAlign == 0 && m * k < (int64_t(1) << 31) &&
                            2 * i * k < (int64_t(1) << 31) && ff_aligned(qw_packed, 16);
   if (!packed_fits) return gemm_swiglu_static_rowmajor(qa, sa, qw, sw, hq, ldh, inv, m, i, k, (hipStream_t)stream);
   const int64_t tiles_m = (m + bm - 1) / bm;
-#define FF_SWIGLU(BM)                                                                                               \
-  if (bm == BM)                                                                                                     \
-    hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<BM, kPkCW, kPkP, kPkD, kPkG, true>),                          \
+#define FF_SWIGLU(BM, CW)                                                                                           \
+  if (bm == BM && cw == CW)                                                                                         \
+    hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<BM, CW, kPkP, kPkD, kPkG, true>),                             \
                        dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads), 0, (hipStream_t)stream,                 \
                        (const uint8_t*)qa, sa, (const uint8_t*)qw_packed, sw, nullptr, ldh, nullptr, (int)m, (int)i, \
                        (int)k, (int)tiles_m, (int)tiles_n, (uint8_t*)hq, inv);
-  FF_SWIGLU(144) FF_SWIGLU(128) FF_SWIGLU(112) FF_SWIGLU(96) FF_SWIGLU(80)
+  FF_SWIGLU(144, 96) FF_SWIGLU(128, 96) FF_SWIGLU(112, 96) FF_SWIGLU(96, 96) FF_SWIGLU(80, 96)
+  FF_SWIGLU(144, 64) FF_SWIGLU(128, 64) FF_SWIGLU(112, 64) FF_SWIGLU(96, 64) FF_SWIGLU(80, 64)
 #undef FF_SWIGLU
   FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu_static");
   return FF_OK;
@@ -804,18 +844,14 @@ int gemm_fp8_pk_partials(const void* qa, const float* sa, int sa_rows, const voi
   const int64_t need = split_workspace(m, n, k);
   FF_REQUIRE(workspace && workspace_bytes >= need && ff_aligned(workspace, 16),
              "ff_gemm_fp8_pk: workspace of %lld bytes (16-byte aligned) required", (long long)need);
-  const int64_t tiles_m = (m + kSpBM - 1) / kSpBM, tiles_n = n / kSpBN;
-#define FF_SPLIT(S)                                                                                                 \
-  if (s == S)                                                                                                       \
-    hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<kSpBM, kSpCW, kSpP, kSpD, kSpG, S>),                           \
-                       dim3((unsigned)(tiles_m * tiles_n * S)), dim3(kThreads), 0, st, (const uint8_t*)qa, sa,      \
-                       sa_rows, (const uint8_t*)qw_packed, sw, sw_cols, (bf16_t*)nullptr, (int64_t)0, (int)m,       \
-                       (int)n, (int)k, (int)tiles_m, (int)tiles_n, (float*)workspace);
-  FF_SPLIT(2) FF_SPLIT(3) FF_SPLIT(4) FF_SPLIT(8)
-#undef FF_SPLIT
+  const int bm = split_bm();
+  if (bm == 80)
+    launch_splits<80>(s, qa, sa, sa_rows, qw_packed, sw, sw_cols, nullptr, 0, m, n, k, workspace, st);
+  else
+    launch_splits<kSpBM>(s, qa, sa, sa_rows, qw_packed, sw, sw_cols, nullptr, 0, m, n, k, workspace, st);
   FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
   *splits = s;
-  *mp = tiles_m * kSpBM;
+  *mp = (m + bm - 1) / bm * bm;
   return FF_OK;
 }
 }  // namespace ff
@@ -841,12 +877,11 @@ extern "C" int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, cons
     FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
     return FF_OK;
   }
-  const int64_t tiles_m = (m + kSpBM - 1) / kSpBM, tiles_n = n / kSpBN;
   if (s == 1) {
-    hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<kSpBM, kSpCW, kSpP, kSpD, kSpG, 1>),
-                       dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows,
-                       (const uint8_t*)qw_packed, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)n, (int)k, (int)tiles_m,
-                       (int)tiles_n, (float*)nullptr);
+    if (split_bm() == 80)
+      launch_splits<80>(1, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, nullptr, st);
+    else
+      launch_splits<kSpBM>(1, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, nullptr, st);
     FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
     return FF_OK;
   }

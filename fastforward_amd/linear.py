@@ -81,6 +81,7 @@ class FP8Linear:
         call("ff_quant_weight_fp8", ptr(w), ptr(self.weight), ptr(scale), None, n, k, 1, stream())
         self.scale = scale.reshape(1, n)
         self.packed = None
+        self.pack()   # the packed tile kernels are the GEMM path of every caller
 
     def pack(self):
         """Add the MFMA-fragment copy of the weight (ff_pack_weight_fp8) that the

@@ -59,6 +59,7 @@ class LMConfig:
 
 PRESETS = {
     "qwen3vl-2b": LMConfig("qwen3vl-2b", 28, 2048, 16, 8, 128, 6144, 151936, tie_embed=True),
+    "qwen3vl-4b": LMConfig("qwen3vl-4b", 36, 2560, 32, 8, 128, 9728, 151936, tie_embed=True),
     "qwen3vl-8b": LMConfig("qwen3vl-8b", 36, 4096, 32, 8, 128, 12288, 151936),
     "qwen3vl-32b": LMConfig("qwen3vl-32b", 64, 5120, 64, 8, 128, 25600, 151936),
 }

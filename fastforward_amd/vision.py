@@ -59,6 +59,7 @@ class VisionConfig:
 
 VISION_PRESETS = {
     "qwen3vl-2b": VisionConfig("qwen3vl-2b", 24, 1024, 16, 4096, 2048, (5, 11, 17)),
+    "qwen3vl-4b": VisionConfig("qwen3vl-4b", 24, 1024, 16, 4096, 2560, (5, 11, 17)),
     "qwen3vl-8b": VisionConfig("qwen3vl-8b", 27, 1152, 16, 4304, 4096, (8, 16, 24)),
     "qwen3vl-32b": VisionConfig("qwen3vl-32b", 27, 1152, 16, 4304, 5120, (8, 16, 24)),
 }

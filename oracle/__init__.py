@@ -29,6 +29,10 @@ PINNING = {
     "quant_static": "numpy multiply + exhaustive e4m3 (test_fp8_static_*)",
     "fp8_weight_quant": "numpy per-channel / per-tensor amax (test_fp8_weight_*)",
     "fp8_linear": "fp64 numpy GEMM of decoded codes x scales (test_fp8_linear_matches_fp64)",
+    "fp8_gemm_exact": "pure-Python integer sums of the decoded codes (test_fp8_gemm_exact_and_blocks_brute_force)",
+    "fp8_gemm_blocks / round_sig_": "pure-Python brute force of the block model on small GEMMs (exact block sums as "
+                                    "Fractions, math.frexp rounding, float32 accumulation); rounding of ties, "
+                                    "signs and binade carries against math.frexp (test_round_sig_*)",
     "int4_quantize": "pure-Python loops on tiny matrices: nibble order, [K/g,N,2] indexing (test_int4_*)",
     "w4a16_linear": "fp64 numpy dequant GEMM (test_w4a16_linear_matches_fp64)",
     "mrope_positions": "transformers Qwen3-VL get_rope_index (test_mrope_positions_match_hf)",

@@ -277,6 +277,55 @@ def fp8_gemm(qa, sa, qw, sw):
     return (acc * sa.reshape(-1, 1) * sw.reshape(1, -1)).to(BF16)
 
 
+def fp8_gemm_exact(qa, sa, qw, sw):
+    """``fp8_gemm`` with exact accumulation: the sum of e4m3 products is formed
+    in fp64, where every such sum of up to 2^22 terms is exact, then scaled and
+    rounded like ``fp8_gemm``. The formulation's value without any summation
+    error (a sensitivity check, not a reference kernel)."""
+    acc = qa.double() @ qw.double().T
+    return (acc * sa.double().reshape(-1, 1) * sw.double().reshape(1, -1)).to(BF16)
+
+
+def round_sig_(x, bits):
+    """Round the fp64 tensor x in place to ``bits`` significant bits, nearest
+    even (normal values and zero; the fp64 bit pattern's low 53 - bits bits are
+    rounded away)."""
+    u = x.view(torch.int64)
+    drop = 53 - bits
+    u.add_(((u >> drop) & 1) + ((1 << (drop - 1)) - 1))
+    u.bitwise_and_(~((1 << drop) - 1))
+    return x
+
+
+def fp8_gemm_blocks(qa, sa, qw, sw, bits=14, block=32, chunk=2048):
+    """``fp8_gemm`` on a model of a matrix unit with reduced-precision block sums:
+    k is cut into blocks of ``block`` products, each block's sum (exact) is rounded
+    to ``bits`` significant bits, and the blocks are added into an fp32
+    accumulator in k order; then the scaling and bf16 rounding of ``fp8_gemm``.
+
+    Not a restatement of the reference: its ``_scaled_mm`` runs on FP8 tensor
+    cores whose block accumulation is of this class (about 14 significant bits
+    retained per block), and so does gfx950's v_mfma_f32_16x16x128_f8f6f4. The
+    oracle with this GEMM in place of the fp32 one measures how far a
+    correctly computed step moves when only the GEMMs' accumulation has the
+    precision of such a unit."""
+    m, k = qa.shape
+    n = qw.shape[0]
+    assert k % block == 0 and 2 <= bits <= 52
+    a = qa.double().reshape(m, k // block, block).permute(1, 0, 2).contiguous()
+    wd = qw.double()
+    out = torch.empty(m, n, dtype=BF16)
+    sa_, sw_ = sa.to(F32).reshape(-1, 1), sw.to(F32).reshape(1, -1).expand(1, n)
+    for c0 in range(0, n, chunk):
+        w = wd[c0:c0 + chunk].reshape(-1, k // block, block).permute(1, 2, 0).contiguous()
+        blk = round_sig_(torch.bmm(a, w), bits).to(F32)      # exact block sums -> bits -> fp32 (exact)
+        acc = blk[0].clone()
+        for b in range(1, blk.shape[0]):
+            acc.add_(blk[b])
+        out[:, c0:c0 + chunk] = ((acc * sa_) * sw_[:, c0:c0 + chunk]).to(BF16)
+    return out
+
+
 def fp8_linear_dynamic(x, qw, sw):
     """``FP8Linear.__call__`` (_legacy/fp8_private.py:29-38)."""
     qa, sa = quant_rows_dynamic(x)

@@ -80,7 +80,10 @@ def _check_vs_oracle(z, want, what, tol):
     assert O.choose(z.tolist()) == O.choose(want.tolist()), what
 
 
+# Layers without a derived bar: about 1.2x the largest sensitivity measured (FP8: the block
+# model moves layer 0 of the 2B / 8B shapes by 4.6-5.0 %; W4A16: exact accumulation 0.4 %).
 LAYER_BOUND = {"fp8": 0.06, "fp8_static": 0.06, "w4a16": 0.02, "int4_half": 0.06, "int4_ffn": 0.06}
+DERIVED_MULTIPLE = 1.5
 
 
 def _rel(a, b):
@@ -99,11 +102,8 @@ def _oracle_layer(shape, ow, j, h, cos, sin, deep=None, start=0, nv=0):
     return hn
 
 
-def _exact_gemm(qa, sa, qw, sw):
-    """The FP8 GEMM with exact (fp64) accumulation: sums of e4m3 products span
-    < 53 bits, so this is the exact value of the formulation's sum."""
-    acc = qa.double() @ qw.double().T
-    return (acc * sa.double().reshape(-1, 1) * sw.double().reshape(1, -1)).to(torch.bfloat16)
+_exact_gemm = O.fp8_gemm_exact
+BLOCK_BITS = 14     # the block model's kept bits (see _swapped)
 
 
 def _exact_w4a16(x, packed, scales, group, weight_bf16=False):
@@ -117,10 +117,65 @@ def _exact_w4a16(x, packed, scales, group, weight_bf16=False):
     return (flat @ w.double().T).to(torch.bfloat16).reshape(*x.shape[:-1], w.shape[0])
 
 
-def _check_teacher_forced(cfg, w, mode, ids, pos, pick, layers, what, copy_all=True, tail_tol=TAIL_TOL):
+class _swapped:
+    """Swap one oracle function for another inside a ``with`` block."""
+
+    def __init__(self, module, name, fn):
+        self.module, self.name, self.fn = module, name, fn
+
+    def __enter__(self):
+        self.orig = getattr(self.module, self.name)
+        setattr(self.module, self.name, self.fn)
+
+    def __exit__(self, *exc):
+        setattr(self.module, self.name, self.orig)
+
+
+def _accumulation_variants(mode):
+    """(name, module, function, fn) of the oracle's accumulation variants: its
+    GEMM with exact accumulation, and for the FP8 modes its GEMM on the
+    reduced-precision block model (32-product block sums kept to BLOCK_BITS
+    significant bits: the class of the FP8 matrix units, whose rate of outputs
+    differing from the fp32 GEMM, 2.0 % at 14 bits against 1.4-1.9 % measured
+    on gfx950, it matches)."""
+    if mode == "w4a16":
+        return [("exact", O, "w4a16_linear", _exact_w4a16)]
+    blocks = lambda qa, sa, qw, sw: O.fp8_gemm_blocks(qa, sa, qw, sw, bits=BLOCK_BITS)  # noqa: E731
+    return [("exact", O, "fp8_gemm", _exact_gemm), ("blocks", O, "fp8_gemm", blocks)]
+
+
+def _gpu_linears(w, ow, layers):
+    """omodel.linear replaced by the product's own linear op of the same weights
+    (FP8: per-token quantisation + GEMM, bit-equal to the step's fused launches;
+    W4A16: the packed GEMM), so that the oracle composes the rest of the layer
+    around the GPU's GEMM products."""
+    by_spec = {}
+    for j in layers:
+        for role in ("qkv", "o", "gateup", "down"):
+            by_spec[id(getattr(ow.layers[j], role))] = getattr(w.layers[j], role)
+    orig = omodel.linear
+
+    def linear(x, spec):
+        op = by_spec.get(id(spec))
+        if op is None:
+            return orig(x, spec)
+        y = op(x.to(DEV).contiguous())
+        return y.cpu().reshape(*x.shape[:-1], y.shape[-1])
+    return linear
+
+
+def _check_teacher_forced(cfg, w, mode, ids, pos, pick, layers, what, copy_all=True, tail_tol=TAIL_TOL,
+                          derive=()):
     """Run the GPU step with a residual trace, then check the chosen layers and the
     tail against the oracle fed with the GPU's own layer inputs. W4A16 linears
-    use the oracle's bf16-operand form."""
+    use the oracle's bf16-operand form.
+
+    For the layers in ``derive`` the layer's gap is also set beside the oracle's
+    own sensitivity to its GEMMs' accumulation (the same layer with exact
+    accumulation, and for FP8 on the block model) and split into its GEMM part
+    (the oracle composing the layer around the GPU's own GEMM products) and the
+    rest (the GPU layer against that); returns {layer: {gap, exact, blocks,
+    gemm, rest}}."""
     from fastforward_amd.runtime import Runtime
     rt = Runtime(cfg, w, pos.shape[1])
     rt.set_inputs(ids, pos, pick)
@@ -134,12 +189,34 @@ def _check_teacher_forced(cfg, w, mode, ids, pos, pick, layers, what, copy_all=T
     full = torch.zeros(pos.shape[1], dtype=torch.int64)
     full[: ids.numel()] = ids
     hin = [ow.embed[full][None]] + [t[None] for t in trace]
+    derived = {}
     for j in layers:
-        got = _rel(trace[j], _oracle_layer(shape, ow, j, hin[j], cos, sin)[0])
-        print(f"{what} layer {j}: teacher-forced rel L2 {got:.4f}", flush=True)
+        ref = _oracle_layer(shape, ow, j, hin[j], cos, sin)[0]
+        got = _rel(trace[j], ref)
+        line = f"{what} layer {j}: teacher-forced rel L2 {got:.4f}"
+        if j in derive:
+            d = derived[j] = dict(gap=got)
+            for name, module, fn_name, fn in _accumulation_variants(mode):
+                with _swapped(module, fn_name, fn):
+                    d[name] = _rel(_oracle_layer(shape, ow, j, hin[j], cos, sin)[0], ref)
+            with _swapped(omodel, "linear", _gpu_linears(w, ow, [j])):
+                forced = _oracle_layer(shape, ow, j, hin[j], cos, sin)[0]
+            d["gemm"], d["rest"] = _rel(forced, ref), _rel(trace[j], forced)
+            line += "; " + ", ".join(f"{k} {v:.4f}" for k, v in d.items() if k != "gap")
+        print(line, flush=True)
         assert got <= LAYER_BOUND[mode], (what, j, got)
+        if j in derive:
+            # the derived bars: the layer's gap against the oracle's own sensitivity to its GEMMs'
+            # accumulation precision (FP8: the block model of the FP8 matrix units; W4A16, whose
+            # bf16 MFMA keeps fp32 sums: exact accumulation), and the GPU's non-GEMM ops, given the
+            # GPU's own GEMM products, no further from the oracle than that sensitivity
+            sens = d["blocks"] if "blocks" in d else d["exact"]
+            assert got <= DERIVED_MULTIPLE * sens, (what, j, d)
+            assert d["rest"] <= DERIVED_MULTIPLE * sens, (what, j, d)
     zt = omodel.tail(shape, ow.layers[-1], ow, hin[-1], cos, sin, pick)
     _check_vs_oracle(z, zt, f"{what} teacher-forced tail", tail_tol)
+    if derive:
+        return z, shape, ow, derived
     return z, shape, ow
 
 
@@ -317,7 +394,9 @@ def test_full_model_vs_oracle(gpu, preset, tokens, grid, choices, mode):
             torch.cuda.synchronize()
             assert torch.equal(z_graph, z_eager)
         del rt
-        z, shape, ow = _check_teacher_forced(cfg, w, mode, ids, pos, pick, layers, what)
+        derive = (0, 1, 2, cfg.layers // 2, cfg.layers - 2) if n == 0 else ()
+        out = _check_teacher_forced(cfg, w, mode, ids, pos, pick, layers, what, derive=derive)
+        z, shape, ow = out[:3]
         assert torch.equal(z, z_eager.cpu())
         del w
         torch.cuda.empty_cache()
@@ -344,6 +423,32 @@ def test_full_model_vs_oracle(gpu, preset, tokens, grid, choices, mode):
     sys.stdout.flush()
 
 
+@pytest.mark.timeout(900)
+def test_4b_shape_teacher_forced(gpu):
+    """The 4B shape (36 layers, hidden 2560, 32/8 heads of 128 with HQ*D = 4096 !=
+    H, MLP 9728 on the 128-channel gate/up tiles, tied embeddings; 576 tokens
+    on a 16 x 32 image grid, 8 choices, FP8): graph replay equals the eager step,
+    the fused step equals the reference op sequence, and every layer and the
+    tail are teacher-forced against the oracle."""
+    from fastforward_amd.runtime import PRESETS, Runtime
+    from fastforward_amd.synthetic import make_model, make_request
+    cfg = PRESETS["qwen3vl-4b"]
+    w = make_model(cfg, mode="fp8", seed=12, n_options=8)
+    ids, pos, pick = make_request(cfg, 576, 16, 32, seed=12)
+    rt = Runtime(cfg, w, 576)
+    rt.set_inputs(ids, pos, pick)
+    z_eager = rt.step().clone()
+    rt.capture()
+    z_graph = rt.replay().clone()
+    torch.cuda.synchronize()
+    assert torch.equal(z_graph, z_eager)
+    del rt
+    _, z_generic = _run(cfg, w, 576, ids, pos, pick, path="generic")
+    assert torch.equal(z_generic, z_eager.cpu())
+    z, _, _ = _check_teacher_forced(cfg, w, "fp8", ids, pos, pick, range(cfg.layers - 1), "qwen3vl-4b fp8")
+    assert torch.equal(z, z_eager.cpu())
+
+
 @pytest.mark.timeout(1200)
 def test_32b_shape_on_one_gpu(gpu):
     """The 32B shape (64 layers, hidden 5120, 64/8 heads with HQ*D = 8192 != H,
@@ -367,3 +472,64 @@ def test_32b_shape_on_one_gpu(gpu):
     torch.cuda.empty_cache()
     z, _, _ = _check_teacher_forced(cfg, w, "fp8", ids, pos, pick, range(cfg.layers - 1), "qwen3vl-32b fp8")
     assert torch.equal(z, z_eager.cpu())
+
+
+DEPTHS = (0, 1, 2, 4, 8)
+DEPTH_SEEDS = (7, 8)
+
+
+@pytest.mark.timeout(1500)
+def test_end_to_end_by_depth(gpu):
+    """The north-star bar end to end, not teacher-forced: at the 8B layer widths
+    (hidden 4096, 32/8 heads, MLP 12288; 576 tokens on a 16 x 32 image grid, 8
+    choices) with 0 (the pick-only final layer and the readout alone), 1, 2, 4
+    and 8 full decoder layers before the pick-only tail, the GPU's choice logits
+    against the oracle's, beside the oracle's own gaps when only its GEMM
+    accumulation changes (exact; the block model of the FP8 matrix units).
+    Where both of the oracle's own gaps stay below 1e-2 (the depths at which the
+    formulation itself reproduces to that bar), the GPU must hold max_c |dz_c|
+    <= 1e-2 max_c |z_c| with the identical argmax for every seed; the depth at
+    which each gap first exceeds 1e-2 is printed (on these random-init weights
+    the oracle's own gaps exceed it from depth 0: one layer over the embedding
+    rows already moves the logits by up to 6 % under exact accumulation).
+    Pooled over depths and seeds, the GPU's gap is held to 2x the block model's:
+    the GPU perturbs the GEMMs like the block model and, in addition, every
+    non-GEMM reduction (per layer up to two thirds of the GEMM part)."""
+    from fastforward_amd.synthetic import make_model, make_request
+    rows, pooled = [], [[], []]
+    for depth in DEPTHS:
+        cfg = _wide(depth + 1)
+        gap, ex, bl, same = [], [], [], []
+        for seed in DEPTH_SEEDS:
+            w = make_model(cfg, mode="fp8", seed=seed, n_options=8)
+            ids, pos, pick = make_request(cfg, 576, 16, 32, seed=seed)
+            _, z = _run(cfg, w, 576, ids, pos, pick)
+            shape, ow = to_oracle(cfg, w)
+            del w
+            ze = omodel.step(shape, ow, ids, pos, pick)
+            with _swapped(O, "fp8_gemm", _exact_gemm):
+                zx = omodel.step(shape, ow, ids, pos, pick)
+            with _swapped(O, "fp8_gemm", lambda qa, sa, qw, sw: O.fp8_gemm_blocks(qa, sa, qw, sw, bits=BLOCK_BITS)):
+                zb = omodel.step(shape, ow, ids, pos, pick)
+            gap.append(rel_err(z, ze))
+            ex.append(rel_err(zx, ze))
+            bl.append(rel_err(zb, ze))
+            same.append(O.choose(z.tolist()) == O.choose(ze.tolist()))
+            pooled[0].append(gap[-1])
+            pooled[1].append(bl[-1])
+            print(f"depth {depth} seed {seed}: gpu-vs-oracle {gap[-1]:.4f}, oracle exact-acc {ex[-1]:.4f}, "
+                  f"oracle block model {bl[-1]:.4f}, argmax gpu {'same' if same[-1] else 'DIFFERS'}, "
+                  f"block model {'same' if O.choose(zb.tolist()) == O.choose(ze.tolist()) else 'DIFFERS'}",
+                  flush=True)
+        rows.append((depth, max(gap), max(ex), max(bl), all(same)))
+        torch.cuda.empty_cache()
+    for name, col in (("gpu-vs-oracle", 1), ("oracle exact-acc", 2), ("oracle block model", 3)):
+        over = [r[0] for r in rows if r[col] > 1e-2]
+        print(f"{name}: first depth above 1e-2: {over[0] if over else 'none up to ' + str(DEPTHS[-1])}", flush=True)
+    for depth, g, x, b, same in rows:
+        if max(x, b) < 1e-2:
+            assert g <= 1e-2 and same, (depth, g, x, b, same)
+    mg, mb = sum(pooled[0]) / len(pooled[0]), sum(pooled[1]) / len(pooled[1])
+    print(f"pooled over depths {DEPTHS} and seeds {DEPTH_SEEDS}: gpu-vs-oracle {mg:.4f}, block model {mb:.4f} "
+          f"(ratio {mg / mb:.2f})", flush=True)
+    assert mg <= 2.0 * mb, (mg, mb)

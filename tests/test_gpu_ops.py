@@ -334,16 +334,19 @@ def test_pack_weight_fp8_layout(gpu):
 
 
 # 12288 channels (64 column tiles) take row tiles of 144 (576 tokens), 80 (176),
-# 112 (400), 96 (700) and 128 (1000)
+# 112 (400), 96 (700) and 128 (1000); MLP widths that 192 does not divide take
+# 128-channel tiles (4096; the 32B shape's 25600 at 1024 tokens; the 4B shape's
+# 9728)
 @pytest.mark.parametrize("m,i,k", [(576, 12288, 4096), (300, 12288, 2048), (433, 6144, 4096), (3, 12288, 4096),
                                    (576, 4096, 4096), (176, 12288, 4096), (400, 12288, 4096), (700, 12288, 4096),
-                                   (1000, 12288, 4096)])
+                                   (1000, 12288, 4096), (1024, 25600, 5120), (576, 9728, 2560), (300, 4160, 2048)])
 def test_gemm_fp8_swiglu_packed_equals_rowmajor(gpu, m, i, k):
-    """The gate/up GEMM on the packed weight copy (BM x 384 tiles, BM = 80..144 by grid, weights
-    straight into the MFMA operands) gives the same bits as ff_gemm_fp8_swiglu on
-    the row-major weight, SwiGLU output and row maxima, including a ragged last
-    token tile; shapes it does not take (3 rows, i % 192 != 0, too few tiles)
-    go to the row-major kernels."""
+    """The gate/up GEMM on the packed weight copy (BM x 384 tiles, or BM x 256 where
+    192 does not divide the MLP width, BM = 80..144 by grid, weights straight into
+    the MFMA operands) gives the same bits as ff_gemm_fp8_swiglu on the row-major
+    weight, SwiGLU output and row maxima, including a ragged last token tile;
+    shapes it does not take (3 rows, i % 128 != 0, too few tiles) go to the
+    row-major kernels."""
     from fastforward_amd._lib import call, ptr, stream
     from fastforward_amd.linear import FP8Linear
     x = (torch.randn(m, k, generator=_g(51)) * 2).to(BF16).to(DEV)

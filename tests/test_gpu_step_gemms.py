@@ -44,7 +44,8 @@ BF16 = torch.bfloat16
 DEV = "cuda"
 
 # preset -> (tokens, hidden, q heads, kv heads, mlp)
-SHAPES = {"2b": (320, 2048, 16, 8, 6144), "8b": (576, 4096, 32, 8, 12288), "32b": (1024, 5120, 64, 8, 25600)}
+SHAPES = {"2b": (320, 2048, 16, 8, 6144), "4b": (576, 2560, 32, 8, 9728), "8b": (576, 4096, 32, 8, 12288),
+          "32b": (1024, 5120, 64, 8, 25600)}
 D = 128
 
 
@@ -172,7 +173,7 @@ def test_step_qkv_epilogue_vs_oracle(gpu, preset):
     qn = (1 + 0.3 * torch.randn(D, generator=_g(360))).to(BF16)
     kn = (1 + 0.3 * torch.randn(D, generator=_g(361))).to(BF16)
     qn_d, kn_d = RMSNorm(qn.to(DEV)), RMSNorm(kn.to(DEV))
-    grid = {"2b": (16, 16), "8b": (16, 32), "32b": (30, 32)}[preset]
+    grid = {"2b": (16, 16), "4b": (16, 32), "8b": (16, 32), "32b": (30, 32)}[preset]
     cos, sin = O.mrope_cos_sin(O.mrope_positions(4, *grid, t), 5e6, D)
     cos_d, sin_d = cos[0].to(DEV), sin[0].to(DEV)
     yq = torch.full((hq, t, D), float("nan"), device=DEV, dtype=BF16)

@@ -345,6 +345,62 @@ def test_fp8_linear_matches_fp64():
     assert np.abs(y - ref).max() < 0.05 * np.abs(ref).max()
 
 
+def _rne_sig(v, bits):
+    """v (a Python float) rounded to ``bits`` significant bits, nearest even, by
+    math.frexp and Python's round (ties to even on an exact double)."""
+    if v == 0.0:
+        return v
+    m, e = math.frexp(v)
+    return math.ldexp(round(m * 2.0 ** bits), e - bits)
+
+
+@pytest.mark.parametrize("bits", [8, 13, 14, 24])
+def test_round_sig_matches_frexp_rounding(bits):
+    g = _gen(40)
+    x = torch.randn(2000, generator=g, dtype=torch.float64) * torch.exp2(torch.randint(-60, 60, (2000,),
+                                                                                    generator=g).double())
+    # exact ties (half an ulp of the kept width, both parities) and carries into the next binade
+    base = torch.tensor([1.0, 1.5, -1.25, 3.0, -0.75], dtype=torch.float64)
+    ulp = torch.exp2(torch.floor(torch.log2(base.abs())) - (bits - 1))
+    ties = torch.cat([base + ulp / 2, base + 3 * ulp / 2, -(base.abs() + ulp / 2),
+                      torch.tensor([2.0 - 2.0 ** -(bits + 1), -(2.0 - 2.0 ** -(bits + 1)), 0.0])])
+    for v in (x, ties):
+        got = ops.round_sig_(v.clone(), bits).tolist()
+        want = [_rne_sig(a, bits) for a in v.tolist()]
+        assert got == want
+
+
+def test_fp8_gemm_exact_and_blocks_brute_force():
+    """The exact-accumulation GEMM and the reduced-precision block model against
+    pure-Python sums of the decoded codes (Fractions): the exact block sums,
+    their rounding to the kept bits, fp32 accumulation in k order (numpy
+    float32), then the scaling and bf16 rounding."""
+    from fractions import Fraction
+    g = _gen(41)
+    m, k, n, block = 3, 128, 5, 32
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16)
+    qa, sa = ops.quant_rows_dynamic(x)
+    qw, sw = ops.fp8_weight_quant(w)
+    a = e4m3_decode_np(qa.view(torch.uint8).numpy())
+    b = e4m3_decode_np(qw.view(torch.uint8).numpy())
+    exact = ops.fp8_gemm_exact(qa, sa, qw, sw).float().numpy()
+    for bits in (10, 14):
+        blocks = ops.fp8_gemm_blocks(qa, sa, qw, sw, bits=bits, block=block, chunk=2).float().numpy()
+        for i in range(m):
+            for j in range(n):
+                prods = [Fraction(float(a[i, t])) * Fraction(float(b[j, t])) for t in range(k)]
+                tot = float(sum(prods, Fraction(0)))                   # exact in fp64
+                want_exact = bf16_round_np(np.float32(tot * float(sa[i]) * float(sw[j])))
+                assert exact[i, j] == want_exact
+                acc = np.float32(0.0)
+                for c in range(k // block):
+                    part = float(sum(prods[c * block:(c + 1) * block], Fraction(0)))
+                    acc = np.float32(acc + np.float32(_rne_sig(part, bits)))
+                want = bf16_round_np(np.float32(np.float32(acc * np.float32(sa[i])) * np.float32(sw[j])))
+                assert blocks[i, j] == want, (bits, i, j)
+
+
 # ------------------------------------------------------------------ int4
 
 def test_int4_asym_pack_and_scale_indexing_by_loops():
