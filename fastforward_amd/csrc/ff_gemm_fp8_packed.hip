@@ -491,7 +491,20 @@ constexpr int kPkKAlign = 128 * lcm3(kPkP, kPkD, 2 * kPkG);  // k multiple of th
 // tiles) where i allows it, else 64 (128-channel tiles: the 32B shape's 25600
 // and the 4B shape's 9728 channels); 0 when neither divides i (the row-major
 // kernel runs then).
-int swiglu_cw(int64_t i) { return i % 192 == 0 ? 96 : (i % 128 == 0 ? 64 : 0); }
+// Row tiles of the 64-channel tile (CW = 32) for short m: one row tile of the
+// smallest height that holds m.
+constexpr int kSwNarrowBM[5] = {64, 80, 112, 144, 176};
+
+int swiglu_cw(int64_t m, int64_t i) {
+  const int forced = ff_tuning(FF_TUNE_SWIGLU_PK_TILE) % 1000;
+  if (forced == 32 || forced == 64 || forced == 96) return i % (2 * forced) == 0 ? forced : 0;
+  // Short m with at least 192 channel tiles of 64: one row tile of 64
+  // channels x up to 176 tokens per workgroup, so each weight is read by one
+  // workgroup (176 tokens, 8B: 192 workgroups; the 4.47 ms step takes 4.18
+  // ms, against 80 x 384 tiles).
+  if (m > 4 && m <= kSwNarrowBM[4] && i % 64 == 0 && i / 64 >= 192) return 32;
+  return i % 192 == 0 ? 96 : (i % 128 == 0 ? 64 : 0);
+}
 
 // Row-tile height of the packed gate/up GEMM for m tokens and tiles_n column
 // tiles: the candidate whose grid takes the fewest row steps per CU, counted as
@@ -501,7 +514,15 @@ int swiglu_cw(int64_t i) { return i % 192 == 0 ? 96 : (i % 128 == 0 ? 64 : 0); }
 // kernel runs then). 8B gate/up (64 column tiles): 576 tokens 144 x 384 tiles
 // in one round; 640 tokens 80 (two rounds of 80 against two of 144); 176 and
 // 320 tokens 80; 2048 tokens 128.
-int swiglu_bm(int64_t m, int64_t tiles_n) {
+int swiglu_bm(int64_t m, int64_t tiles_n, int cw) {
+  // ff_set_tuning(FF_TUNE_SWIGLU_PK_TILE, 1000 bm + cw) forces the tile for measurement sweeps
+  const int forced = ff_tuning(FF_TUNE_SWIGLU_PK_TILE) / 1000;
+  if (forced) return forced;
+  if (cw == 32) {
+    for (const int bm : kSwNarrowBM)
+      if (bm >= m) return bm;
+    return 0;
+  }
   constexpr int cand[5] = {144, 128, 112, 96, 80};
   int best = 0;
   int64_t best_cost = 0;
@@ -523,38 +544,64 @@ constexpr int kSpBM = 144, kSpCW = 64, kSpP = 2, kSpD = 2, kSpG = 2;
 constexpr int kSpBN = 4 * kSpCW;
 constexpr int kSpU = lcm3(kSpP, kSpD, 2 * kSpG);
 
-// Splits for an m x n x k plain GEMM on the packed path, 0 if it does not take
-// it: one launch when the tiles fill the GPU, else 4 splits when k is long
-// enough that the extra reduction launch pays off (the 8B down projection,
-// 576 x 4096 x 12288); shorter k takes small_plan's tiles (below) or the
-// row-major kernels.
-// Row-tile height of the plain packed GEMM: 144, or 80 when FF_TUNE_FP8_SPLIT_BM
-// asks for it (80-row tiles at two workgroups per CU take half the k splits of
-// the 144-row ones on the same grid).
-int split_bm() { return ff_tuning(FF_TUNE_FP8_SPLIT_BM) == 80 ? 80 : kSpBM; }
-
-int split_plan(int64_t m, int64_t n, int64_t k) {
-  if (m <= 4 || n % kSpBN || k % 128 || m * k >= (int64_t(1) << 31) || n * k >= (int64_t(1) << 31)) return 0;
-  const int bm = split_bm();
-  const int64_t tiles = (m + bm - 1) / bm * (n / kSpBN), kt = k / 128;
-  if (tiles >= 192) return kt % kSpU == 0 ? 1 : 0;
-  if (kt < 64) return 0;
+// The plain packed GEMM's plan for an m x n x k product: row tile bm (x 256
+// weight rows) and k splits s (1: unsplit, 0: the kernel does not take it).
+// One launch when 144-row tiles fill the GPU, else 144-row tiles with k split
+// when k is long enough that the extra reduction pays off (the 8B down
+// projection, 576 x 4096 x 12288); shorter k takes small_plan's tiles (below)
+// or the row-major kernels. ff_set_tuning(FF_TUNE_FP8_PK_SPLIT, 100 bm + s)
+// forces bm in {64, 144} and s in {1, 2, 3, 4, 8} for measurement sweeps.
+// (80-row tiles at two workgroups per CU with half the k splits, fewer fp32
+// partials on the same grid, measured slower: the 8B FP8 step 6.35 -> 6.85 ms
+// with the down projection on 80 x 256 tiles split 2 ways instead of 144 x 256
+// split 4 ways.)
+struct SplitPlan {
+  int bm = 0, s = 0;
+};
+SplitPlan split_plan(int64_t m, int64_t n, int64_t k) {
+  SplitPlan p;
+  if (m <= 4 || n % kSpBN || k % 128 || m * k >= (int64_t(1) << 31) || n * k >= (int64_t(1) << 31)) return p;
+  const int64_t kt = k / 128;
+  const int forced = ff_tuning(FF_TUNE_FP8_PK_SPLIT);
+  if (forced) {
+    const int bm = forced / 100, sp = forced % 100;
+    if ((bm == 64 || bm == kSpBM) && (sp == 1 || sp == 2 || sp == 3 || sp == 4 || sp == 8) && kt % (sp * kSpU) == 0) {
+      p.bm = bm;
+      p.s = sp;
+    }
+    return p;
+  }
+  const int64_t tiles = (m + kSpBM - 1) / kSpBM * (n / kSpBN);
+  if (tiles >= 192) {
+    if (kt % kSpU == 0) p = SplitPlan{kSpBM, 1};
+    return p;
+  }
+  if (m <= 256) {
+    // Short m (up to four 64-row tiles): 64 x 256 tiles at two workgroups per
+    // CU, k split 8, 4 or 2 ways, the most that keeps the grid within 256
+    // workgroups: 176 tokens of the 8B shape, o and down 48 tiles x 4 splits
+    // (the 4.47 ms step takes 4.31 ms with both on it, against small_plan's
+    // 64 x 128 tiles for o and 144 x 256 tiles split 8 ways for down).
+    const int64_t t64 = (m + 63) / 64 * (n / kSpBN);
+    for (int sp = 8; sp >= 2; sp /= 2)
+      if (t64 * sp <= 256 && kt % (sp * kSpU) == 0) return SplitPlan{64, sp};
+  }
+  if (kt < 64) return p;
   // The split count (2, 3, 4 or 8) with the fewest k steps per CU: rounds of
   // 256 workgroups (one per CU) x kt / S steps each, ties to fewer splits
   // (less partial traffic). 8B down (k = 12288): 176 tokens 8 splits, 576
   // tokens 4 in one round, 640 tokens 3 in one round (4 would take two),
   // 1152 tokens 2.
-  int best = 0;
   int64_t best_steps = 0;
   for (int sp = 2; sp <= 8; sp += sp < 4 ? 1 : 4) {
     if (kt % (sp * kSpU)) continue;
     const int64_t steps = (tiles * sp + 255) / 256 * (kt / sp);
-    if (best == 0 || steps < best_steps) {
-      best = sp;
+    if (p.s == 0 || steps < best_steps) {
+      p = SplitPlan{kSpBM, sp};
       best_steps = steps;
     }
   }
-  return best;
+  return p;
 }
 
 // Unsplit plain GEMMs whose 144 x 256 tiles are too few and whose k is too
@@ -607,9 +654,9 @@ void launch_small(const void* qa, const float* sa, int sa_rows, const void* qw_p
 }
 
 int64_t split_workspace(int64_t m, int64_t n, int64_t k) {
-  const int s = split_plan(m, n, k), bm = split_bm();
-  if (s <= 1) return 0;
-  return (m + bm - 1) / bm * (n / kSpBN) * s * bm * kSpBN * 4;
+  const SplitPlan p = split_plan(m, n, k);
+  if (p.s <= 1) return 0;
+  return (m + p.bm - 1) / p.bm * (n / kSpBN) * p.s * p.bm * kSpBN * 4;
 }
 
 // The plain packed kernel at row tile BM with S k splits (S == 1: y directly).
@@ -777,23 +824,26 @@ extern "C" int ff_gemm_fp8_swiglu_pk(const void* qa, const float* sa, const void
                                      const float* sw, void* h, int64_t ldh, float* pmax, int64_t m, int64_t i,
                                      int64_t k, ff_stream_t stream) {
   FF_REQUIRE(qa && sa && qw && sw && h && pmax, "ff_gemm_fp8_swiglu_pk: null pointer");
-  const int cw = swiglu_cw(i);
+  const int cw = swiglu_cw(m, i);
   const int64_t tiles_n = cw ? i / (2 * cw) : 0;
-  const int bm = cw ? swiglu_bm(m, tiles_n) : 0;
+  const int bm = cw ? swiglu_bm(m, tiles_n, cw) : 0;
   const bool packed_fits = qw_packed && bm && m > 4 && k % kPkKAlign == 0 && ldh % 8 == 0 && ldh >= i &&
                            m * k < (int64_t(1) << 31) && 2 * i * k < (int64_t(1) << 31) && ff_aligned(qa, 16) &&
                            ff_aligned(qw_packed, 16) && ff_aligned(h, 16);
   if (!packed_fits) return ff_gemm_fp8_swiglu(qa, sa, qw, sw, h, ldh, pmax, m, i, k, stream);
   const int64_t tiles_m = (m + bm - 1) / bm;
+  bool launched = false;
 #define FF_SWIGLU(BM, CW)                                                                                           \
-  if (bm == BM && cw == CW)                                                                                         \
+  if (bm == BM && cw == CW && (launched = true))                                                                    \
     hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<BM, CW, kPkP, kPkD, kPkG>),                                   \
                        dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads), 0, (hipStream_t)stream,                 \
                        (const uint8_t*)qa, sa, (const uint8_t*)qw_packed, sw, (bf16_t*)h, ldh, pmax, (int)m,        \
                        (int)i, (int)k, (int)tiles_m, (int)tiles_n, nullptr, 0.f);
   FF_SWIGLU(144, 96) FF_SWIGLU(128, 96) FF_SWIGLU(112, 96) FF_SWIGLU(96, 96) FF_SWIGLU(80, 96)
   FF_SWIGLU(144, 64) FF_SWIGLU(128, 64) FF_SWIGLU(112, 64) FF_SWIGLU(96, 64) FF_SWIGLU(80, 64)
+  FF_SWIGLU(176, 32) FF_SWIGLU(144, 32) FF_SWIGLU(112, 32) FF_SWIGLU(80, 32) FF_SWIGLU(64, 32)
 #undef FF_SWIGLU
+  FF_REQUIRE(launched, "ff_gemm_fp8_swiglu_pk: no %d x %d tile (tuning override)", bm, 8 * cw);
   FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu_pk");
   return FF_OK;
 }
@@ -807,22 +857,25 @@ extern "C" int ff_gemm_fp8_swiglu_static(const void* qa, const float* sa, const 
              "ff_gemm_fp8_swiglu_static: bad sizes (i %% 64, k %% 128, ldh %% 8)");
   FF_REQUIRE(ff_aligned(qa, 16) && ff_aligned(qw, 16) && ff_aligned(hq, 16),
              "ff_gemm_fp8_swiglu_static: operands must be 16-byte aligned");
-  const int cw = swiglu_cw(i);
+  const int cw = swiglu_cw(m, i);
   const int64_t tiles_n = cw ? i / (2 * cw) : 0;
-  const int bm = cw ? swiglu_bm(m, tiles_n) : 0;
+  const int bm = cw ? swiglu_bm(m, tiles_n, cw) : 0;
   const bool packed_fits = qw_packed && bm && m > 4 && k % kPkKAlign == 0 && m * k < (int64_t(1) << 31) &&
                            2 * i * k < (int64_t(1) << 31) && ff_aligned(qw_packed, 16);
   if (!packed_fits) return gemm_swiglu_static_rowmajor(qa, sa, qw, sw, hq, ldh, inv, m, i, k, (hipStream_t)stream);
   const int64_t tiles_m = (m + bm - 1) / bm;
+  bool launched = false;
 #define FF_SWIGLU(BM, CW)                                                                                           \
-  if (bm == BM && cw == CW)                                                                                         \
+  if (bm == BM && cw == CW && (launched = true))                                                                    \
     hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<BM, CW, kPkP, kPkD, kPkG, true>),                             \
                        dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads), 0, (hipStream_t)stream,                 \
                        (const uint8_t*)qa, sa, (const uint8_t*)qw_packed, sw, nullptr, ldh, nullptr, (int)m, (int)i, \
                        (int)k, (int)tiles_m, (int)tiles_n, (uint8_t*)hq, inv);
   FF_SWIGLU(144, 96) FF_SWIGLU(128, 96) FF_SWIGLU(112, 96) FF_SWIGLU(96, 96) FF_SWIGLU(80, 96)
   FF_SWIGLU(144, 64) FF_SWIGLU(128, 64) FF_SWIGLU(112, 64) FF_SWIGLU(96, 64) FF_SWIGLU(80, 64)
+  FF_SWIGLU(176, 32) FF_SWIGLU(144, 32) FF_SWIGLU(112, 32) FF_SWIGLU(80, 32) FF_SWIGLU(64, 32)
 #undef FF_SWIGLU
+  FF_REQUIRE(launched, "ff_gemm_fp8_swiglu_static: no %d x %d tile (tuning override)", bm, 8 * cw);
   FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu_static");
   return FF_OK;
 }
@@ -839,19 +892,19 @@ int gemm_fp8_pk_partials(const void* qa, const float* sa, int sa_rows, const voi
                          hipStream_t st, int* splits, int64_t* mp) {
   *splits = 0;
   *mp = 0;
-  const int s = qw_packed && ff_aligned(qa, 16) && ff_aligned(qw_packed, 16) ? split_plan(m, n, k) : 0;
+  const SplitPlan p = qw_packed && ff_aligned(qa, 16) && ff_aligned(qw_packed, 16) ? split_plan(m, n, k) : SplitPlan{};
+  const int s = p.s;
   if (s <= 1) return FF_OK;
   const int64_t need = split_workspace(m, n, k);
   FF_REQUIRE(workspace && workspace_bytes >= need && ff_aligned(workspace, 16),
              "ff_gemm_fp8_pk: workspace of %lld bytes (16-byte aligned) required", (long long)need);
-  const int bm = split_bm();
-  if (bm == 80)
-    launch_splits<80>(s, qa, sa, sa_rows, qw_packed, sw, sw_cols, nullptr, 0, m, n, k, workspace, st);
+  if (p.bm == 64)
+    launch_splits<64>(s, qa, sa, sa_rows, qw_packed, sw, sw_cols, nullptr, 0, m, n, k, workspace, st);
   else
     launch_splits<kSpBM>(s, qa, sa, sa_rows, qw_packed, sw, sw_cols, nullptr, 0, m, n, k, workspace, st);
   FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
   *splits = s;
-  *mp = (m + bm - 1) / bm * bm;
+  *mp = (m + p.bm - 1) / p.bm * p.bm;
   return FF_OK;
 }
 }  // namespace ff
@@ -862,7 +915,8 @@ extern "C" int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, cons
   FF_REQUIRE(qa && sa && qw && sw && y, "ff_gemm_fp8_pk: null pointer");
   const bool pk = qw_packed && ldy % 8 == 0 && ldy >= n && ff_aligned(qa, 16) && ff_aligned(qw_packed, 16) &&
                   ff_aligned(y, 16);
-  const int s = pk ? split_plan(m, n, k) : 0;
+  const SplitPlan plan = pk ? split_plan(m, n, k) : SplitPlan{};
+  const int s = plan.s;
   hipStream_t st = (hipStream_t)stream;
   if (s == 0) {
     const SmallTile t = pk ? small_plan(m, n, k) : SmallTile{};
@@ -878,8 +932,8 @@ extern "C" int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, cons
     return FF_OK;
   }
   if (s == 1) {
-    if (split_bm() == 80)
-      launch_splits<80>(1, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, nullptr, st);
+    if (plan.bm == 64)
+      launch_splits<64>(1, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, nullptr, st);
     else
       launch_splits<kSpBM>(1, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, nullptr, st);
     FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
@@ -907,9 +961,19 @@ extern "C" int ff_gemm_fp8_qkv_pk(const void* qa, const float* sa, int sa_rows, 
                                   const void* q_norm, const void* k_norm, float eps_q, float eps_k, const void* cos,
                                   const void* sin, void* yq, void* yk, void* vt, int64_t t_pad, ff_stream_t stream) {
   const int64_t n = (hq + 2 * hk) * kHeadDim;
-  const int64_t tiles_m = (m + kQkBM - 1) / kQkBM, tiles_n = n / (4 * kQkCW), tiles = tiles_m * tiles_n;
-  const bool fits = qw_packed && m > 4 && hq > 0 && hk > 0 && hq % hk == 0 && n % (4 * kQkCW) == 0 &&
-                    k > 0 && k % (128 * kSpU) == 0 && tiles >= 192 && tiles <= 512 && t_pad >= m && t_pad % 64 == 0 &&
+  // ff_set_tuning(FF_TUNE_QKV_PK_TILE, 1 | 2 | 3): 64 x 256 packed tiles, 64 x 128 packed tiles, the
+  // row-major kernel, for measurement sweeps
+  // The library's choice: 64 x 128 tiles (one head) while their grid is at most 512 workgroups (two
+  // per CU; 8B shape: 576 tokens 432 workgroups, 6.260 -> 6.229 ms against 64 x 256; 176 tokens 144
+  // workgroups, 4.467 -> 4.393 ms against the row-major kernel), else 64 x 256.
+  const int forced = ff_tuning(FF_TUNE_QKV_PK_TILE);
+  const int64_t tiles_m = (m + kQkBM - 1) / kQkBM;
+  const int cw = forced == 2 || (!forced && tiles_m * (n / 128) <= 512) ? 32 : kQkCW;
+  const int64_t tiles_n = n / (4 * cw), tiles = tiles_m * tiles_n;
+  const bool fits = forced != 3 && qw_packed && m > 4 && hq > 0 && hk > 0 && hq % hk == 0 && n % (4 * cw) == 0 &&
+                    k > 0 && k % (128 * kSpU) == 0 && (forced || cw == 32 || (tiles >= 192 && tiles <= 512)) &&
+                    t_pad >= m &&
+                    t_pad % 64 == 0 &&
                     t_pad <= tiles_m * kQkBM && m * k < (int64_t(1) << 31) && n * k < (int64_t(1) << 31) &&
                     ff_aligned(qa, 16) && ff_aligned(qw_packed, 16) && ff_aligned(cos, 16) && ff_aligned(sin, 16) &&
                     ff_aligned(q_norm, 16) && ff_aligned(k_norm, 16) && ff_aligned(yq, 16) && ff_aligned(yk, 16) &&
@@ -920,9 +984,14 @@ extern "C" int ff_gemm_fp8_qkv_pk(const void* qa, const float* sa, int sa_rows, 
   FF_REQUIRE(sa && sw && q_norm && k_norm && yq && yk && vt, "ff_gemm_fp8_qkv_pk: null pointer");
   PkQkv qe{(const bf16_t*)q_norm, (const bf16_t*)k_norm, eps_q, eps_k, (const bf16_t*)cos, (const bf16_t*)sin,
            (bf16_t*)yq, (bf16_t*)yk, (bf16_t*)vt, (int)hq, (int)hk, (int)t_pad};
-  hipLaunchKernelGGL((gemm_fp8_qkv_packed_kernel<kQkBM, kQkCW, kSpP, kSpD, kSpG>), dim3((unsigned)tiles),
-                     dim3(kThreads), 0, (hipStream_t)stream, (const uint8_t*)qa, sa, sa_rows, (const uint8_t*)qw_packed,
-                     sw, sw_cols, (int)m, (int)n, (int)k, (int)tiles_m, (int)tiles_n, qe);
+  if (cw == 32)
+    hipLaunchKernelGGL((gemm_fp8_qkv_packed_kernel<kQkBM, 32, kSpP, kSpD, kSpG>), dim3((unsigned)tiles),
+                       dim3(kThreads), 0, (hipStream_t)stream, (const uint8_t*)qa, sa, sa_rows,
+                       (const uint8_t*)qw_packed, sw, sw_cols, (int)m, (int)n, (int)k, (int)tiles_m, (int)tiles_n, qe);
+  else
+    hipLaunchKernelGGL((gemm_fp8_qkv_packed_kernel<kQkBM, kQkCW, kSpP, kSpD, kSpG>), dim3((unsigned)tiles),
+                       dim3(kThreads), 0, (hipStream_t)stream, (const uint8_t*)qa, sa, sa_rows,
+                       (const uint8_t*)qw_packed, sw, sw_cols, (int)m, (int)n, (int)k, (int)tiles_m, (int)tiles_n, qe);
   FF_LAUNCH_CHECK("ff_gemm_fp8_qkv_pk");
   return FF_OK;
 }

@@ -92,17 +92,19 @@ def test_w4a16_swiglu_shape_query_without_a_gpu(lib_path):
     assert fits(576, 12288, 4096, 96) == 0         # group not a power of two
 
 
-# (m, n, k, splits) the packed FP8 plain GEMM takes: the 8B down projection at
-# the bucket sizes that pick 8, 4, 3 and 2 splits (k = 12288), unsplit grids and
-# shapes left to the small tiles or the row-major kernels (0). The plan is host
-# code, so the workspace query pins it without a GPU.
-PLAN_SHAPES = [(176, 4096, 12288, 8), (576, 4096, 12288, 4), (640, 4096, 12288, 3), (1152, 4096, 12288, 2),
-               (300, 2048, 8192, 8), (1000, 6144, 8192, 4), (576, 12288, 4096, 1), (576, 4096, 4096, 0),
-               (176, 4096, 4096, 0), (300, 4096, 2048, 0), (3, 4096, 4096, 0), (1024, 5120, 25600, 2)]
+# (m, n, k, row tile, splits) the packed FP8 plain GEMM takes: the 8B down
+# projection at the bucket sizes that pick 4 (64-row tiles, short m), 4, 3 and 2
+# splits (k = 12288), the 176-token o projection on 64-row tiles split 4 ways,
+# unsplit grids and shapes left to the small tiles or the row-major kernels (0).
+# The plan is host code, so the workspace query pins it without a GPU.
+PLAN_SHAPES = [(176, 4096, 12288, 64, 4), (576, 4096, 12288, 144, 4), (640, 4096, 12288, 144, 3),
+               (1152, 4096, 12288, 144, 2), (300, 2048, 8192, 144, 8), (1000, 6144, 8192, 144, 4),
+               (576, 12288, 4096, 144, 1), (576, 4096, 4096, 0, 0), (176, 4096, 4096, 64, 4), (64, 2048, 2048, 64, 4),
+               (300, 4096, 2048, 0, 0), (3, 4096, 4096, 0, 0), (1024, 5120, 25600, 144, 2)]
 
 
-@pytest.mark.parametrize("m,n,k,splits", PLAN_SHAPES)
-def test_fp8_pk_split_plan(lib_path, m, n, k, splits):
+@pytest.mark.parametrize("m,n,k,bm,splits", PLAN_SHAPES)
+def test_fp8_pk_split_plan(lib_path, m, n, k, bm, splits):
     from fastforward_amd.linear import gemm_pk_workspace
     need = gemm_pk_workspace(m, n, k)
-    assert need == ((m + 143) // 144 * (n // 256) * splits * 144 * 256 * 4 if splits > 1 else 0)
+    assert need == ((m + bm - 1) // bm * (n // 256) * splits * bm * 256 * 4 if splits > 1 else 0)

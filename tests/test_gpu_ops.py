@@ -333,13 +333,15 @@ def test_pack_weight_fp8_layout(gpu):
                 assert np.array_equal(got[f, kt, 0, lane], row[:16]) and np.array_equal(got[f, kt, 1, lane], row[16:])
 
 
-# 12288 channels (64 column tiles) take row tiles of 144 (576 tokens), 80 (176),
-# 112 (400), 96 (700) and 128 (1000); MLP widths that 192 does not divide take
+# 12288 channels (64 column tiles) take row tiles of 144 (576 tokens), 112
+# (400), 96 (700) and 128 (1000); MLP widths that 192 does not divide take
 # 128-channel tiles (4096; the 32B shape's 25600 at 1024 tokens; the 4B shape's
-# 9728)
+# 9728); up to 176 tokens, 64-channel tiles of one row tile (176, 100, 150, 17
+# tokens: 176, 112, 144 and 64 rows)
 @pytest.mark.parametrize("m,i,k", [(576, 12288, 4096), (300, 12288, 2048), (433, 6144, 4096), (3, 12288, 4096),
                                    (576, 4096, 4096), (176, 12288, 4096), (400, 12288, 4096), (700, 12288, 4096),
-                                   (1000, 12288, 4096), (1024, 25600, 5120), (576, 9728, 2560), (300, 4160, 2048)])
+                                   (1000, 12288, 4096), (1024, 25600, 5120), (576, 9728, 2560), (300, 4160, 2048),
+                                   (100, 12288, 4096), (150, 12288, 2048), (17, 12288, 4096)])
 def test_gemm_fp8_swiglu_packed_equals_rowmajor(gpu, m, i, k):
     """The gate/up GEMM on the packed weight copy (BM x 384 tiles, or BM x 256 where
     192 does not divide the MLP width, BM = 80..144 by grid, weights straight into
@@ -364,19 +366,20 @@ def test_gemm_fp8_swiglu_packed_equals_rowmajor(gpu, m, i, k):
     assert torch.equal(h0, h1) and torch.equal(p0, p1)
 
 
-# (m, n, k, splits the packed path takes); 0 = unsplit on the small packed tiles
-# (576 x 4096 x 4096: 96 x 128; 576 / 500 x 6144 x 4096: 64 x 256, the last
-# tile ragged; 300 x 4096 x 2048 and the 176-token o projection 176 x 4096 x
-# 4096: 64 x 128, the candidate with the most workgroups on a short grid) or the
-# row-major kernels (3 rows, n % 128)
-PK_SHAPES = [(576, 4096, 12288, 4), (300, 2048, 8192, 8), (1000, 6144, 8192, 4), (576, 12288, 4096, 1),
-             (640, 4096, 12288, 3), (1152, 4096, 12288, 2), (176, 4096, 12288, 8),
-             (576, 4096, 4096, 0), (576, 6144, 4096, 0), (500, 6144, 4096, 0), (300, 4096, 2048, 0),
-             (176, 4096, 4096, 0), (3, 4096, 4096, 0), (576, 4160, 12288, 0)]
+# (m, n, k, row tile, splits the packed path takes); 0 = unsplit on the small
+# packed tiles (576 x 4096 x 4096: 96 x 128; 576 / 500 x 6144 x 4096: 64 x 256,
+# the last tile ragged; 300 x 4096 x 2048: 64 x 128, the candidate with the most
+# workgroups on a short grid) or the row-major kernels (3 rows, n % 128); short m
+# (176 tokens, 2B widths at 64) takes 64-row tiles with a k split
+PK_SHAPES = [(576, 4096, 12288, 144, 4), (300, 2048, 8192, 144, 8), (1000, 6144, 8192, 144, 4),
+             (576, 12288, 4096, 144, 1), (640, 4096, 12288, 144, 3), (1152, 4096, 12288, 144, 2),
+             (176, 4096, 12288, 64, 4), (176, 4096, 4096, 64, 4), (64, 2048, 2048, 64, 4), (250, 2048, 6144, 64, 4),
+             (576, 4096, 4096, 0, 0), (576, 6144, 4096, 0, 0), (500, 6144, 4096, 0, 0), (300, 4096, 2048, 0, 0),
+             (3, 4096, 4096, 0, 0), (576, 4160, 12288, 0, 0)]
 
 
-@pytest.mark.parametrize("m,n,k,splits", PK_SHAPES)
-def test_gemm_fp8_pk_matches_rowmajor(gpu, m, n, k, splits):
+@pytest.mark.parametrize("m,n,k,bm,splits", PK_SHAPES)
+def test_gemm_fp8_pk_matches_rowmajor(gpu, m, n, k, bm, splits):
     """ff_gemm_fp8_pk on the packed weight: the same bits as ff_gemm_fp8 unsplit
     or where it falls back; with a k split, at most 1 bf16 ulp from it (only the
     fp32 order of adding the partials differs), identical bits on repeated calls
@@ -387,8 +390,8 @@ def test_gemm_fp8_pk_matches_rowmajor(gpu, m, n, k, splits):
     op = FP8Linear((torch.randn(n, k, generator=_g(61)) * 0.03).to(BF16).to(DEV)).pack()
     qa, sa = op.quantize(x)
     need = gemm_pk_workspace(m, n, k)
-    # the split count itself: fp32 partials of 144 x 256 tiles over the rows padded to whole tiles
-    assert need == ((m + 143) // 144 * (n // 256) * splits * 144 * 256 * 4 if splits > 1 else 0)
+    # the split count itself: fp32 partials of bm x 256 tiles over the rows padded to whole tiles
+    assert need == ((m + bm - 1) // bm * (n // 256) * splits * bm * 256 * 4 if splits > 1 else 0)
     ws = torch.full((max(need, 256),), 0xFF, device=DEV, dtype=torch.uint8)  # no zeroing needed
     ref = torch.empty(m, n, device=DEV, dtype=BF16)
     call("ff_gemm_fp8", ptr(qa), ptr(sa), 1, ptr(op.weight), ptr(op.scale), 1, ptr(ref), n, m, n, k, stream())
@@ -574,7 +577,7 @@ def test_w4a16_dequant_bit_exact_via_one_hot(gpu, tuning, tile):
 
 # ------------------------------------------------------------------ attention
 
-@pytest.mark.parametrize("t,hq,hk", [(576, 32, 8), (320, 16, 8), (70, 64, 8)])
+@pytest.mark.parametrize("t,hq,hk", [(576, 32, 8), (320, 16, 8), (70, 64, 8), (640, 32, 8), (176, 32, 8), (641, 32, 8)])
 def test_attention_causal(gpu, t, hq, hk):
     from fastforward_amd import ops
     d = 128
@@ -741,13 +744,16 @@ def test_gemm_fp8_qkv_equals_unfused(gpu, t, k, hq, hk):
 
 @pytest.mark.parametrize("t,k,hq,hk,static", [(576, 4096, 32, 8, False), (500, 4096, 32, 8, False),
                                                (1024, 4096, 32, 8, False), (576, 4096, 32, 8, True),
-                                               (300, 2048, 16, 8, False), (3, 4096, 32, 8, False)])
+                                               (300, 2048, 16, 8, False), (3, 4096, 32, 8, False),
+                                               (176, 4096, 32, 8, False), (176, 4096, 32, 8, True),
+                                               (1200, 4096, 64, 8, False)])
 def test_gemm_fp8_qkv_packed_equals_rowmajor(gpu, t, k, hq, hk, static):
-    """ff_gemm_fp8_qkv_pk (64-token x two-head tiles on the packed weight: 576,
-    ragged 500 and 1024 tokens at 32/8 heads, per-token and per-tensor scales)
-    equals ff_gemm_fp8_qkv bit for bit, V^T zero padding included; shapes
-    outside its plan (300 tokens at 16/8 heads: 80 tiles; 3 tokens) run
-    ff_gemm_fp8_qkv itself."""
+    """ff_gemm_fp8_qkv_pk on the packed weight -- 64-token x one-head tiles while
+    their grid is at most 512 workgroups (576, ragged 500, 176 and 300 tokens),
+    else 64-token x two-head tiles (1024 tokens at 32/8 heads) -- equals
+    ff_gemm_fp8_qkv bit for bit, V^T zero padding included, per-token and
+    per-tensor scales; shapes outside its plan (1200 tokens at 64/8 heads; 3
+    tokens) run ff_gemm_fp8_qkv itself."""
     from fastforward_amd._lib import call, ptr, stream
     d = 128
     tp, n = (t + 63) // 64 * 64, (hq + 2 * hk) * d
