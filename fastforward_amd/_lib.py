@@ -41,6 +41,7 @@ SIGNATURES = {
     "ff_gemm_fp8": [P, P, I32, P, P, I32, P, I64, I64, I64, I64, P],
     "ff_gemm_fp8_swiglu": [P, P, P, P, P, I64, P, I64, I64, I64, P],
     "ff_pack_weight_fp8": [P, P, I64, I64, P],
+    "ff_unpack_weight_fp8": [P, P, I64, I64, P],
     "ff_gemm_fp8_swiglu_pk": [P, P, P, P, P, P, I64, P, I64, I64, I64, P],
     "ff_gemm_fp8_pk_workspace": [I64, I64, I64, PI64],
     "ff_gemm_fp8_pk": [P, P, I32, P, P, P, I32, P, I64, I64, I64, I64, P, I64, P],

@@ -538,6 +538,26 @@ int swiglu_bm(int64_t m, int64_t tiles_n, int cw) {
   return best;
 }
 
+// Gate/up tile for callers without the row-major weight (every m > 4 must run
+// on the packed copy): where the library's plan declines (too few workgroups),
+// the instantiated tile with the most workgroups, ties to the taller tile.
+void swiglu_any_tile(int64_t m, int64_t i, int* cw_out, int* bm_out) {
+  constexpr int cands[15][2] = {{144, 96}, {128, 96}, {112, 96}, {96, 96}, {80, 96},
+                                {144, 64}, {128, 64}, {112, 64}, {96, 64}, {80, 64},
+                                {176, 32}, {144, 32}, {112, 32}, {80, 32}, {64, 32}};
+  int64_t most = 0;
+  *cw_out = *bm_out = 0;
+  for (const auto& c : cands) {
+    if (i % (2 * c[1])) continue;
+    const int64_t wg = (m + c[0] - 1) / c[0] * (i / (2 * c[1]));
+    if (wg > most) {
+      most = wg;
+      *bm_out = c[0];
+      *cw_out = c[1];
+    }
+  }
+}
+
 // Plain GEMM: 144 x 256 tiles, k split so that about 256 workgroups run (the
 // 8B o and down projections: 4 x 16 tiles, 4 splits).
 constexpr int kSpBM = 144, kSpCW = 64, kSpP = 2, kSpD = 2, kSpG = 2;
@@ -615,7 +635,7 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k) {
 struct SmallTile {
   int bm = 0, cw = 0;
 };
-SmallTile small_plan(int64_t m, int64_t n, int64_t k) {
+SmallTile small_plan(int64_t m, int64_t n, int64_t k, bool any_count = false) {
   SmallTile t;
   if (m <= 4 || k % (128 * kSpU) || m * k >= (int64_t(1) << 31) || n * k >= (int64_t(1) << 31)) return t;
   constexpr int cand[3][2] = {{64, 64}, {96, 32}, {64, 32}};
@@ -630,8 +650,8 @@ SmallTile small_plan(int64_t m, int64_t n, int64_t k) {
   }
   // Short m (no candidate reaches 192 workgroups): the candidate with the
   // most workgroups, if it has at least 64 (the row-major kernel's 64 x 128
-  // tiles give no more).
-  int64_t most = 63;
+  // tiles give no more) or there is no row-major weight (any_count).
+  int64_t most = any_count ? 0 : 63;
   for (const auto& c : cand) {
     if (n % (4 * c[1])) continue;
     const int64_t tiles = (m + c[0] - 1) / c[0] * (n / (4 * c[1]));
@@ -805,6 +825,228 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_fp8_qkv_packed_kernel(
 // Fused QKV tile: 64 tokens x 256 channels (two heads).
 constexpr int kQkBM = 64, kQkCW = 64;
 
+// ---------------------------------------------------------------- unpacking
+// The row-major (N, K) codes back from the fragment copy (the inverse of
+// pack_fp8_kernel), for callers that read the codes themselves.
+__global__ __launch_bounds__(kThreads) void unpack_fp8_kernel(const uint8_t* __restrict__ p, uint8_t* __restrict__ w,
+                                                              int64_t n, int64_t k) {
+  const int64_t kt_n = k / 128;
+  const int64_t lanes = (n / 16) * kt_n * 64;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < lanes; i += (int64_t)gridDim.x * blockDim.x) {
+    const int l = (int)(i & 63);
+    const int64_t f = i >> 6;
+    const int64_t kt = f % kt_n, f16 = f / kt_n;
+    const int64_t nf = n / 16;
+    const int64_t row = f16 * 16 + (l & 15);
+    const uint8_t* src = p + (kt * nf + f16) * 2048 + 16 * l;
+    u32x4* dst = reinterpret_cast<u32x4*>(w + row * k + kt * 128 + 32 * (l >> 4));
+    dst[0] = *reinterpret_cast<const u32x4*>(src);
+    dst[1] = *reinterpret_cast<const u32x4*>(src + 1024);
+  }
+}
+
+// ---------------------------------------------------------------- rows <= 4 on packed weights
+//
+// The pick-only tail's products (m <= 4 rows) straight from the fragment copy.
+// Lane 16 g + r of a wave holds, for each k step kt, the 32 k bytes [128 kt +
+// 32 g, +32) of row r of a 16-row fragment group (its two 16-byte pieces): it
+// decodes them with v_cvt_pk_f32_fp8 and adds the exact products with the
+// activations in fp32 FMAs; the four lane groups of a row are then added with
+// row swaps. Plain product: one workgroup per 16-row group, its 4 waves taking
+// every 4th k step and their sums added in wave order through LDS. SwiGLU: one
+// workgroup per 64 channels, wave w the gate and up rows of channels 16 w ..
+// + 15 over all k steps. Loads of four k steps are issued before their
+// products.
+constexpr int kGemvPkMaxM = 4;
+constexpr int kGemvPkU = 4;  // k steps whose loads are in flight together
+
+__device__ __forceinline__ void e4m3x16_to_f32(const u32x4 v, float* f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[q], false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[q], true);
+    f[4 * q + 0] = lo[0];
+    f[4 * q + 1] = lo[1];
+    f[4 * q + 2] = hi[0];
+    f[4 * q + 3] = hi[1];
+  }
+}
+
+// acc[m] += the products of this lane's 32 k bytes of step kt with rows m of qa,
+// k in order, one 16-byte piece at a time.
+template <int MM>
+__device__ __forceinline__ void gemv_pk_step(const uint8_t* __restrict__ qa, int K, int kt, int g, const u32x4& wlo,
+                                             const u32x4& whi, float (&acc)[MM]) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float wf[16];
+    e4m3x16_to_f32(h ? whi : wlo, wf);
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      float af[16];
+      e4m3x16_to_f32(*reinterpret_cast<const u32x4*>(qa + (size_t)m * K + 128 * kt + 32 * g + 16 * h), af);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[m] = __builtin_fmaf(af[e], wf[e], acc[m]);
+    }
+  }
+}
+
+template <int MM>
+__global__ __launch_bounds__(kThreads) void gemv_fp8_packed_kernel(const uint8_t* __restrict__ qa,
+                                                                   const float* __restrict__ sa, int sa_rows,
+                                                                   const uint8_t* __restrict__ qwp,
+                                                                   const float* __restrict__ sw, int sw_cols,
+                                                                   bf16_t* __restrict__ y, int64_t ldy, int N, int K) {
+  __shared__ float red[4][MM][16];
+  const int f = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int KT = K / 128, nf = N / 16;
+  float acc[MM];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) acc[m] = 0.f;
+  for (int kb = wave; kb < KT; kb += 4 * kGemvPkU) {
+    u32x4 lo[kGemvPkU], hi[kGemvPkU];
+#pragma unroll
+    for (int u = 0; u < kGemvPkU; ++u) {
+      const int kt = min(kb + 4 * u, KT - 1);
+      const uint8_t* src = qwp + ((size_t)kt * nf + f) * 2048 + 16 * lane;
+      lo[u] = *reinterpret_cast<const u32x4*>(src);
+      hi[u] = *reinterpret_cast<const u32x4*>(src + 1024);
+    }
+#pragma unroll
+    for (int u = 0; u < kGemvPkU; ++u)
+      if (kb + 4 * u < KT) gemv_pk_step<MM>(qa, K, kb + 4 * u, g, lo[u], hi[u], acc);
+  }
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    const float v = sum_rows(acc[m]);
+    if (g == 0) red[wave][m][r] = v;
+  }
+  __syncthreads();
+  if (wave == 0 && g == 0) {
+    const int n = 16 * f + r;
+    const float swv = sw[sw_cols ? n : 0];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      const float tot = ((red[0][m][r] + red[1][m][r]) + red[2][m][r]) + red[3][m][r];
+      y[(size_t)m * ldy + n] = (bf16_t)f32_to_bf16((tot * sa[sa_rows ? m : 0]) * swv);
+    }
+  }
+}
+
+// SwiGLU: h = bf16(bf16(silu(g)) * u) for the 64 channels of workgroup
+// blockIdx.x, g and u = bf16((dot * sa) * sw) of gate row c and up row half + c,
+// and the workgroup's max |h| into pmax[m, blockIdx.x] (the 64-channel row
+// maxima of the tile kernels); SQ: h written as e4m3(clamp(h * qinv, +-448))
+// into hq instead, without maxima. 16 waves: wave 4 j + w takes channels
+// 16 j .. + 15 over the k steps kt = w mod 4, and the four k phases are added in
+// order through LDS, so g and u are the bits of the plain kernel above on the
+// same rows.
+template <int MM, bool SQ>
+__global__ __launch_bounds__(1024) void gemv_fp8_swiglu_packed_kernel(
+    const uint8_t* __restrict__ qa, const float* __restrict__ sa, int sa_rows, const uint8_t* __restrict__ qwp,
+    const float* __restrict__ sw, int sw_cols, bf16_t* __restrict__ h, int64_t ldh, float* __restrict__ pmax,
+    uint8_t* __restrict__ hq, float qinv, int half, int K) {
+  __shared__ float red[2][4][4][MM][16];  // [gate / up][channel group][k phase][row][channel]
+  __shared__ float hmax[4][MM];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int grp = wave >> 2, ph = wave & 3;
+  const int KT = K / 128, nf = 2 * half / 16;
+  const int c0 = 64 * (int)blockIdx.x + 16 * grp;  // first channel of this wave's group
+  const int fg = c0 / 16, fu = (half + c0) / 16;
+  float ag[MM], au[MM];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) ag[m] = au[m] = 0.f;
+  constexpr int U = 2;  // 16 waves per workgroup: 128 registers each
+  for (int kb = ph; kb < KT; kb += 4 * U) {
+    u32x4 glo[U], ghi[U], ulo[U], uhi[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kt = min(kb + 4 * u, KT - 1);
+      const uint8_t* sg = qwp + ((size_t)kt * nf + fg) * 2048 + 16 * lane;
+      const uint8_t* su = qwp + ((size_t)kt * nf + fu) * 2048 + 16 * lane;
+      glo[u] = *reinterpret_cast<const u32x4*>(sg);
+      ghi[u] = *reinterpret_cast<const u32x4*>(sg + 1024);
+      ulo[u] = *reinterpret_cast<const u32x4*>(su);
+      uhi[u] = *reinterpret_cast<const u32x4*>(su + 1024);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (kb + 4 * u < KT) {
+        gemv_pk_step<MM>(qa, K, kb + 4 * u, g, glo[u], ghi[u], ag);
+        gemv_pk_step<MM>(qa, K, kb + 4 * u, g, ulo[u], uhi[u], au);
+      }
+  }
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    const float vg = sum_rows(ag[m]), vu = sum_rows(au[m]);
+    if (g == 0) {
+      red[0][grp][ph][m][r] = vg;
+      red[1][grp][ph][m][r] = vu;
+    }
+  }
+  __syncthreads();
+  if (ph == 0) {  // waves 0, 4, 8, 12: one channel group each
+    const int c = c0 + r;
+    const float swg = sw[sw_cols ? c : 0], swu = sw[sw_cols ? half + c : 0];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      const float sav = sa[sa_rows ? m : 0];
+      const float tg = ((red[0][grp][0][m][r] + red[0][grp][1][m][r]) + red[0][grp][2][m][r]) + red[0][grp][3][m][r];
+      const float tu = ((red[1][grp][0][m][r] + red[1][grp][1][m][r]) + red[1][grp][2][m][r]) + red[1][grp][3][m][r];
+      const float gv = round_bf16((tg * sav) * swg);
+      const float uv = round_bf16((tu * sav) * swu);
+      const float hv = round_bf16(round_bf16(silu(gv)) * uv);
+      if constexpr (SQ) {
+        if (g == 0) hq[(size_t)m * ldh + c] = (uint8_t)(e4m3x4(clamp448(hv * qinv), 0.f, 0.f, 0.f) & 0xFFu);
+      } else {
+        if (g == 0) h[(size_t)m * ldh + c] = (bf16_t)f32_to_bf16(hv);
+        float mx = fabsf(hv);
+        mx = fmaxf(mx, dpp<kDppXor1>(mx));
+        mx = fmaxf(mx, dpp<kDppXor2>(mx));
+        mx = fmaxf(mx, dpp<kDppHalfMirror>(mx));
+        mx = fmaxf(mx, dpp<kDppRowMirror>(mx));
+        if (lane == 0) hmax[grp][m] = mx;
+      }
+    }
+  }
+  if constexpr (SQ) return;
+  __syncthreads();
+  if (threadIdx.x < MM) {
+    const int m = threadIdx.x;
+    pmax[(size_t)m * (half / 64) + blockIdx.x] = fmaxf(fmaxf(hmax[0][m], hmax[1][m]), fmaxf(hmax[2][m], hmax[3][m]));
+  }
+}
+
+// Launch the packed single-row kernels for m in 1..4.
+void launch_gemv_pk(const void* qa, const float* sa, int sa_rows, const void* qwp, const float* sw, int sw_cols,
+                    void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, hipStream_t s) {
+#define FF_GEMVPK(MM)                                                                                       \
+  case MM:                                                                                                  \
+    hipLaunchKernelGGL(gemv_fp8_packed_kernel<MM>, dim3((unsigned)(n / 16)), dim3(kThreads), 0, s,         \
+                       (const uint8_t*)qa, sa, sa_rows, (const uint8_t*)qwp, sw, sw_cols, (bf16_t*)y, ldy,   \
+                       (int)n, (int)k);                                                                     \
+    break;
+  switch (m) { FF_GEMVPK(1) FF_GEMVPK(2) FF_GEMVPK(3) FF_GEMVPK(4) }
+#undef FF_GEMVPK
+}
+
+template <bool SQ>
+void launch_gemv_swiglu_pk(const void* qa, const float* sa, int sa_rows, const void* qwp, const float* sw,
+                           int sw_cols, void* h, int64_t ldh, float* pmax, void* hq, float qinv, int64_t m, int64_t i,
+                           int64_t k, hipStream_t s) {
+#define FF_GEMVSPK(MM)                                                                                      \
+  case MM:                                                                                                  \
+    hipLaunchKernelGGL((gemv_fp8_swiglu_packed_kernel<MM, SQ>), dim3((unsigned)(i / 64)), dim3(1024), 0,    \
+                       s, (const uint8_t*)qa, sa, sa_rows, (const uint8_t*)qwp, sw, sw_cols, (bf16_t*)h, ldh, pmax, \
+                       (uint8_t*)hq, qinv, (int)i, (int)k);                                                 \
+    break;
+  switch (m) { FF_GEMVSPK(1) FF_GEMVSPK(2) FF_GEMVSPK(3) FF_GEMVSPK(4) }
+#undef FF_GEMVSPK
+}
+
 }  // namespace
 
 extern "C" int ff_pack_weight_fp8(const void* w, void* packed, int64_t n, int64_t k, ff_stream_t stream) {
@@ -820,18 +1062,44 @@ extern "C" int ff_pack_weight_fp8(const void* w, void* packed, int64_t n, int64_
   return FF_OK;
 }
 
+extern "C" int ff_unpack_weight_fp8(const void* packed, void* w, int64_t n, int64_t k, ff_stream_t stream) {
+  FF_REQUIRE(w && packed, "ff_unpack_weight_fp8: null pointer");
+  FF_REQUIRE(n > 0 && n % 16 == 0 && k > 0 && k % 128 == 0 && n * k < (int64_t(1) << 40),
+             "ff_unpack_weight_fp8: bad sizes (n %% 16, k %% 128)");
+  FF_REQUIRE(ff_aligned(w, 16) && ff_aligned(packed, 16), "ff_unpack_weight_fp8: alignment");
+  const int64_t lanes = (n / 16) * (k / 128) * 64;
+  const int64_t blocks = (lanes + kThreads - 1) / kThreads;
+  hipLaunchKernelGGL(unpack_fp8_kernel, dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const uint8_t*)packed, (uint8_t*)w, n, k);
+  FF_LAUNCH_CHECK("ff_unpack_weight_fp8");
+  return FF_OK;
+}
+
 extern "C" int ff_gemm_fp8_swiglu_pk(const void* qa, const float* sa, const void* qw, const void* qw_packed,
                                      const float* sw, void* h, int64_t ldh, float* pmax, int64_t m, int64_t i,
                                      int64_t k, ff_stream_t stream) {
-  FF_REQUIRE(qa && sa && qw && sw && h && pmax, "ff_gemm_fp8_swiglu_pk: null pointer");
-  const int cw = swiglu_cw(m, i);
-  const int64_t tiles_n = cw ? i / (2 * cw) : 0;
-  const int bm = cw ? swiglu_bm(m, tiles_n, cw) : 0;
-  const bool packed_fits = qw_packed && bm && m > 4 && k % kPkKAlign == 0 && ldh % 8 == 0 && ldh >= i &&
-                           m * k < (int64_t(1) << 31) && 2 * i * k < (int64_t(1) << 31) && ff_aligned(qa, 16) &&
-                           ff_aligned(qw_packed, 16) && ff_aligned(h, 16);
+  FF_REQUIRE(qa && sa && (qw || qw_packed) && sw && h && pmax, "ff_gemm_fp8_swiglu_pk: null pointer");
+  int cw = swiglu_cw(m, i);
+  int bm = cw ? swiglu_bm(m, i / (2 * cw), cw) : 0;
+  const bool aligned = qw_packed && k % kPkKAlign == 0 && i % 64 == 0 && ldh % 8 == 0 && ldh >= i &&
+                       m * k < (int64_t(1) << 31) && 2 * i * k < (int64_t(1) << 31) && ff_aligned(qa, 16) &&
+                       ff_aligned(qw_packed, 16) && ff_aligned(h, 16);
+  if (!qw) {
+    // only the packed copy: the single-row kernel for m <= 4, else a packed tile whatever its grid
+    FF_REQUIRE(aligned, "ff_gemm_fp8_swiglu_pk: without the row-major weight, i %% 64, k %% %d, ldh %% 8 and "
+                        "16-byte alignment", kPkKAlign);
+    if (m == 0) return FF_OK;
+    if (m <= kGemvPkMaxM) {
+      launch_gemv_swiglu_pk<false>(qa, sa, 1, qw_packed, sw, 1, h, ldh, pmax, nullptr, 0.f, m, i, k,
+                                   (hipStream_t)stream);
+      FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu_pk");
+      return FF_OK;
+    }
+    if (!bm) swiglu_any_tile(m, i, &cw, &bm);
+  }
+  const bool packed_fits = aligned && bm && m > 4;
   if (!packed_fits) return ff_gemm_fp8_swiglu(qa, sa, qw, sw, h, ldh, pmax, m, i, k, stream);
-  const int64_t tiles_m = (m + bm - 1) / bm;
+  const int64_t tiles_n = i / (2 * cw), tiles_m = (m + bm - 1) / bm;
   bool launched = false;
 #define FF_SWIGLU(BM, CW)                                                                                           \
   if (bm == BM && cw == CW && (launched = true))                                                                    \
@@ -851,19 +1119,31 @@ extern "C" int ff_gemm_fp8_swiglu_pk(const void* qa, const float* sa, const void
 extern "C" int ff_gemm_fp8_swiglu_static(const void* qa, const float* sa, const void* qw, const void* qw_packed,
                                          const float* sw, void* hq, int64_t ldh, float inv, int64_t m, int64_t i,
                                          int64_t k, ff_stream_t stream) {
-  FF_REQUIRE(qa && sa && qw && sw && hq, "ff_gemm_fp8_swiglu_static: null pointer");
+  FF_REQUIRE(qa && sa && (qw || qw_packed) && sw && hq, "ff_gemm_fp8_swiglu_static: null pointer");
   FF_REQUIRE(m >= 0 && i > 0 && i % 64 == 0 && k > 0 && k % 128 == 0 && ldh >= i && ldh % 8 == 0 &&
                  m < (1 << 30) && i < (1 << 29) && k < (1 << 30),
              "ff_gemm_fp8_swiglu_static: bad sizes (i %% 64, k %% 128, ldh %% 8)");
-  FF_REQUIRE(ff_aligned(qa, 16) && ff_aligned(qw, 16) && ff_aligned(hq, 16),
+  FF_REQUIRE(ff_aligned(qa, 16) && ff_aligned(qw ? qw : qw_packed, 16) && ff_aligned(hq, 16),
              "ff_gemm_fp8_swiglu_static: operands must be 16-byte aligned");
-  const int cw = swiglu_cw(m, i);
-  const int64_t tiles_n = cw ? i / (2 * cw) : 0;
-  const int bm = cw ? swiglu_bm(m, tiles_n, cw) : 0;
-  const bool packed_fits = qw_packed && bm && m > 4 && k % kPkKAlign == 0 && m * k < (int64_t(1) << 31) &&
-                           2 * i * k < (int64_t(1) << 31) && ff_aligned(qw_packed, 16);
+  int cw = swiglu_cw(m, i);
+  int bm = cw ? swiglu_bm(m, i / (2 * cw), cw) : 0;
+  const bool aligned = qw_packed && k % kPkKAlign == 0 && m * k < (int64_t(1) << 31) &&
+                       2 * i * k < (int64_t(1) << 31) && ff_aligned(qw_packed, 16);
+  if (!qw) {
+    FF_REQUIRE(aligned, "ff_gemm_fp8_swiglu_static: without the row-major weight, k %% %d and 16-byte alignment",
+               kPkKAlign);
+    if (m == 0) return FF_OK;
+    if (m <= kGemvPkMaxM) {
+      launch_gemv_swiglu_pk<true>(qa, sa, 0, qw_packed, sw, 0, nullptr, ldh, nullptr, hq, inv, m, i, k,
+                                  (hipStream_t)stream);
+      FF_LAUNCH_CHECK("ff_gemm_fp8_swiglu_static");
+      return FF_OK;
+    }
+    if (!bm) swiglu_any_tile(m, i, &cw, &bm);
+  }
+  const bool packed_fits = aligned && bm && m > 4;
   if (!packed_fits) return gemm_swiglu_static_rowmajor(qa, sa, qw, sw, hq, ldh, inv, m, i, k, (hipStream_t)stream);
-  const int64_t tiles_m = (m + bm - 1) / bm;
+  const int64_t tiles_n = i / (2 * cw), tiles_m = (m + bm - 1) / bm;
   bool launched = false;
 #define FF_SWIGLU(BM, CW)                                                                                           \
   if (bm == BM && cw == CW && (launched = true))                                                                    \
@@ -912,22 +1192,36 @@ int gemm_fp8_pk_partials(const void* qa, const float* sa, int sa_rows, const voi
 extern "C" int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, const void* qw, const void* qw_packed,
                               const float* sw, int sw_cols, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k,
                               void* workspace, int64_t workspace_bytes, ff_stream_t stream) {
-  FF_REQUIRE(qa && sa && qw && sw && y, "ff_gemm_fp8_pk: null pointer");
+  FF_REQUIRE(qa && sa && (qw || qw_packed) && sw && y, "ff_gemm_fp8_pk: null pointer");
   const bool pk = qw_packed && ldy % 8 == 0 && ldy >= n && ff_aligned(qa, 16) && ff_aligned(qw_packed, 16) &&
                   ff_aligned(y, 16);
+  hipStream_t st = (hipStream_t)stream;
+  if (!qw) {
+    // only the packed copy: every shape runs on it (the single-row kernels for m <= 4)
+    FF_REQUIRE(pk && n % 16 == 0 && k % 128 == 0 && n * k < (int64_t(1) << 31),
+               "ff_gemm_fp8_pk: without the row-major weight, n %% 16, k %% 128, ldy %% 8 and 16-byte alignment");
+    if (m == 0) return FF_OK;
+    if (m <= kGemvPkMaxM) {
+      launch_gemv_pk(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, st);
+      FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
+      return FF_OK;
+    }
+  }
   const SplitPlan plan = pk ? split_plan(m, n, k) : SplitPlan{};
   const int s = plan.s;
-  hipStream_t st = (hipStream_t)stream;
   if (s == 0) {
-    const SmallTile t = pk ? small_plan(m, n, k) : SmallTile{};
+    const SmallTile t = pk ? small_plan(m, n, k, !qw) : SmallTile{};
     if (t.bm == 64 && t.cw == 64)
       launch_small<64, 64>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, st);
     else if (t.bm == 96)
       launch_small<96, 32>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, st);
     else if (t.bm == 64)
       launch_small<64, 32>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, st);
-    else
+    else if (qw)
       return ff_gemm_fp8(qa, sa, sa_rows, qw, sw, sw_cols, y, ldy, m, n, k, stream);
+    else
+      FF_REQUIRE(false, "ff_gemm_fp8_pk: %lld x %lld x %lld needs the row-major weight (n %% 128, k %% 512)",
+                 (long long)m, (long long)n, (long long)k);
     FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
     return FF_OK;
   }
@@ -970,17 +1264,20 @@ extern "C" int ff_gemm_fp8_qkv_pk(const void* qa, const float* sa, int sa_rows, 
   const int64_t tiles_m = (m + kQkBM - 1) / kQkBM;
   const int cw = forced == 2 || (!forced && tiles_m * (n / 128) <= 512) ? 32 : kQkCW;
   const int64_t tiles_n = n / (4 * cw), tiles = tiles_m * tiles_n;
-  const bool fits = forced != 3 && qw_packed && m > 4 && hq > 0 && hk > 0 && hq % hk == 0 && n % (4 * cw) == 0 &&
-                    k > 0 && k % (128 * kSpU) == 0 && (forced || cw == 32 || (tiles >= 192 && tiles <= 512)) &&
-                    t_pad >= m &&
+  const bool fits = forced != 3 && qw_packed && (m > 4 || !qw) && m > 0 && hq > 0 && hk > 0 && hq % hk == 0 &&
+                    n % (4 * cw) == 0 && k > 0 && k % (128 * kSpU) == 0 &&
+                    (forced || cw == 32 || !qw || (tiles >= 192 && tiles <= 512)) && t_pad >= m &&
                     t_pad % 64 == 0 &&
                     t_pad <= tiles_m * kQkBM && m * k < (int64_t(1) << 31) && n * k < (int64_t(1) << 31) &&
                     ff_aligned(qa, 16) && ff_aligned(qw_packed, 16) && ff_aligned(cos, 16) && ff_aligned(sin, 16) &&
                     ff_aligned(q_norm, 16) && ff_aligned(k_norm, 16) && ff_aligned(yq, 16) && ff_aligned(yk, 16) &&
                     ff_aligned(vt, 16);
-  if (!fits)
+  if (!fits) {
+    FF_REQUIRE(qw, "ff_gemm_fp8_qkv_pk: this shape needs the row-major weight (k %% %d, 16-byte alignment)",
+               128 * kSpU);
     return ff_gemm_fp8_qkv(qa, sa, sa_rows, qw, sw, sw_cols, m, k, hq, hk, q_norm, k_norm, eps_q, eps_k, cos, sin, yq,
                            yk, vt, t_pad, stream);
+  }
   FF_REQUIRE(sa && sw && q_norm && k_norm && yq && yk && vt, "ff_gemm_fp8_qkv_pk: null pointer");
   PkQkv qe{(const bf16_t*)q_norm, (const bf16_t*)k_norm, eps_q, eps_k, (const bf16_t*)cos, (const bf16_t*)sin,
            (bf16_t*)yq, (bf16_t*)yk, (bf16_t*)vt, (int)hq, (int)hk, (int)t_pad};

@@ -412,7 +412,7 @@ int gemm_add_rms(const char* name, const void* qa, const float* sa, int sa_rows,
                  float* scales, float inv, float eps, int64_t start, int64_t nv, ff_stream_t stream) {
   int st = check_rows(name, a, m, n);
   if (st) return st;
-  FF_REQUIRE(qa && sa && qw && sw && y && w && residual && q && (QUANT != kDynamic || scales),
+  FF_REQUIRE(qa && sa && (qw || qw_packed) && sw && y && w && residual && q && (QUANT != kDynamic || scales),
              "%s: null pointer", name);
   FF_REQUIRE(ff_aligned(y, 16) && ff_aligned(w, 16) && ff_aligned(residual, 16) && ff_aligned(q, 8),
              "%s: y, w and residual must be 16-byte aligned, q 8-byte", name);

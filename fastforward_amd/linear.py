@@ -68,11 +68,73 @@ class Linear:
         return op(x).reshape(*x.shape[:-1], op.weight.shape[0])
 
 
+class PackedCodes:
+    """The ``weight`` of a linear that keeps only the MFMA-fragment copy of its
+    e4m3 codes: ``shape``, ``dtype`` and ``device`` of the row-major (N, K)
+    tensor it replaces, and a NULL data pointer, so the entry points that take
+    both copies run on the packed one. A caller that reads the codes gets them
+    unpacked on the device (``rowmajor()``, ``cpu()``, ``view()``), each time."""
+
+    def __init__(self, packed, shape):
+        self._packed = packed
+        self.shape = torch.Size(shape)
+        self.dtype, self.device = E4M3, packed.device
+
+    def data_ptr(self):
+        return 0
+
+    def numel(self):
+        return self.shape[0] * self.shape[1]
+
+    def rowmajor(self):
+        n, k = self.shape
+        w = torch.empty((n, k), device=self.device, dtype=E4M3)
+        call("ff_unpack_weight_fp8", ptr(self._packed), ptr(w), n, k, stream())
+        return w
+
+    def cpu(self):
+        return self.rowmajor().cpu()
+
+    def view(self, dtype):
+        return self.rowmajor().view(dtype)
+
+
+def _single_copy(op, keep_rowmajor):
+    """Pack ``op``'s codes and, unless ``keep_rowmajor``, keep the packed copy
+    alone where the packed kernels take every row count of its shape (n % 128,
+    k % 512): one copy of the weights in HBM."""
+    op.pack()
+    n, k = op.weight.shape
+    if not keep_rowmajor and op.packed is not None and n % 128 == 0 and k % 512 == 0:
+        op.weight = PackedCodes(op.packed, (n, k))
+
+
+def _packed_gemm(op, q, s, s_rows, sw, sw_cols, y):
+    """y = bf16((q . W^T * s) * sw) through ff_gemm_fp8_pk on ``op``'s packed
+    copy, with a k-split workspace the op keeps (calls ordered on one stream)."""
+    m, k = q.shape
+    n = op.weight.shape[0]
+    need = gemm_pk_workspace(m, n, k)
+    ws = getattr(op, "_ws", None)
+    if need and (ws is None or ws.numel() < need):
+        op._ws = ws = torch.empty(need, device=q.device, dtype=torch.uint8)
+    call("ff_gemm_fp8_pk", ptr(q), ptr(s), s_rows, ptr(op.weight), ptr(op.packed), ptr(sw), sw_cols, ptr(y),
+         y.stride(0), m, n, k, ptr(ws) if need else None, need, stream())
+    return y
+
+
 class FP8Linear:
     """Per-channel e4m3 weights + per-token dynamic activation quant
-    (_legacy/fp8_private.py:21-38). ``scale`` is (1, N) fp32 as in the reference."""
+    (_legacy/fp8_private.py:21-38). ``scale`` is (1, N) fp32 as in the reference.
 
-    def __init__(self, weight):
+    The codes are packed into MFMA-fragment order at construction
+    (ff_pack_weight_fp8), the layout every GEMM of this op reads; where the
+    packed kernels take every row count of the shape (n % 128 == 0, k % 512 ==
+    0) that copy is the only one kept and ``weight`` is a ``PackedCodes``
+    (``keep_rowmajor`` keeps the row-major tensor too, for callers of the
+    row-major entry points)."""
+
+    def __init__(self, weight, keep_rowmajor=False):
         assert weight.is_cuda and weight.ndim == 2 and weight.shape[0] % 16 == weight.shape[1] % 16 == 0
         w = weight.detach().to(BF16).contiguous()
         n, k = w.shape
@@ -81,14 +143,14 @@ class FP8Linear:
         call("ff_quant_weight_fp8", ptr(w), ptr(self.weight), ptr(scale), None, n, k, 1, stream())
         self.scale = scale.reshape(1, n)
         self.packed = None
-        self.pack()   # the packed tile kernels are the GEMM path of every caller
+        _single_copy(self, keep_rowmajor)
 
     def pack(self):
         """Add the MFMA-fragment copy of the weight (ff_pack_weight_fp8) that the
-        packed tile kernels read; ``weight`` stays row-major for the other paths."""
+        packed tile kernels read (once; construction already does it)."""
         n, k = self.weight.shape
         if self.packed is None and n % 16 == 0 and k % 128 == 0:
-            self.packed = torch.empty_like(self.weight)
+            self.packed = torch.empty((n, k), device=self.weight.device, dtype=E4M3)
             call("ff_pack_weight_fp8", ptr(self.weight), ptr(self.packed), n, k, stream())
         return self
 
@@ -105,9 +167,9 @@ class FP8Linear:
 
     def gemm(self, q, s, out=None, workspace=None):
         """y = bf16(q_a . W^T * s_a * s_w) from pre-quantized activations. With the
-        packed copy (``pack()``) this is ff_gemm_fp8_pk, whose k split needs a
-        workspace: ``workspace`` if given (a caller's, reused across calls that
-        are ordered on one stream), else one this op keeps."""
+        packed copy this is ff_gemm_fp8_pk, whose k split needs a workspace:
+        ``workspace`` if given (a caller's, reused across calls that are ordered
+        on one stream), else one this op keeps."""
         m, k = q.shape
         n = self.weight.shape[0]
         y = torch.empty((m, n), device=q.device, dtype=BF16) if out is None else out
@@ -116,13 +178,9 @@ class FP8Linear:
                  m, n, k, stream())
             return y
         if workspace is None:
-            need = gemm_pk_workspace(m, n, k)
-            ws = getattr(self, "_ws", None)
-            if need and (ws is None or ws.numel() < need):
-                self._ws = ws = torch.empty(need, device=q.device, dtype=torch.uint8)
-            workspace = ws if need else None
+            return _packed_gemm(self, q, s, 1, self.scale, 1, y)
         call("ff_gemm_fp8_pk", ptr(q), ptr(s), 1, ptr(self.weight), ptr(self.packed), ptr(self.scale), 1, ptr(y),
-             y.stride(0), m, n, k, ptr(workspace), 0 if workspace is None else workspace.numel(), stream())
+             y.stride(0), m, n, k, ptr(workspace), workspace.numel(), stream())
         return y
 
     def __call__(self, x):
@@ -137,7 +195,7 @@ class StaticFP8Linear:
     tensor that callers may update in place (``select``,
     _family/night_runtime.py:48-54); ``inverse_scale`` is the quant multiplier."""
 
-    def __init__(self, weight, inverse_scale=16.):
+    def __init__(self, weight, inverse_scale=16., keep_rowmajor=False):
         w = weight.detach().to(BF16).contiguous()
         n, k = w.shape
         self.weight = torch.empty((n, k), device=w.device, dtype=E4M3)
@@ -149,6 +207,7 @@ class StaticFP8Linear:
         self.input_scale = torch.tensor([1. / inverse_scale], device=w.device, dtype=torch.float32)
         self.fast_accum = True
         self.packed = None
+        _single_copy(self, keep_rowmajor)     # as FP8Linear: the packed copy alone where it serves every shape
 
     pack = FP8Linear.pack
 
@@ -169,6 +228,8 @@ class StaticFP8Linear:
         q = torch.empty((m, k), device=x.device, dtype=E4M3)
         call("ff_quant_static_fp8", ptr(flat), ptr(q), m, m, k, float(self.inverse_scale), stream())
         y = torch.empty((m, n), device=x.device, dtype=BF16)
+        if self.packed is not None:
+            return _packed_gemm(self, q, self.input_scale, 0, self.weight_scale, 0, y)
         call("ff_gemm_fp8", ptr(q), ptr(self.input_scale), 0, ptr(self.weight), ptr(self.weight_scale), 0,
              ptr(y), n, m, n, k, stream())
         return y
@@ -190,8 +251,11 @@ def parity(op, x):
     exact = torch.equal(q.view(torch.uint8), ref.view(torch.uint8))
     new = op(flat)
     prev = torch.empty((m, n), device=flat.device, dtype=BF16)
-    call("ff_gemm_fp8", ptr(ref), ptr(op.input_scale), 0, ptr(op.weight), ptr(op.weight_scale), 0, ptr(prev), n, m, n,
-         k, stream())
+    if op.packed is not None:
+        _packed_gemm(op, ref, op.input_scale, 0, op.weight_scale, 0, prev)
+    else:
+        call("ff_gemm_fp8", ptr(ref), ptr(op.input_scale), 0, ptr(op.weight), ptr(op.weight_scale), 0, ptr(prev), n,
+             m, n, k, stream())
     result = dict(shape=[m, k], inverse_scale=op.inverse_scale, quant_bytes_exact=exact,
                   output_exact=torch.equal(new.reshape(m, n), prev))
     assert exact and result["output_exact"], result

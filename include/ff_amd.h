@@ -179,13 +179,21 @@ int ff_gemm_fp8_swiglu(const void* qa, const float* sa, const void* qw, const fl
  * [128 kt + 32 g + 16, +16) at 1024 + 16 l (two 1 KB planes, one load
  * instruction each). packed holds n * k bytes. n % 16 == 0, k % 128 == 0. */
 int ff_pack_weight_fp8(const void* w, void* packed, int64_t n, int64_t k, ff_stream_t stream);
+/* The inverse (no reference counterpart): the row-major (n, k) codes w from the
+ * packed copy, for callers that keep only the packed copy and read the codes
+ * themselves. n % 16 == 0, k % 128 == 0. */
+int ff_unpack_weight_fp8(const void* packed, void* w, int64_t n, int64_t k, ff_stream_t stream);
 
 /* ff_gemm_fp8_swiglu with an optional packed copy of the same weight
  * (ff_pack_weight_fp8 of qw): identical results (same products and summation
- * order); when qw_packed is given and the shape suits it (i % 192 == 0,
- * k % 512 == 0, m > 4, enough 144 x 384 tiles to fill the GPU) the weights are
- * read from the packed copy straight into the matrix-core operands, otherwise
- * this is ff_gemm_fp8_swiglu on qw. */
+ * order); when qw_packed is given and the shape suits it (k % 512 == 0, m > 4,
+ * i % 192 == 0 for BM x 384 tiles or i % 128 == 0 for BM x 256 tiles with
+ * enough tiles to fill the GPU, or up to 176 tokens with i / 64 >= 192 for one
+ * row tile of 64 channels per workgroup) the weights are read from the packed
+ * copy straight into the matrix-core operands, otherwise this is
+ * ff_gemm_fp8_swiglu on qw. qw may be NULL when the caller keeps only the
+ * packed copy (i % 64 == 0, k % 512 == 0): every m then runs on it, m <= 4 on a
+ * single-row kernel whose fp32 sums differ in order from the row-major one. */
 int ff_gemm_fp8_swiglu_pk(const void* qa, const float* sa, const void* qw, const void* qw_packed,
                           const float* sw, void* h, int64_t ldh, float* pmax, int64_t m, int64_t i, int64_t k,
                           ff_stream_t stream);
@@ -193,12 +201,16 @@ int ff_gemm_fp8_swiglu_pk(const void* qa, const float* sa, const void* qw, const
 /* ff_gemm_fp8 with an optional packed copy of the weight (ff_pack_weight_fp8 of
  * qw) and a workspace (no reference counterpart: the down projection of the
  * step, Linear.apply of scaled_qwen_runtime.py:35-39). When qw_packed is given
- * and the shape suits it (n % 256 == 0, m > 4, and either 192 or more 144 x 256
- * tiles or k >= 8192 with k % 2048 == 0) the weights are read from the packed
- * copy; with fewer tiles k is split 4 ways, each split writes its fp32 partial
- * tile to the workspace and a second launch adds the partials in split order
- * (same math as ff_gemm_fp8 up to the fp32 order of adding the 4 partials;
- * repeatable bit for bit). Otherwise this is ff_gemm_fp8 on qw. workspace:
+ * and the shape suits it the weights are read from the packed copy: 144 x 256
+ * tiles when 192 or more fill the GPU; with fewer tiles and k >= 8192 k split
+ * 2, 3, 4 or 8 ways; up to 256 tokens 64 x 256 tiles with k split 2, 4 or 8
+ * ways; else smaller unsplit tiles (n % 128 == 0, k % 512 == 0). Each split
+ * writes its fp32 partial tile to the workspace and a second launch adds the
+ * partials in split order (same math as ff_gemm_fp8 up to the fp32 order of
+ * adding the partials; repeatable bit for bit). Otherwise this is ff_gemm_fp8
+ * on qw. qw may be NULL when the caller keeps only the packed copy (n % 128 ==
+ * 0, k % 512 == 0): every m then runs on it, m <= 4 on a single-row kernel
+ * whose fp32 sums differ in order from the row-major one. workspace:
  * ff_gemm_fp8_pk_workspace bytes (0 when no split is used), 16-byte aligned;
  * calls that overlap must not share it. */
 int ff_gemm_fp8_pk_workspace(int64_t m, int64_t n, int64_t k, int64_t* bytes);
@@ -240,11 +252,13 @@ int ff_gemm_fp8_qkv(const void* qa, const float* sa, int sa_rows, const void* qw
                     float eps_q, float eps_k, const void* cos, const void* sin, void* yq, void* yk, void* vt,
                     int64_t t_pad, ff_stream_t stream);
 /* ff_gemm_fp8_qkv on the MFMA-fragment copy of qw (ff_pack_weight_fp8):
- * 64-token x 256-channel tiles (two heads) when m > 4, (hq + 2 hk) is even, k
- * % 512 == 0, the grid has 192..512 tiles and t_pad <= the tiles' token range
- * (the 8B step's 576 x 4096 x 6144); the same bits as ff_gemm_fp8_qkv, which
- * it calls for every other shape (qw_packed may then be NULL). Same
- * reference replacement as ff_gemm_fp8_qkv. */
+ * 64-token x 128-channel tiles (one head) while their grid has at most 512
+ * tiles (the 8B step at 576 tokens), else 64-token x 256-channel tiles (two
+ * heads) when the grid has 192..512 tiles, for m > 4, k % 512 == 0 and t_pad
+ * <= the tiles' token range; the same bits as ff_gemm_fp8_qkv, which it calls
+ * for every other shape (qw_packed may then be NULL). qw may be NULL when the
+ * caller keeps only the packed copy: every m then runs on the packed tiles.
+ * Same reference replacement as ff_gemm_fp8_qkv. */
 int ff_gemm_fp8_qkv_pk(const void* qa, const float* sa, int sa_rows, const void* qw, const void* qw_packed,
                        const float* sw, int sw_cols, int64_t m, int64_t k, int64_t hq, int64_t hk,
                        const void* q_norm, const void* k_norm, float eps_q, float eps_k, const void* cos,
@@ -271,7 +285,8 @@ int ff_attention_vt_q(const void* q, const void* k, const void* vt, void* yq, fl
  * e4m3(clamp(h * inv, +-448)) (m, i) with row pitch ldh bytes (inv: the down
  * projection's inverse_scale). The packed tile when qw_packed is given and
  * the shape suits it (as ff_gemm_fp8_swiglu_pk), else the row-major tile or,
- * for m <= 4, the GEMV kernel. */
+ * for m <= 4, the GEMV kernel; with qw NULL (only the packed copy kept) every
+ * m runs on the packed copy, as in ff_gemm_fp8_swiglu_pk. */
 int ff_gemm_fp8_swiglu_static(const void* qa, const float* sa, const void* qw, const void* qw_packed, const float* sw,
                               void* hq, int64_t ldh, float inv, int64_t m, int64_t i, int64_t k, ff_stream_t stream);
 

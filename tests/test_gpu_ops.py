@@ -352,7 +352,7 @@ def test_gemm_fp8_swiglu_packed_equals_rowmajor(gpu, m, i, k):
     from fastforward_amd._lib import call, ptr, stream
     from fastforward_amd.linear import FP8Linear
     x = (torch.randn(m, k, generator=_g(51)) * 2).to(BF16).to(DEV)
-    op = FP8Linear((torch.randn(2 * i, k, generator=_g(52)) * 0.05).to(BF16).to(DEV)).pack()
+    op = FP8Linear((torch.randn(2 * i, k, generator=_g(52)) * 0.05).to(BF16).to(DEV), keep_rowmajor=True)
     qa, sa = op.quantize(x)
     outs = []
     for entry in ("ff_gemm_fp8_swiglu", "ff_gemm_fp8_swiglu_pk"):
@@ -387,7 +387,7 @@ def test_gemm_fp8_pk_matches_rowmajor(gpu, m, n, k, bm, splits):
     from fastforward_amd._lib import call, ptr, stream
     from fastforward_amd.linear import FP8Linear, gemm_pk_workspace
     x = (torch.randn(m, k, generator=_g(60)) * 2).to(BF16).to(DEV)
-    op = FP8Linear((torch.randn(n, k, generator=_g(61)) * 0.03).to(BF16).to(DEV)).pack()
+    op = FP8Linear((torch.randn(n, k, generator=_g(61)) * 0.03).to(BF16).to(DEV), keep_rowmajor=True)
     qa, sa = op.quantize(x)
     need = gemm_pk_workspace(m, n, k)
     # the split count itself: fp32 partials of bm x 256 tiles over the rows padded to whole tiles
@@ -429,7 +429,7 @@ def test_gemm_fp8_pk_add_rms_equals_unfused(gpu, m, n, k, static, deep):
     from fastforward_amd._lib import call, ptr, stream
     from fastforward_amd.linear import FP8Linear, gemm_pk_workspace
     x = (torch.randn(m, k, generator=_g(64)) * 2).to(BF16).to(DEV)
-    op = FP8Linear((torch.randn(n, k, generator=_g(65)) * 0.03).to(BF16).to(DEV)).pack()
+    op = FP8Linear((torch.randn(n, k, generator=_g(65)) * 0.03).to(BF16).to(DEV))
     qa, sa = op.quantize(x)
     a = (torch.randn(m, n, generator=_g(66)) * 4).to(BF16).to(DEV)
     w = (1 + 0.1 * torch.randn(n, generator=_g(67))).to(BF16).to(DEV)
@@ -470,7 +470,7 @@ def test_gemm_fp8_pk_scalar_scales(gpu):
     from fastforward_amd.linear import FP8Linear, gemm_pk_workspace
     m, n, k = 576, 4096, 8192
     x = (torch.randn(m, k, generator=_g(62))).to(BF16).to(DEV)
-    op = FP8Linear((torch.randn(n, k, generator=_g(63)) * 0.03).to(BF16).to(DEV)).pack()
+    op = FP8Linear((torch.randn(n, k, generator=_g(63)) * 0.03).to(BF16).to(DEV), keep_rowmajor=True)
     qa, _ = op.quantize(x)
     sa, sw = torch.tensor([0.01], device=DEV), torch.tensor([0.002], device=DEV)
     ws = torch.zeros(gemm_pk_workspace(m, n, k), device=DEV, dtype=torch.uint8)
@@ -850,7 +850,8 @@ def test_gemm_swiglu_static_equals_unfused(gpu, m, i, k):
     from fastforward_amd import ops
     from fastforward_amd._lib import call, ptr, stream
     from fastforward_amd.linear import StaticFP8Linear
-    op = StaticFP8Linear((torch.randn(2 * i, k, generator=_g(77)) * 0.03).to(BF16).to(DEV), 448.0 / 5.0).pack()
+    op = StaticFP8Linear((torch.randn(2 * i, k, generator=_g(77)) * 0.03).to(BF16).to(DEV), 448.0 / 5.0,
+                         keep_rowmajor=True)
     x = torch.randn(m, k, generator=_g(78)).to(BF16).to(DEV)
     qa = torch.empty(m, k, device=DEV, dtype=torch.uint8)
     call("ff_quant_static_fp8", ptr(x), ptr(qa), m, m, k, float(op.inverse_scale), stream())
@@ -893,3 +894,116 @@ def test_gemm_qkv_static_scales_equal_unfused(gpu):
     call("ff_gemm_fp8_qkv", ptr(qa_d), ptr(sa), 0, ptr(qw_d), ptr(sw), 0, t, k, hq, hk, ptr(qn.weight),
          ptr(kn.weight), 1e-6, 1e-6, ptr(cos), ptr(sin), ptr(yq), ptr(yk), ptr(vt), tp, stream())
     assert torch.equal(yq, rq) and torch.equal(yk, rk) and torch.equal(vt, rv)
+
+
+# ------------------------------------------------------------------ one weight copy
+
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 4096), (3, 12288, 4096), (4, 4096, 6144), (5, 4096, 4096),
+                                   (17, 4096, 6144), (176, 4096, 4096), (576, 12288, 4096)])
+def test_fp8linear_keeps_one_copy(gpu, m, k, n):
+    """FP8Linear keeps only the MFMA-fragment copy of its codes: ``weight`` is a
+    stand-in with a NULL data pointer whose unpacked codes (ff_unpack_weight_fp8)
+    equal the oracle's quantisation bit for bit, and op(x) runs on the packed
+    copy alone: bit-identical to the op that also keeps the row-major codes for
+    m > 4 (the same packed tiles), and within the exact-product bound for the
+    single-row kernel (m <= 4; its fp32 sums are in another order than the
+    row-major GEMV's)."""
+    from fastforward_amd.linear import FP8Linear, PackedCodes
+    x = torch.randn(m, k, generator=_g(90))
+    x[torch.rand(m, k, generator=_g(91)) < 0.001] *= 20
+    x = x.to(BF16)
+    w = (torch.randn(n, k, generator=_g(92)) * 0.02).to(BF16)
+    one = FP8Linear(w.to(DEV))
+    two = FP8Linear(w.to(DEV), keep_rowmajor=True)
+    assert isinstance(one.weight, PackedCodes) and one.weight.data_ptr() == 0 and tuple(one.weight.shape) == (n, k)
+    qw, sw = O.fp8_weight_quant(w)
+    assert torch.equal(one.weight.cpu().view(torch.uint8), qw.view(torch.uint8))
+    xd = x.to(DEV)
+    y1, y2 = one(xd), two(xd)
+    if m > 4:
+        assert torch.equal(y1, y2)
+    qa, sa = O.quant_rows_dynamic(x)
+    _assert_fp8_gemm(y1.cpu(), qa, sa, qw, sw, O.fp8_gemm(qa, sa, qw, sw), f"one-copy FP8Linear {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("m,i,k", [(1, 12288, 4096), (3, 6144, 2048), (4, 640, 512), (20, 6144, 2048)])
+def test_swiglu_single_copy_rows(gpu, m, i, k):
+    """The gate/up + SwiGLU launch on the packed copy alone (qw NULL): for m <= 4
+    the single-row kernel adds g and u in the order of the plain single-row
+    kernel, so h equals the oracle's swiglu of ff_gemm_fp8_pk's g and u on the
+    same codes (<= 1 ulp from the SiLU rounding) with its row maxima, and the
+    static form writes the runtime-scale cast of that h; m > 4 takes a packed
+    tile whatever its grid (20 rows: fewer than 192 workgroups) and equals the
+    launch that keeps the row-major weight."""
+    from fastforward_amd import ops
+    from fastforward_amd._lib import call, ptr, stream
+    from fastforward_amd.linear import FP8Linear, StaticFP8Linear
+    w = (torch.randn(2 * i, k, generator=_g(93)) * 0.04).to(BF16).to(DEV)
+    op = FP8Linear(w)
+    x = torch.randn(m, k, generator=_g(94)).to(BF16).to(DEV)
+    qa, sa = op.quantize(x)
+    h = torch.full((m, i), float("nan"), device=DEV, dtype=BF16)
+    pmax = torch.full((m, i // 64), float("nan"), device=DEV)
+    call("ff_gemm_fp8_swiglu_pk", ptr(qa), ptr(sa), None, ptr(op.packed), ptr(op.scale), ptr(h), i, ptr(pmax), m, i,
+         k, stream())
+    if m > 4:
+        two = FP8Linear(w, keep_rowmajor=True)
+        h2 = torch.full((m, i), float("nan"), device=DEV, dtype=BF16)
+        p2 = torch.full((m, i // 64), float("nan"), device=DEV)
+        call("ff_gemm_fp8_swiglu_pk", ptr(qa), ptr(sa), ptr(two.weight), ptr(two.packed), ptr(two.scale), ptr(h2), i,
+             ptr(p2), m, i, k, stream())
+        assert torch.equal(h, h2) and torch.equal(pmax, p2)
+        return
+    raw = op.gemm(qa, sa)
+    want = ops.swiglu(*raw.chunk(2, -1))
+    assert_bf16_close(h.cpu(), want.cpu(), 1, 1e-3, "single-row swiglu vs swiglu(plain single-row product)")
+    assert torch.equal(pmax.cpu(), h.cpu().float().abs().view(m, i // 64, 64).amax(-1))
+    # the static form: per-tensor scales, h written as its runtime-scale cast
+    st = StaticFP8Linear(w, 448.0 / 4.0)
+    qs = torch.empty(m, k, device=DEV, dtype=torch.uint8)
+    call("ff_quant_static_fp8", ptr(x), ptr(qs), m, m, k, float(st.inverse_scale), stream())
+    inv = 448.0 / 0.5
+    got = torch.full((m, i), 0xAA, device=DEV, dtype=torch.uint8)
+    call("ff_gemm_fp8_swiglu_static", ptr(qs), ptr(st.input_scale), None, ptr(st.packed), ptr(st.weight_scale),
+         ptr(got), i, inv, m, i, k, stream())
+    raw_s = torch.empty(m, 2 * i, device=DEV, dtype=BF16)
+    call("ff_gemm_fp8_pk", ptr(qs), ptr(st.input_scale), 0, None, ptr(st.packed), ptr(st.weight_scale), 0,
+         ptr(raw_s), 2 * i, m, 2 * i, k, None, 0, stream())
+    hs = ops.swiglu(*raw_s.chunk(2, -1)).contiguous()
+    want_q = torch.empty(m, i, device=DEV, dtype=torch.uint8)
+    call("ff_quant_static_fp8", ptr(hs), ptr(want_q), m, m, i, inv, stream())
+    d = (got.cpu().view(torch.float8_e4m3fn).float() - want_q.cpu().view(torch.float8_e4m3fn).float()).abs()
+    # codes of h values one bf16 ulp apart (the SiLU rounding) can differ by one e4m3 step
+    assert float((d > 0).float().mean()) <= 2e-3
+
+
+@pytest.mark.parametrize("t", [3, 33])
+def test_qkv_single_copy_short(gpu, t):
+    """The QKV launch on the packed copy alone (qw NULL) for prompts the packed
+    tile's plan would leave to the row-major kernel (3 and 33 tokens) runs the
+    packed tile and equals ff_gemm_fp8_qkv on the row-major codes bit for bit."""
+    from fastforward_amd._lib import call, ptr, stream
+    from fastforward_amd.linear import FP8Linear
+    d, hq, hk, k = 128, 32, 8, 4096
+    tp, n = (t + 63) // 64 * 64, (hq + 2 * hk) * d
+    op = FP8Linear((torch.randn(n, k, generator=_g(95)) * 0.02).to(BF16).to(DEV), keep_rowmajor=True)
+    x = torch.randn(t, k, generator=_g(96)).to(BF16).to(DEV)
+    qa, sa = op.quantize(x)
+    qn = (1 + 0.2 * torch.randn(d, generator=_g(97))).to(BF16).to(DEV)
+    kn = (1 + 0.2 * torch.randn(d, generator=_g(98))).to(BF16).to(DEV)
+    cos = torch.randn(t, d, generator=_g(99)).to(BF16).to(DEV)
+    sin = torch.randn(t, d, generator=_g(100)).to(BF16).to(DEV)
+    outs = []
+    for qw in (ptr(op.weight), None):
+        yq = torch.full((hq, t, d), float("nan"), device=DEV, dtype=BF16)
+        yk = torch.full((hk, t, d), float("nan"), device=DEV, dtype=BF16)
+        vt = torch.full((hk, d, tp), float("nan"), device=DEV, dtype=BF16)
+        if qw is None:
+            call("ff_gemm_fp8_qkv_pk", ptr(qa), ptr(sa), 1, None, ptr(op.packed), ptr(op.scale), 1, t, k, hq, hk,
+                 ptr(qn), ptr(kn), 1e-6, 1e-6, ptr(cos), ptr(sin), ptr(yq), ptr(yk), ptr(vt), tp, stream())
+        else:
+            call("ff_gemm_fp8_qkv", ptr(qa), ptr(sa), 1, qw, ptr(op.scale), 1, t, k, hq, hk, ptr(qn), ptr(kn), 1e-6,
+                 1e-6, ptr(cos), ptr(sin), ptr(yq), ptr(yk), ptr(vt), tp, stream())
+        outs.append((yq, yk, vt))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
