@@ -497,6 +497,7 @@ def main():
             extras[key] = production_extras(cfg, mode, args)
             log(f"{key} {extras[key]}")
         for key, preset, mode, tokens, gx, n_opt in (
+                ("fp8_8b_176_lm_step_ms", args.preset, "fp8", 176, (10, 10), 8),
                 ("fp8_static_8b_576_step_ms", args.preset, "fp8_static", T, grid, 8),
                 ("w4a16_g128_8b_576_step_ms", args.preset, "w4a16", T, grid, 8),
                 ("fp8_2b_320_step_ms", "qwen3vl-2b", "fp8", 320, (16, 16), 4),
