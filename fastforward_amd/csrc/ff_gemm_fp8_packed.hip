@@ -607,6 +607,17 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k) {
       if (t64 * sp <= 256 && kt % (sp * kSpU) == 0) return SplitPlan{64, sp};
   }
   if (kt < 64) return p;
+  // 64 k steps (the 32B o projection, 1024 x 8192 x 5120): where an unsplit
+  // small tile (small_plan) fills the GPU on its own, no split: 8 splits of
+  // 144 x 256 tiles wrote and read back 168 MB of fp32 partials (32B step
+  // 47.40 -> 43.97 ms on unsplit 64 x 256 tiles; 44.57 ms split 2 ways).
+  if (kt == 64) {
+    constexpr int cand[3][2] = {{64, 64}, {96, 32}, {64, 32}};
+    for (const auto& c : cand) {
+      const int64_t t = (m + c[0] - 1) / c[0] * (n / (4 * c[1]));
+      if (n % (4 * c[1]) == 0 && t >= 192 && t <= 512) return p;
+    }
+  }
   // The split count (2, 3, 4 or 8) with the fewest k steps per CU: rounds of
   // 256 workgroups (one per CU) x kt / S steps each, ties to fewer splits
   // (less partial traffic). 8B down (k = 12288): 176 tokens 8 splits, 576
