@@ -421,14 +421,19 @@ __global__ __launch_bounds__(kThreads, BM < 144 ? 2 : 1) void gemm_fp8_split_pac
   const int split = rest % S, tn = rest / S;
   const int m0 = tm * BM, n0 = tn * BN;
   const int tid = threadIdx.x, wave = tid >> 6;
-  const int KT = K / 128, nk = KT / S;
+  // this split's k steps: the kt / U blocks of U steps (U = the main loop's
+  // unrolled steps) dealt out as evenly as whole blocks allow, so k need not
+  // divide by S U (32B down, 200 steps: 3 splits of 68, 68 and 64)
+  constexpr int U = lcm3(P, D, 2 * G);
+  const int nbk = K / (128 * U);
+  const int kt0 = split * nbk / S * U, nk = (split + 1) * nbk / S * U - kt0;
 
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   uint32_t sB[TJ];
 #pragma unroll
   for (int j = 0; j < TJ; ++j) sB[j] = (uint32_t)((n0 + wave_s * CW + 16 * j) / 16) * 2048u;
   f32x4 acc[RA][TJ];
-  pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, split * nk, nk, [] {});
+  pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, kt0, nk, [] {});
   if constexpr (S > 1) {
     // the fp32 partial tile, row-major over the rows padded to whole tiles
     store_tile_rows_lds<BM, CW, SMEM>(acc, smem, part + ((int64_t)split * tiles_m * BM + m0) * N + n0, N, tid);
@@ -585,7 +590,8 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k) {
   const int forced = ff_tuning(FF_TUNE_FP8_PK_SPLIT);
   if (forced) {
     const int bm = forced / 100, sp = forced % 100;
-    if ((bm == 64 || bm == kSpBM) && (sp == 1 || sp == 2 || sp == 3 || sp == 4 || sp == 8) && kt % (sp * kSpU) == 0) {
+    if ((bm == 64 || bm == kSpBM) && (sp == 1 || sp == 2 || sp == 3 || sp == 4 || sp == 8) && kt % kSpU == 0 &&
+        kt / kSpU >= sp) {
       p.bm = bm;
       p.s = sp;
     }
@@ -619,14 +625,18 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k) {
     }
   }
   // The split count (2, 3, 4 or 8) with the fewest k steps per CU: rounds of
-  // 256 workgroups (one per CU) x kt / S steps each, ties to fewer splits
-  // (less partial traffic). 8B down (k = 12288): 176 tokens 8 splits, 576
-  // tokens 4 in one round, 640 tokens 3 in one round (4 would take two),
-  // 1152 tokens 2.
+  // 256 workgroups (one per CU) x the longest split's steps (whole blocks of
+  // kSpU steps, dealt out as evenly as they go), ties to fewer splits (less
+  // partial traffic). 8B down (k = 12288): 576 tokens 4 in one round, 640
+  // tokens 3 in one round (4 would take two), 1152 tokens 2; 32B down (1024 x
+  // 25600 x 5120, 160 tiles) 3 in two rounds of 68 steps, where 2 splits took
+  // two rounds of 100.
+  if (kt % kSpU) return p;
+  const int64_t nbk = kt / kSpU;
   int64_t best_steps = 0;
   for (int sp = 2; sp <= 8; sp += sp < 4 ? 1 : 4) {
-    if (kt % (sp * kSpU)) continue;
-    const int64_t steps = (tiles * sp + 255) / 256 * (kt / sp);
+    if (nbk < sp) continue;
+    const int64_t steps = (tiles * sp + 255) / 256 * ((nbk + sp - 1) / sp * kSpU);
     if (p.s == 0 || steps < best_steps) {
       p = SplitPlan{kSpBM, sp};
       best_steps = steps;
