@@ -79,6 +79,9 @@ SIGNATURES = {
     "ff_gemm_bf16": [P, I64, P, P, P, I64, P, I64, I64, I64, I64, I32, P],
     "ff_pack_weight_bf16": [P, P, I64, I64, P],
     "ff_gemm_bf16_pk": [P, I64, P, P, P, P, I64, P, I64, I64, I64, I64, I32, P],
+    "ff_gemm_bf16_pk_workspace": [I64, I64, I64, PI64],
+    "ff_gemm_bf16_pk_ws": [P, I64, P, P, P, P, I64, P, I64, I64, I64, I64, I32, P, I64, P],
+    "ff_gemm_bf16_pk_ln": [P, I64, P, P, P, P, I64, P, I64, I64, I64, I64, P, I64, P, P, F32, P, I64, P],
     "ff_vision_rope": [P, P, I64, I64, P, P, P, P, I64, I64, I64, I64, I64, I64, P],
     "ff_vision_vt": [P, I64, I64, P, I64, I64, I64, I64, P],
     "ff_attention_full": [P, P, P, P, I64, I64, I64, I64, F32, P],

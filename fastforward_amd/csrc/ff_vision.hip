@@ -73,10 +73,53 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return t;
 }
 
+// Columns [col, col + 8) of row `row` of a k-split GEMM's output: the S fp32
+// partial rows added in split order, then bf16(sum + bias) and, with a
+// residual row r, bf16(r + that): the epilogue of gemm_bf16_kernel (no
+// activation) on the split sums. The results are bf16 values held as floats.
+__device__ __forceinline__ void split_row8(const float* __restrict__ part, int splits, int64_t mp, int n, int64_t row,
+                                           int col, const bf16_t* __restrict__ bias, const bf16_t* r, float (&v)[8]) {
+  const float* src = part + row * n + col;
+  f32x4 s0 = *reinterpret_cast<const f32x4*>(src), s1 = *reinterpret_cast<const f32x4*>(src + 4);
+  for (int sp = 1; sp < splits; ++sp) {
+    const f32x4 t0 = *reinterpret_cast<const f32x4*>(src + sp * mp * n);
+    const f32x4 t1 = *reinterpret_cast<const f32x4*>(src + sp * mp * n + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      s0[e] += t0[e];
+      s1[e] += t1[e];
+    }
+  }
+  float bv[8];
+  unpack8(*reinterpret_cast<const u32x4*>(bias + col), bv);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = round_bf16(s0[e] + bv[e]);
+    v[4 + e] = round_bf16(s1[e] + bv[4 + e]);
+  }
+  if (r) {
+    float rv[8];
+    unpack8(*reinterpret_cast<const u32x4*>(r + col), rv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = round_bf16(rv[e] + v[e]);
+  }
+}
+
+// PART: the row is first formed from the S fp32 partial rows of a k-split
+// GEMM (added in split order) as that GEMM's epilogue would: y = bf16(r +
+// bf16(sum + bias)) with the residual r; y is stored (yres, which may be r
+// itself: each element is read and written by one thread) and normalised.
+// x is unused then.
+template <bool PART = false>
 __global__ __launch_bounds__(kThreads) void layer_norm_kernel(const bf16_t* __restrict__ x, int64_t x_rs,
                                                               const bf16_t* __restrict__ w,
                                                               const bf16_t* __restrict__ b, bf16_t* __restrict__ y,
-                                                              int64_t y_rs, int h, float eps) {
+                                                              int64_t y_rs, int h, float eps,
+                                                              const float* __restrict__ part = nullptr,
+                                                              int splits = 0, int64_t mp = 0,
+                                                              const bf16_t* __restrict__ bias = nullptr,
+                                                              const bf16_t* resid = nullptr, int64_t ldr = 0,
+                                                              bf16_t* yres = nullptr, int64_t ldyres = 0) {
   __shared__ float red[kThreads / 64];
   const int64_t row = blockIdx.x;
   const bf16_t* xr = x + row * x_rs;
@@ -86,7 +129,12 @@ __global__ __launch_bounds__(kThreads) void layer_norm_kernel(const bf16_t* __re
   for (int c = 0; c < kLnChunks; ++c) {
     const int col = 8 * (threadIdx.x + kThreads * c);
     if (col < h) {
-      unpack8(*reinterpret_cast<const u32x4*>(xr + col), v[c]);
+      if constexpr (PART) {
+        split_row8(part, splits, mp, h, row, col, bias, resid ? resid + row * ldr : nullptr, v[c]);
+        *reinterpret_cast<u32x4*>(yres + row * ldyres + col) = pack8(v[c]);
+      } else {
+        unpack8(*reinterpret_cast<const u32x4*>(xr + col), v[c]);
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) s += v[c][e];
     }
@@ -293,10 +341,16 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_bf16_kernel(
 // step kt is reloaded with step kt + 2's right after its MFMAs issue.
 constexpr int kBfStep = 128;  // k per step of the packed kernel
 
-template <int BM, int CW, int ACT, bool RESID>
+// PART (k split): workgroup (tile, split) runs k steps [split KT / S, (split
+// + 1) KT / S) and stores its fp32 sums, row-major over the rows padded to
+// whole tiles, at part[(split tiles_m BM + row) N + col] instead of y; the
+// launch that follows adds the S partials in split order and applies the
+// epilogue (bf16_split_reduce_kernel, or layer_norm_kernel<true>).
+template <int BM, int CW, int ACT, bool RESID, bool PART = false>
 __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_pk_kernel(
     const bf16_t* __restrict__ a, int64_t lda, const uint8_t* __restrict__ wp, const bf16_t* __restrict__ bias,
-    bf16_t* y, int64_t ldy, const bf16_t* resid, int64_t ldr, int M, int N, int K, int tiles_m, int tiles_n) {
+    bf16_t* y, int64_t ldy, const bf16_t* resid, int64_t ldr, int M, int N, int K, int tiles_m, int tiles_n,
+    int splits = 1, float* __restrict__ part = nullptr) {
   constexpr int RA = BM / 16, TJ = CW / 16;
   constexpr int A_CHUNKS = BM * 16;  // 16-byte chunks of one stage
   constexpr int FULL = A_CHUNKS / kThreads, REM = A_CHUNKS % kThreads;
@@ -305,14 +359,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_pk_kernel(
   static_assert(A_CHUNKS >= kThreads, "at least one full activation round");
   __shared__ __align__(1024) uint8_t smem[2 * STAGE];
 
-  const int nblk = tiles_m * tiles_n;
+  const int S = PART ? splits : 1;
+  const int nblk = tiles_m * tiles_n * S;
   int logical = blockIdx.x;
   if (nblk % kXcds == 0) logical = (blockIdx.x % kXcds) * (nblk / kXcds) + blockIdx.x / kXcds;
-  const int tm = logical % tiles_m, tn = logical / tiles_m;  // M fastest: an XCD's tiles share weight slabs
+  const int tm = logical % tiles_m, rest = logical / tiles_m;  // M fastest: an XCD's tiles share weight slabs
+  const int split = rest % S, tn = rest / S;
   const int m0 = tm * BM, n0 = tn * 4 * CW;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g = lane >> 4;
   const int KT = K / kBfStep;
+  const int kt0 = split * KT / S, kt1 = (split + 1) * KT / S;  // S <= KT: every split has a step
 
   // Activations: chunk c = tid + 256 i is row c / 16, chunk c % 16 (a partial
   // last round is moved back over the last 256 chunks, writing the overlap
@@ -361,23 +418,23 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_pk_kernel(
 #pragma unroll
     for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  loadA(0);
-  loadB(0, 0);
+  loadA(kt0);
+  loadB(kt0, 0);
   writeA(0);
-  loadA(min(1, KT - 1));
-  loadB(min(1, KT - 1), 1);
+  loadA(min(kt0 + 1, kt1 - 1));
+  loadB(min(kt0 + 1, kt1 - 1), 1);
 
   const int frag = 128 * (r16 & 7) + 1024 * (r16 >> 3);
   const int cA[2] = {16 * ((2 * g) ^ (r16 >> 1)), 16 * ((2 * g + 1) ^ (r16 >> 1))};
-  for (int kb = 0; kb < KT; kb += 2) {
+  for (int kb = kt0; kb < kt1; kb += 2) {
     static_for<0, 2>([&](auto U_) {
       constexpr int u = decltype(U_)::value;
       const int kt = kb + u;
-      if (kt < KT) {  // uniform: an odd step count ends on u = 0
+      if (kt < kt1) {  // uniform: an odd step count ends on u = 0
         // stage u (written during the previous step) is visible; stage u ^ 1,
         // read in the previous step, is free for step kt + 1
         __syncthreads();
-        const int kta = min(kt + 2, KT - 1);
+        const int kta = min(kt + 2, kt1 - 1);
         writeA(u ^ 1);
         loadA(kta);
         const uint8_t* st = smem + u * STAGE + frag;
@@ -406,6 +463,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_pk_kernel(
 
   // lane (r16, g) of fragment (i, j): row m0 + 16 i + r16, columns
   // n0 + wave CW + 16 j + 4 g .. + 3; the epilogue of gemm_bf16_kernel
+  if constexpr (PART) {
+    float* dst = part + ((int64_t)split * tiles_m * BM + m0 + r16) * N + n0 + wave * CW + 4 * g;
+#pragma unroll
+    for (int i = 0; i < RA; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) *reinterpret_cast<f32x4*>(dst + (int64_t)16 * i * N + 16 * j) = acc[i][j];
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < RA; ++i) {
     const int m = m0 + 16 * i + r16;
@@ -433,6 +498,35 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_pk_kernel(
       *reinterpret_cast<u32x2*>(y + (int64_t)m * ldy + n) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
     }
   }
+}
+
+// The epilogue of gemm_bf16_kernel on a k-split launch's S fp32 partial rows
+// (added in split order): y = bf16(sum + bias), then the activation, then the
+// residual add; one thread per 8 columns.
+template <int ACT, bool RESID>
+__global__ __launch_bounds__(kThreads) void bf16_split_reduce_kernel(const float* __restrict__ part, int splits,
+                                                                     int64_t mp, const bf16_t* __restrict__ bias,
+                                                                     bf16_t* y, int64_t ldy, const bf16_t* resid,
+                                                                     int64_t ldr, int M, int N) {
+  const int nc = N / 8;
+  const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (e >= (int64_t)M * nc) return;
+  const int64_t m = e / nc;
+  const int col = (int)(e % nc) * 8;
+  float v[8];
+  split_row8(part, splits, mp, N, m, col, bias, nullptr, v);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if constexpr (ACT == kGeluTanh) v[i] = round_bf16(gelu_tanh(v[i]));
+    if constexpr (ACT == kGeluErf) v[i] = round_bf16(gelu_erf(v[i]));
+  }
+  if constexpr (RESID) {
+    float rv[8];
+    unpack8(*reinterpret_cast<const u32x4*>(resid + m * ldr + col), rv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = round_bf16(rv[i] + v[i]);
+  }
+  *reinterpret_cast<u32x4*>(y + m * ldy + col) = pack8(v);
 }
 
 // Weight copy in the packed kernel's operand order: one thread per 16-byte
@@ -685,6 +779,72 @@ void launch_gemm_pk(const void* a, int64_t lda, const void* wp, const void* bias
 #undef FF_G
 }
 
+// k split of the packed GEMM for grids with no one-round tile (bf16pk_tile 0:
+// the tower at short patch counts, e.g. 400 patches: proj and fc2 have 63 tiles
+// of 64 x 128, the mergers 72): the (BM, CW) tile and split count S in {2, 3,
+// 4, 8} whose grid of tiles x S workgroups lies in 192 .. 256 (one round at
+// one per CU) with the least work per workgroup (k steps per split x BM x CW);
+// s = 0 when none. ff_set_tuning(FF_TUNE_BF16_PK_SPLIT, 1) turns splits off,
+// 2 .. 8 forces the split count.
+struct Bf16Split {
+  int bm = 0, cw = 0, s = 0;
+};
+Bf16Split bf16pk_split(int64_t m, int64_t n, int64_t k) {
+  Bf16Split p;
+  const int forced = ff_tuning(FF_TUNE_BF16_PK_SPLIT);
+  if (forced == 1 || m <= 0 || k % kBfStep || bf16pk_tile(m, n)) return p;
+  const int64_t kt = k / kBfStep;
+  constexpr int cand[4][2] = {{64, 32}, {64, 48}, {64, 64}, {128, 48}};
+  constexpr int spl[4] = {2, 3, 4, 8};
+  int64_t best = 0;
+  for (const auto& c : cand) {
+    if (n % (4 * c[1])) continue;
+    const int64_t t = (m + c[0] - 1) / c[0] * (n / (4 * c[1]));
+    for (const int sp : spl) {
+      if ((forced && sp != forced) || sp > kt || t * sp < 192 || t * sp > 256) continue;
+      const int64_t cost = (kt + sp - 1) / sp * c[0] * c[1];
+      if (p.s == 0 || cost < best) {
+        p = Bf16Split{c[0], c[1], sp};
+        best = cost;
+      }
+    }
+  }
+  return p;
+}
+
+int64_t bf16pk_split_bytes(const Bf16Split& p, int64_t m, int64_t n) {
+  return p.s < 2 ? 0 : (m + p.bm - 1) / p.bm * p.bm * n * p.s * 4;
+}
+
+template <int BM, int CW>
+void launch_gemm_pk_part(const void* a, int64_t lda, const void* wp, int64_t m, int64_t n, int64_t k, int splits,
+                         void* part, hipStream_t st) {
+  const int tiles_m = (int)((m + BM - 1) / BM), tiles_n = (int)(n / (4 * CW));
+  hipLaunchKernelGGL((gemm_bf16_pk_kernel<BM, CW, kActNone, false, true>), dim3((unsigned)(tiles_m * tiles_n * splits)),
+                     dim3(kThreads), 0, st, (const bf16_t*)a, lda, (const uint8_t*)wp, nullptr, nullptr, 0, nullptr, 0,
+                     (int)m, (int)n, (int)k, tiles_m, tiles_n, splits, (float*)part);
+}
+
+// The split GEMM's partials for plan p (the packed kernel's conditions and the
+// workspace already checked).
+void launch_split_part(const Bf16Split& p, const void* a, int64_t lda, const void* wp, int64_t m, int64_t n, int64_t k,
+                       void* part, hipStream_t st) {
+  if (p.bm == 64 && p.cw == 32) launch_gemm_pk_part<64, 32>(a, lda, wp, m, n, k, p.s, part, st);
+  else if (p.bm == 64 && p.cw == 48) launch_gemm_pk_part<64, 48>(a, lda, wp, m, n, k, p.s, part, st);
+  else if (p.bm == 64 && p.cw == 64) launch_gemm_pk_part<64, 64>(a, lda, wp, m, n, k, p.s, part, st);
+  else launch_gemm_pk_part<128, 48>(a, lda, wp, m, n, k, p.s, part, st);
+}
+
+// Whether a call can take the k split: the packed kernel's operand limits and
+// the 16-byte accesses of the split epilogue.
+bool bf16_split_ok(const void* a, int64_t lda, const void* w_packed, const void* bias, const void* y, int64_t ldy,
+                   const void* resid, int64_t ldr, int64_t m, int64_t n, int64_t k) {
+  return w_packed && a && bias && y && m > 0 && lda >= k && lda % 8 == 0 && ldy >= n && ldy % 8 == 0 &&
+         (!resid || (ldr >= n && ldr % 8 == 0 && ff_aligned(resid, 16))) && ff_aligned(w_packed, 16) &&
+         ff_aligned(a, 16) && ff_aligned(bias, 16) && ff_aligned(y, 16) && m * lda * 2 < (int64_t(1) << 31) &&
+         n * k * 2 < (int64_t(1) << 31);
+}
+
 }  // namespace
 
 extern "C" int ff_pack_pixels(const void* rgb, void* out, int64_t height, int64_t width, ff_stream_t stream) {
@@ -709,7 +869,7 @@ extern "C" int ff_layer_norm(const void* x, int64_t x_rs, const void* w, const v
   FF_REQUIRE(ff_aligned(x, 16) && ff_aligned(w, 16) && ff_aligned(b, 16) && ff_aligned(y, 16),
              "ff_layer_norm: alignment");
   if (rows == 0) return FF_OK;
-  hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)rows), dim3(kThreads), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(layer_norm_kernel<false>, dim3((unsigned)rows), dim3(kThreads), 0, (hipStream_t)stream,
                      (const bf16_t*)x, x_rs, (const bf16_t*)w, (const bf16_t*)b, (bf16_t*)y, y_rs, (int)h, eps);
   FF_LAUNCH_CHECK("ff_layer_norm");
   return FF_OK;
@@ -784,6 +944,72 @@ extern "C" int ff_gemm_bf16_pk(const void* a, int64_t lda, const void* w, const 
   else
     launch_gemm_pk<64, 32>(a, lda, w_packed, bias, y, ldy, resid, ldr, m, n, k, act, st);
   FF_LAUNCH_CHECK("ff_gemm_bf16_pk");
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_bf16_pk_workspace(int64_t m, int64_t n, int64_t k, int64_t* bytes) {
+  FF_REQUIRE(bytes && m >= 0 && n >= 0 && k >= 0, "ff_gemm_bf16_pk_workspace: bad arguments");
+  *bytes = bf16pk_split_bytes(bf16pk_split(m, n, k), m, n);
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_bf16_pk_ws(const void* a, int64_t lda, const void* w, const void* w_packed, const void* bias,
+                                  void* y, int64_t ldy, const void* resid, int64_t ldr, int64_t m, int64_t n, int64_t k,
+                                  int act, void* workspace, int64_t workspace_bytes, ff_stream_t stream) {
+  const Bf16Split p = bf16_split_ok(a, lda, w_packed, bias, y, ldy, resid, ldr, m, n, k) ? bf16pk_split(m, n, k)
+                                                                                          : Bf16Split{};
+  if (p.s < 2) return ff_gemm_bf16_pk(a, lda, w, w_packed, bias, y, ldy, resid, ldr, m, n, k, act, stream);
+  FF_REQUIRE(act == kActNone || act == kGeluTanh || act == kGeluErf, "ff_gemm_bf16_pk_ws: act %d unknown", act);
+  FF_REQUIRE(!resid || act == kActNone, "ff_gemm_bf16_pk_ws: a residual add takes no activation");
+  const int64_t need = bf16pk_split_bytes(p, m, n);
+  FF_REQUIRE(workspace && workspace_bytes >= need && ff_aligned(workspace, 16),
+             "ff_gemm_bf16_pk_ws: workspace of %lld bytes (16-byte aligned) required", (long long)need);
+  hipStream_t st = (hipStream_t)stream;
+  launch_split_part(p, a, lda, w_packed, m, n, k, workspace, st);
+  const int64_t mp = (m + p.bm - 1) / p.bm * p.bm;
+  const unsigned blocks = (unsigned)((m * (n / 8) + kThreads - 1) / kThreads);
+#define FF_R(ACT, RES)                                                                                            \
+  if (act == ACT && (resid != nullptr) == RES)                                                                    \
+    hipLaunchKernelGGL((bf16_split_reduce_kernel<ACT, RES>), dim3(blocks), dim3(kThreads), 0, st,                \
+                       (const float*)workspace, p.s, mp, (const bf16_t*)bias, (bf16_t*)y, ldy, (const bf16_t*)resid, \
+                       ldr, (int)m, (int)n);
+  FF_R(kActNone, false) FF_R(kActNone, true) FF_R(kGeluTanh, false) FF_R(kGeluErf, false)
+#undef FF_R
+  FF_LAUNCH_CHECK("ff_gemm_bf16_pk_ws");
+  return FF_OK;
+}
+
+extern "C" int ff_gemm_bf16_pk_ln(const void* a, int64_t lda, const void* w, const void* w_packed, const void* bias,
+                                  void* y, int64_t ldy, const void* resid, int64_t ldr, int64_t m, int64_t n, int64_t k,
+                                  void* workspace, int64_t workspace_bytes, const void* ln_w, const void* ln_b,
+                                  float eps, void* ln_out, int64_t ln_ld, ff_stream_t stream) {
+  FF_REQUIRE(resid, "ff_gemm_bf16_pk_ln: the residual is required");
+  FF_REQUIRE(!ln_w || (ln_b && ln_out && ln_ld >= n && ln_ld % 8 == 0 && n % 8 == 0 && n <= 8 * kThreads * kLnChunks &&
+                       ff_aligned(ln_w, 16) && ff_aligned(ln_b, 16) && ff_aligned(ln_out, 16)),
+             "ff_gemm_bf16_pk_ln: LayerNorm arguments (n %% 8, n <= %d, 16-byte alignment)", 8 * kThreads * kLnChunks);
+  const Bf16Split p = bf16_split_ok(a, lda, w_packed, bias, y, ldy, resid, ldr, m, n, k) ? bf16pk_split(m, n, k)
+                                                                                          : Bf16Split{};
+  if (p.s < 2) {
+    const int rc = ff_gemm_bf16_pk(a, lda, w, w_packed, bias, y, ldy, resid, ldr, m, n, k, kActNone, stream);
+    if (rc != FF_OK || !ln_w) return rc;
+    return ff_layer_norm(y, ldy, ln_w, ln_b, ln_out, ln_ld, m, n, eps, stream);
+  }
+  const int64_t need = bf16pk_split_bytes(p, m, n);
+  FF_REQUIRE(workspace && workspace_bytes >= need && ff_aligned(workspace, 16),
+             "ff_gemm_bf16_pk_ln: workspace of %lld bytes (16-byte aligned) required", (long long)need);
+  hipStream_t st = (hipStream_t)stream;
+  launch_split_part(p, a, lda, w_packed, m, n, k, workspace, st);
+  const int64_t mp = (m + p.bm - 1) / p.bm * p.bm;
+  if (ln_w)
+    hipLaunchKernelGGL(layer_norm_kernel<true>, dim3((unsigned)m), dim3(kThreads), 0, st, (const bf16_t*)y, ldy,
+                       (const bf16_t*)ln_w, (const bf16_t*)ln_b, (bf16_t*)ln_out, ln_ld, (int)n, eps,
+                       (const float*)workspace, p.s, mp, (const bf16_t*)bias, (const bf16_t*)resid, ldr, (bf16_t*)y,
+                       ldy);
+  else
+    hipLaunchKernelGGL((bf16_split_reduce_kernel<kActNone, true>), dim3((unsigned)((m * (n / 8) + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, st, (const float*)workspace, p.s, mp, (const bf16_t*)bias, (bf16_t*)y, ldy,
+                       (const bf16_t*)resid, ldr, (int)m, (int)n);
+  FF_LAUNCH_CHECK("ff_gemm_bf16_pk_ln");
   return FF_OK;
 }
 

@@ -20,6 +20,7 @@ The outputs feed the LM step: ``merged`` (n/4, out_hidden) are the image-token
 embeddings that ``Runtime`` scatters into the hidden states, and ``deep`` the
 DeepStack features its first layers add (``add_rms`` with ``deep``).
 """
+import ctypes
 import types
 from dataclasses import dataclass
 
@@ -261,14 +262,39 @@ def pack_rgb(rgb):
     return out
 
 
-def linear(x, lin, act=ACT_NONE, resid=None, out=None):
-    """bf16 linear with its fused neighbours (bias, GELU, residual add)."""
+def linear(x, lin, act=ACT_NONE, resid=None, out=None, ws=None):
+    """bf16 linear with its fused neighbours (bias, GELU, residual add). With a
+    workspace ``ws`` (at least ``split_workspace`` bytes) short grids split k."""
     m, k = x.shape
     n = lin.w.shape[0]
     y = torch.empty((m, n), device=x.device, dtype=BF16) if out is None else out
-    call("ff_gemm_bf16_pk", ptr(x), x.stride(0), ptr(lin.w), ptr(lin.p), ptr(lin.b), ptr(y), y.stride(0),
-         ptr(resid), 0 if resid is None else resid.stride(0), m, n, k, act, stream())
+    args = [ptr(x), x.stride(0), ptr(lin.w), ptr(lin.p), ptr(lin.b), ptr(y), y.stride(0), ptr(resid),
+            0 if resid is None else resid.stride(0), m, n, k, act]
+    if ws is None:
+        call("ff_gemm_bf16_pk", *args, stream())
+    else:
+        call("ff_gemm_bf16_pk_ws", *args, ptr(ws), ws.numel() * ws.element_size(), stream())
     return y
+
+
+def linear_ln(x, lin, resid, out, ws, norm=None, eps=0.0, ln_out=None):
+    """A block's residual linear, out = bf16(resid + bf16(x . w^T + b)), and the
+    LayerNorm ``norm`` of its output into ``ln_out`` (None: no LayerNorm), as
+    two launches: with a k split the LayerNorm launch adds the partials."""
+    m, k = x.shape
+    n = lin.w.shape[0]
+    call("ff_gemm_bf16_pk_ln", ptr(x), x.stride(0), ptr(lin.w), ptr(lin.p), ptr(lin.b), ptr(out), out.stride(0),
+         ptr(resid), resid.stride(0), m, n, k, ptr(ws), ws.numel() * ws.element_size(),
+         None if norm is None else ptr(norm.w), None if norm is None else ptr(norm.b), float(eps),
+         None if ln_out is None else ptr(ln_out), 0 if ln_out is None else ln_out.stride(0), stream())
+    return out
+
+
+def split_workspace(m, n, k):
+    """Bytes of fp32 partials the k-split bf16 GEMM needs for an m x n x k product."""
+    b = ctypes.c_int64(0)
+    call("ff_gemm_bf16_pk_workspace", m, n, k, ctypes.byref(b))
+    return b.value
 
 
 def layer_norm(x, norm, eps, out=None):
@@ -284,8 +310,9 @@ def layer_norm(x, norm, eps, out=None):
 def _lay_out_vision(rt, cfg, n, n_pad, nm, a):
     """Give ``rt`` the tower's activation buffers, each from ``a(*shape, dt=dtype)``
     (an arena carve, a plain allocation, or a byte counter), in a fixed order.
-    Every size grows with the patch count, so the largest canvas of a variant
-    has the largest layout."""
+    The activations grow with the patch count; the k-split partials ``part``
+    exist only for grids too short to fill the GPU, so a variant's arena is
+    sized by the largest layout over its canvases."""
     H, NH = cfg.hidden, cfg.heads
     W4 = H * cfg.merge ** 2
     rt.pixels = a(n, 1536)
@@ -298,6 +325,11 @@ def _lay_out_vision(rt, cfg, n, n_pad, nm, a):
     rt.u = a(n, cfg.inter_pad)
     rt.x4 = a(nm, W4)
     rt.u4 = a(nm, W4)
+    ip = cfg.inter_pad
+    need = max(split_workspace(n, H, 1536), split_workspace(n, 3 * H, H), split_workspace(n, H, H),
+               split_workspace(n, ip, H), split_workspace(n, H, ip), split_workspace(nm, W4, W4),
+               split_workspace(nm, cfg.out_hidden, W4))
+    rt.part = a(max(need // 4, 64), dt=torch.float32)
 
 
 class VisionRuntime:
@@ -374,8 +406,8 @@ class VisionRuntime:
             layer_norm(h.view(self.nm, W4), mg.norm, cfg.eps, out=self.x4)
         else:                # LayerNorm per patch, then the 4 patches side by side
             layer_norm(h, mg.norm, cfg.eps, out=self.x4.view(self.n, cfg.hidden))
-        linear(self.x4, mg.fc1, ACT_GELU_ERF, out=self.u4)
-        linear(self.u4, mg.fc2, out=out)
+        linear(self.x4, mg.fc1, ACT_GELU_ERF, out=self.u4, ws=self.part)
+        linear(self.u4, mg.fc2, out=out, ws=self.part)
         return s
 
     def step(self, trace=None):
@@ -384,18 +416,19 @@ class VisionRuntime:
         cfg, w, s = self.cfg, self.w, stream()
         n, H, HD, NH = self.n, cfg.hidden, cfg.head_dim, cfg.heads
         call("ff_pack_pixels", ptr(self.rgb), ptr(self.pixels), 16 * self.gh, 16 * self.gw, s)
-        linear(self.pixels, w.patch, resid=self.pos, out=self.h)
+        # each residual linear carries the LayerNorm that reads its output: the
+        # patch embedding block 0's norm1, proj norm2, fc2 the next block's norm1
+        linear_ln(self.pixels, w.patch, self.pos, self.h, self.part, w.blocks[0].norm1, cfg.eps, self.x)
         for j, blk in enumerate(w.blocks):
-            layer_norm(self.h, blk.norm1, cfg.eps, out=self.x)
-            linear(self.x, blk.qkv, out=self.qkv)
+            linear(self.x, blk.qkv, out=self.qkv, ws=self.part)
             call("ff_vision_qkv", ptr(self.qkv), ptr(self.cos), ptr(self.sin), ptr(self.q), ptr(self.k),
                  ptr(self.vt), n, self.n_pad, NH, HD, s)
             call("ff_attention_full", ptr(self.q), ptr(self.k), ptr(self.vt), ptr(self.z), n, self.n_pad, NH, HD,
                  float(HD ** -0.5), s)
-            linear(self.z, blk.proj, resid=self.h, out=self.h)
-            layer_norm(self.h, blk.norm2, cfg.eps, out=self.x)
-            linear(self.x, blk.fc1, ACT_GELU_TANH, out=self.u)
-            linear(self.u, blk.fc2, resid=self.h, out=self.h)
+            linear_ln(self.z, blk.proj, self.h, self.h, self.part, blk.norm2, cfg.eps, self.x)
+            linear(self.x, blk.fc1, ACT_GELU_TANH, out=self.u, ws=self.part)
+            nxt = w.blocks[j + 1].norm1 if j + 1 < len(w.blocks) else None
+            linear_ln(self.u, blk.fc2, self.h, self.h, self.part, nxt, cfg.eps, self.x)
             if j in cfg.deepstack:
                 self._merge(w.deep[cfg.deepstack.index(j)], self.h, self.deep[cfg.deepstack.index(j)])
             if trace is not None:

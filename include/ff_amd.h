@@ -47,6 +47,7 @@ int ff_device_check(void);
 #define FF_TUNE_QKV_PK_TILE 7     /* ff_gemm_fp8_qkv_pk: 1 64x256 packed, 2 64x128 packed, 3 row-major */
 #define FF_TUNE_SWIGLU_PK_TILE 8  /* ff_gemm_fp8_swiglu_pk / _static: 1000 BM + CW (BM x 8 CW tile) */
 #define FF_TUNE_FP8_PK_SPLIT 9    /* ff_gemm_fp8_pk: 100 BM + k splits, BM 64 or 144 */
+#define FF_TUNE_BF16_PK_SPLIT 10  /* ff_gemm_bf16_pk_ws / _ln: 1 no k split, 2..8 the split count */
 int ff_set_tuning(int knob, int value);
 
 /* fast_norm(x, module): out = bf16(bf16(x*rsqrt(sum(x^2)/h + eps)) * w), one row
@@ -490,6 +491,34 @@ int ff_pack_weight_bf16(const void* w, void* packed, int64_t n, int64_t k, ff_st
 int ff_gemm_bf16_pk(const void* a, int64_t lda, const void* w, const void* w_packed, const void* bias, void* y,
                     int64_t ldy, const void* resid, int64_t ldr, int64_t m, int64_t n, int64_t k, int act,
                     ff_stream_t stream);
+
+/* Bytes of workspace ff_gemm_bf16_pk_ws / ff_gemm_bf16_pk_ln need for an
+ * m x n x k product (0: it runs unsplit). Host-only. */
+int ff_gemm_bf16_pk_workspace(int64_t m, int64_t n, int64_t k, int64_t* bytes);
+/* ff_gemm_bf16_pk with a k split where the packed kernel has no tile whose
+ * grid fills the GPU in one round (short m: the tower at 400 patches, the
+ * patch mergers): the split launches store fp32 partials in workspace
+ * (ff_gemm_bf16_pk_workspace bytes, 16-byte aligned) and a second launch adds
+ * them in split order and applies the epilogue (bias, act, resid). The same
+ * products summed in another order: within an fp32 rounding of the unsplit
+ * sums before the bf16 rounding. Splits need 16-byte aligned a, bias, y,
+ * resid and ldy, ldr % 8; otherwise, or with no split planned, this is
+ * ff_gemm_bf16_pk. Same reference replacement as ff_gemm_bf16. */
+int ff_gemm_bf16_pk_ws(const void* a, int64_t lda, const void* w, const void* w_packed, const void* bias, void* y,
+                       int64_t ldy, const void* resid, int64_t ldr, int64_t m, int64_t n, int64_t k, int act,
+                       void* workspace, int64_t workspace_bytes, ff_stream_t stream);
+/* A vision block's residual linear and the LayerNorm that reads its output
+ * (attn.proj + residual + norm2, mlp.linear_fc2 + residual + the next block's
+ * norm1: transformers modeling_qwen3_vl.py:196-306, NativeNormVision.core,
+ * scaled_qwen_runtime.py:42-55): y = bf16(resid + bf16(a . w^T + bias)) as
+ * ff_gemm_bf16_pk_ws (resid required, may be y), then ln_out = LayerNorm(y)
+ * with ln_w, ln_b, eps as ff_layer_norm (row stride ln_ld; ln_w NULL: no
+ * LayerNorm). With a k split the LayerNorm launch adds the partials, stores y
+ * and normalises it: two launches either way. */
+int ff_gemm_bf16_pk_ln(const void* a, int64_t lda, const void* w, const void* w_packed, const void* bias, void* y,
+                       int64_t ldy, const void* resid, int64_t ldr, int64_t m, int64_t n, int64_t k, void* workspace,
+                       int64_t workspace_bytes, const void* ln_w, const void* ln_b, float eps, void* ln_out,
+                       int64_t ln_ld, ff_stream_t stream);
 
 /* vision_rope (_legacy/search_kernels.py:111-134): yq/yk = bf16(x * cos +
  * rotate_half(x) * sin) in fp32, cos/sin (n, hd) fp32. q, k with token stride

@@ -161,6 +161,105 @@ def test_gemm_bf16_packed_equals_rowmajor(gpu, m, k, n, act, resid):
     assert torch.equal(outs[0], outs[1])
 
 
+# (m, k, n, act, resid): grids with no one-round packed tile, which the
+# workspace entry points split along k: the tower at 400 patches (proj and fc2
+# with the residual in place, the patch embedding, qkv) and at 256 patches
+# (fc1 + GELU-tanh), the mergers at 100 merged tokens (fc1 + GELU-erf, fc2)
+SPLIT_VISION = [(400, 1152, 1152, 0, True), (400, 4352, 1152, 0, True), (400, 1536, 1152, 0, False),
+                (400, 1152, 3456, 0, False), (256, 1152, 4352, 1, False), (100, 4608, 4608, 2, False),
+                (100, 4608, 4096, 0, False)]
+FF_TUNE_BF16_PK_SPLIT = 10
+
+
+@pytest.mark.parametrize("m,k,n,act,resid", SPLIT_VISION)
+def test_gemm_bf16_split_matches_unsplit(gpu, m, k, n, act, resid):
+    """ff_gemm_bf16_pk_ws with its k split (the partials added in split order by
+    the epilogue launch) against the unsplit packed kernel: the same products
+    summed in fp32 in another order, so within twice the fp32-accumulation
+    bound of the exact product (plus the bf16 roundings after it) and nearly
+    all equal; inside that bound of the exact product itself; identical on
+    repeated calls; with the split turned off, the unsplit bits."""
+    from fastforward_amd._lib import call
+    from fastforward_amd.vision import Lin, linear, split_workspace
+    need = split_workspace(m, n, k)
+    assert need > 0, "the shape must split"
+    x = torch.randn(m, k, generator=_g(m + n + 5)).to(BF16)
+    w = (torch.randn(n, k, generator=_g(k + 1)) * 0.03).to(BF16)
+    b = (torch.randn(n, generator=_g(n + 4)) * 0.1).to(BF16)
+    h = torch.randn(m, n, generator=_g(n + 6)).to(BF16).to(DEV) if resid else None
+    lin = Lin(w.to(DEV), b.to(DEV)).pack()
+    ws = torch.full((need // 4,), float("nan"), device=DEV)
+    xd = x.to(DEV)
+
+    def run(split):
+        y = h.clone() if resid else torch.full((m, n), float("nan"), device=DEV, dtype=BF16)
+        linear(xd, lin, act=act, resid=y if resid else None, out=y, ws=ws if split else None)
+        return y
+    ref = run(False)
+    got = [run(True) for _ in range(2)]
+    assert torch.equal(got[0], got[1]) and not torch.isnan(got[0].float()).any()
+    # both sums lie within the fp32-accumulation bound of the exact product, so
+    # they differ by at most twice it (carried through the GELU, |gelu'| <=
+    # 1.13) plus a bf16 rounding of the term and, with a residual, of y
+    _, bound = _linear_bound(x, w, b)
+    g64, r64 = got[0].cpu().to(torch.float64), ref.cpu().to(torch.float64)
+    t64 = r64 - h.cpu().to(torch.float64) if resid else r64
+    allowed = 2 * bound * (1.13 if act else 1.0) + _ulp(t64) + (_ulp(r64) if resid else 0)
+    assert bool(((g64 - r64).abs() <= allowed).all()), "split result outside the bound of the unsplit one"
+    d = bf16_ulps(got[0], ref)
+    assert float((d > 0).float().mean()) < 0.02
+    if not act and not resid:
+        exact, bound = _linear_bound(x, w, b)
+        assert bool(((g64 - exact).abs() <= bound).all())
+    call("ff_set_tuning", FF_TUNE_BF16_PK_SPLIT, 1)
+    try:
+        assert torch.equal(run(True), ref)
+    finally:
+        call("ff_set_tuning", FF_TUNE_BF16_PK_SPLIT, 0)
+
+
+@pytest.mark.parametrize("m,k,n,in_place", [(400, 1152, 1152, True), (400, 4352, 1152, True),
+                                            (400, 1536, 1152, False), (2048, 1152, 1152, True)])
+def test_gemm_bf16_pk_ln(gpu, m, k, n, in_place):
+    """linear_ln (a residual linear and the LayerNorm of its output): unsplit
+    (2048 rows) bit for bit the linear followed by layer_norm; split (400 rows)
+    the stored output within the split bound of the unsplit one (twice the
+    fp32-accumulation bound plus the roundings) and the LayerNorm bit
+    for bit ff_layer_norm of the output it stored; without a LayerNorm only
+    the output is written. The residual in place (proj, fc2) or separate (the
+    patch embedding's position embedding)."""
+    from fastforward_amd.vision import Lin, Norm, layer_norm, linear, linear_ln, split_workspace
+    x = torch.randn(m, k, generator=_g(m + 11)).to(BF16).to(DEV)
+    w = (torch.randn(n, k, generator=_g(k + 12)) * 0.03).to(BF16).to(DEV)
+    b = (torch.randn(n, generator=_g(n + 13)) * 0.1).to(BF16).to(DEV)
+    r = torch.randn(m, n, generator=_g(n + 14)).to(BF16).to(DEV)
+    nw = (1 + 0.1 * torch.randn(n, generator=_g(15))).to(BF16).to(DEV)
+    nb = (0.1 * torch.randn(n, generator=_g(16))).to(BF16).to(DEV)
+    norm = Norm(nw, nb)
+    lin = Lin(w, b).pack()
+    ws = torch.full((max(split_workspace(m, n, k) // 4, 64),), float("nan"), device=DEV)
+    # unsplit reference: the linear with its residual, then the LayerNorm
+    y_ref = r.clone() if in_place else torch.empty(m, n, device=DEV, dtype=BF16)
+    linear(x, lin, resid=y_ref if in_place else r, out=y_ref)
+    ln_ref = layer_norm(y_ref, norm, 1e-6)
+    y = r.clone() if in_place else torch.full((m, n), float("nan"), device=DEV, dtype=BF16)
+    ln = torch.full((m, n), float("nan"), device=DEV, dtype=BF16)
+    linear_ln(x, lin, y if in_place else r, y, ws, norm, 1e-6, ln)
+    split = split_workspace(m, n, k) > 0
+    assert split == (m == 400)
+    if split:
+        _, bound = _linear_bound(x.cpu(), w.cpu(), b.cpu())
+        y64, ref64, r64 = (v.cpu().to(torch.float64) for v in (y, y_ref, r))
+        assert bool(((y64 - ref64).abs() <= 2 * bound + _ulp(ref64 - r64) + _ulp(ref64)).all())
+        assert float((bf16_ulps(y, y_ref) > 0).float().mean()) < 0.02
+        assert torch.equal(ln, layer_norm(y, norm, 1e-6))
+    else:
+        assert torch.equal(y, y_ref) and torch.equal(ln, ln_ref)
+    y2 = r.clone() if in_place else torch.full((m, n), float("nan"), device=DEV, dtype=BF16)
+    linear_ln(x, lin, y2 if in_place else r, y2, ws)
+    assert torch.equal(y2, y)
+
+
 def test_pack_weight_bf16_layout(gpu):
     """ff_pack_weight_bf16: fragment (f, kt) at (kt n/16 + f) 4 KB, sub-block s,
     lane 16 g + r: row 16 f + r, k 128 kt + 64 (s / 2) + 16 g + 8 (s % 2) .. + 8."""
