@@ -779,13 +779,15 @@ void launch_gemm_pk(const void* a, int64_t lda, const void* wp, const void* bias
 #undef FF_G
 }
 
-// k split of the packed GEMM for grids with no one-round tile (bf16pk_tile 0:
-// the tower at short patch counts, e.g. 400 patches: proj and fc2 have 63 tiles
-// of 64 x 128, the mergers 72): the (BM, CW) tile and split count S in {2, 3,
-// 4, 8} whose grid of tiles x S workgroups lies in 192 .. 256 (one round at
-// one per CU) with the least work per workgroup (k steps per split x BM x CW);
-// s = 0 when none. ff_set_tuning(FF_TUNE_BF16_PK_SPLIT, 1) turns splits off,
-// 2 .. 8 forces the split count.
+// k split of the packed GEMM for grids with no one-round tile (bf16pk_tile 0)
+// whose unsplit fallback, 64 x 128 tiles, fills less than half the GPU (the
+// tower at short patch counts, e.g. 400 patches: proj and fc2 have 63 such
+// tiles, the mergers 72; its qkv, 189, runs unsplit: 13.9 us against 15.0 +
+// 4.9 us split 2 ways): the (BM, CW) tile and split count S in {2, 3, 4, 8}
+// whose grid of tiles x S workgroups lies in 192 .. 256 (one round at one per
+// CU) with the least work per workgroup (k steps per split x BM x CW); s = 0
+// when none. ff_set_tuning(FF_TUNE_BF16_PK_SPLIT, 1) turns splits off, 2 .. 8
+// forces the split count.
 struct Bf16Split {
   int bm = 0, cw = 0, s = 0;
 };
@@ -793,6 +795,7 @@ Bf16Split bf16pk_split(int64_t m, int64_t n, int64_t k) {
   Bf16Split p;
   const int forced = ff_tuning(FF_TUNE_BF16_PK_SPLIT);
   if (forced == 1 || m <= 0 || k % kBfStep || bf16pk_tile(m, n)) return p;
+  if (!forced && (m + 63) / 64 * ((n + 127) / 128) >= 128) return p;
   const int64_t kt = k / kBfStep;
   constexpr int cand[4][2] = {{64, 32}, {64, 48}, {64, 64}, {128, 48}};
   constexpr int spl[4] = {2, 3, 4, 8};

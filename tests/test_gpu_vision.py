@@ -161,13 +161,13 @@ def test_gemm_bf16_packed_equals_rowmajor(gpu, m, k, n, act, resid):
     assert torch.equal(outs[0], outs[1])
 
 
-# (m, k, n, act, resid): grids with no one-round packed tile, which the
-# workspace entry points split along k: the tower at 400 patches (proj and fc2
-# with the residual in place, the patch embedding, qkv) and at 256 patches
-# (fc1 + GELU-tanh), the mergers at 100 merged tokens (fc1 + GELU-erf, fc2)
+# (m, k, n, act, resid): grids with no one-round packed tile whose unsplit
+# fallback fills less than half the GPU, which the workspace entry points split
+# along k: the tower at 400 patches (proj and fc2 with the residual in place,
+# the patch embedding) and at 128 patches (fc1 + GELU-tanh), the mergers at 100
+# merged tokens (fc1 + GELU-erf, fc2)
 SPLIT_VISION = [(400, 1152, 1152, 0, True), (400, 4352, 1152, 0, True), (400, 1536, 1152, 0, False),
-                (400, 1152, 3456, 0, False), (256, 1152, 4352, 1, False), (100, 4608, 4608, 2, False),
-                (100, 4608, 4096, 0, False)]
+                (128, 1152, 4352, 1, False), (100, 4608, 4608, 2, False), (100, 4608, 4096, 0, False)]
 FF_TUNE_BF16_PK_SPLIT = 10
 
 
