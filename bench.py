@@ -109,8 +109,10 @@ def time_gemm(cfg, role, q, s, layers, m, T, reps=3):
     launch stream bracket reps x len(layers) launches."""
     n = getattr(layers[0], role).weight.shape[0]
     b = gemm_buffers(cfg, role, n, m, T)
-    for lw in layers:
-        launch_gemm(cfg, role, lw, q, s, m, b)
+    # two untimed passes: the first launches after an idle GPU (buffer set-up) run slow
+    for _ in range(2):
+        for lw in layers:
+            launch_gemm(cfg, role, lw, q, s, m, b)
     torch.cuda.synchronize()
     a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()

@@ -23,9 +23,9 @@ void ff_set_error(const char* fmt, ...) {
 extern "C" int ff_version(void) { return 100; }  // 0.1.0
 
 namespace {
-constexpr int kTuneKnobs = 11;
+constexpr int kTuneKnobs = 12;
 // Upper bound of each knob's values (index = FF_TUNE_*).
-constexpr int kTuneMax[kTuneKnobs] = {0, 4, 3, 2, 8, 4, 3, 3, 176096, 14408, 8};
+constexpr int kTuneMax[kTuneKnobs] = {0, 4, 3, 2, 8, 4, 3, 6, 176096, 114408, 8, 114408};
 int g_tuning[kTuneKnobs] = {};
 }  // namespace
 

@@ -403,7 +403,7 @@ __device__ __forceinline__ void pk_store_tile(const f32x4 (&acc)[BM / 16][CW / 1
 // launch adds the partials: split_reduce_kernel, or the add_rms row kernel
 // that takes them in place of its bf16 addend.
 template <int BM, int CW, int P, int D, int G, int S>
-__global__ __launch_bounds__(kThreads, BM < 144 ? 2 : 1) void gemm_fp8_split_packed_kernel(
+__global__ __launch_bounds__(kThreads, BM <= 96 ? 2 : 1) void gemm_fp8_split_packed_kernel(
     const uint8_t* __restrict__ qa, const float* __restrict__ sa, int sa_rows, const uint8_t* __restrict__ qwp,
     const float* __restrict__ sw, int sw_cols, bf16_t* __restrict__ y, int64_t ldy, int M, int N, int K,
     int tiles_m, int tiles_n, float* __restrict__ part) {
@@ -580,23 +580,31 @@ constexpr int kSpU = lcm3(kSpP, kSpD, 2 * kSpG);
 // partials on the same grid, measured slower: the 8B FP8 step 6.35 -> 6.85 ms
 // with the down projection on 80 x 256 tiles split 2 ways instead of 144 x 256
 // split 4 ways.)
+// cw: the wave width (weight rows per wave; 4 cw per tile): kSpCW, or 32 for
+// one-head-wide (128-column) tiles.
 struct SplitPlan {
-  int bm = 0, s = 0;
+  int bm = 0, s = 0, cw = kSpCW;
 };
 SplitPlan split_plan(int64_t m, int64_t n, int64_t k) {
   SplitPlan p;
-  if (m <= 4 || n % kSpBN || k % 128 || m * k >= (int64_t(1) << 31) || n * k >= (int64_t(1) << 31)) return p;
+  if (m <= 4 || n % 128 || k % 128 || m * k >= (int64_t(1) << 31) || n * k >= (int64_t(1) << 31)) return p;
   const int64_t kt = k / 128;
-  const int forced = ff_tuning(FF_TUNE_FP8_PK_SPLIT);
+  const int forced_short = k <= 4096 ? ff_tuning(FF_TUNE_FP8_PK_SPLIT_SHORT_K) : 0;
+  const int forced = forced_short ? forced_short : ff_tuning(FF_TUNE_FP8_PK_SPLIT);
   if (forced) {
-    const int bm = forced / 100, sp = forced % 100;
-    if ((bm == 64 || bm == kSpBM) && (sp == 1 || sp == 2 || sp == 3 || sp == 4 || sp == 8) && kt % kSpU == 0 &&
+    // 100 bm + s: 256-column tiles, bm 64 or 144; 100000 + 100 bm + s: 128-column tiles, bm 96, 128 or 144
+    const int cw = forced >= 100000 ? 32 : kSpCW, f = forced % 100000;
+    const int bm = f / 100, sp = f % 100;
+    const bool bm_ok = cw == 32 ? (bm == 96 || bm == 128 || bm == kSpBM) : (bm == 64 || bm == kSpBM);
+    if (bm_ok && n % (4 * cw) == 0 && (sp == 1 || sp == 2 || sp == 3 || sp == 4 || sp == 8) && kt % kSpU == 0 &&
         kt / kSpU >= sp) {
       p.bm = bm;
       p.s = sp;
+      p.cw = cw;
     }
     return p;
   }
+  if (n % kSpBN) return p;
   const int64_t tiles = (m + kSpBM - 1) / kSpBM * (n / kSpBN);
   if (tiles >= 192) {
     if (kt % kSpU == 0) p = SplitPlan{kSpBM, 1};
@@ -697,36 +705,54 @@ void launch_small(const void* qa, const float* sa, int sa_rows, const void* qw_p
 int64_t split_workspace(int64_t m, int64_t n, int64_t k) {
   const SplitPlan p = split_plan(m, n, k);
   if (p.s <= 1) return 0;
-  return (m + p.bm - 1) / p.bm * (n / kSpBN) * p.s * p.bm * kSpBN * 4;
+  return (m + p.bm - 1) / p.bm * (n / (4 * p.cw)) * p.s * p.bm * (4 * p.cw) * 4;
 }
 
-// The plain packed kernel at row tile BM with S k splits (S == 1: y directly).
-template <int BM, int S>
+// The plain packed kernel at row tile BM x 4 CW with S k splits (S == 1: y directly).
+template <int BM, int S, int CW = kSpCW>
 void launch_split(const void* qa, const float* sa, int sa_rows, const void* qw_packed, const float* sw, int sw_cols,
                   void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, void* part, hipStream_t st) {
-  const int64_t tiles_m = (m + BM - 1) / BM, tiles_n = n / kSpBN;
-  hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<BM, kSpCW, kSpP, kSpD, kSpG, S>),
+  const int64_t tiles_m = (m + BM - 1) / BM, tiles_n = n / (4 * CW);
+  hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<BM, CW, kSpP, kSpD, kSpG, S>),
                      dim3((unsigned)(tiles_m * tiles_n * S)), dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows,
                      (const uint8_t*)qw_packed, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)n, (int)k, (int)tiles_m,
                      (int)tiles_n, (float*)part);
 }
 
-template <int BM>
+template <int BM, int CW = kSpCW>
 void launch_splits(int s, const void* qa, const float* sa, int sa_rows, const void* qw_packed, const float* sw,
                    int sw_cols, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, void* part, hipStream_t st) {
   switch (s) {
-    case 1: launch_split<BM, 1>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
-    case 2: launch_split<BM, 2>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
-    case 3: launch_split<BM, 3>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
-    case 4: launch_split<BM, 4>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
-    case 8: launch_split<BM, 8>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
+    case 1: launch_split<BM, 1, CW>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
+    case 2: launch_split<BM, 2, CW>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
+    case 3: launch_split<BM, 3, CW>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
+    case 4: launch_split<BM, 4, CW>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
+    case 8: launch_split<BM, 8, CW>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
     default: break;
+  }
+}
+
+// The plan's tile: bm x 4 cw (bm 64 or 144 at cw = kSpCW; 96, 128 or 144 at cw = 32).
+void launch_plan(const SplitPlan& p, int s, const void* qa, const float* sa, int sa_rows, const void* qw_packed,
+                 const float* sw, int sw_cols, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, void* part,
+                 hipStream_t st) {
+  if (p.cw == 32) {
+    if (p.bm == 96)
+      launch_splits<96, 32>(s, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st);
+    else if (p.bm == 128)
+      launch_splits<128, 32>(s, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st);
+    else
+      launch_splits<kSpBM, 32>(s, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st);
+  } else if (p.bm == 64) {
+    launch_splits<64>(s, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st);
+  } else {
+    launch_splits<kSpBM>(s, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st);
   }
 }
 
 // Fused QKV on fragment-packed weights: BM tokens x BN = 4 CW channels (BN /
 // 128 whole heads) per workgroup, the packed main loop at two workgroups per
-// CU. The tile y = bf16((acc * sa) * sw) is written to LDS as a row-major
+// CU up to 96 rows (one above: 128 and 144 rows need the registers). The tile y = bf16((acc * sa) * sw) is written to LDS as a row-major
 // bf16 tile (lane 16 g + r of fragment (i, j) holds token 16 i + r, columns
 // wave CW + 16 j + 4 g .. + 3: one 8-byte store), then each head of the tile
 // gets the epilogue of the row-major QKV kernel, the same code on the same
@@ -746,7 +772,7 @@ struct PkQkv {
 };
 
 template <int BM, int CW, int P, int D, int G>
-__global__ __launch_bounds__(kThreads, 2) void gemm_fp8_qkv_packed_kernel(
+__global__ __launch_bounds__(kThreads, BM <= 96 ? 2 : 1) void gemm_fp8_qkv_packed_kernel(
     const uint8_t* __restrict__ qa, const float* __restrict__ sa, int sa_rows, const uint8_t* __restrict__ qwp,
     const float* __restrict__ sw, int sw_cols, int M, int N, int K, int tiles_m, int tiles_n, PkQkv qe) {
   constexpr int BN = 4 * CW, RA = BM / 16, TJ = CW / 16;
@@ -756,7 +782,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_fp8_qkv_packed_kernel(
   constexpr int ROWS = BM / (kThreads / 16);  // token rows per 16-lane group
   constexpr int SMEM_LOOP = pk_smem<BM, G>(), SMEM_TILE = BM * LD * 2;
   constexpr int SMEM = SMEM_LOOP > SMEM_TILE ? SMEM_LOOP : SMEM_TILE;
-  static_assert(SMEM <= 80 * 1024, "two workgroups per CU");
+  static_assert(SMEM <= (BM <= 96 ? 80 : 160) * 1024, "two workgroups per CU up to 96 rows");
   __shared__ __align__(1024) uint8_t smem[SMEM];
 
   const int nblk = tiles_m * tiles_n;
@@ -1199,10 +1225,7 @@ int gemm_fp8_pk_partials(const void* qa, const float* sa, int sa_rows, const voi
   const int64_t need = split_workspace(m, n, k);
   FF_REQUIRE(workspace && workspace_bytes >= need && ff_aligned(workspace, 16),
              "ff_gemm_fp8_pk: workspace of %lld bytes (16-byte aligned) required", (long long)need);
-  if (p.bm == 64)
-    launch_splits<64>(s, qa, sa, sa_rows, qw_packed, sw, sw_cols, nullptr, 0, m, n, k, workspace, st);
-  else
-    launch_splits<kSpBM>(s, qa, sa, sa_rows, qw_packed, sw, sw_cols, nullptr, 0, m, n, k, workspace, st);
+  launch_plan(p, s, qa, sa, sa_rows, qw_packed, sw, sw_cols, nullptr, 0, m, n, k, workspace, st);
   FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
   *splits = s;
   *mp = (m + p.bm - 1) / p.bm * p.bm;
@@ -1247,10 +1270,7 @@ extern "C" int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, cons
     return FF_OK;
   }
   if (s == 1) {
-    if (plan.bm == 64)
-      launch_splits<64>(1, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, nullptr, st);
-    else
-      launch_splits<kSpBM>(1, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, nullptr, st);
+    launch_plan(plan, 1, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, nullptr, st);
     FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
     return FF_OK;
   }
@@ -1276,20 +1296,33 @@ extern "C" int ff_gemm_fp8_qkv_pk(const void* qa, const float* sa, int sa_rows, 
                                   const void* q_norm, const void* k_norm, float eps_q, float eps_k, const void* cos,
                                   const void* sin, void* yq, void* yk, void* vt, int64_t t_pad, ff_stream_t stream) {
   const int64_t n = (hq + 2 * hk) * kHeadDim;
-  // ff_set_tuning(FF_TUNE_QKV_PK_TILE, 1 | 2 | 3): 64 x 256 packed tiles, 64 x 128 packed tiles, the
-  // row-major kernel, for measurement sweeps
-  // The library's choice: 64 x 128 tiles (one head) while their grid is at most 512 workgroups (two
-  // per CU; 8B shape: 576 tokens 432 workgroups, 6.260 -> 6.229 ms against 64 x 256; 176 tokens 144
-  // workgroups, 4.467 -> 4.393 ms against the row-major kernel), else 64 x 256.
+  // ff_set_tuning(FF_TUNE_QKV_PK_TILE, 1 | 2 | 3 | 4 | 5 | 6): 64 x 256 packed tiles, 64 x 128 packed
+  // tiles, the row-major kernel, 96 x 128, 144 x 128, 128 x 128 packed tiles, for measurement sweeps.
+  // The library's choice: one-head tiles (128 columns) of the fewest rows among 64, 96 and 128 whose
+  // grid fits one round of one workgroup per CU (256 workgroups; 8B shape: 176 tokens 64 rows, 144
+  // workgroups, 4.467 -> 4.393 ms against the row-major kernel; 576 tokens 128 rows, 240 workgroups,
+  // 29.1 -> 25.3 us per launch and 6.202 -> 6.118 ms per step against 64 rows at two workgroups per
+  // CU, 96 rows 28.0 us, 144 rows 27.6 us); else 64 x 128 while the grid is at most 512 workgroups
+  // (two per CU), else 64 x 256.
   const int forced = ff_tuning(FF_TUNE_QKV_PK_TILE);
-  const int64_t tiles_m = (m + kQkBM - 1) / kQkBM;
-  const int cw = forced == 2 || (!forced && tiles_m * (n / 128) <= 512) ? 32 : kQkCW;
+  int bm = forced == 4 ? 96 : forced == 5 ? 144 : forced == 6 ? 128 : kQkBM;
+  if (!forced) {
+    for (const int c : {64, 96, 128}) {
+      const int64_t tm = (m + c - 1) / c;
+      if (tm * (n / 128) <= 256 && t_pad <= tm * c) {
+        bm = c;
+        break;
+      }
+    }
+  }
+  const int64_t tiles_m = (m + bm - 1) / bm;
+  const int cw = forced >= 4 || forced == 2 || bm != kQkBM || (!forced && tiles_m * (n / 128) <= 512) ? 32 : kQkCW;
   const int64_t tiles_n = n / (4 * cw), tiles = tiles_m * tiles_n;
   const bool fits = forced != 3 && qw_packed && (m > 4 || !qw) && m > 0 && hq > 0 && hk > 0 && hq % hk == 0 &&
                     n % (4 * cw) == 0 && k > 0 && k % (128 * kSpU) == 0 &&
                     (forced || cw == 32 || !qw || (tiles >= 192 && tiles <= 512)) && t_pad >= m &&
                     t_pad % 64 == 0 &&
-                    t_pad <= tiles_m * kQkBM && m * k < (int64_t(1) << 31) && n * k < (int64_t(1) << 31) &&
+                    t_pad <= tiles_m * bm && m * k < (int64_t(1) << 31) && n * k < (int64_t(1) << 31) &&
                     ff_aligned(qa, 16) && ff_aligned(qw_packed, 16) && ff_aligned(cos, 16) && ff_aligned(sin, 16) &&
                     ff_aligned(q_norm, 16) && ff_aligned(k_norm, 16) && ff_aligned(yq, 16) && ff_aligned(yk, 16) &&
                     ff_aligned(vt, 16);
@@ -1302,7 +1335,15 @@ extern "C" int ff_gemm_fp8_qkv_pk(const void* qa, const float* sa, int sa_rows, 
   FF_REQUIRE(sa && sw && q_norm && k_norm && yq && yk && vt, "ff_gemm_fp8_qkv_pk: null pointer");
   PkQkv qe{(const bf16_t*)q_norm, (const bf16_t*)k_norm, eps_q, eps_k, (const bf16_t*)cos, (const bf16_t*)sin,
            (bf16_t*)yq, (bf16_t*)yk, (bf16_t*)vt, (int)hq, (int)hk, (int)t_pad};
-  if (cw == 32)
+#define FF_QKV_BM(BM)                                                                                         \
+  if (bm == BM)                                                                                               \
+    hipLaunchKernelGGL((gemm_fp8_qkv_packed_kernel<BM, 32, kSpP, kSpD, kSpG>), dim3((unsigned)tiles),          \
+                       dim3(kThreads), 0, (hipStream_t)stream, (const uint8_t*)qa, sa, sa_rows,               \
+                       (const uint8_t*)qw_packed, sw, sw_cols, (int)m, (int)n, (int)k, (int)tiles_m,          \
+                       (int)tiles_n, qe);
+  if (bm != kQkBM) {
+    FF_QKV_BM(96) FF_QKV_BM(144) FF_QKV_BM(128)
+  } else if (cw == 32)
     hipLaunchKernelGGL((gemm_fp8_qkv_packed_kernel<kQkBM, 32, kSpP, kSpD, kSpG>), dim3((unsigned)tiles),
                        dim3(kThreads), 0, (hipStream_t)stream, (const uint8_t*)qa, sa, sa_rows,
                        (const uint8_t*)qw_packed, sw, sw_cols, (int)m, (int)n, (int)k, (int)tiles_m, (int)tiles_n, qe);
@@ -1310,6 +1351,7 @@ extern "C" int ff_gemm_fp8_qkv_pk(const void* qa, const float* sa, int sa_rows, 
     hipLaunchKernelGGL((gemm_fp8_qkv_packed_kernel<kQkBM, kQkCW, kSpP, kSpD, kSpG>), dim3((unsigned)tiles),
                        dim3(kThreads), 0, (hipStream_t)stream, (const uint8_t*)qa, sa, sa_rows,
                        (const uint8_t*)qw_packed, sw, sw_cols, (int)m, (int)n, (int)k, (int)tiles_m, (int)tiles_n, qe);
+#undef FF_QKV_BM
   FF_LAUNCH_CHECK("ff_gemm_fp8_qkv_pk");
   return FF_OK;
 }

@@ -750,14 +750,18 @@ def test_gemm_fp8_qkv_equals_unfused(gpu, t, k, hq, hk):
                                                (1024, 4096, 32, 8, False), (576, 4096, 32, 8, True),
                                                (300, 2048, 16, 8, False), (3, 4096, 32, 8, False),
                                                (176, 4096, 32, 8, False), (176, 4096, 32, 8, True),
-                                               (1200, 4096, 64, 8, False)])
+                                               (400, 4096, 32, 8, False), (460, 4096, 32, 8, False),
+                                               (640, 4096, 32, 8, False), (1200, 4096, 64, 8, False)])
 def test_gemm_fp8_qkv_packed_equals_rowmajor(gpu, t, k, hq, hk, static):
-    """ff_gemm_fp8_qkv_pk on the packed weight -- 64-token x one-head tiles while
-    their grid is at most 512 workgroups (576, ragged 500, 176 and 300 tokens),
-    else 64-token x two-head tiles (1024 tokens at 32/8 heads) -- equals
-    ff_gemm_fp8_qkv bit for bit, V^T zero padding included, per-token and
-    per-tensor scales; shapes outside its plan (1200 tokens at 64/8 heads; 3
-    tokens) run ff_gemm_fp8_qkv itself."""
+    """ff_gemm_fp8_qkv_pk on the packed weight -- one-head tiles of the fewest
+    rows among 64, 96 and 128 whose grid fits 256 workgroups and whose rows
+    cover the V^T padding (176 and 300 tokens 64 rows; 400 tokens 96 rows; 460
+    tokens 128 rows, since 96-row tiles would leave V^T columns 480..511
+    unwritten; 576, 640 and ragged 500 tokens 128 rows), else 64-token x
+    two-head tiles (1024 tokens at 32/8 heads) -- equals ff_gemm_fp8_qkv bit
+    for bit, V^T zero padding included, per-token and per-tensor scales; shapes
+    outside its plan (1200 tokens at 64/8 heads; 3 tokens) run ff_gemm_fp8_qkv
+    itself."""
     from fastforward_amd._lib import call, ptr, stream
     d = 128
     tp, n = (t + 63) // 64 * 64, (hq + 2 * hk) * d
