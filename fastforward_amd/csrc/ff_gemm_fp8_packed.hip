@@ -592,10 +592,11 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k) {
   const int forced_short = k <= 4096 ? ff_tuning(FF_TUNE_FP8_PK_SPLIT_SHORT_K) : 0;
   const int forced = forced_short ? forced_short : ff_tuning(FF_TUNE_FP8_PK_SPLIT);
   if (forced) {
-    // 100 bm + s: 256-column tiles, bm 64 or 144; 100000 + 100 bm + s: 128-column tiles, bm 96, 128 or 144
+    // 100 bm + s: 256-column tiles, bm 64 or 144; 100000 + 100 bm + s: 128-column tiles, bm 64, 80, 96, 128 or 144
     const int cw = forced >= 100000 ? 32 : kSpCW, f = forced % 100000;
     const int bm = f / 100, sp = f % 100;
-    const bool bm_ok = cw == 32 ? (bm == 96 || bm == 128 || bm == kSpBM) : (bm == 64 || bm == kSpBM);
+    const bool bm_ok =
+        cw == 32 ? (bm == 64 || bm == 80 || bm == 96 || bm == 128 || bm == kSpBM) : (bm == 64 || bm == kSpBM);
     if (bm_ok && n % (4 * cw) == 0 && (sp == 1 || sp == 2 || sp == 3 || sp == 4 || sp == 8) && kt % kSpU == 0 &&
         kt / kSpU >= sp) {
       p.bm = bm;
@@ -656,8 +657,11 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k) {
 // Unsplit plain GEMMs whose 144 x 256 tiles are too few and whose k is too
 // short to split (the 8B o projection, 576 x 4096 x 4096; a QKV-shaped plain
 // GEMM): smaller packed tiles at two workgroups per CU. BM x 4 CW with BM =
-// 64, CW = 64, else BM = 96, CW = 32, else BM = 64, CW = 32, the first whose
-// grid has 192 .. 512 workgroups. A wave still owns all BM rows of its CW
+// 64, CW = 64, else BM = 80, CW = 32 where that grid fits one round of one
+// workgroup per CU, else BM = 96, CW = 32, else BM = 64, CW = 32, the first
+// whose grid has 192 .. 512 workgroups (8B o projection: 80 x 128 tiles, 256
+// workgroups, 20.4 / 19.3 -> 19.3 / 17.8 us per launch against 96 x 128
+// tiles at 192 workgroups; 64 x 128 at 288 workgroups 20.9 us). A wave still owns all BM rows of its CW
 // weight rows, so each weight fragment feeds BM / 16 MFMAs and the
 // activations alone go through LDS (the row-major kernels' 2 x 2 waves at 64
 // x 128 read both operands from LDS: 1.8-2.5 us slower at these shapes).
@@ -667,11 +671,11 @@ struct SmallTile {
 SmallTile small_plan(int64_t m, int64_t n, int64_t k, bool any_count = false) {
   SmallTile t;
   if (m <= 4 || k % (128 * kSpU) || m * k >= (int64_t(1) << 31) || n * k >= (int64_t(1) << 31)) return t;
-  constexpr int cand[3][2] = {{64, 64}, {96, 32}, {64, 32}};
+  constexpr int cand[4][2] = {{64, 64}, {80, 32}, {96, 32}, {64, 32}};
   for (const auto& c : cand) {
     if (n % (4 * c[1])) continue;
     const int64_t tiles = (m + c[0] - 1) / c[0] * (n / (4 * c[1]));
-    if (tiles >= 192 && tiles <= 512) {
+    if (tiles >= 192 && tiles <= (c[0] == 80 ? 256 : 512)) {
       t.bm = c[0];
       t.cw = c[1];
       return t;
@@ -682,7 +686,7 @@ SmallTile small_plan(int64_t m, int64_t n, int64_t k, bool any_count = false) {
   // tiles give no more) or there is no row-major weight (any_count).
   int64_t most = any_count ? 0 : 63;
   for (const auto& c : cand) {
-    if (n % (4 * c[1])) continue;
+    if (n % (4 * c[1]) || c[0] == 80) continue;
     const int64_t tiles = (m + c[0] - 1) / c[0] * (n / (4 * c[1]));
     if (tiles > most && tiles <= 512) {
       most = tiles;
@@ -732,12 +736,16 @@ void launch_splits(int s, const void* qa, const float* sa, int sa_rows, const vo
   }
 }
 
-// The plan's tile: bm x 4 cw (bm 64 or 144 at cw = kSpCW; 96, 128 or 144 at cw = 32).
+// The plan's tile: bm x 4 cw (bm 64 or 144 at cw = kSpCW; 64, 80, 96, 128 or 144 at cw = 32).
 void launch_plan(const SplitPlan& p, int s, const void* qa, const float* sa, int sa_rows, const void* qw_packed,
                  const float* sw, int sw_cols, void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, void* part,
                  hipStream_t st) {
   if (p.cw == 32) {
-    if (p.bm == 96)
+    if (p.bm == 64)
+      launch_splits<64, 32>(s, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st);
+    else if (p.bm == 80)
+      launch_splits<80, 32>(s, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st);
+    else if (p.bm == 96)
       launch_splits<96, 32>(s, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st);
     else if (p.bm == 128)
       launch_splits<128, 32>(s, qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st);
@@ -1257,6 +1265,8 @@ extern "C" int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, cons
     const SmallTile t = pk ? small_plan(m, n, k, !qw) : SmallTile{};
     if (t.bm == 64 && t.cw == 64)
       launch_small<64, 64>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, st);
+    else if (t.bm == 80)
+      launch_small<80, 32>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, st);
     else if (t.bm == 96)
       launch_small<96, 32>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, st);
     else if (t.bm == 64)

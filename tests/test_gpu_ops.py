@@ -367,7 +367,8 @@ def test_gemm_fp8_swiglu_packed_equals_rowmajor(gpu, m, i, k):
 
 
 # (m, n, k, row tile, splits the packed path takes); 0 = unsplit on the small
-# packed tiles (576 x 4096 x 4096: 96 x 128; 576 / 500 x 6144 x 4096: 64 x 256,
+# packed tiles (576 x 4096 x 4096: 80 x 128, 256 workgroups; 500 x 4096 x 4096:
+# 80 x 128, the last tile ragged; 576 / 500 x 6144 x 4096: 64 x 256,
 # the last tile ragged; 300 x 4096 x 2048: 64 x 128, the candidate with the most
 # workgroups on a short grid; k = 8192 wherever a small tile fills the GPU:
 # 1000 x 6144 and the 32B o projection, 1024 x 5120, on 64 x 256) or the
@@ -378,7 +379,8 @@ PK_SHAPES = [(576, 4096, 12288, 144, 4), (300, 2048, 8192, 144, 8), (1000, 6144,
              (1024, 5120, 8192, 0, 0), (576, 2560, 9728, 144, 4),
              (576, 12288, 4096, 144, 1), (640, 4096, 12288, 144, 3), (1152, 4096, 12288, 144, 2),
              (176, 4096, 12288, 64, 4), (176, 4096, 4096, 64, 4), (64, 2048, 2048, 64, 4), (250, 2048, 6144, 64, 4),
-             (576, 4096, 4096, 0, 0), (576, 6144, 4096, 0, 0), (500, 6144, 4096, 0, 0), (300, 4096, 2048, 0, 0),
+             (576, 4096, 4096, 0, 0), (500, 4096, 4096, 0, 0), (576, 6144, 4096, 0, 0), (500, 6144, 4096, 0, 0),
+             (300, 4096, 2048, 0, 0),
              (3, 4096, 4096, 0, 0), (576, 4160, 12288, 0, 0)]
 
 
