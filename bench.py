@@ -30,8 +30,9 @@ PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 GEMM_KERNELS = ("FP8 GEMM launches of the step: gemm_fp8_swiglu_packed_kernel (gate/up), "
                 "gemm_fp8_split_packed_kernel (down, timed with split_reduce_kernel adding its partials, which "
-                "the step's next add_rms launch does; 96 x 128 tiles unsplit for o), "
-                "gemm_fp8_qkv_packed_kernel (qkv with its epilogue), gemv_fp8 kernels (the tail's single row)")
+                "the step's next add_rms launch does; 80 x 128 tiles unsplit for o), "
+                "gemm_fp8_qkv_packed_kernel (qkv, 128 x 128 tiles, with its epilogue), gemv_fp8 kernels (the tail's "
+                "single row)")
 MICRO_SHAPES = [(320, 2048, 6144), (320, 6144, 2048), (576, 4096, 12288), (576, 12288, 4096),
                 (1024, 5120, 25600)]
 
