@@ -854,7 +854,12 @@ extern "C" int ff_attention_full(const void* q, const void* k, const void* vt, v
   FF_REQUIRE(ff_aligned(q, 16) && ff_aligned(k, 16) && ff_aligned(vt, 16) && ff_aligned(y, 8),
              "ff_attention_full: alignment");
   const float c2 = (float)((double)scale * 1.4426950408889634);  // scale * log2(e)
-  const int qt = t <= 1024 ? 1 : 2;
+  // One query tile per wave while that grid fits two workgroups per CU (512;
+  // the 8B tower at 2048 patches, 16 heads: 512 workgroups, tower step 5.97
+  // -> 5.87 ms against two tiles at 256, same bits), else two.
+  // ff_set_tuning(FF_TUNE_ATTN_QT, 1 | 2) overrides the query tiles per wave.
+  const int qt_env = ff_tuning(FF_TUNE_ATTN_QT);
+  const int qt = qt_env == 1 || qt_env == 2 ? qt_env : ((t + 63) / 64 * heads <= 512 ? 1 : 2);
   const int qb = 16 * qt * 4;  // one head per workgroup: 4 waves x QT tiles of 16 queries
   const int nqb = (int)((t + qb - 1) / qb);
   const dim3 grid((unsigned)(nqb * heads)), block(kThreads);

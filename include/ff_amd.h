@@ -42,7 +42,7 @@ int ff_device_check(void);
 #define FF_TUNE_GEMM_BF16_TILE 2  /* ff_gemm_bf16: 1 64x128, 2 128x128, 3 64x128 at three per CU */
 #define FF_TUNE_W4A16_TILE 3      /* ff_gemm_w4a16*: 1 64x256, 2 192x192 */
 #define FF_TUNE_W4A16_SPLITS 4    /* ff_gemm_w4a16_ws: k splits of the 64x256 tile, 1..8 */
-#define FF_TUNE_ATTN_QT 5         /* ff_attention_vt prefill: query tiles per wave, 1, 2 or 4 */
+#define FF_TUNE_ATTN_QT 5         /* ff_attention_vt prefill (1, 2 or 4) / ff_attention_full (1 or 2): query tiles per wave */
 #define FF_TUNE_ATTN_NS 6         /* ff_attention_vt prefill: K/V LDS stages, 2 or 3 */
 #define FF_TUNE_QKV_PK_TILE 7     /* ff_gemm_fp8_qkv_pk: 1 64x256 packed, 2 64x128 packed, 3 row-major,
                                      4 96x128, 5 144x128, 6 128x128 packed */

@@ -363,6 +363,15 @@ def test_attention_full(gpu, n, nh, hd):
     got = y.cpu().float()
     assert float((got - want).abs().max()) <= 1 / 64
     assert float(((got - want).norm() / want.norm())) <= 5e-3
+    # one and two query tiles per wave (the built-in choice depends on the grid) give the same bits
+    y2 = torch.empty_like(y)
+    call("ff_set_tuning", 5, 2)  # FF_TUNE_ATTN_QT
+    try:
+        call("ff_attention_full", ptr(qd), ptr(kd), ptr(vtd), ptr(y2), n, n_pad, nh, hd, float(hd ** -0.5),
+             stream())
+    finally:
+        call("ff_set_tuning", 5, 0)
+    assert torch.equal(y2, y)
 
 
 def test_pos_interp_bit_exact(gpu):
