@@ -464,8 +464,8 @@ extern "C" int ff_gemm_w4a16_ws(const void* x, int64_t ldx, const void* packed, 
 // BM tokens x CW rows, so each weight is dequantised once per workgroup by the
 // wave that owns it, in registers. The bf16 activations go global -> registers
 // -> LDS: two 128-k stages and one barrier per step; each 256-byte row sits as
-// two 128-byte halves, each half in the FP8 GEMM's swizzled layout (1 KB
-// blocks of 8 rows, 16-byte chunk c of row r at slot c ^ ((r % 16) / 2)).
+// two 128-byte halves, each half in the packed FP8 GEMM's swizzled layout (1 KB
+// blocks of 8 rows, 16-byte chunk c of row r at slot c ^ (r % 8) ^ ((r / 8) % 2)).
 // The weight fragment is the MFMA's first operand, so the accumulator holds the
 // transposed tile: lane 16 g + r of fragment (i, j) holds token 16 i + r,
 // weight rows 16 j + 4 g .. + 3, and the epilogues store 8-byte row pieces
@@ -616,7 +616,7 @@ __device__ __forceinline__ void w4pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], ui
     const int c = i < FULL ? tid + kThreads * i : A_CHUNKS - kThreads + tid;
     const int row = c >> 4, ch = c & 15;
     voffA[i] = (uint32_t)min(m0 + row, M - 1) * (uint32_t)(2 * ldx) + 16 * ch;
-    dstA[i] = (ch >> 3) * HALF + (row >> 3) * 1024 + 128 * (row & 7) + 16 * ((ch & 7) ^ ((row & 15) >> 1));
+    dstA[i] = (ch >> 3) * HALF + (row >> 3) * 1024 + 128 * (row & 7) + 16 * ((ch & 7) ^ (row & 7) ^ ((row >> 3) & 1));
   }
   i32x4v ast[NA];
   auto loadA1 = [&](int kt, int i) { ast[i] = bload16(rA, voffA[i], (uint32_t)kt * 256u); };
@@ -680,7 +680,8 @@ __device__ __forceinline__ void w4pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], ui
   loadB(min(kt0 + 1, kend - 1), I1{});
 
   const int frag = 128 * (r16 & 7) + 1024 * (r16 >> 3);
-  const int cA[2] = {16 * ((2 * g) ^ (r16 >> 1)), 16 * ((2 * g + 1) ^ (r16 >> 1))};
+  const int sw = (r16 & 7) ^ (r16 >> 3);
+  const int cA[2] = {16 * ((2 * g) ^ sw), 16 * ((2 * g + 1) ^ sw)};
   // The first fragment of every step is dequantised in the step before (the
   // first step's here).
   u32x4 bfirst;
