@@ -248,6 +248,144 @@ constexpr int pk_smem() {
   return 2 * G * BM * 128;
 }
 
+// The main loop in fragment-outer order (same operands, same k order per
+// accumulator as pk_mainloop, so the same bits). In pk_mainloop a step's
+// activation-fragment reads issue only once the previous step's last MFMA
+// has: the four waves then wait together for the whole LDS delivery before
+// their first MFMAs of the step (a tile whose LDS reads take about as long as
+// its MFMAs runs the two phases back to back). Here two LDS stages and one
+// barrier at the start of each step, after the step's waves have written the
+// next step's stage; each activation fragment register is refilled from that
+// stage as soon as its last MFMA of the step has issued, so the next step's
+// reads stream under this step's MFMAs. The weight fragments are refilled at
+// the end of the step for step k + P (P one more than pk_mainloop's for the
+// same lead).
+template <int BM, int CW, int P, int D, typename Pre>
+__device__ __forceinline__ void pk_mainloop_io(f32x4 (&acc)[BM / 16][CW / 16], uint8_t* smem,
+                                               const uint8_t* __restrict__ qa, int M, int K, int m0,
+                                               const uint8_t* __restrict__ qwp, uint32_t wbytes,
+                                               const uint32_t (&sB)[CW / 16], int kt0, int nk, Pre&& pre) {
+  constexpr int RA = BM / 16, TJ = CW / 16;
+  constexpr int A_CHUNKS = BM * 8;
+  constexpr int FULL = A_CHUNKS / kThreads, REM = A_CHUNKS % kThreads;
+  constexpr int NA = FULL + (REM ? 1 : 0);
+  constexpr int STAGE = BM * 128;
+  constexpr int U = lcm3(P, D, 2);  // k steps per unrolled loop iteration
+  static_assert(A_CHUNKS >= kThreads, "at least one full activation round");
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int kend = kt0 + nk;
+
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(qa, (uint32_t)M * (uint32_t)K);
+  uint32_t voffA[NA];
+  int dstA[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int c = i < FULL ? tid + kThreads * i : A_CHUNKS - kThreads + tid;
+    const int row = c >> 3, ch = c & 7;
+    voffA[i] = (uint32_t)min(m0 + row, M - 1) * (uint32_t)K + 16 * ch;
+    dstA[i] = (row >> 3) * 1024 + 128 * (row & 7) + 16 * (ch ^ (row & 7) ^ ((row >> 3) & 1));
+  }
+  i32x4v ast[D][NA];
+  auto loadA = [&](int kt, auto SLOT) {
+    constexpr int slot = decltype(SLOT)::value;
+    static_for<0, NA>([&](auto I_) {
+      constexpr int i = decltype(I_)::value;
+      ast[slot][i] = bload16(rA, voffA[i], (uint32_t)kt * 128);
+    });
+  };
+  auto writeA = [&](auto SLOT, auto BUF) {
+    constexpr int slot = decltype(SLOT)::value, buf = decltype(BUF)::value;
+    static_for<0, NA>([&](auto I_) {
+      constexpr int i = decltype(I_)::value;
+      *reinterpret_cast<i32x4v*>(smem + buf * STAGE + dstA[i]) = ast[slot][i];
+    });
+  };
+
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(qwp, wbytes);
+  const uint32_t kstride = wbytes / (uint32_t)(K / 128);
+  const uint32_t voffB = 16u * (uint32_t)lane;
+  i32x8 bq[P][TJ];
+  auto loadB = [&](int kt, auto SLOT) {
+    constexpr int slot = decltype(SLOT)::value;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const i32x4v lo = bload16(rB, voffB, sB[j] + (uint32_t)kt * kstride);
+      const i32x4v hi = bload16(rB, voffB + 1024u, sB[j] + (uint32_t)kt * kstride);
+      bq[slot][j] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    }
+  };
+  const int frag = 128 * (r16 & 7) + 1024 * (r16 >> 3);
+  const int sw = (r16 & 7) ^ (r16 >> 3);
+  const int c0 = 16 * ((2 * g) ^ sw), c1 = 16 * ((2 * g + 1) ^ sw);
+  i32x8 af[RA];
+  auto readA = [&](int buf, int i) {
+    const uint8_t* st = smem + buf * STAGE + frag + 2 * i * 1024;
+    const i32x4v lo = *reinterpret_cast<const i32x4v*>(st + c0);
+    const i32x4v hi = *reinterpret_cast<const i32x4v*>(st + c1);
+    af[i] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  };
+
+#pragma unroll
+  for (int i = 0; i < RA; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#define ACC_PIN()                                     \
+  do {                                                \
+    _Pragma("unroll") for (int i_ = 0; i_ < RA; ++i_) \
+    _Pragma("unroll") for (int j_ = 0; j_ < TJ; ++j_) \
+      asm volatile("" : "+a"(acc[i_][j_]));           \
+  } while (0)
+#define ACC_NOPS() asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(acc[RA - 1][TJ - 1]))
+  ACC_PIN();
+  ACC_NOPS();
+
+  // Prologue: stage 0 = step kt0; staging slots (s) % D = steps kt0 + s for
+  // s = 1..D; weight stages = steps kt0..kt0+P-1; then step kt0's fragments.
+  using I0 = std::integral_constant<int, 0>;
+  loadA(kt0, I0{});
+  __builtin_amdgcn_sched_barrier(0);
+  pre();
+  __builtin_amdgcn_sched_barrier(0);
+  writeA(I0{}, I0{});
+  static_for<0, (D > P ? D : P)>([&](auto S_) {
+    constexpr int s = decltype(S_)::value;
+    if constexpr (s < D) loadA(min(kt0 + 1 + s, kend - 1), std::integral_constant<int, (1 + s) % D>{});
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (s < P) loadB(min(kt0 + s, kend - 1), std::integral_constant<int, s>{});
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < RA; ++i) readA(0, i);
+
+  for (int kb = kt0; kb < kend; kb += U) {
+    static_for<0, U>([&](auto U_) {
+      constexpr int u = decltype(U_)::value;
+      const int kt = kb + u;
+      // step kt + 1's stage (its buffer last held step kt - 1, whose fragments
+      // every wave read before the previous step's barrier)
+      writeA(std::integral_constant<int, (u + 1) % D>{}, std::integral_constant<int, (u + 1) % 2>{});
+      __syncthreads();
+      loadA(min(kt + 1 + D, kend - 1), std::integral_constant<int, (u + 1) % D>{});
+#pragma unroll
+      for (int i = 0; i < RA; ++i) {
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) mfma_acc(acc[i][j], bq[u % P][j], af[i]);
+        readA((u + 1) % 2, i);
+      }
+      loadB(min(kt + P, kend - 1), std::integral_constant<int, u % P>{});
+    });
+  }
+  ACC_NOPS();
+  ACC_PIN();
+#undef ACC_PIN
+#undef ACC_NOPS
+}
+
+// Weight register stages of pk_mainloop_io.
+constexpr int kIoP = 4;
+
 // Gate/up: BM tokens x (BN/2 gate + BN/2 up channels), BN = 4 CW; wave w takes
 // gate channels [w CW/2, (w + 1) CW/2) of the tile and the matching up
 // channels, as fragments j = 2 t (gate, channels 16 t ..) and j = 2 t + 1 (up,
@@ -407,14 +545,14 @@ __device__ __forceinline__ void pk_store_tile(const f32x4 (&acc)[BM / 16][CW / 1
 // whole tiles, part[(split Mp + row) N + col] (Mp = tiles_m BM), and the next
 // launch adds the partials: split_reduce_kernel, or the add_rms row kernel
 // that takes them in place of its bf16 addend.
-template <int BM, int CW, int P, int D, int G, int S>
-__global__ __launch_bounds__(kThreads, BM <= 96 ? 2 : 1) void gemm_fp8_split_packed_kernel(
+template <int BM, int CW, int P, int D, int G, int S, bool IO = false>
+__global__ __launch_bounds__(kThreads, BM <= 96 && !IO ? 2 : 1) void gemm_fp8_split_packed_kernel(
     const uint8_t* __restrict__ qa, const float* __restrict__ sa, int sa_rows, const uint8_t* __restrict__ qwp,
     const float* __restrict__ sw, int sw_cols, bf16_t* __restrict__ y, int64_t ldy, int M, int N, int K,
     int tiles_m, int tiles_n, float* __restrict__ part) {
   constexpr int BN = 4 * CW;
   constexpr int RA = BM / 16, TJ = CW / 16;
-  constexpr int SMEM = pk_smem<BM, G>();
+  constexpr int SMEM = pk_smem<BM, G>();  // pk_mainloop_io uses the first two stages
   static_assert(SMEM <= 160 * 1024, "LDS budget");
   __shared__ __align__(1024) uint8_t smem[SMEM];
 
@@ -429,7 +567,7 @@ __global__ __launch_bounds__(kThreads, BM <= 96 ? 2 : 1) void gemm_fp8_split_pac
   // this split's k steps: the kt / U blocks of U steps (U = the main loop's
   // unrolled steps) dealt out as evenly as whole blocks allow, so k need not
   // divide by S U (32B down, 200 steps: 3 splits of 68, 68 and 64)
-  constexpr int U = lcm3(P, D, 2 * G);
+  constexpr int U = IO ? lcm3(P, D, 2) : lcm3(P, D, 2 * G);
   const int nbk = K / (128 * U);
   const int kt0 = split * nbk / S * U, nk = (split + 1) * nbk / S * U - kt0;
 
@@ -438,7 +576,10 @@ __global__ __launch_bounds__(kThreads, BM <= 96 ? 2 : 1) void gemm_fp8_split_pac
 #pragma unroll
   for (int j = 0; j < TJ; ++j) sB[j] = (uint32_t)((n0 + wave_s * CW + 16 * j) / 16) * 2048u;
   f32x4 acc[RA][TJ];
-  pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, kt0, nk, [] {});
+  if constexpr (IO)
+    pk_mainloop_io<BM, CW, P, D>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, kt0, nk, [] {});
+  else
+    pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, kt0, nk, [] {});
   if constexpr (S > 1) {
     // the fp32 partial tile, row-major over the rows padded to whole tiles
     store_tile_rows_lds<BM, CW, SMEM>(acc, smem, part + ((int64_t)split * tiles_m * BM + m0) * N + n0, N, tid);
@@ -706,7 +847,12 @@ template <int BM, int CW>
 void launch_small(const void* qa, const float* sa, int sa_rows, const void* qw_packed, const float* sw, int sw_cols,
                   void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, hipStream_t st) {
   const int64_t tm = (m + BM - 1) / BM, tn = n / (4 * CW);
-  hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<BM, CW, kSpP, kSpD, kSpG, 1>), dim3((unsigned)(tm * tn)),
+  // The 80 x 128 tile (the 8B o projection at 576 tokens) on the fragment-outer
+  // loop: same bits, 17.3 -> 16.9 us per launch, with the qkv one below the
+  // step 6.213-6.231 -> 6.166-6.183 ms (same box); the other small tiles were
+  // not faster on it.
+  constexpr bool io = BM == 80 && CW == 32;
+  hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<BM, CW, io ? kIoP : kSpP, kSpD, kSpG, 1, io>), dim3((unsigned)(tm * tn)),
                      dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows, (const uint8_t*)qw_packed, sw, sw_cols,
                      (bf16_t*)y, ldy, (int)m, (int)n, (int)k, (int)tm, (int)tn, (float*)nullptr);
 }
@@ -784,8 +930,8 @@ struct PkQkv {
   int hq, hk, t_pad;
 };
 
-template <int BM, int CW, int P, int D, int G>
-__global__ __launch_bounds__(kThreads, BM <= 96 ? 2 : 1) void gemm_fp8_qkv_packed_kernel(
+template <int BM, int CW, int P, int D, int G, bool IO = false>
+__global__ __launch_bounds__(kThreads, BM <= 96 && !IO ? 2 : 1) void gemm_fp8_qkv_packed_kernel(
     const uint8_t* __restrict__ qa, const float* __restrict__ sa, int sa_rows, const uint8_t* __restrict__ qwp,
     const float* __restrict__ sw, int sw_cols, int M, int N, int K, int tiles_m, int tiles_n, PkQkv qe) {
   constexpr int BN = 4 * CW, RA = BM / 16, TJ = CW / 16;
@@ -793,7 +939,7 @@ __global__ __launch_bounds__(kThreads, BM <= 96 ? 2 : 1) void gemm_fp8_qkv_packe
   constexpr int HPT = BN / kHeadDim;         // heads per tile
   constexpr int LD = BN + 8;                 // bf16 row pitch of the LDS tile
   constexpr int ROWS = BM / (kThreads / 16);  // token rows per 16-lane group
-  constexpr int SMEM_LOOP = pk_smem<BM, G>(), SMEM_TILE = BM * LD * 2;
+  constexpr int SMEM_LOOP = IO ? 2 * BM * 128 : pk_smem<BM, G>(), SMEM_TILE = BM * LD * 2;
   constexpr int SMEM = SMEM_LOOP > SMEM_TILE ? SMEM_LOOP : SMEM_TILE;
   static_assert(SMEM <= (BM <= 96 ? 80 : 160) * 1024, "two workgroups per CU up to 96 rows");
   __shared__ __align__(1024) uint8_t smem[SMEM];
@@ -813,7 +959,10 @@ __global__ __launch_bounds__(kThreads, BM <= 96 ? 2 : 1) void gemm_fp8_qkv_packe
 #pragma unroll
   for (int j = 0; j < TJ; ++j) sB[j] = (uint32_t)((n0 + wave_s * CW + 16 * j) / 16) * 2048u;
   f32x4 acc[RA][TJ];
-  pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, 0, KT, [] {});
+  if constexpr (IO)
+    pk_mainloop_io<BM, CW, P, D>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, 0, KT, [] {});
+  else
+    pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, 0, KT, [] {});
 
   // The epilogue's global loads (norm weights, this thread's cos / sin rows)
   // are issued before the tile is staged.
@@ -1350,14 +1499,17 @@ extern "C" int ff_gemm_fp8_qkv_pk(const void* qa, const float* sa, int sa_rows, 
   FF_REQUIRE(sa && sw && q_norm && k_norm && yq && yk && vt, "ff_gemm_fp8_qkv_pk: null pointer");
   PkQkv qe{(const bf16_t*)q_norm, (const bf16_t*)k_norm, eps_q, eps_k, (const bf16_t*)cos, (const bf16_t*)sin,
            (bf16_t*)yq, (bf16_t*)yk, (bf16_t*)vt, (int)hq, (int)hk, (int)t_pad};
-#define FF_QKV_BM(BM)                                                                                         \
+  // The 128 x 128 tile (576 tokens) on the fragment-outer loop: same bits,
+  // 24.1 -> 23.9 us per launch (the step's A/B is at launch_small); the
+  // 64 x 128 tile at 176 tokens was not faster on it.
+#define FF_QKV_BM(BM, IO)                                                                                     \
   if (bm == BM)                                                                                               \
-    hipLaunchKernelGGL((gemm_fp8_qkv_packed_kernel<BM, 32, kSpP, kSpD, kSpG>), dim3((unsigned)tiles),          \
-                       dim3(kThreads), 0, (hipStream_t)stream, (const uint8_t*)qa, sa, sa_rows,               \
-                       (const uint8_t*)qw_packed, sw, sw_cols, (int)m, (int)n, (int)k, (int)tiles_m,          \
+    hipLaunchKernelGGL((gemm_fp8_qkv_packed_kernel<BM, 32, IO ? kIoP : kSpP, kSpD, kSpG, IO>),                \
+                       dim3((unsigned)tiles), dim3(kThreads), 0, (hipStream_t)stream, (const uint8_t*)qa, sa, \
+                       sa_rows, (const uint8_t*)qw_packed, sw, sw_cols, (int)m, (int)n, (int)k, (int)tiles_m, \
                        (int)tiles_n, qe);
   if (bm != kQkBM) {
-    FF_QKV_BM(96) FF_QKV_BM(144) FF_QKV_BM(128)
+    FF_QKV_BM(96, false) FF_QKV_BM(144, false) FF_QKV_BM(128, true)
   } else if (cw == 32)
     hipLaunchKernelGGL((gemm_fp8_qkv_packed_kernel<kQkBM, 32, kSpP, kSpD, kSpG>), dim3((unsigned)tiles),
                        dim3(kThreads), 0, (hipStream_t)stream, (const uint8_t*)qa, sa, sa_rows,
