@@ -248,20 +248,20 @@ constexpr int pk_smem() {
   return 2 * G * BM * 128;
 }
 
-// The main loop in fragment-outer order (same operands, same k order per
-// accumulator as pk_mainloop, so the same bits). In pk_mainloop a step's
-// activation-fragment reads issue only once the previous step's last MFMA
-// has: the four waves then wait together for the whole LDS delivery before
-// their first MFMAs of the step (a tile whose LDS reads take about as long as
-// its MFMAs runs the two phases back to back). Here two LDS stages and one
-// barrier at the start of each step, after the step's waves have written the
-// next step's stage; each activation fragment register is refilled from that
-// stage as soon as its last MFMA of the step has issued, so the next step's
-// reads stream under this step's MFMAs. The weight fragments are refilled at
-// the end of the step for step k + P (P one more than pk_mainloop's for the
-// same lead).
+// The main loop with the next step's activation fragments read under this
+// step's last MFMAs (same operands, same k order per accumulator as
+// pk_mainloop, so the same bits). In pk_mainloop a step's fragment reads issue
+// only once the previous step's last MFMA has: the four waves then wait together
+// for the whole LDS delivery while their first MFMAs of the step trail it. Here
+// two LDS stages; each step writes the next step's stage from registers first,
+// runs its MFMAs weight fragment by weight fragment (each weight fragment
+// refilled for step k + P right after its MFMAs, as in pk_mainloop), and takes
+// its one barrier before the last weight fragment's MFMAs, each of which is
+// followed by the read of the same activation fragment for the next step. The
+// stage a step writes last held step k - 1, whose fragments every wave read
+// before the previous step's barrier.
 template <int BM, int CW, int P, int D, typename Pre>
-__device__ __forceinline__ void pk_mainloop_io(f32x4 (&acc)[BM / 16][CW / 16], uint8_t* smem,
+__device__ __forceinline__ void pk_mainloop_pf(f32x4 (&acc)[BM / 16][CW / 16], uint8_t* smem,
                                                const uint8_t* __restrict__ qa, int M, int K, int m0,
                                                const uint8_t* __restrict__ qwp, uint32_t wbytes,
                                                const uint32_t (&sB)[CW / 16], int kt0, int nk, Pre&& pre) {
@@ -366,15 +366,25 @@ __device__ __forceinline__ void pk_mainloop_io(f32x4 (&acc)[BM / 16][CW / 16], u
       // step kt + 1's stage (its buffer last held step kt - 1, whose fragments
       // every wave read before the previous step's barrier)
       writeA(std::integral_constant<int, (u + 1) % D>{}, std::integral_constant<int, (u + 1) % 2>{});
-      __syncthreads();
       loadA(min(kt + 1 + D, kend - 1), std::integral_constant<int, (u + 1) % D>{});
+      const uint32_t ktn = (uint32_t)min(kt + P, kend - 1);
+      static_for<0, TJ - 1>([&](auto J_) {
+        constexpr int j = decltype(J_)::value;
+#pragma unroll
+        for (int i = 0; i < RA; ++i) mfma_acc(acc[i][j], bq[u % P][j], af[i]);
+        const i32x4v lo = bload16(rB, voffB, sB[j] + ktn * kstride);
+        const i32x4v hi = bload16(rB, voffB + 1024u, sB[j] + ktn * kstride);
+        bq[u % P][j] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      });
+      __syncthreads();
 #pragma unroll
       for (int i = 0; i < RA; ++i) {
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) mfma_acc(acc[i][j], bq[u % P][j], af[i]);
+        mfma_acc(acc[i][TJ - 1], bq[u % P][TJ - 1], af[i]);
         readA((u + 1) % 2, i);
       }
-      loadB(min(kt + P, kend - 1), std::integral_constant<int, u % P>{});
+      const i32x4v lo = bload16(rB, voffB, sB[TJ - 1] + ktn * kstride);
+      const i32x4v hi = bload16(rB, voffB + 1024u, sB[TJ - 1] + ktn * kstride);
+      bq[u % P][TJ - 1] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
     });
   }
   ACC_NOPS();
@@ -383,8 +393,6 @@ __device__ __forceinline__ void pk_mainloop_io(f32x4 (&acc)[BM / 16][CW / 16], u
 #undef ACC_NOPS
 }
 
-// Weight register stages of pk_mainloop_io.
-constexpr int kIoP = 4;
 
 // Gate/up: BM tokens x (BN/2 gate + BN/2 up channels), BN = 4 CW; wave w takes
 // gate channels [w CW/2, (w + 1) CW/2) of the tile and the matching up
@@ -393,7 +401,7 @@ constexpr int kIoP = 4;
 // SQ (static quantisation of the output): sa[0] and sw[0] are per-tensor
 // scales and h is written as e4m3(clamp(h * qinv, +-448)) into hq (ldh bytes
 // per row), without row maxima.
-template <int BM, int CW, int P, int D, int G, bool SQ = false>
+template <int BM, int CW, int P, int D, int G, bool SQ = false, bool PF = false>
 __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
     const uint8_t* __restrict__ qa, const float* __restrict__ sa, const uint8_t* __restrict__ qwp,
     const float* __restrict__ sw, bf16_t* __restrict__ h, int64_t ldh, float* __restrict__ pmax, int M, int half,
@@ -428,8 +436,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
     sB[j] = (uint32_t)(row / 16) * 2048u;
   }
   f32x4 acc[RA][TJ];
-  pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)(2 * half) * (uint32_t)K, sB, 0, KT,
-                               [&] { silu_table_fill<kThreads>(silu_tab, tid); });
+  if constexpr (PF)
+    pk_mainloop_pf<BM, CW, P, D>(acc, smem, qa, M, K, m0, qwp, (uint32_t)(2 * half) * (uint32_t)K, sB, 0, KT,
+                                 [&] { silu_table_fill<kThreads>(silu_tab, tid); });
+  else
+    pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)(2 * half) * (uint32_t)K, sB, 0, KT,
+                                 [&] { silu_table_fill<kThreads>(silu_tab, tid); });
 
   // g, u = bf16((acc * sa) * sw); h = bf16(bf16(silu(g)) * u), in registers:
   // lane 16 g + r holds token 16 i + r, channels c + 4 g .. + 3 of block t.
@@ -545,14 +557,14 @@ __device__ __forceinline__ void pk_store_tile(const f32x4 (&acc)[BM / 16][CW / 1
 // whole tiles, part[(split Mp + row) N + col] (Mp = tiles_m BM), and the next
 // launch adds the partials: split_reduce_kernel, or the add_rms row kernel
 // that takes them in place of its bf16 addend.
-template <int BM, int CW, int P, int D, int G, int S, bool IO = false>
-__global__ __launch_bounds__(kThreads, BM <= 96 && !IO ? 2 : 1) void gemm_fp8_split_packed_kernel(
+template <int BM, int CW, int P, int D, int G, int S, bool PF = false>
+__global__ __launch_bounds__(kThreads, BM <= 96 && !PF ? 2 : 1) void gemm_fp8_split_packed_kernel(
     const uint8_t* __restrict__ qa, const float* __restrict__ sa, int sa_rows, const uint8_t* __restrict__ qwp,
     const float* __restrict__ sw, int sw_cols, bf16_t* __restrict__ y, int64_t ldy, int M, int N, int K,
     int tiles_m, int tiles_n, float* __restrict__ part) {
   constexpr int BN = 4 * CW;
   constexpr int RA = BM / 16, TJ = CW / 16;
-  constexpr int SMEM = pk_smem<BM, G>();  // pk_mainloop_io uses the first two stages
+  constexpr int SMEM = pk_smem<BM, G>();  // pk_mainloop_pf uses the first two stages
   static_assert(SMEM <= 160 * 1024, "LDS budget");
   __shared__ __align__(1024) uint8_t smem[SMEM];
 
@@ -567,7 +579,7 @@ __global__ __launch_bounds__(kThreads, BM <= 96 && !IO ? 2 : 1) void gemm_fp8_sp
   // this split's k steps: the kt / U blocks of U steps (U = the main loop's
   // unrolled steps) dealt out as evenly as whole blocks allow, so k need not
   // divide by S U (32B down, 200 steps: 3 splits of 68, 68 and 64)
-  constexpr int U = IO ? lcm3(P, D, 2) : lcm3(P, D, 2 * G);
+  constexpr int U = PF ? lcm3(P, D, 2) : lcm3(P, D, 2 * G);
   const int nbk = K / (128 * U);
   const int kt0 = split * nbk / S * U, nk = (split + 1) * nbk / S * U - kt0;
 
@@ -576,8 +588,8 @@ __global__ __launch_bounds__(kThreads, BM <= 96 && !IO ? 2 : 1) void gemm_fp8_sp
 #pragma unroll
   for (int j = 0; j < TJ; ++j) sB[j] = (uint32_t)((n0 + wave_s * CW + 16 * j) / 16) * 2048u;
   f32x4 acc[RA][TJ];
-  if constexpr (IO)
-    pk_mainloop_io<BM, CW, P, D>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, kt0, nk, [] {});
+  if constexpr (PF)
+    pk_mainloop_pf<BM, CW, P, D>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, kt0, nk, [] {});
   else
     pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, kt0, nk, [] {});
   if constexpr (S > 1) {
@@ -847,12 +859,9 @@ template <int BM, int CW>
 void launch_small(const void* qa, const float* sa, int sa_rows, const void* qw_packed, const float* sw, int sw_cols,
                   void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, hipStream_t st) {
   const int64_t tm = (m + BM - 1) / BM, tn = n / (4 * CW);
-  // The 80 x 128 tile (the 8B o projection at 576 tokens) on the fragment-outer
-  // loop: same bits, 17.3 -> 16.9 us per launch, with the qkv one below the
-  // step 6.213-6.231 -> 6.166-6.183 ms (same box); the other small tiles were
-  // not faster on it.
-  constexpr bool io = BM == 80 && CW == 32;
-  hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<BM, CW, io ? kIoP : kSpP, kSpD, kSpG, 1, io>), dim3((unsigned)(tm * tn)),
+  // The 80 x 128 tile (the 8B o projection at 576 tokens) on pk_mainloop_pf.
+  constexpr bool pf = BM == 80 && CW == 32;
+  hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<BM, CW, kSpP, kSpD, kSpG, 1, pf>), dim3((unsigned)(tm * tn)),
                      dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows, (const uint8_t*)qw_packed, sw, sw_cols,
                      (bf16_t*)y, ldy, (int)m, (int)n, (int)k, (int)tm, (int)tn, (float*)nullptr);
 }
@@ -868,7 +877,9 @@ template <int BM, int S, int CW = kSpCW>
 void launch_split(const void* qa, const float* sa, int sa_rows, const void* qw_packed, const float* sw, int sw_cols,
                   void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, void* part, hipStream_t st) {
   const int64_t tiles_m = (m + BM - 1) / BM, tiles_n = n / (4 * CW);
-  hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<BM, CW, kSpP, kSpD, kSpG, S>),
+  // 144 x 256 tiles split 4 ways (the 8B down projection at 576 tokens) on pk_mainloop_pf.
+  constexpr bool pf = BM == 144 && CW == 64 && S == 4;
+  hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<BM, CW, kSpP, kSpD, kSpG, S, pf>),
                      dim3((unsigned)(tiles_m * tiles_n * S)), dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows,
                      (const uint8_t*)qw_packed, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)n, (int)k, (int)tiles_m,
                      (int)tiles_n, (float*)part);
@@ -930,8 +941,8 @@ struct PkQkv {
   int hq, hk, t_pad;
 };
 
-template <int BM, int CW, int P, int D, int G, bool IO = false>
-__global__ __launch_bounds__(kThreads, BM <= 96 && !IO ? 2 : 1) void gemm_fp8_qkv_packed_kernel(
+template <int BM, int CW, int P, int D, int G, bool PF = false>
+__global__ __launch_bounds__(kThreads, BM <= 96 && !PF ? 2 : 1) void gemm_fp8_qkv_packed_kernel(
     const uint8_t* __restrict__ qa, const float* __restrict__ sa, int sa_rows, const uint8_t* __restrict__ qwp,
     const float* __restrict__ sw, int sw_cols, int M, int N, int K, int tiles_m, int tiles_n, PkQkv qe) {
   constexpr int BN = 4 * CW, RA = BM / 16, TJ = CW / 16;
@@ -939,7 +950,7 @@ __global__ __launch_bounds__(kThreads, BM <= 96 && !IO ? 2 : 1) void gemm_fp8_qk
   constexpr int HPT = BN / kHeadDim;         // heads per tile
   constexpr int LD = BN + 8;                 // bf16 row pitch of the LDS tile
   constexpr int ROWS = BM / (kThreads / 16);  // token rows per 16-lane group
-  constexpr int SMEM_LOOP = IO ? 2 * BM * 128 : pk_smem<BM, G>(), SMEM_TILE = BM * LD * 2;
+  constexpr int SMEM_LOOP = PF ? 2 * BM * 128 : pk_smem<BM, G>(), SMEM_TILE = BM * LD * 2;
   constexpr int SMEM = SMEM_LOOP > SMEM_TILE ? SMEM_LOOP : SMEM_TILE;
   static_assert(SMEM <= (BM <= 96 ? 80 : 160) * 1024, "two workgroups per CU up to 96 rows");
   __shared__ __align__(1024) uint8_t smem[SMEM];
@@ -959,8 +970,8 @@ __global__ __launch_bounds__(kThreads, BM <= 96 && !IO ? 2 : 1) void gemm_fp8_qk
 #pragma unroll
   for (int j = 0; j < TJ; ++j) sB[j] = (uint32_t)((n0 + wave_s * CW + 16 * j) / 16) * 2048u;
   f32x4 acc[RA][TJ];
-  if constexpr (IO)
-    pk_mainloop_io<BM, CW, P, D>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, 0, KT, [] {});
+  if constexpr (PF)
+    pk_mainloop_pf<BM, CW, P, D>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, 0, KT, [] {});
   else
     pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, 0, KT, [] {});
 
@@ -1310,9 +1321,10 @@ extern "C" int ff_gemm_fp8_swiglu_pk(const void* qa, const float* sa, const void
   if (!packed_fits) return ff_gemm_fp8_swiglu(qa, sa, qw, sw, h, ldh, pmax, m, i, k, stream);
   const int64_t tiles_n = i / (2 * cw), tiles_m = (m + bm - 1) / bm;
   bool launched = false;
+  // The 144 x 384 tile (576 tokens) on pk_mainloop_pf.
 #define FF_SWIGLU(BM, CW)                                                                                           \
   if (bm == BM && cw == CW && (launched = true))                                                                    \
-    hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<BM, CW, kPkP, kPkD, kPkG>),                                   \
+    hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<BM, CW, kPkP, kPkD, kPkG, false, BM == 144 && CW == 96>), \
                        dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads), 0, (hipStream_t)stream,                 \
                        (const uint8_t*)qa, sa, (const uint8_t*)qw_packed, sw, (bf16_t*)h, ldh, pmax, (int)m,        \
                        (int)i, (int)k, (int)tiles_m, (int)tiles_n, nullptr, 0.f);
@@ -1499,12 +1511,10 @@ extern "C" int ff_gemm_fp8_qkv_pk(const void* qa, const float* sa, int sa_rows, 
   FF_REQUIRE(sa && sw && q_norm && k_norm && yq && yk && vt, "ff_gemm_fp8_qkv_pk: null pointer");
   PkQkv qe{(const bf16_t*)q_norm, (const bf16_t*)k_norm, eps_q, eps_k, (const bf16_t*)cos, (const bf16_t*)sin,
            (bf16_t*)yq, (bf16_t*)yk, (bf16_t*)vt, (int)hq, (int)hk, (int)t_pad};
-  // The 128 x 128 tile (576 tokens) on the fragment-outer loop: same bits,
-  // 24.1 -> 23.9 us per launch (the step's A/B is at launch_small); the
-  // 64 x 128 tile at 176 tokens was not faster on it.
-#define FF_QKV_BM(BM, IO)                                                                                     \
+  // The 128 x 128 tile (576 tokens) on pk_mainloop_pf.
+#define FF_QKV_BM(BM, PF)                                                                                     \
   if (bm == BM)                                                                                               \
-    hipLaunchKernelGGL((gemm_fp8_qkv_packed_kernel<BM, 32, IO ? kIoP : kSpP, kSpD, kSpG, IO>),                \
+    hipLaunchKernelGGL((gemm_fp8_qkv_packed_kernel<BM, 32, kSpP, kSpD, kSpG, PF>),                            \
                        dim3((unsigned)tiles), dim3(kThreads), 0, (hipStream_t)stream, (const uint8_t*)qa, sa, \
                        sa_rows, (const uint8_t*)qw_packed, sw, sw_cols, (int)m, (int)n, (int)k, (int)tiles_m, \
                        (int)tiles_n, qe);
