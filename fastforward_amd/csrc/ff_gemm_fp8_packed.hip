@@ -877,8 +877,9 @@ template <int BM, int S, int CW = kSpCW>
 void launch_split(const void* qa, const float* sa, int sa_rows, const void* qw_packed, const float* sw, int sw_cols,
                   void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, void* part, hipStream_t st) {
   const int64_t tiles_m = (m + BM - 1) / BM, tiles_n = n / (4 * CW);
-  // 144 x 256 tiles split 4 ways (the 8B down projection at 576 tokens) on pk_mainloop_pf.
-  constexpr bool pf = BM == 144 && CW == 64 && S == 4;
+  // pk_mainloop_pf for 144 x 256 tiles split 4 ways (the 8B down projection at
+  // 576 tokens) and 64 x 256 tiles split 4 ways (o and down at 176 tokens).
+  constexpr bool pf = (BM == 144 || BM == 64) && CW == 64 && S == 4;
   hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<BM, CW, kSpP, kSpD, kSpG, S, pf>),
                      dim3((unsigned)(tiles_m * tiles_n * S)), dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows,
                      (const uint8_t*)qw_packed, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)n, (int)k, (int)tiles_m,
@@ -1321,10 +1322,11 @@ extern "C" int ff_gemm_fp8_swiglu_pk(const void* qa, const float* sa, const void
   if (!packed_fits) return ff_gemm_fp8_swiglu(qa, sa, qw, sw, h, ldh, pmax, m, i, k, stream);
   const int64_t tiles_n = i / (2 * cw), tiles_m = (m + bm - 1) / bm;
   bool launched = false;
-  // The 144 x 384 tile (576 tokens) on pk_mainloop_pf.
+  // The 144 x 384 (576 tokens) and 176 x 128 (176 tokens) tiles on pk_mainloop_pf.
 #define FF_SWIGLU(BM, CW)                                                                                           \
   if (bm == BM && cw == CW && (launched = true))                                                                    \
-    hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<BM, CW, kPkP, kPkD, kPkG, false, BM == 144 && CW == 96>), \
+    hipLaunchKernelGGL((gemm_fp8_swiglu_packed_kernel<BM, CW, kPkP, kPkD, kPkG, false,                              \
+                                                      (BM == 144 && CW == 96) || (BM == 176 && CW == 32)>),         \
                        dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads), 0, (hipStream_t)stream,                 \
                        (const uint8_t*)qa, sa, (const uint8_t*)qw_packed, sw, (bf16_t*)h, ldh, pmax, (int)m,        \
                        (int)i, (int)k, (int)tiles_m, (int)tiles_n, nullptr, 0.f);
@@ -1520,8 +1522,8 @@ extern "C" int ff_gemm_fp8_qkv_pk(const void* qa, const float* sa, int sa_rows, 
                        (int)tiles_n, qe);
   if (bm != kQkBM) {
     FF_QKV_BM(96, false) FF_QKV_BM(144, false) FF_QKV_BM(128, true)
-  } else if (cw == 32)
-    hipLaunchKernelGGL((gemm_fp8_qkv_packed_kernel<kQkBM, 32, kSpP, kSpD, kSpG>), dim3((unsigned)tiles),
+  } else if (cw == 32)  // 64 x 128 (176 tokens) on pk_mainloop_pf
+    hipLaunchKernelGGL((gemm_fp8_qkv_packed_kernel<kQkBM, 32, kSpP, kSpD, kSpG, true>), dim3((unsigned)tiles),
                        dim3(kThreads), 0, (hipStream_t)stream, (const uint8_t*)qa, sa, sa_rows,
                        (const uint8_t*)qw_packed, sw, sw_cols, (int)m, (int)n, (int)k, (int)tiles_m, (int)tiles_n, qe);
   else
