@@ -682,6 +682,15 @@ __device__ __forceinline__ void w4pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], ui
   const int frag = 128 * (r16 & 7) + 1024 * (r16 >> 3);
   const int sw = (r16 & 7) ^ (r16 >> 3);
   const int cA[2] = {16 * ((2 * g) ^ sw), 16 * ((2 * g + 1) ^ sw)};
+  // A fragments of the current substep (a[sub & 1]); a step's first substep is
+  // read during the previous step's last group (the first step's here).
+  i32x4v a[2][RA];
+  auto readA = [&](const uint8_t* st, int sub, int i, i32x4v& dst) {
+    dst = *reinterpret_cast<const i32x4v*>(st + (sub >> 1) * HALF + 2 * i * 1024 + cA[sub & 1]);
+  };
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < RA; ++i) readA(smem + frag, 0, i, a[0][i]);
   // The first fragment of every step is dequantised in the step before (the
   // first step's here).
   u32x4 bfirst;
@@ -697,9 +706,10 @@ __device__ __forceinline__ void w4pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], ui
     static_for<0, 2>([&](auto U_) {
       constexpr int u = decltype(U_)::value;
       const int kt = kb + u;
-      // stage u (written during the previous step) is visible; stage u ^ 1, read
-      // in the previous step, is free for step kt + 1
-      __syncthreads();
+      // Stage u was written during the previous step and made visible by its
+      // barrier; stage u ^ 1, read in the previous step before that barrier, is
+      // written here for step kt + 1. This step's one barrier comes before its
+      // last group, whose MFMAs carry the reads of step kt + 1's first substep.
       const int kta = min(kt + 2, kend - 1);  // the step whose activations and weights are loaded here
       // The step's MFMAs as 4 TJ groups g = (substep s = g / TJ, fragment j =
       // g % TJ), each RA MFMAs on one dequantised weight fragment. The wave
@@ -708,13 +718,8 @@ __device__ __forceinline__ void w4pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], ui
       // before a new substep, its A fragments are spread between this group's
       // MFMAs, a few VALU instructions after each, where they run under them.
       const uint8_t* st = smem + u * STAGE + frag;
+      const uint8_t* stn = smem + (u ^ 1) * STAGE + frag;
       constexpr int NG = 4 * TJ;
-      i32x4v a[2][RA];
-      auto readA = [&](int sub, int i, i32x4v& dst) {
-        dst = *reinterpret_cast<const i32x4v*>(st + (sub >> 1) * HALF + 2 * i * 1024 + cA[sub & 1]);
-      };
-#pragma unroll
-      for (int i = 0; i < RA; ++i) readA(0, i, a[0][i]);
       u32x4 bcur = bfirst;
       static_for<0, NG>([&](auto G_) {
         constexpr int gg = decltype(G_)::value, sub = gg / TJ, j = gg % TJ;
@@ -730,11 +735,13 @@ __device__ __forceinline__ void w4pk_mainloop(f32x4 (&acc)[BM / 16][CW / 16], ui
           d.s16 = sq[u ^ 1][0][0][0];
           d.z = sq[u ^ 1][0][0][1];
         }
+        if constexpr (!in_step) __syncthreads();  // every wave's writes of stage u ^ 1 are done
         static_for<0, RA>([&](auto I_) {
           constexpr int i = decltype(I_)::value;
           mfma_bf16_acc(acc[i][j], bcur, a[sub & 1][i]);
           if constexpr (i < 7) d.template piece<i>();
-          if constexpr (in_step && jn == 0) readA(subn, i, a[subn & 1][i]);
+          if constexpr (in_step && jn == 0) readA(st, subn, i, a[subn & 1][i]);
+          if constexpr (!in_step) readA(stn, 0, i, a[0][i]);  // substep 3 runs on a[1]
           // The step's memory work, one instruction group per MFMA slot: the
           // activation staging (each chunk written to stage u ^ 1, then its
           // register reloaded for step kt + 2) over the first groups, and each
