@@ -426,21 +426,25 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_pk_kernel(
 
   const int frag = 128 * (r16 & 7) + 1024 * (r16 >> 3);
   const int cA[2] = {16 * ((2 * g) ^ (r16 >> 1)), 16 * ((2 * g + 1) ^ (r16 >> 1))};
+  // A fragments of the current substep (af[sub & 1]); a step's first substep is
+  // read at the start of the previous step's last substep (the first step's here).
+  i32x4v af[2][RA];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < RA; ++i) af[0][i] = *reinterpret_cast<const i32x4v*>(smem + frag + 2 * i * 1024 + cA[0]);
   for (int kb = kt0; kb < kt1; kb += 2) {
     static_for<0, 2>([&](auto U_) {
       constexpr int u = decltype(U_)::value;
       const int kt = kb + u;
       if (kt < kt1) {  // uniform: an odd step count ends on u = 0
-        // stage u (written during the previous step) is visible; stage u ^ 1,
-        // read in the previous step, is free for step kt + 1
-        __syncthreads();
+        // Stage u was written during the previous step and made visible by its
+        // barrier; stage u ^ 1, read in the previous step before that barrier,
+        // is written here for step kt + 1. This step's one barrier comes before
+        // its last substep, which reads step kt + 1's first substep into af[0].
         const int kta = min(kt + 2, kt1 - 1);
         writeA(u ^ 1);
         loadA(kta);
         const uint8_t* st = smem + u * STAGE + frag;
-        i32x4v af[2][RA];
-#pragma unroll
-        for (int i = 0; i < RA; ++i) af[0][i] = *reinterpret_cast<const i32x4v*>(st + 2 * i * 1024 + cA[0]);
         static_for<0, 4>([&](auto S_) {
           constexpr int sub = decltype(S_)::value;
           if constexpr (sub < 3) {
@@ -448,6 +452,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_pk_kernel(
             for (int i = 0; i < RA; ++i)
               af[(sub + 1) & 1][i] =
                   *reinterpret_cast<const i32x4v*>(st + ((sub + 1) >> 1) * HALF + 2 * i * 1024 + cA[(sub + 1) & 1]);
+          } else {
+            __syncthreads();  // every wave's writes of stage u ^ 1 are done
+            const uint8_t* stn = smem + (u ^ 1) * STAGE + frag;
+#pragma unroll
+            for (int i = 0; i < RA; ++i) af[0][i] = *reinterpret_cast<const i32x4v*>(stn + 2 * i * 1024 + cA[0]);
           }
 #pragma unroll
           for (int j = 0; j < TJ; ++j) {
