@@ -755,7 +755,7 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k) {
     const int bm = f / 100, sp = f % 100;
     const bool bm_ok =
         cw == 32 ? (bm == 64 || bm == 80 || bm == 96 || bm == 128 || bm == kSpBM) : (bm == 64 || bm == kSpBM);
-    if (bm_ok && n % (4 * cw) == 0 && (sp == 1 || sp == 2 || sp == 3 || sp == 4 || sp == 8) && kt % kSpU == 0 &&
+    if (bm_ok && n % (4 * cw) == 0 && (sp >= 1 && sp <= 6 || sp == 8) && kt % kSpU == 0 &&
         kt / kSpU >= sp) {
       p.bm = bm;
       p.s = sp;
@@ -770,14 +770,19 @@ SplitPlan split_plan(int64_t m, int64_t n, int64_t k) {
     return p;
   }
   if (m <= 256) {
-    // Short m (up to four 64-row tiles): 64 x 256 tiles at two workgroups per
-    // CU, k split 8, 4 or 2 ways, the most that keeps the grid within 256
-    // workgroups: 176 tokens of the 8B shape, o and down 48 tiles x 4 splits
-    // (the 4.47 ms step takes 4.31 ms with both on it, against small_plan's
-    // 64 x 128 tiles for o and 144 x 256 tiles split 8 ways for down).
+    // Short m (up to four 64-row tiles): 64 x 256 tiles, k split the most ways
+    // among 8, 6, 5, 4 and 2 that keeps the grid within 256 workgroups (8, 4
+    // and 2 where they divide k into whole unrolled blocks; 6 and 5, whose
+    // split kernels run pk_mainloop_pf and deal out 2-step blocks, where every
+    // split gets at least two of them): 176 tokens of the 8B shape, o and down
+    // 48 tiles x 5 splits, 240 workgroups (4 splits, 192 workgroups, took the
+    // 4.47 ms step to 4.31 ms against small_plan's 64 x 128 tiles for o and
+    // 144 x 256 tiles split 8 ways for down).
     const int64_t t64 = (m + 63) / 64 * (n / kSpBN);
-    for (int sp = 8; sp >= 2; sp /= 2)
-      if (t64 * sp <= 256 && kt % (sp * kSpU) == 0) return SplitPlan{64, sp};
+    for (const int sp : {8, 6, 5, 4, 2}) {
+      const bool even = sp == 8 || sp == 4 || sp == 2;
+      if (t64 * sp <= 256 && (even ? kt % (sp * kSpU) == 0 : kt >= 4 * sp)) return SplitPlan{64, sp};
+    }
   }
   if (kt < 64) return p;
   // 64 k steps (the 32B o projection, 1024 x 8192 x 5120): where an unsplit
@@ -878,8 +883,9 @@ void launch_split(const void* qa, const float* sa, int sa_rows, const void* qw_p
                   void* y, int64_t ldy, int64_t m, int64_t n, int64_t k, void* part, hipStream_t st) {
   const int64_t tiles_m = (m + BM - 1) / BM, tiles_n = n / (4 * CW);
   // pk_mainloop_pf for 144 x 256 tiles split 4 ways (the 8B down projection at
-  // 576 tokens) and 64 x 256 tiles split 4 ways (o and down at 176 tokens).
-  constexpr bool pf = (BM == 144 || BM == 64) && CW == 64 && S == 4;
+  // 576 tokens) and 64 x 256 tiles split 4, 5 or 6 ways (o and down at 176
+  // tokens; 5 and 6 deal their k steps out in pk_mainloop_pf's 2-step blocks).
+  constexpr bool pf = (BM == 144 && CW == 64 && S == 4) || (BM == 64 && CW == 64 && S >= 4 && S <= 6);
   hipLaunchKernelGGL((gemm_fp8_split_packed_kernel<BM, CW, kSpP, kSpD, kSpG, S, pf>),
                      dim3((unsigned)(tiles_m * tiles_n * S)), dim3(kThreads), 0, st, (const uint8_t*)qa, sa, sa_rows,
                      (const uint8_t*)qw_packed, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)n, (int)k, (int)tiles_m,
@@ -894,6 +900,8 @@ void launch_splits(int s, const void* qa, const float* sa, int sa_rows, const vo
     case 2: launch_split<BM, 2, CW>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
     case 3: launch_split<BM, 3, CW>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
     case 4: launch_split<BM, 4, CW>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
+    case 5: launch_split<BM, 5, CW>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
+    case 6: launch_split<BM, 6, CW>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
     case 8: launch_split<BM, 8, CW>(qa, sa, sa_rows, qw_packed, sw, sw_cols, y, ldy, m, n, k, part, st); break;
     default: break;
   }
@@ -1463,7 +1471,7 @@ extern "C" int ff_gemm_fp8_pk(const void* qa, const float* sa, int sa_rows, cons
   if (splits == S)                                                                                                  \
     hipLaunchKernelGGL((split_reduce_kernel<S>), rgrid, dim3(kThreads), 0, st, (const float*)workspace, mp, sa,     \
                        sa_rows, sw, sw_cols, (bf16_t*)y, ldy, (int)m, (int)n);
-  FF_REDUCE(2) FF_REDUCE(3) FF_REDUCE(4) FF_REDUCE(8)
+  FF_REDUCE(2) FF_REDUCE(3) FF_REDUCE(4) FF_REDUCE(5) FF_REDUCE(6) FF_REDUCE(8)
 #undef FF_REDUCE
   FF_LAUNCH_CHECK("ff_gemm_fp8_pk");
   return FF_OK;

@@ -93,18 +93,22 @@ def test_w4a16_swiglu_shape_query_without_a_gpu(lib_path):
 
 
 # (m, n, k, row tile, splits) the packed FP8 plain GEMM takes: the 8B down
-# projection at the bucket sizes that pick 4 (64-row tiles, short m), 4, 3 and 2
-# splits (k = 12288), the 176-token o projection on 64-row tiles split 4 ways,
+# projection at the bucket sizes that pick 5 (64-row tiles, short m), 4, 3 and 2
+# splits (k = 12288), the 176-token o projection on 64-row tiles split 5 ways
+# (short m: 6 or 5 splits with uneven k ranges where 8, 4 or 2 do not fit: the
+# 2B down at 250 tokens 6, the 4B o at 176 tokens 5; the 2B o at 176 tokens, 16
+# k steps, keeps 4),
 # splits of unequal length where k is not a multiple of 4 x splits x 128 (the
 # 4B and 32B down projections, k = 9728 and 25600),
 # unsplit grids and shapes left to the small tiles or the row-major kernels (0):
 # at k = 8192 a split only where no small tile fills the GPU (the 32B o
 # projection at 1024 and 576 tokens runs unsplit on small tiles).
 # The plan is host code, so the workspace query pins it without a GPU.
-PLAN_SHAPES = [(176, 4096, 12288, 64, 4), (576, 4096, 12288, 144, 4), (640, 4096, 12288, 144, 3),
+PLAN_SHAPES = [(176, 4096, 12288, 64, 5), (576, 4096, 12288, 144, 4), (640, 4096, 12288, 144, 3),
                (1152, 4096, 12288, 144, 2), (300, 2048, 8192, 144, 8), (1000, 6144, 8192, 0, 0),
                (1024, 5120, 8192, 0, 0), (576, 5120, 8192, 0, 0),
-               (576, 12288, 4096, 144, 1), (576, 4096, 4096, 0, 0), (176, 4096, 4096, 64, 4), (64, 2048, 2048, 64, 4),
+               (576, 12288, 4096, 144, 1), (576, 4096, 4096, 0, 0), (176, 4096, 4096, 64, 5), (64, 2048, 2048, 64, 4),
+               (250, 2048, 6144, 64, 6), (176, 2560, 2560, 64, 5), (176, 2048, 2048, 64, 4),
                (300, 4096, 2048, 0, 0), (3, 4096, 4096, 0, 0), (1024, 5120, 25600, 144, 3),
                (576, 2560, 9728, 144, 4), (576, 5120, 25600, 144, 3)]
 

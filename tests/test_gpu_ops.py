@@ -373,12 +373,15 @@ def test_gemm_fp8_swiglu_packed_equals_rowmajor(gpu, m, i, k):
 # workgroups on a short grid; k = 8192 wherever a small tile fills the GPU:
 # 1000 x 6144 and the 32B o projection, 1024 x 5120, on 64 x 256) or the
 # row-major kernels (3 rows, n % 128); short m (176 tokens, 2B widths at 64)
-# takes 64-row tiles with a k split; 576 x 2560 x 9728 (4B down) splits 76 k
+# takes 64-row tiles with a k split (8, 4 or 2 ways where they divide k, 6 or 5
+# ways with uneven k ranges: 176 tokens of the 8B shape 5, the 2B down at 250
+# tokens 6, the 4B down at 176 tokens 6); 576 x 2560 x 9728 (4B down) splits 76 k
 # steps into 20, 20, 20 and 16
 PK_SHAPES = [(576, 4096, 12288, 144, 4), (300, 2048, 8192, 144, 8), (1000, 6144, 8192, 0, 0),
              (1024, 5120, 8192, 0, 0), (576, 2560, 9728, 144, 4),
              (576, 12288, 4096, 144, 1), (640, 4096, 12288, 144, 3), (1152, 4096, 12288, 144, 2),
-             (176, 4096, 12288, 64, 4), (176, 4096, 4096, 64, 4), (64, 2048, 2048, 64, 4), (250, 2048, 6144, 64, 4),
+             (176, 4096, 12288, 64, 5), (176, 4096, 4096, 64, 5), (64, 2048, 2048, 64, 4), (250, 2048, 6144, 64, 6),
+             (176, 2560, 9728, 64, 6),
              (576, 4096, 4096, 0, 0), (500, 4096, 4096, 0, 0), (576, 6144, 4096, 0, 0), (500, 6144, 4096, 0, 0),
              (300, 4096, 2048, 0, 0),
              (3, 4096, 4096, 0, 0), (576, 4160, 12288, 0, 0)]
