@@ -733,7 +733,7 @@ constexpr int kSpU = lcm3(kSpP, kSpD, 2 * kSpG);
 // when k is long enough that the extra reduction pays off (the 8B down
 // projection, 576 x 4096 x 12288); shorter k takes small_plan's tiles (below)
 // or the row-major kernels. ff_set_tuning(FF_TUNE_FP8_PK_SPLIT, 100 bm + s)
-// forces bm in {64, 144} and s in {1, 2, 3, 4, 8} for measurement sweeps.
+// forces bm in {64, 144} and s in {1, ..., 6, 8} for measurement sweeps.
 // (80-row tiles at two workgroups per CU with half the k splits, fewer fp32
 // partials on the same grid, measured slower: the 8B FP8 step 6.35 -> 6.85 ms
 // with the down projection on 80 x 256 tiles split 2 ways instead of 144 x 256

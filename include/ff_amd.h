@@ -47,8 +47,9 @@ int ff_device_check(void);
 #define FF_TUNE_QKV_PK_TILE 7     /* ff_gemm_fp8_qkv_pk: 1 64x256 packed, 2 64x128 packed, 3 row-major,
                                      4 96x128, 5 144x128, 6 128x128 packed */
 #define FF_TUNE_SWIGLU_PK_TILE 8  /* ff_gemm_fp8_swiglu_pk / _static: 1000 BM + CW (BM x 8 CW tile) */
-#define FF_TUNE_FP8_PK_SPLIT 9    /* ff_gemm_fp8_pk: 100 BM + k splits, BM 64 or 144 (256-column tiles);
-                                     100000 + 100 BM + k splits, BM 64, 80, 96, 128 or 144 (128-column tiles) */
+#define FF_TUNE_FP8_PK_SPLIT 9    /* ff_gemm_fp8_pk: 100 BM + k splits (1..6 or 8), BM 64 or 144 (256-column
+                                     tiles); 100000 + 100 BM + k splits, BM 64, 80, 96, 128 or 144 (128-column
+                                     tiles) */
 #define FF_TUNE_BF16_PK_SPLIT 10  /* ff_gemm_bf16_pk_ws / _ln: 1 no k split, 2..8 the split count */
 #define FF_TUNE_FP8_PK_SPLIT_SHORT_K 11 /* as FF_TUNE_FP8_PK_SPLIT, for k <= 4096 only (ahead of it there) */
 int ff_set_tuning(int knob, int value);
