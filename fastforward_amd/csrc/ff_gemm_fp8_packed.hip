@@ -415,6 +415,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
   __shared__ __align__(1024) uint8_t smem[SMEM];
   __shared__ float pm16[BM][Q16];  // max |h| per token and 16-channel block of the tile
   __shared__ uint16_t silu_tab[kSiluEntries];
+  // sw of the tile's gate then up channels, sa of its tokens: copied in the
+  // prologue (behind the table fill), so the epilogue reads them from LDS
+  // instead of starting with their memory latency (no registers are left to
+  // hold them through the main loop)
+  __shared__ float sc_w[2 * CH], sc_a[BM];
 
   const int nblk = tiles_m * tiles_n;
   const int b = blockIdx.x;
@@ -436,12 +441,27 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
     sB[j] = (uint32_t)(row / 16) * 2048u;
   }
   f32x4 acc[RA][TJ];
+  auto pre = [&] {
+    constexpr int NSC = (2 * CH + BM + kThreads - 1) / kThreads;
+    float v[NSC];
+#pragma unroll
+    for (int c = 0; c < NSC; ++c) {  // the loads first: the table fill runs under them
+      const int e = tid + c * kThreads;
+      if (e < 2 * CH) v[c] = sw[SQ ? 0 : (e < CH ? 0 : half - CH) + tn * CH + e];
+      else if (e < 2 * CH + BM) v[c] = sa[SQ ? 0 : min(m0 + e - 2 * CH, M - 1)];
+    }
+    silu_table_fill<kThreads>(silu_tab, tid);
+#pragma unroll
+    for (int c = 0; c < NSC; ++c) {
+      const int e = tid + c * kThreads;
+      if (e < 2 * CH) sc_w[e] = v[c];
+      else if (e < 2 * CH + BM) sc_a[e - 2 * CH] = v[c];
+    }
+  };
   if constexpr (PF)
-    pk_mainloop_pf<BM, CW, P, D>(acc, smem, qa, M, K, m0, qwp, (uint32_t)(2 * half) * (uint32_t)K, sB, 0, KT,
-                                 [&] { silu_table_fill<kThreads>(silu_tab, tid); });
+    pk_mainloop_pf<BM, CW, P, D>(acc, smem, qa, M, K, m0, qwp, (uint32_t)(2 * half) * (uint32_t)K, sB, 0, KT, pre);
   else
-    pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)(2 * half) * (uint32_t)K, sB, 0, KT,
-                                 [&] { silu_table_fill<kThreads>(silu_tab, tid); });
+    pk_mainloop<BM, CW, P, D, G>(acc, smem, qa, M, K, m0, qwp, (uint32_t)(2 * half) * (uint32_t)K, sB, 0, KT, pre);
 
   // g, u = bf16((acc * sa) * sw); h = bf16(bf16(silu(g)) * u), in registers:
   // lane 16 g + r holds token 16 i + r, channels c + 4 g .. + 3 of block t.
@@ -455,8 +475,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
   for (int t = 0; t < TT; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      swg[t][r] = sw[SQ ? 0 : c_base + 16 * t + r];
-      swu[t][r] = sw[SQ ? 0 : half + c_base + 16 * t + r];
+      swg[t][r] = sc_w[wave * WCH + 4 * g + 16 * t + r];
+      swu[t][r] = sc_w[CH + wave * WCH + 4 * g + 16 * t + r];
     }
   // First every g of the tile and its table read (the reads are all in flight
   // before the first result is needed), then h.
@@ -464,7 +484,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
   float sav[RA];
 #pragma unroll
   for (int i = 0; i < RA; ++i) {
-    sav[i] = sa[SQ ? 0 : min(m0 + 16 * i + r16, M - 1)];
+    sav[i] = sc_a[16 * i + r16];
 #pragma unroll
     for (int t = 0; t < TT; ++t)
 #pragma unroll
@@ -524,22 +544,38 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_swiglu_packed_kernel(
 // 16 g + r of fragment (i, j) writes token m0 + 16 i + r, columns
 // n0 + wave CW + 16 j + 4 g .. + 3. sa per row if sa_rows else one value; sw
 // per column if sw_cols else one value.
+// The scales of this lane's outputs of a BM x 4 CW tile in the transposed
+// accumulator layout: sa of tokens m0 + 16 i + r16, sw of columns c0 + 16 j +
+// 4 g .. + 3 (c0 = the wave's first column). Loaded before the main loop, so
+// the epilogue does not start with their memory latency.
+template <int RA, int TJ>
+struct PkScales {
+  float sav[RA];
+  float swv[TJ][4];
+  __device__ __forceinline__ void load(const float* __restrict__ sa, int sa_rows, const float* __restrict__ sw,
+                                       int sw_cols, int M, int m0, int c0) {
+    const int lane = threadIdx.x & 63, r16 = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < RA; ++i) sav[i] = sa[sa_rows ? min(m0 + 16 * i + r16, M - 1) : 0];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) swv[j][r] = sw[sw_cols ? c0 + 16 * j + 4 * g + r : 0];
+  }
+};
+
 template <int BM, int CW>
-__device__ __forceinline__ void pk_store_tile(const f32x4 (&acc)[BM / 16][CW / 16], const float* __restrict__ sa,
-                                              int sa_rows, const float* __restrict__ sw, int sw_cols,
-                                              bf16_t* __restrict__ y, int64_t ldy, int M, int m0, int n0) {
+__device__ __forceinline__ void pk_store_tile(const f32x4 (&acc)[BM / 16][CW / 16],
+                                              const PkScales<BM / 16, CW / 16>& sc, bf16_t* __restrict__ y,
+                                              int64_t ldy, int M, int m0, int n0) {
   constexpr int RA = BM / 16, TJ = CW / 16;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g = lane >> 4;
-  float sav[RA];
-#pragma unroll
-  for (int i = 0; i < RA; ++i) sav[i] = sa[sa_rows ? min(m0 + 16 * i + r16, M - 1) : 0];
+  const float(&sav)[RA] = sc.sav;
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
     const int col = n0 + wave * CW + 16 * j + 4 * g;
-    float swv[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) swv[r] = sw[sw_cols ? col + r : 0];
+    const float(&swv)[4] = sc.swv[j];
 #pragma unroll
     for (int i = 0; i < RA; ++i) {
       const int m = m0 + 16 * i + r16;
@@ -588,6 +624,8 @@ __global__ __launch_bounds__(kThreads, BM <= 96 && !PF ? 2 : 1) void gemm_fp8_sp
 #pragma unroll
   for (int j = 0; j < TJ; ++j) sB[j] = (uint32_t)((n0 + wave_s * CW + 16 * j) / 16) * 2048u;
   f32x4 acc[RA][TJ];
+  PkScales<RA, TJ> sc;
+  if constexpr (S == 1) sc.load(sa, sa_rows, sw, sw_cols, M, m0, n0 + wave_s * CW);
   if constexpr (PF)
     pk_mainloop_pf<BM, CW, P, D>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, kt0, nk, [] {});
   else
@@ -596,7 +634,7 @@ __global__ __launch_bounds__(kThreads, BM <= 96 && !PF ? 2 : 1) void gemm_fp8_sp
     // the fp32 partial tile, row-major over the rows padded to whole tiles
     store_tile_rows_lds<BM, CW, SMEM>(acc, smem, part + ((int64_t)split * tiles_m * BM + m0) * N + n0, N, tid);
   } else {
-    pk_store_tile<BM, CW>(acc, sa, sa_rows, sw, sw_cols, y, ldy, M, m0, n0);
+    pk_store_tile<BM, CW>(acc, sc, y, ldy, M, m0, n0);
   }
 }
 
@@ -979,6 +1017,8 @@ __global__ __launch_bounds__(kThreads, BM <= 96 && !PF ? 2 : 1) void gemm_fp8_qk
 #pragma unroll
   for (int j = 0; j < TJ; ++j) sB[j] = (uint32_t)((n0 + wave_s * CW + 16 * j) / 16) * 2048u;
   f32x4 acc[RA][TJ];
+  PkScales<RA, TJ> sc;
+  sc.load(sa, sa_rows, sw, sw_cols, M, m0, n0 + wave_s * CW);
   if constexpr (PF)
     pk_mainloop_pf<BM, CW, P, D>(acc, smem, qa, M, K, m0, qwp, (uint32_t)N * (uint32_t)K, sB, 0, KT, [] {});
   else
@@ -1003,15 +1043,11 @@ __global__ __launch_bounds__(kThreads, BM <= 96 && !PF ? 2 : 1) void gemm_fp8_qk
 
   __syncthreads();  // every wave's last activation-stage reads are done before the tile overwrites them
   bf16_t* tile = reinterpret_cast<bf16_t*>(smem);
-  float sav[RA];
-#pragma unroll
-  for (int i = 0; i < RA; ++i) sav[i] = sa[sa_rows ? min(m0 + 16 * i + r16, M - 1) : 0];
+  const float(&sav)[RA] = sc.sav;
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
     const int col = wave * CW + 16 * j + 4 * g;
-    float swv[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) swv[r] = sw[sw_cols ? n0 + col + r : 0];
+    const float(&swv)[4] = sc.swv[j];
 #pragma unroll
     for (int i = 0; i < RA; ++i)
       *reinterpret_cast<u32x2*>(tile + (16 * i + r16) * LD + col) =
