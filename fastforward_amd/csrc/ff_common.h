@@ -43,6 +43,12 @@ __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds) {
                : "memory", "m0");
 }
 
+// The 4-byte form: lane l's dword lands at lds + 4 l.
+__device__ __forceinline__ void lds_dma4(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(src), "s"(lds)
+               : "memory", "m0");
+}
+
 // Wait until at most N vector-memory operations of this wave are outstanding.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

@@ -219,6 +219,8 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_bf16_kernel(
     bf16_t* y, int64_t ldy, const bf16_t* resid, int64_t ldr, int M, int N, int K, int tiles_m, int tiles_n) {
   using C = GemmCfg<BM, BN, S>;
   __shared__ __align__(1024) uint8_t smem[C::SMEM];
+  __shared__ __align__(16) bf16_t sbias[BN];  // the tile's bias columns
+  static_assert(BN == 128, "one wave's dword DMA carries the tile's bias");
   const int nblk = tiles_m * tiles_n;
   const int blk_id = blockIdx.x;
   int logical = blk_id;
@@ -259,6 +261,11 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_bf16_kernel(
     for (int j = 0; j < C::WJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int KT = K / 64;
+  // Wave 0 copies the tile's bias into LDS ahead of the first stage (one
+  // dword DMA: two columns a lane, the address clamped in bounds past N);
+  // issued before the stages, it has landed when the loop's first wait for
+  // stage 0 returns, and that iteration's barrier publishes it.
+  if (wave == 0) lds_dma4(bias + min(n0 + 2 * lane, N - 2), lds_addr(sbias));
 #pragma unroll
   for (int st = 0; st < S - 1; ++st)
     if (st < KT) issue(st, st);
@@ -297,7 +304,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_bf16_kernel(
     for (int j = 0; j < C::WJ; ++j) {
       const int n = n0 + wn * (BN / 2) + 16 * j + 4 * g;
       if (n >= N) continue;  // N % 4 == 0: a 4-column group is all in or all out
-      const u32x2 bb = *reinterpret_cast<const u32x2*>(bias + n);
+      const u32x2 bb = *reinterpret_cast<const u32x2*>(sbias + n - n0);
       float v[4] = {bf16_to_f32(bb.x & 0xFFFFu), bf16_to_f32(bb.x >> 16), bf16_to_f32(bb.y & 0xFFFFu),
                     bf16_to_f32(bb.y >> 16)};
 #pragma unroll
@@ -358,6 +365,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_pk_kernel(
   constexpr int HALF = BM * 128, STAGE = 2 * HALF;
   static_assert(A_CHUNKS >= kThreads, "at least one full activation round");
   __shared__ __align__(1024) uint8_t smem[2 * STAGE];
+  __shared__ __align__(16) float sbias[PART ? 1 : 4 * CW];  // the tile's bias columns, as fp32
 
   const int S = PART ? splits : 1;
   const int nblk = tiles_m * tiles_n * S;
@@ -418,9 +426,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_pk_kernel(
 #pragma unroll
     for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // The bias is read ahead of the first step (its latency then passes under
+  // the prologue's loads) and kept in LDS for the epilogue.
+  uint32_t braw = 0;
+  if constexpr (!PART)
+    if (tid < 4 * CW) braw = bias[n0 + tid];
   loadA(kt0);
   loadB(kt0, 0);
   writeA(0);
+  if constexpr (!PART)
+    if (tid < 4 * CW) sbias[tid] = bf16_to_f32(braw);
   loadA(min(kt0 + 1, kt1 - 1));
   loadB(min(kt0 + 1, kt1 - 1), 1);
 
@@ -487,12 +502,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_pk_kernel(
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
       const int n = n0 + wave * CW + 16 * j + 4 * g;
-      const u32x2 bb = *reinterpret_cast<const u32x2*>(bias + n);
-      float v[4] = {bf16_to_f32(bb.x & 0xFFFFu), bf16_to_f32(bb.x >> 16), bf16_to_f32(bb.y & 0xFFFFu),
-                    bf16_to_f32(bb.y >> 16)};
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(sbias + n - n0);
+      float v[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float t = round_bf16(acc[i][j][r] + v[r]);
+        float t = round_bf16(acc[i][j][r] + bv[r]);
         if constexpr (ACT == kGeluTanh) t = round_bf16(gelu_tanh(t));
         if constexpr (ACT == kGeluErf) t = round_bf16(gelu_erf(t));
         v[r] = t;
