@@ -366,6 +366,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_pk_kernel(
   static_assert(A_CHUNKS >= kThreads, "at least one full activation round");
   __shared__ __align__(1024) uint8_t smem[2 * STAGE];
   __shared__ __align__(16) float sbias[PART ? 1 : 4 * CW];  // the tile's bias columns, as fp32
+  // The residual tile (RESID): wave w's BM x CW columns at sres + w BM CW,
+  // row-major, copied in by 16-byte LDS DMA after the prologue's loads so that
+  // the epilogue reads it from LDS. Needs 16-byte aligned rows (resid and ldr);
+  // otherwise the epilogue reads it from global memory.
+  constexpr bool RT = RESID && !PART;
+  constexpr int RCH = CW / 8, RQ = BM * RCH / 64;  // chunks per slab row, DMAs per wave
+  static_assert(BM * RCH % 64 == 0, "whole DMA instructions per slab");
+  __shared__ __align__(16) bf16_t sres[RT ? BM * 4 * CW : 1];
 
   const int S = PART ? splits : 1;
   const int nblk = tiles_m * tiles_n * S;
@@ -438,6 +446,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_pk_kernel(
     if (tid < 4 * CW) sbias[tid] = bf16_to_f32(braw);
   loadA(min(kt0 + 1, kt1 - 1));
   loadB(min(kt0 + 1, kt1 - 1), 1);
+  const bool rdma = RT && ((uintptr_t)resid & 15) == 0 && (ldr & 7) == 0;
+  if constexpr (RT) {
+    if (rdma) {
+      const uint32_t slab = lds_addr(sres) + (uint32_t)wave_s * (BM * CW * 2);
+#pragma unroll
+      for (int q = 0; q < RQ; ++q) {
+        const int c = 64 * q + lane, row = c / RCH, ch = c % RCH;
+        lds_dma16(resid + (int64_t)min(m0 + row, M - 1) * ldr + n0 + wave * CW + 8 * ch, slab + 1024u * q);
+      }
+    }
+  }
 
   const int frag = 128 * (r16 & 7) + 1024 * (r16 >> 3);
   const int cA[2] = {16 * ((2 * g) ^ (r16 >> 1)), 16 * ((2 * g + 1) ^ (r16 >> 1))};
@@ -495,6 +514,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_pk_kernel(
       for (int j = 0; j < TJ; ++j) *reinterpret_cast<f32x4*>(dst + (int64_t)16 * i * N + 16 * j) = acc[i][j];
     return;
   }
+  if constexpr (RT)
+    if (rdma) {
+      wait_vmcnt<0>();  // this wave's residual DMAs have landed (each wave reads only its own slab)
+      asm volatile("" : : : "memory");
+    }
 #pragma unroll
   for (int i = 0; i < RA; ++i) {
     const int m = m0 + 16 * i + r16;
@@ -512,7 +536,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_pk_kernel(
         v[r] = t;
       }
       if constexpr (RESID) {
-        const u32x2 rr = *reinterpret_cast<const u32x2*>(resid + (int64_t)m * ldr + n);
+        const u32x2 rr = rdma ? *reinterpret_cast<const u32x2*>(sres + (wave * BM + 16 * i + r16) * CW + 16 * j + 4 * g)
+                              : *reinterpret_cast<const u32x2*>(resid + (int64_t)m * ldr + n);
         v[0] += bf16_to_f32(rr.x & 0xFFFFu);
         v[1] += bf16_to_f32(rr.x >> 16);
         v[2] += bf16_to_f32(rr.y & 0xFFFFu);

@@ -161,6 +161,29 @@ def test_gemm_bf16_packed_equals_rowmajor(gpu, m, k, n, act, resid):
     assert torch.equal(outs[0], outs[1])
 
 
+@pytest.mark.parametrize("m,k,n", [(2048, 1152, 1152), (2000, 1536, 1152)])
+@pytest.mark.parametrize("pad", [8, 4])
+def test_gemm_bf16_packed_strided_residual(gpu, m, k, n, pad):
+    """The packed kernel's residual add with the residual a strided view
+    (row stride n + pad elements) and the output a separate array: pad 8 keeps
+    the residual rows 16-byte aligned (the epilogue reads the tile that was
+    copied into LDS ahead of the main loop), pad 4 does not (it reads global
+    memory); both == the LDS-staged kernel on the row-major weight, bit for bit,
+    and the residual is left unchanged."""
+    from fastforward_amd.vision import Lin, linear
+    x = torch.randn(m, k, generator=_g(m + n + 11)).to(BF16).to(DEV)
+    w = (torch.randn(n, k, generator=_g(k + 12)) * 0.03).to(BF16).to(DEV)
+    b = (torch.randn(n, generator=_g(n + 13)) * 0.1).to(BF16).to(DEV)
+    wide = torch.randn(m, n + pad, generator=_g(n + 14)).to(BF16).to(DEV)
+    h = wide[:, pad: pad + n]
+    assert h.stride(0) == n + pad and (h.data_ptr() % 16 == 0 and h.stride(0) % 8 == 0) == (pad == 8)
+    before = wide.clone()
+    outs = [linear(x, lin, resid=h) for lin in (Lin(w, b), Lin(w, b).pack())]
+    assert not torch.isnan(outs[1].float()).any()
+    assert torch.equal(outs[0], outs[1])
+    assert torch.equal(wide, before)
+
+
 # (m, k, n, act, resid): grids with no one-round packed tile whose unsplit
 # fallback fills less than half the GPU, which the workspace entry points split
 # along k: the tower at 400 patches (proj and fc2 with the residual in place,
