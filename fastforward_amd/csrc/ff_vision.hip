@@ -650,40 +650,35 @@ __global__ __launch_bounds__(kThreads) void vision_rope_kernel(
 
 // V^T with zero padding: v (token stride v_ts, head stride v_hs, hd columns)
 // -> vt (heads, 128, t_pad), rows [hd, 128) and tokens [n, t_pad) zero. One
-// workgroup per (head, 64 tokens): the 64 x hd block is staged in LDS, then
-// each thread writes 8 consecutive tokens of one d row.
-__device__ __forceinline__ void vision_vt_block(int blk, float (&tile)[64][129], const bf16_t* __restrict__ v,
+// workgroup per (head, 64 tokens): the 64 x hd block is staged in LDS as raw
+// bf16 (17 KB, so that a launch that also runs other workgroups keeps eight
+// workgroups per CU), then each thread writes 8 consecutive tokens of one d row.
+constexpr int kVtPitch = 136;  // bf16 per staged token row (128 + 8: 8-byte aligned rows)
+__device__ __forceinline__ void vision_vt_block(int blk, uint16_t (&tile)[64][kVtPitch], const bf16_t* __restrict__ v,
                                                 int64_t v_ts, int64_t v_hs, bf16_t* __restrict__ vt, int n, int t_pad,
                                                 int heads, int hd) {
   const int head = blk % heads, t0 = (blk / heads) * 64;
   for (int c = threadIdx.x; c < 64 * 32; c += kThreads) {
     const int tt = c / 32, d = (c % 32) * 4;
     const int tok = t0 + tt;
-    float f[4] = {0.f, 0.f, 0.f, 0.f};
-    if (tok < n && d < hd) {
-      const u32x2 x = *reinterpret_cast<const u32x2*>(v + (int64_t)tok * v_ts + (int64_t)head * v_hs + d);
-      f[0] = bf16_to_f32(x.x & 0xFFFFu);
-      f[1] = bf16_to_f32(x.x >> 16);
-      f[2] = bf16_to_f32(x.y & 0xFFFFu);
-      f[3] = bf16_to_f32(x.y >> 16);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) tile[tt][d + e] = f[e];
+    u32x2 x{0u, 0u};
+    if (tok < n && d < hd) x = *reinterpret_cast<const u32x2*>(v + (int64_t)tok * v_ts + (int64_t)head * v_hs + d);
+    *reinterpret_cast<u32x2*>(&tile[tt][d]) = x;
   }
   __syncthreads();
   for (int c = threadIdx.x; c < 128 * 8; c += kThreads) {
     const int d = c % 128, tb = (c / 128) * 8;
-    float f[8];
+    uint32_t w[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = tile[tb + e][d];
-    *reinterpret_cast<u32x4*>(vt + ((int64_t)head * 128 + d) * t_pad + t0 + tb) = pack8(f);
+    for (int e = 0; e < 4; ++e) w[e] = (uint32_t)tile[tb + 2 * e][d] | ((uint32_t)tile[tb + 2 * e + 1][d] << 16);
+    *reinterpret_cast<u32x4*>(vt + ((int64_t)head * 128 + d) * t_pad + t0 + tb) = u32x4{w[0], w[1], w[2], w[3]};
   }
 }
 
 __global__ __launch_bounds__(kThreads) void vision_vt_kernel(const bf16_t* __restrict__ v, int64_t v_ts,
                                                              int64_t v_hs, bf16_t* __restrict__ vt, int n, int t_pad,
                                                              int heads, int hd) {
-  __shared__ float tile[64][129];
+  __shared__ __align__(16) uint16_t tile[64][kVtPitch];
   vision_vt_block(blockIdx.x, tile, v, v_ts, v_hs, vt, n, t_pad, heads, hd);
 }
 
@@ -743,7 +738,7 @@ __global__ __launch_bounds__(kThreads) void vision_qkv_kernel(const bf16_t* __re
                                                               const float* __restrict__ sin, bf16_t* __restrict__ yq,
                                                               bf16_t* __restrict__ yk, bf16_t* __restrict__ vt, int n,
                                                               int t_pad, int heads, int hd, int nrope) {
-  __shared__ float tile[64][129];
+  __shared__ __align__(16) uint16_t tile[64][kVtPitch];
   const int64_t ts = 3 * (int64_t)heads * hd;
   if ((int)blockIdx.x < nrope) {
     vision_rope8_block(blockIdx.x, qkv, ts, cos, sin, yq, yk, n, heads, hd);
