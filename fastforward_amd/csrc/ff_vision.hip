@@ -682,52 +682,69 @@ __global__ __launch_bounds__(kThreads) void vision_vt_kernel(const bf16_t* __res
   vision_vt_block(blockIdx.x, tile, v, v_ts, v_hs, vt, n, t_pad, heads, hd);
 }
 
-// The rotary of vision_rope_block for the packed qkv output, 8 columns (one
-// 16-byte store) per thread: thread -> (q or k, token, head, 8-column group
-// of the 128-column output row); the partners (hd / 2 away, hd % 8 == 0 so
-// each 4-column half of a group lies on one side of hd / 2) come as two 8-byte
-// loads, cos / sin as two 16-byte loads each. The same two fp32 products and
-// sum per element, rounded once.
+// The rotary of vision_rope_block for the packed qkv output, two 8-column
+// groups (two 16-byte stores) per thread: thread -> (q or k, token, head,
+// group pair c and c + 64 of the 128-column output row, c in 0, 8, .., 56);
+// the partners (hd / 2 away, hd % 8 == 0 so each 4-column half of a group
+// lies on one side of hd / 2) come as two 8-byte loads, cos / sin as two
+// 16-byte loads each; both groups' loads are issued before either's
+// arithmetic. The same two fp32 products and sum per element, rounded once.
 __device__ __forceinline__ void vision_rope8_block(int64_t blk, const bf16_t* __restrict__ qkv, int64_t ts,
                                                    const float* __restrict__ cos, const float* __restrict__ sin,
                                                    bf16_t* __restrict__ yq, bf16_t* __restrict__ yk, int n,
                                                    int heads, int hd) {
   const int64_t i = blk * kThreads + threadIdx.x;
-  const int64_t per = (int64_t)n * heads * 16;
+  const int64_t per = (int64_t)n * heads * 8;
   if (i >= 2 * per) return;
   const bool isk = i >= per;
   const int64_t r = isk ? i - per : i;
-  const int c = (int)(r & 15) * 8;
-  const int64_t th = r >> 4;
+  const int64_t th = r >> 3;
   const int head = (int)(th % heads);
   const int64_t tok = th / heads;
-  bf16_t* dst = (isk ? yk : yq) + ((int64_t)head * n + tok) * 128 + c;
-  if (c >= hd) {
-    *reinterpret_cast<u32x4*>(dst) = u32x4{0u, 0u, 0u, 0u};
-    return;
-  }
+  bf16_t* row = (isk ? yk : yq) + ((int64_t)head * n + tok) * 128;
   const bf16_t* xr = qkv + tok * ts + (int64_t)(isk ? heads + head : head) * hd;
   const int half = hd / 2;
-  float x8[8], p8[8], c8[8], s8[8];
-  unpack8(*reinterpret_cast<const u32x4*>(xr + c), x8);
+  u32x4 xv[2];
+  u32x2 pv[2][2];
+  float4 cv[2][2], sv[2][2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int cc = c + 4 * h;
-    const bool lo = cc < half;
-    const u32x2 pv = *reinterpret_cast<const u32x2*>(xr + (lo ? cc + half : cc - half));
-    const float4 cv = *reinterpret_cast<const float4*>(cos + tok * hd + cc);
-    const float4 sv = *reinterpret_cast<const float4*>(sin + tok * hd + cc);
-    const float pf[4] = {bf16_to_f32(pv.x & 0xFFFFu), bf16_to_f32(pv.x >> 16), bf16_to_f32(pv.y & 0xFFFFu),
-                         bf16_to_f32(pv.y >> 16)};
+  for (int u = 0; u < 2; ++u) {
+    const int c = (int)(r & 7) * 8 + 64 * u;
+    if (c < hd) {
+      xv[u] = *reinterpret_cast<const u32x4*>(xr + c);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) p8[4 * h + e] = lo ? -pf[e] : pf[e];
-    c8[4 * h] = cv.x; c8[4 * h + 1] = cv.y; c8[4 * h + 2] = cv.z; c8[4 * h + 3] = cv.w;
-    s8[4 * h] = sv.x; s8[4 * h + 1] = sv.y; s8[4 * h + 2] = sv.z; s8[4 * h + 3] = sv.w;
+      for (int h = 0; h < 2; ++h) {
+        const int cc = c + 4 * h;
+        pv[u][h] = *reinterpret_cast<const u32x2*>(xr + (cc < half ? cc + half : cc - half));
+        cv[u][h] = *reinterpret_cast<const float4*>(cos + tok * hd + cc);
+        sv[u][h] = *reinterpret_cast<const float4*>(sin + tok * hd + cc);
+      }
+    }
   }
-  float o[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = x8[e] * c8[e] + p8[e] * s8[e];
-  *reinterpret_cast<u32x4*>(dst) = pack8(o);
+  for (int u = 0; u < 2; ++u) {
+    const int c = (int)(r & 7) * 8 + 64 * u;
+    if (c >= hd) {
+      *reinterpret_cast<u32x4*>(row + c) = u32x4{0u, 0u, 0u, 0u};
+      continue;
+    }
+    float x8[8], p8[8], c8[8], s8[8];
+    unpack8(xv[u], x8);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const bool lo = c + 4 * h < half;
+      const float pf[4] = {bf16_to_f32(pv[u][h].x & 0xFFFFu), bf16_to_f32(pv[u][h].x >> 16),
+                           bf16_to_f32(pv[u][h].y & 0xFFFFu), bf16_to_f32(pv[u][h].y >> 16)};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p8[4 * h + e] = lo ? -pf[e] : pf[e];
+      c8[4 * h] = cv[u][h].x; c8[4 * h + 1] = cv[u][h].y; c8[4 * h + 2] = cv[u][h].z; c8[4 * h + 3] = cv[u][h].w;
+      s8[4 * h] = sv[u][h].x; s8[4 * h + 1] = sv[u][h].y; s8[4 * h + 2] = sv[u][h].z; s8[4 * h + 3] = sv[u][h].w;
+    }
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = x8[e] * c8[e] + p8[e] * s8[e];
+    *reinterpret_cast<u32x4*>(row + c) = pack8(o);
+  }
 }
 
 // Both of the above for the packed qkv output (n, 3, heads, hd) in one launch:
@@ -1114,7 +1131,7 @@ extern "C" int ff_vision_qkv(const void* qkv, const float* cos, const float* sin
   FF_REQUIRE(ff_aligned(qkv, 16) && ff_aligned(cos, 16) && ff_aligned(sin, 16) && ff_aligned(yq, 16) &&
                  ff_aligned(yk, 16) && ff_aligned(vt, 16),
              "ff_vision_qkv: alignment (16 bytes)");
-  const int64_t rope_threads = 2 * n * heads * (128 / 8);
+  const int64_t rope_threads = 2 * n * heads * (128 / 16);
   const int nrope = (int)((rope_threads + kThreads - 1) / kThreads);
   const int nvt = (int)(heads * (t_pad / 64));
   hipLaunchKernelGGL(vision_qkv_kernel, dim3((unsigned)(nrope + nvt)), dim3(kThreads), 0, (hipStream_t)stream,
