@@ -1120,10 +1120,11 @@ __global__ __launch_bounds__(kThreads) void unpack_fp8_kernel(const uint8_t* __r
 // row swaps. Plain product: one workgroup per 16-row group, its 4 waves taking
 // every 4th k step and their sums added in wave order through LDS. SwiGLU: one
 // workgroup per 64 channels, wave w the gate and up rows of channels 16 w ..
-// + 15 over all k steps. Loads of four k steps are issued before their
-// products.
+// + 15 over all k steps. The plain product issues a wave's loads of eight k
+// steps before their products (each wave still adds its k steps in order, so
+// the batch size does not change the sums).
 constexpr int kGemvPkMaxM = 4;
-constexpr int kGemvPkU = 4;  // k steps whose loads are in flight together
+constexpr int kGemvPkU = 8;  // k steps whose loads are in flight together
 
 __device__ __forceinline__ void e4m3x16_to_f32(const u32x4 v, float* f) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
